@@ -1,0 +1,430 @@
+// C ABI of the gfx950 sampler: contexts, workspace, per-row plans, argument
+// validation and the host / device entry points declared in
+// include/hachiue_sampler.h.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "hachiue_sampler.h"
+#include "sampler_internal.h"
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int status, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return status;
+}
+
+#define HS_HIP(call)                                                                \
+  do {                                                                              \
+    hipError_t e_ = (call);                                                         \
+    if (e_ != hipSuccess)                                                           \
+      return fail(HS_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_));       \
+  } while (0)
+
+// Grow-only device buffer.
+struct DevBuf {
+  void *p = nullptr;
+  size_t bytes = 0;
+  hipError_t ensure(size_t need) {
+    if (need <= bytes) return hipSuccess;
+    if (p) {
+      hipError_t e = hipDeviceSynchronize();   // no launch may still use it
+      if (e != hipSuccess) return e;
+      (void)hipFree(p);
+      p = nullptr;
+      bytes = 0;
+    }
+    size_t b = need + need / 4;
+    hipError_t e = hipMalloc(&p, b);
+    if (e != hipSuccess) { p = nullptr; return e; }
+    bytes = b;
+    return hipSuccess;
+  }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+};
+
+std::mutex g_prep_mu;
+std::vector<int> g_prepared;
+
+}  // namespace
+
+struct hs_context {
+  int device = 0;
+  // workspace
+  DevBuf plans, cand, cand_count, info;
+  int64_t cand_count_rows = 0;     // rows whose counter is known to be zero
+  // plan upload cache
+  std::vector<hs::RowPlan> last_plans;
+  hs::RowPlan *plan_staging = nullptr;   // pinned
+  size_t plan_staging_rows = 0;
+  hipEvent_t plan_done = nullptr;
+  bool plan_pending = false;
+  // host entry points
+  DevBuf h_logits, h_hist, h_off, h_u, h_tok;
+  hipStream_t stream = nullptr;
+};
+
+namespace {
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    if (prev != dev) (void)hipSetDevice(dev);
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+  }
+};
+
+// src/sampler.ts:49 k = Math.max(1, Math.min(topK > 0 ? topK : 64, vocab)),
+// truncated as `new Int32Array(k)` truncates a fractional length.
+int64_t resolve_k(double top_k, int64_t vocab) {
+  const double t = (top_k > 0) ? top_k : 64.0;
+  const double m = t < (double)vocab ? t : (double)vocab;
+  const double k = m > 1.0 ? m : 1.0;
+  return (int64_t)floor(k);
+}
+
+int build_plans(const hs_sample_config *cfgs, int rows, int vocab, std::vector<hs::RowPlan> &out,
+                bool *any_pf) {
+  out.resize((size_t)rows);
+  *any_pf = false;
+  for (int r = 0; r < rows; ++r) {
+    const hs_sample_config &c = cfgs[r];
+    hs::RowPlan p;
+    memset(&p, 0, sizeof p);
+    p.temperature = c.temperature;
+    p.top_p = c.top_p;
+    p.min_p = c.min_p;
+    p.rep = c.repetition_penalty;
+    p.pres = c.presence_penalty;
+    p.freq = c.frequency_penalty;
+    p.pen = (c.repetition_penalty != 1.0 ? hs::kPenRep : 0) |
+            ((c.presence_penalty != 0.0 || c.frequency_penalty != 0.0) ? hs::kPenPF : 0);
+    if (p.pen & hs::kPenPF) *any_pf = true;
+    if (c.temperature <= 0) {   // src/sampler.ts:36 (NaN is not <= 0)
+      p.mode = hs::kModeGreedy;
+      p.k = 1;
+    } else {
+      const int64_t k = resolve_k(c.top_k, vocab);
+      p.k = (int32_t)k;
+      if (k <= hs::kSmallK) p.mode = hs::kModeSmall;
+      else if (k <= hs::kMaxK) p.mode = hs::kModeGeneric;
+      else
+        return fail(HS_ERR_UNSUPPORTED,
+                    "row %d: top-k %lld exceeds %d, the largest k this build selects", r,
+                    (long long)k, hs::kMaxK);
+    }
+    out[(size_t)r] = p;
+  }
+  return HS_OK;
+}
+
+int upload_plans(hs_context *ctx, const std::vector<hs::RowPlan> &plans, hipStream_t stream) {
+  const size_t rows = plans.size();
+  const size_t bytes = rows * sizeof(hs::RowPlan);
+  if (ctx->last_plans.size() == rows && ctx->plans.bytes >= bytes &&
+      memcmp(ctx->last_plans.data(), plans.data(), bytes) == 0)
+    return HS_OK;
+  HS_HIP(ctx->plans.ensure(bytes));
+  if (ctx->plan_pending) {   // the staging buffer may still be read by a copy
+    HS_HIP(hipEventSynchronize(ctx->plan_done));
+    ctx->plan_pending = false;
+  }
+  if (ctx->plan_staging_rows < rows) {
+    if (ctx->plan_staging) (void)hipHostFree(ctx->plan_staging);
+    ctx->plan_staging = nullptr;
+    ctx->plan_staging_rows = 0;
+    HS_HIP(hipHostMalloc(reinterpret_cast<void **>(&ctx->plan_staging), bytes));
+    ctx->plan_staging_rows = rows;
+  }
+  memcpy(ctx->plan_staging, plans.data(), bytes);
+  HS_HIP(hipMemcpyAsync(ctx->plans.p, ctx->plan_staging, bytes, hipMemcpyHostToDevice, stream));
+  HS_HIP(hipEventRecord(ctx->plan_done, stream));
+  ctx->plan_pending = true;
+  try {
+    ctx->last_plans = plans;
+  } catch (const std::bad_alloc &) {
+    ctx->last_plans.clear();
+    return fail(HS_ERR_OUT_OF_MEMORY, "host allocation failed");
+  }
+  return HS_OK;
+}
+
+int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_stride,
+                  int32_t vocab, const int32_t *d_hist_ids, const int64_t *d_hist_offsets,
+                  const hs_sample_config *configs, const double *d_uniforms, int32_t *d_tokens,
+                  int32_t cand_stride, int32_t *d_cand_ids, float *d_cand_probs,
+                  int32_t *d_cand_count, int32_t *d_cutoff, uint32_t *d_row_flags,
+                  hipStream_t stream) {
+  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  if (rows < 0) return fail(HS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %d)", rows);
+  if (rows == 0) return HS_OK;
+  if (!configs || !d_uniforms || !d_tokens)
+    return fail(HS_ERR_INVALID_ARGUMENT, "configs, uniforms and tokens must not be null");
+  if ((d_hist_ids == nullptr) != (d_hist_offsets == nullptr))
+    return fail(HS_ERR_INVALID_ARGUMENT, "history ids and offsets must both be given or both null");
+  if (cand_stride < 0) return fail(HS_ERR_INVALID_ARGUMENT, "cand_stride must be >= 0");
+  if ((d_cand_ids || d_cand_probs) && cand_stride == 0)
+    return fail(HS_ERR_INVALID_ARGUMENT, "candidate outputs need cand_stride > 0");
+  DeviceGuard guard(ctx->device);
+  if (vocab <= 0) {
+    // src/sampler.ts: no logit is read; every path returns 0.
+    HS_HIP(hipMemsetAsync(d_tokens, 0, sizeof(int32_t) * (size_t)rows, stream));
+    if (d_cand_count) HS_HIP(hipMemsetAsync(d_cand_count, 0, sizeof(int32_t) * rows, stream));
+    if (d_cutoff) HS_HIP(hipMemsetAsync(d_cutoff, 0, sizeof(int32_t) * rows, stream));
+    if (d_row_flags) HS_HIP(hipMemsetAsync(d_row_flags, 0, sizeof(uint32_t) * rows, stream));
+    return HS_OK;
+  }
+  if (!d_logits) return fail(HS_ERR_INVALID_ARGUMENT, "logits must not be null");
+  if (row_stride < vocab)
+    return fail(HS_ERR_INVALID_ARGUMENT, "row_stride %lld < vocab %d", (long long)row_stride, vocab);
+  const int64_t S = (vocab + hs::kChunk - 1) / hs::kChunk;
+  if (S * hs::kChunkCap > 0x7FFFFFFF / 2 || (int64_t)rows * S > 0x7FFFFFFF)
+    return fail(HS_ERR_UNSUPPORTED, "vocab %d x rows %d too large", vocab, rows);
+
+  std::vector<hs::RowPlan> plans;
+  bool any_pf = false;
+  try {
+    int rc = build_plans(configs, rows, vocab, plans, &any_pf);
+    if (rc) return rc;
+  } catch (const std::bad_alloc &) {
+    return fail(HS_ERR_OUT_OF_MEMORY, "host allocation failed");
+  }
+
+  // workspace
+  const size_t cand_bytes = (size_t)rows * (size_t)S * hs::kChunkCap * sizeof(uint2);
+  HS_HIP(ctx->cand.ensure(cand_bytes));
+  HS_HIP(ctx->info.ensure((size_t)rows * (size_t)S * sizeof(hs::ChunkInfo)));
+  if (ctx->cand_count.bytes < sizeof(int32_t) * (size_t)rows) {
+    HS_HIP(ctx->cand_count.ensure(sizeof(int32_t) * (size_t)rows));
+    HS_HIP(hipMemset(ctx->cand_count.p, 0, ctx->cand_count.bytes));
+  }
+  int rc = upload_plans(ctx, plans, stream);
+  if (rc) return rc;
+
+  hs::Workspace ws;
+  ws.plans = static_cast<hs::RowPlan *>(ctx->plans.p);
+  ws.cand = static_cast<uint2 *>(ctx->cand.p);
+  ws.cand_count = static_cast<int32_t *>(ctx->cand_count.p);
+  ws.info = static_cast<hs::ChunkInfo *>(ctx->info.p);
+
+  hs::LaunchArgs a;
+  memset(&a, 0, sizeof a);
+  a.logits = d_logits;
+  a.stride = row_stride;
+  a.rows = rows;
+  a.vocab = vocab;
+  a.chunks = (int32_t)S;
+  a.vec = ((reinterpret_cast<uintptr_t>(d_logits) & 15u) == 0 && (row_stride & 3) == 0) ? 1 : 0;
+  a.any_pf = any_pf ? 1 : 0;
+  a.want_cands = (d_cand_ids || d_cand_probs) ? 1 : 0;
+  a.hist_ids = d_hist_ids;
+  a.hist_off = d_hist_offsets;
+  a.uniforms = d_uniforms;
+  a.tokens = d_tokens;
+  a.cand_stride = cand_stride;
+  a.cand_ids = d_cand_ids;
+  a.cand_probs = d_cand_probs;
+  a.cand_count_out = d_cand_count;
+  a.cutoff_out = d_cutoff;
+  a.row_flags = d_row_flags;
+  hipError_t e = hs::launch_sample(a, ws, stream);
+  if (e != hipSuccess) {
+    (void)hipMemsetAsync(ctx->cand_count.p, 0, ctx->cand_count.bytes, stream);
+    return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  }
+  return HS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hs_abi_version(void) { return HS_ABI_VERSION; }
+
+const char *hs_last_error(void) { return g_error.c_str(); }
+
+void hs_config_default(hs_sample_config *c) {
+  if (!c) return;
+  c->temperature = 0.6;
+  c->top_k = 20.0;
+  c->top_p = 0.95;
+  c->min_p = 0.0;
+  c->repetition_penalty = 1.0;
+  c->presence_penalty = 0.0;
+  c->frequency_penalty = 0.0;
+}
+
+int hs_context_create(int device, hs_context **out) {
+  if (!out) return fail(HS_ERR_INVALID_ARGUMENT, "out must not be null");
+  *out = nullptr;
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n <= 0)
+    return fail(HS_ERR_HIP, "no HIP device available (%s)", hipGetErrorString(e));
+  if (device < 0 || device >= n)
+    return fail(HS_ERR_INVALID_ARGUMENT, "device %d out of range [0, %d)", device, n);
+  DeviceGuard guard(device);
+  {
+    std::lock_guard<std::mutex> lk(g_prep_mu);
+    bool done = false;
+    for (int d : g_prepared) done |= d == device;
+    if (!done) {
+      HS_HIP(hs::prepare_kernels());
+      g_prepared.push_back(device);
+    }
+  }
+  hs_context *ctx = new (std::nothrow) hs_context();
+  if (!ctx) return fail(HS_ERR_OUT_OF_MEMORY, "host allocation failed");
+  ctx->device = device;
+  e = hipEventCreateWithFlags(&ctx->plan_done, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    hs_context_destroy(ctx);
+    return fail(HS_ERR_HIP, "context setup failed: %s", hipGetErrorString(e));
+  }
+  *out = ctx;
+  return HS_OK;
+}
+
+int hs_context_destroy(hs_context *ctx) {
+  if (!ctx) return HS_OK;
+  {
+    DeviceGuard guard(ctx->device);
+    (void)hipDeviceSynchronize();
+    ctx->plans.release();
+    ctx->cand.release();
+    ctx->cand_count.release();
+    ctx->info.release();
+    ctx->h_logits.release();
+    ctx->h_hist.release();
+    ctx->h_off.release();
+    ctx->h_u.release();
+    ctx->h_tok.release();
+    if (ctx->plan_staging) (void)hipHostFree(ctx->plan_staging);
+    if (ctx->plan_done) (void)hipEventDestroy(ctx->plan_done);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  }
+  delete ctx;
+  return HS_OK;
+}
+
+int hs_sample_batch_device_ex(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_stride,
+                              int32_t vocab, const int32_t *d_hist_ids,
+                              const int64_t *d_hist_offsets, const hs_sample_config *configs,
+                              const double *d_uniforms, int32_t *d_tokens, int32_t cand_stride,
+                              int32_t *d_cand_ids, float *d_cand_probs, int32_t *d_cand_count,
+                              int32_t *d_cutoff, uint32_t *d_row_flags, void *stream) {
+  return sample_device(ctx, d_logits, rows, row_stride, vocab, d_hist_ids, d_hist_offsets, configs,
+                       d_uniforms, d_tokens, cand_stride, d_cand_ids, d_cand_probs, d_cand_count,
+                       d_cutoff, d_row_flags, static_cast<hipStream_t>(stream));
+}
+
+int hs_sample_batch_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_stride,
+                           int32_t vocab, const int32_t *d_hist_ids,
+                           const int64_t *d_hist_offsets, const hs_sample_config *configs,
+                           const double *d_uniforms, int32_t *d_tokens, void *stream) {
+  return sample_device(ctx, d_logits, rows, row_stride, vocab, d_hist_ids, d_hist_offsets, configs,
+                       d_uniforms, d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr,
+                       static_cast<hipStream_t>(stream));
+}
+
+int hs_sample_logits_batch(hs_context *ctx, float *logits, int32_t rows, int64_t row_stride,
+                           int32_t vocab, const int32_t *hist_ids, const int64_t *hist_offsets,
+                           const hs_sample_config *configs, const double *uniforms,
+                           int32_t *tokens_out) {
+  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  if (rows < 0) return fail(HS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %d)", rows);
+  if (rows == 0) return HS_OK;
+  if (!configs || !uniforms || !tokens_out)
+    return fail(HS_ERR_INVALID_ARGUMENT, "configs, uniforms and tokens_out must not be null");
+  if ((hist_ids == nullptr) != (hist_offsets == nullptr))
+    return fail(HS_ERR_INVALID_ARGUMENT, "history ids and offsets must both be given or both null");
+  if (vocab <= 0) {
+    for (int r = 0; r < rows; ++r) tokens_out[r] = 0;
+    return HS_OK;
+  }
+  if (!logits) return fail(HS_ERR_INVALID_ARGUMENT, "logits must not be null");
+  if (row_stride < vocab)
+    return fail(HS_ERR_INVALID_ARGUMENT, "row_stride %lld < vocab %d", (long long)row_stride, vocab);
+  int64_t hist_total = 0;
+  if (hist_offsets) {
+    if (hist_offsets[0] != 0)
+      return fail(HS_ERR_INVALID_ARGUMENT, "hist_offsets[0] must be 0");
+    for (int r = 0; r < rows; ++r)
+      if (hist_offsets[r + 1] < hist_offsets[r])
+        return fail(HS_ERR_INVALID_ARGUMENT, "hist_offsets must be non-decreasing (row %d)", r);
+    hist_total = hist_offsets[rows];
+  }
+  DeviceGuard guard(ctx->device);
+  hipStream_t st = ctx->stream;
+  const size_t lbytes = sizeof(float) * ((size_t)(rows - 1) * (size_t)row_stride + (size_t)vocab);
+  HS_HIP(ctx->h_logits.ensure(lbytes));
+  HS_HIP(ctx->h_u.ensure(sizeof(double) * rows));
+  HS_HIP(ctx->h_tok.ensure(sizeof(int32_t) * rows));
+  HS_HIP(hipMemcpyAsync(ctx->h_logits.p, logits, lbytes, hipMemcpyHostToDevice, st));
+  HS_HIP(hipMemcpyAsync(ctx->h_u.p, uniforms, sizeof(double) * rows, hipMemcpyHostToDevice, st));
+  int32_t *d_ids = nullptr;
+  int64_t *d_off = nullptr;
+  if (hist_offsets) {
+    HS_HIP(ctx->h_off.ensure(sizeof(int64_t) * (rows + 1)));
+    HS_HIP(ctx->h_hist.ensure(sizeof(int32_t) * (size_t)(hist_total > 0 ? hist_total : 1)));
+    d_ids = static_cast<int32_t *>(ctx->h_hist.p);
+    d_off = static_cast<int64_t *>(ctx->h_off.p);
+    if (hist_total > 0)
+      HS_HIP(hipMemcpyAsync(d_ids, hist_ids, sizeof(int32_t) * hist_total, hipMemcpyHostToDevice, st));
+    HS_HIP(hipMemcpyAsync(d_off, hist_offsets, sizeof(int64_t) * (rows + 1), hipMemcpyHostToDevice, st));
+  }
+  int rc = sample_device(ctx, static_cast<float *>(ctx->h_logits.p), rows, row_stride, vocab, d_ids,
+                         d_off, configs, static_cast<double *>(ctx->h_u.p),
+                         static_cast<int32_t *>(ctx->h_tok.p), 0, nullptr, nullptr, nullptr, nullptr,
+                         nullptr, st);
+  if (rc) {
+    (void)hipStreamSynchronize(st);
+    return rc;
+  }
+  bool penalised = false;
+  for (int r = 0; r < rows && !penalised; ++r)
+    penalised = configs[r].repetition_penalty != 1.0 || configs[r].presence_penalty != 0.0 ||
+                configs[r].frequency_penalty != 0.0;
+  HS_HIP(hipMemcpyAsync(tokens_out, ctx->h_tok.p, sizeof(int32_t) * rows, hipMemcpyDeviceToHost, st));
+  if (penalised)   // the reference writes penalised values back (src/sampler.ts:30)
+    HS_HIP(hipMemcpyAsync(logits, ctx->h_logits.p, lbytes, hipMemcpyDeviceToHost, st));
+  HS_HIP(hipStreamSynchronize(st));
+  return HS_OK;
+}
+
+int hs_sample_logits(hs_context *ctx, float *logits, int32_t vocab, const int32_t *history,
+                     int64_t history_len, const hs_sample_config *config, double uniform,
+                     int32_t *token_out) {
+  if (history_len < 0) return fail(HS_ERR_INVALID_ARGUMENT, "history_len must be >= 0");
+  if (history_len > 0 && !history)
+    return fail(HS_ERR_INVALID_ARGUMENT, "history must not be null when history_len > 0");
+  const int64_t off[2] = {0, history_len};
+  return hs_sample_logits_batch(ctx, logits, 1, vocab > 0 ? vocab : 1, vocab,
+                                history_len > 0 ? history : nullptr,
+                                history_len > 0 ? off : nullptr, config, &uniform, token_out);
+}
+
+}  // extern "C"

@@ -1,0 +1,300 @@
+"""Python host layer over the gfx950 sampler's C ABI (libhachiue_sampler.so).
+
+Mirrors hachiue's ``sampleLogits(logits, vocab, history, config)``
+(src/sampler.ts:12-118) and ``SampleConfig`` (src/sampler.ts:1-7): same
+option names, the same `??` defaults (src/sampler.ts:18-22), the logits array
+mutated in place by the penalties (src/sampler.ts:30) and the same
+no-candidate return of 0 (src/sampler.ts:76).  The draw takes an injected
+uniform in [0, 1) instead of ``Math.random()`` (src/sampler.ts:112).
+
+There is no CPU fallback: every call runs the HIP kernels, and loading fails
+loudly when the library or a GPU is missing.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+import random
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import hip
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libhachiue_sampler.so")
+
+HS_OK = 0
+ERROR_NAMES = {1: "HS_ERR_INVALID_ARGUMENT", 2: "HS_ERR_HIP", 3: "HS_ERR_OUT_OF_MEMORY",
+               4: "HS_ERR_UNSUPPORTED"}
+
+ROW_GREEDY, ROW_REPLAYED, ROW_TIES, ROW_SINGLE = 0x1, 0x2, 0x4, 0x8
+
+# Every symbol include/hachiue_sampler.h declares.
+EXPORTS = ("hs_abi_version", "hs_last_error", "hs_config_default", "hs_context_create",
+           "hs_context_destroy", "hs_sample_logits", "hs_sample_logits_batch",
+           "hs_sample_batch_device", "hs_sample_batch_device_ex")
+
+
+class SamplerError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{ERROR_NAMES.get(status, status)}: {message}")
+        self.status = status
+
+
+class SampleConfigC(ctypes.Structure):
+    """hs_sample_config (include/hachiue_sampler.h)."""
+    _fields_ = [("temperature", ctypes.c_double), ("top_k", ctypes.c_double),
+                ("top_p", ctypes.c_double), ("min_p", ctypes.c_double),
+                ("repetition_penalty", ctypes.c_double),
+                ("presence_penalty", ctypes.c_double),
+                ("frequency_penalty", ctypes.c_double)]
+
+
+# SampleConfig option name -> hs_sample_config field, with the reference's
+# defaults (src/sampler.ts:18-22) and 0 for the two extensions.
+OPTIONS = {
+    "temperature": ("temperature", 0.6),
+    "topK": ("top_k", 20.0),
+    "topP": ("top_p", 0.95),
+    "minP": ("min_p", 0.0),
+    "repetitionPenalty": ("repetition_penalty", 1.0),
+    "presencePenalty": ("presence_penalty", 0.0),
+    "frequencyPenalty": ("frequency_penalty", 0.0),
+}
+_FIELD_TO_OPTION = {f: o for o, (f, _) in OPTIONS.items()}
+
+
+def resolve_config(config: dict | None) -> SampleConfigC:
+    """`config.x ?? default` for every option: only a missing key or None takes
+    the default.  Accepts the reference's camelCase names (and the snake_case
+    field names); unknown keys are ignored, as extra GenerateOptions fields
+    are (src/types.ts:187-197)."""
+    c = SampleConfigC()
+    for opt, (field, default) in OPTIONS.items():
+        setattr(c, field, default)
+    for key, val in (config or {}).items():
+        opt = key if key in OPTIONS else _FIELD_TO_OPTION.get(key)
+        if opt is None or val is None:
+            continue
+        setattr(c, OPTIONS[opt][0], float(val))
+    return c
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run __graft_entry__.build() first")
+    L = ctypes.CDLL(LIB_PATH)
+    P, vp = ctypes.POINTER, ctypes.c_void_p
+    i32, i64, dbl = ctypes.c_int32, ctypes.c_int64, ctypes.c_double
+    L.hs_abi_version.restype = ctypes.c_int
+    L.hs_last_error.restype = ctypes.c_char_p
+    L.hs_config_default.argtypes = [P(SampleConfigC)]
+    L.hs_config_default.restype = None
+    L.hs_context_create.argtypes = [ctypes.c_int, P(vp)]
+    L.hs_context_destroy.argtypes = [vp]
+    L.hs_sample_logits.argtypes = [vp, P(ctypes.c_float), i32, P(i32), i64, P(SampleConfigC),
+                                   dbl, P(i32)]
+    L.hs_sample_logits_batch.argtypes = [vp, P(ctypes.c_float), i32, i64, i32, P(i32), P(i64),
+                                         P(SampleConfigC), P(dbl), P(i32)]
+    L.hs_sample_batch_device.argtypes = [vp, vp, i32, i64, i32, vp, vp, P(SampleConfigC), vp,
+                                         vp, vp]
+    L.hs_sample_batch_device_ex.argtypes = [vp, vp, i32, i64, i32, vp, vp, P(SampleConfigC),
+                                            vp, vp, i32, vp, vp, vp, vp, vp, vp]
+    return L
+
+
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        _lib = _load()
+    return _lib
+
+
+def _check(status: int) -> None:
+    if status != HS_OK:
+        raise SamplerError(status, lib().hs_last_error().decode(errors="replace"))
+
+
+def _f32p(a):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+def _histories(histories, rows):
+    """(ids int32, offsets int64) from a list of id sequences, or a given
+    (ids, offsets) pair.  Ids that are not integers in int32 range are
+    stored as -1: in the reference they index nothing (src/sampler.ts:28)."""
+    if histories is None:
+        return None, None
+    if isinstance(histories, tuple) and len(histories) == 2:
+        ids = np.ascontiguousarray(histories[0], dtype=np.int32)
+        off = np.ascontiguousarray(histories[1], dtype=np.int64)
+        assert off.shape == (rows + 1,)
+        return ids, off
+    seqs = list(histories)
+    assert len(seqs) == rows
+    off = np.zeros(rows + 1, np.int64)
+    parts = []
+    for r, h in enumerate(seqs):
+        a = _history_ids(h)
+        parts.append(a)
+        off[r + 1] = off[r] + a.size
+    ids = np.concatenate(parts) if parts else np.zeros(0, np.int32)
+    return np.ascontiguousarray(ids, dtype=np.int32), off
+
+
+def _history_ids(h) -> np.ndarray:
+    if isinstance(h, np.ndarray) and h.dtype.kind in "iu":
+        a = h.astype(np.int64)
+        return np.where((a >= -2**31) & (a < 2**31), a, -1).astype(np.int32)
+    out = np.empty(len(h), np.int32)
+    for i, x in enumerate(h):
+        xf = float(x)
+        out[i] = int(xf) if (math.isfinite(xf) and xf == int(xf) and -2**31 <= xf < 2**31) else -1
+    return out
+
+
+class Sampler:
+    """One sampler context on one HIP device (not thread-safe)."""
+
+    def __init__(self, device: int = 0):
+        self._ctx = ctypes.c_void_p()
+        _check(lib().hs_context_create(int(device), ctypes.byref(self._ctx)))
+        self.device = device
+
+    def close(self) -> None:
+        if self._ctx.value:
+            lib().hs_context_destroy(self._ctx)
+            self._ctx = ctypes.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):  # pragma: no cover
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- drop-in: one host row -------------------------------------------
+    def sample_logits(self, logits: np.ndarray, vocab: int, history=(), config: dict | None = None,
+                      uniform: float | None = None) -> int:
+        """sampleLogits(logits, vocab, history, config) on the GPU.  `logits`
+        (float32, contiguous, length >= vocab) receives the penalised values
+        in place.  Without `uniform`, ``random.random()`` stands in for
+        Math.random() and is drawn only when the reference would draw: a
+        positive temperature and more than one slot."""
+        if not (isinstance(logits, np.ndarray) and logits.dtype == np.float32
+                and logits.flags.c_contiguous):
+            raise TypeError("logits must be a contiguous float32 numpy array")
+        vocab = int(vocab)
+        cfg = resolve_config(config)
+        if vocab > logits.size:
+            raise ValueError("vocab exceeds the logits length")
+        if uniform is None:
+            uniform = random.random() if _may_draw(cfg, vocab) else 0.0
+        ids = _history_ids(list(history) if not isinstance(history, np.ndarray) else history)
+        tok = ctypes.c_int32()
+        _check(lib().hs_sample_logits(self._ctx, _f32p(logits), vocab,
+                                      ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
+                                      int(ids.size), ctypes.byref(cfg), float(uniform),
+                                      ctypes.byref(tok)))
+        return int(tok.value)
+
+    # ---- batch over host buffers ------------------------------------------
+    def sample_logits_batch(self, logits: np.ndarray, vocab: int, histories=None, configs=None,
+                            uniforms=None) -> np.ndarray:
+        """Rows of a [rows, stride] float32 array, each with its own history,
+        config and uniform.  Penalised values are written back in place."""
+        if not (isinstance(logits, np.ndarray) and logits.dtype == np.float32
+                and logits.ndim == 2 and logits.flags.c_contiguous):
+            raise TypeError("logits must be a contiguous 2-D float32 numpy array")
+        rows, stride = logits.shape
+        cfgs = _configs(configs, rows)
+        if uniforms is None:
+            uniforms = np.array([random.random() for _ in range(rows)])
+        u = np.ascontiguousarray(uniforms, dtype=np.float64)
+        ids, off = _histories(histories, rows)
+        tok = np.zeros(rows, np.int32)
+        P = ctypes.POINTER
+        _check(lib().hs_sample_logits_batch(
+            self._ctx, _f32p(logits), rows, stride, int(vocab),
+            ids.ctypes.data_as(P(ctypes.c_int32)) if ids is not None else None,
+            off.ctypes.data_as(P(ctypes.c_int64)) if off is not None else None,
+            cfgs, u.ctypes.data_as(P(ctypes.c_double)), tok.ctypes.data_as(P(ctypes.c_int32))))
+        return tok
+
+    # ---- device-resident batch ----------------------------------------------
+    def sample_device(self, d_logits: int, rows: int, row_stride: int, vocab: int,
+                      d_hist_ids: int | None, d_hist_off: int | None, configs,
+                      d_uniforms: int, d_tokens: int, stream=None,
+                      cand_stride: int = 0, d_cand_ids: int | None = None,
+                      d_cand_probs: int | None = None, d_cand_count: int | None = None,
+                      d_cutoff: int | None = None, d_row_flags: int | None = None) -> None:
+        """Enqueue one sampling step on device buffers (addresses as ints)."""
+        cfgs = configs if isinstance(configs, ctypes.Array) else _configs(configs, rows)
+        vp = ctypes.c_void_p
+        st = stream.handle if isinstance(stream, hip.Stream) else stream
+        _check(lib().hs_sample_batch_device_ex(
+            self._ctx, vp(d_logits), int(rows), int(row_stride), int(vocab), vp(d_hist_ids or 0),
+            vp(d_hist_off or 0), cfgs, vp(d_uniforms), vp(d_tokens), int(cand_stride),
+            vp(d_cand_ids or 0), vp(d_cand_probs or 0), vp(d_cand_count or 0), vp(d_cutoff or 0),
+            vp(d_row_flags or 0), st))
+
+
+def _configs(configs, rows: int):
+    if configs is None or isinstance(configs, dict):
+        one = resolve_config(configs)
+        return (SampleConfigC * rows)(*([one] * rows))
+    configs = list(configs)
+    if len(configs) != rows:
+        raise ValueError("one config per row is required")
+    return (SampleConfigC * rows)(*[resolve_config(c) for c in configs])
+
+
+def make_configs(configs, rows: int):
+    """ctypes array of hs_sample_config for `rows` rows (dict = shared)."""
+    return _configs(configs, rows)
+
+
+def _may_draw(cfg: SampleConfigC, vocab: int) -> bool:
+    """Math.random() is reached only for temperature > 0 with k > 1
+    (src/sampler.ts:36, :49, :77)."""
+    if not (cfg.temperature > 0):
+        return False
+    t = cfg.top_k if cfg.top_k > 0 else 64.0
+    k = math.floor(max(1.0, min(t, float(vocab))))
+    return k > 1
+
+
+@dataclass
+class DeviceOutputs:
+    tokens: hip.DeviceArray
+    cand_ids: hip.DeviceArray | None
+    cand_probs: hip.DeviceArray | None
+    cand_count: hip.DeviceArray | None
+    cutoff: hip.DeviceArray | None
+    row_flags: hip.DeviceArray | None
+
+
+_default: Sampler | None = None
+
+
+def default_sampler() -> Sampler:
+    global _default
+    if _default is None:
+        _default = Sampler(0)
+    return _default
+
+
+def sample_logits(logits: np.ndarray, vocab: int, history=(), config: dict | None = None,
+                  uniform: float | None = None) -> int:
+    """Module-level drop-in for sampleLogits on the default GPU context."""
+    return default_sampler().sample_logits(logits, vocab, history, config, uniform)

@@ -1,0 +1,125 @@
+/*
+ * hachiue_sampler.h - C ABI of the MI355X (gfx950) logits-to-token sampler.
+ *
+ * Drop-in replacement for hachiue's CPU sampler `sampleLogits`
+ * (src/sampler.ts:12-118, exported at src/index.ts:15).  The library runs the
+ * whole sampling step on the GPU: repetition penalty over the last 128
+ * history tokens (plus optional presence / frequency penalties), greedy
+ * argmax, replace-min top-k with the reference's exact tie semantics, stable
+ * sort, temperature softmax, min-p / top-p cutoff and the categorical draw.
+ *
+ * Conventions
+ *  - Every entry point returns an hs_status; on failure hs_last_error() holds
+ *    a message for the calling thread.  No C++ exception crosses the ABI.
+ *  - Logits are mutated in place by the penalties, exactly as the reference
+ *    mutates its Float32Array (src/sampler.ts:30).
+ *  - A context owns one device, a workspace and the staging buffers; it is not
+ *    thread-safe.  Calls on one context are serialised by the caller.
+ *  - "device pointer" arguments must be device memory on the context's device
+ *    (hipMalloc); "stream" is a hipStream_t or NULL for the null stream.
+ */
+#ifndef HACHIUE_SAMPLER_H
+#define HACHIUE_SAMPLER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HS_ABI_VERSION 1
+
+typedef enum hs_status {
+  HS_OK = 0,
+  HS_ERR_INVALID_ARGUMENT = 1, /* null pointer, negative size, bad stride */
+  HS_ERR_HIP = 2,              /* a HIP runtime call failed */
+  HS_ERR_OUT_OF_MEMORY = 3,    /* workspace allocation failed */
+  HS_ERR_UNSUPPORTED = 4       /* input outside what this build handles */
+} hs_status;
+
+/* SampleConfig (src/sampler.ts:1-7) after the `??` defaults of
+ * src/sampler.ts:18-22 are resolved by the host layer.  Fields keep the
+ * JavaScript-number meaning: top_k may be Infinity, NaN or fractional
+ * (k = max(1, min(top_k > 0 ? top_k : 64, vocab)), truncated). */
+typedef struct hs_sample_config {
+  double temperature;        /* <= 0: greedy argmax (src/sampler.ts:36) */
+  double top_k;
+  double top_p;
+  double min_p;
+  double repetition_penalty; /* != 1: last 128 distinct ids (src/sampler.ts:25-33) */
+  double presence_penalty;   /* extension; no reference counterpart */
+  double frequency_penalty;  /* extension; no reference counterpart */
+} hs_sample_config;
+
+/* Per-row diagnostic bits written to row_flags (optional output). */
+#define HS_ROW_GREEDY       0x1u /* temperature <= 0 path */
+#define HS_ROW_REPLAYED     0x2u /* exact replace-min replay was needed (ties) */
+#define HS_ROW_TIES         0x4u /* equal values among or at the candidates */
+#define HS_ROW_SINGLE       0x8u /* 0 or 1 candidate: no draw consumed */
+
+typedef struct hs_context hs_context;
+
+/* Library identity. */
+int hs_abi_version(void);
+const char *hs_last_error(void);
+
+/* Reference defaults of src/sampler.ts:18-22 (temperature 0.6, topK 20,
+ * topP 0.95, minP 0, repetitionPenalty 1) and 0 for the extensions. */
+void hs_config_default(hs_sample_config *config);
+
+/* Context on HIP device `device`.  Allocates the workspace lazily and grows it
+ * when a call needs more; a call that fits the current workspace allocates
+ * nothing. */
+int hs_context_create(int device, hs_context **out);
+int hs_context_destroy(hs_context *ctx);
+
+/* Drop-in for sampleLogits(logits, vocab, history, config)
+ * (src/sampler.ts:12-17) on one HOST row.  `logits` (at least vocab floats)
+ * is updated in place with the penalised values; `uniform` in [0, 1) replaces
+ * Math.random() (src/sampler.ts:112) and is consumed only when a draw
+ * happens.  Blocks until *token_out is written. */
+int hs_sample_logits(hs_context *ctx, float *logits, int32_t vocab,
+                     const int32_t *history, int64_t history_len,
+                     const hs_sample_config *config, double uniform,
+                     int32_t *token_out);
+
+/* Batched host variant: `rows` rows of `row_stride` floats; row r's history
+ * is hist_ids[hist_offsets[r] .. hist_offsets[r+1]) (hist_offsets has rows+1
+ * entries; both may be NULL for no history); configs[r], uniforms[r].  Copies
+ * in, samples, copies tokens and penalised logits back.  Blocks. */
+int hs_sample_logits_batch(hs_context *ctx, float *logits, int32_t rows,
+                           int64_t row_stride, int32_t vocab,
+                           const int32_t *hist_ids, const int64_t *hist_offsets,
+                           const hs_sample_config *configs,
+                           const double *uniforms, int32_t *tokens_out);
+
+/* Device-resident batch, asynchronous on `stream`: d_logits, d_hist_ids,
+ * d_hist_offsets, d_uniforms and d_tokens are device pointers; `configs` is a
+ * HOST array of `rows` configs (staged to the device by the library, skipped
+ * when identical to the previous call's).  Optional device outputs (each may
+ * be NULL): the first `cand_stride` sorted candidates per row (ids, normalised
+ * probabilities), the candidate count, the kept-prefix length and row flags. */
+int hs_sample_batch_device(hs_context *ctx, float *d_logits, int32_t rows,
+                           int64_t row_stride, int32_t vocab,
+                           const int32_t *d_hist_ids,
+                           const int64_t *d_hist_offsets,
+                           const hs_sample_config *configs,
+                           const double *d_uniforms, int32_t *d_tokens,
+                           void *stream);
+
+int hs_sample_batch_device_ex(hs_context *ctx, float *d_logits, int32_t rows,
+                              int64_t row_stride, int32_t vocab,
+                              const int32_t *d_hist_ids,
+                              const int64_t *d_hist_offsets,
+                              const hs_sample_config *configs,
+                              const double *d_uniforms, int32_t *d_tokens,
+                              int32_t cand_stride, int32_t *d_cand_ids,
+                              float *d_cand_probs, int32_t *d_cand_count,
+                              int32_t *d_cutoff, uint32_t *d_row_flags,
+                              void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,241 @@
+"""ctypes binding of the CPU oracle (liborc_sampler.so).
+
+TEST INFRASTRUCTURE ONLY: the oracle is the checker the HIP sampler is
+compared against.  Only tests, the smoke check and the benchmark's CPU
+baseline import this module; the product package never does.
+
+The oracle restates hachiue's ``sampleLogits`` (src/sampler.ts:12-118); see
+``sampler_oracle.c`` for the line-by-line correspondence.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liborc_sampler.so")
+
+LITERAL = 0  # the reference's O(V*k) replace-min rescan, verbatim
+HEAP = 1     # identical slot semantics, O(V + R log k)
+
+
+class OrcConfig(ctypes.Structure):
+    _fields_ = [
+        ("temperature", ctypes.c_double),
+        ("top_k", ctypes.c_double),
+        ("top_p", ctypes.c_double),
+        ("min_p", ctypes.c_double),
+        ("repetition_penalty", ctypes.c_double),
+        ("presence_penalty", ctypes.c_double),
+        ("frequency_penalty", ctypes.c_double),
+    ]
+
+
+class OrcResult(ctypes.Structure):
+    _fields_ = [
+        ("token", ctypes.c_int32),
+        ("path", ctypes.c_int32),
+        ("k", ctypes.c_int32),
+        ("n", ctypes.c_int32),
+        ("cutoff", ctypes.c_int32),
+        ("draw_index", ctypes.c_int32),
+        ("sum_prob", ctypes.c_double),
+        ("kept_sum", ctypes.c_double),
+        ("draw_margin", ctypes.c_double),
+        ("topp_margin", ctypes.c_double),
+    ]
+
+
+# src/sampler.ts:18-22 defaults
+DEFAULTS = dict(temperature=0.6, top_k=20.0, top_p=0.95, min_p=0.0,
+                repetition_penalty=1.0, presence_penalty=0.0,
+                frequency_penalty=0.0)
+
+_CFG_KEYS = {"temperature": "temperature", "topK": "top_k", "topP": "top_p",
+             "minP": "min_p", "repetitionPenalty": "repetition_penalty",
+             "presencePenalty": "presence_penalty",
+             "frequencyPenalty": "frequency_penalty"}
+
+
+def resolve_config(cfg: dict | None) -> dict:
+    """Apply the reference's `??` defaults: only a missing key or None takes
+    the default (src/sampler.ts:18-22).  Accepts camelCase or snake_case."""
+    out = dict(DEFAULTS)
+    for key, val in (cfg or {}).items():
+        name = _CFG_KEYS.get(key, key)
+        if name not in out:
+            raise KeyError(f"unknown sampler option {key!r}")
+        if val is not None:
+            out[name] = float(val)
+    return out
+
+
+def make_config(cfg: dict | None) -> OrcConfig:
+    r = resolve_config(cfg)
+    return OrcConfig(**r)
+
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        P = ctypes.POINTER
+        L.orc_resolve_k.restype = ctypes.c_int64
+        L.orc_resolve_k.argtypes = [ctypes.c_double, ctypes.c_int64]
+        L.orc_apply_penalties.restype = None
+        L.orc_apply_penalties.argtypes = [P(ctypes.c_float), ctypes.c_int64,
+                                          P(ctypes.c_int32), ctypes.c_int64,
+                                          P(OrcConfig)]
+        L.orc_sample_row.restype = ctypes.c_int
+        L.orc_sample_row.argtypes = [P(ctypes.c_float), ctypes.c_int64,
+                                     P(ctypes.c_int32), ctypes.c_int64,
+                                     P(OrcConfig), ctypes.c_double, ctypes.c_int,
+                                     P(OrcResult), P(ctypes.c_int32),
+                                     P(ctypes.c_float), P(ctypes.c_float),
+                                     ctypes.c_int64]
+        L.orc_sample_batch.restype = ctypes.c_int
+        L.orc_sample_batch.argtypes = [P(ctypes.c_float), ctypes.c_int64,
+                                       ctypes.c_int64, ctypes.c_int64,
+                                       P(ctypes.c_int32), P(ctypes.c_int64),
+                                       P(OrcConfig), P(ctypes.c_double),
+                                       ctypes.c_int, P(OrcResult),
+                                       P(ctypes.c_int32), P(ctypes.c_float),
+                                       P(ctypes.c_float), ctypes.c_int64]
+        L.orc_topk_slots.restype = ctypes.c_int
+        L.orc_topk_slots.argtypes = [P(ctypes.c_float), ctypes.c_int64,
+                                     ctypes.c_int64, ctypes.c_int,
+                                     P(ctypes.c_int32), P(ctypes.c_float)]
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray | None, ct):
+    if a is None:
+        return None
+    return a.ctypes.data_as(ctypes.POINTER(ct))
+
+
+@dataclass
+class RowResult:
+    token: int
+    path: int
+    k: int
+    n: int
+    cutoff: int
+    draw_index: int
+    sum_prob: float
+    kept_sum: float
+    draw_margin: float
+    topp_margin: float
+    cand_ids: np.ndarray
+    cand_vals: np.ndarray
+    cand_probs: np.ndarray
+
+
+def resolve_k(top_k: float, vocab: int) -> int:
+    return int(lib().orc_resolve_k(float(top_k), int(vocab)))
+
+
+def apply_penalties(logits: np.ndarray, vocab: int, history, cfg: dict | None) -> None:
+    assert logits.dtype == np.float32 and logits.flags.c_contiguous
+    h = np.ascontiguousarray(np.asarray(history, dtype=np.int32))
+    c = make_config(cfg)
+    lib().orc_apply_penalties(_ptr(logits, ctypes.c_float), int(vocab),
+                              _ptr(h, ctypes.c_int32), int(h.size), ctypes.byref(c))
+
+
+def sample_row(logits: np.ndarray, vocab: int, history, cfg: dict | None,
+               u: float, method: int = HEAP, cap: int | None = None) -> RowResult:
+    """sampleLogits on one row; `logits` (float32, contiguous) is mutated in
+    place like the reference's Float32Array."""
+    assert logits.dtype == np.float32 and logits.flags.c_contiguous
+    h = np.ascontiguousarray(np.asarray(history, dtype=np.int32))
+    c = make_config(cfg)
+    if cap is None:
+        cap = resolve_k(c.top_k, vocab)
+    ids = np.full(cap, -1, np.int32)
+    vals = np.zeros(cap, np.float32)
+    probs = np.zeros(cap, np.float32)
+    res = OrcResult()
+    rc = lib().orc_sample_row(_ptr(logits, ctypes.c_float), int(vocab),
+                              _ptr(h, ctypes.c_int32), int(h.size),
+                              ctypes.byref(c), float(u), int(method),
+                              ctypes.byref(res), _ptr(ids, ctypes.c_int32),
+                              _ptr(vals, ctypes.c_float),
+                              _ptr(probs, ctypes.c_float), int(cap))
+    if rc:
+        raise MemoryError("oracle allocation failed")
+    n = min(res.n, cap)
+    return RowResult(res.token, res.path, res.k, res.n, res.cutoff,
+                     res.draw_index, res.sum_prob, res.kept_sum,
+                     res.draw_margin, res.topp_margin, ids[:n].copy(),
+                     vals[:n].copy(), probs[:n].copy())
+
+
+@dataclass
+class BatchResult:
+    token: np.ndarray
+    path: np.ndarray
+    n: np.ndarray
+    cutoff: np.ndarray
+    draw_index: np.ndarray
+    draw_margin: np.ndarray
+    topp_margin: np.ndarray
+    cand_ids: np.ndarray | None
+    cand_vals: np.ndarray | None
+    cand_probs: np.ndarray | None
+
+
+def sample_batch(logits: np.ndarray, vocab: int, hist_ids: np.ndarray | None,
+                 hist_off: np.ndarray | None, cfgs: list[dict] | dict,
+                 u: np.ndarray, method: int = HEAP, cap: int = 0) -> BatchResult:
+    """Row-by-row oracle over a [rows, stride] float32 batch (mutated in place)."""
+    assert logits.dtype == np.float32 and logits.ndim == 2 and logits.flags.c_contiguous
+    rows, stride = logits.shape
+    if isinstance(cfgs, dict) or cfgs is None:
+        cfgs = [cfgs] * rows
+    carr = (OrcConfig * rows)(*[make_config(c) for c in cfgs])
+    u = np.ascontiguousarray(u, dtype=np.float64)
+    res = (OrcResult * rows)()
+    ids = np.full((rows, max(cap, 1)), -1, np.int32) if cap else None
+    vals = np.zeros((rows, max(cap, 1)), np.float32) if cap else None
+    probs = np.zeros((rows, max(cap, 1)), np.float32) if cap else None
+    if hist_ids is not None:
+        hist_ids = np.ascontiguousarray(hist_ids, dtype=np.int32)
+        hist_off = np.ascontiguousarray(hist_off, dtype=np.int64)
+    rc = lib().orc_sample_batch(_ptr(logits, ctypes.c_float), rows, stride,
+                                int(vocab), _ptr(hist_ids, ctypes.c_int32),
+                                _ptr(hist_off, ctypes.c_int64), carr,
+                                _ptr(u, ctypes.c_double), int(method), res,
+                                _ptr(ids, ctypes.c_int32), _ptr(vals, ctypes.c_float),
+                                _ptr(probs, ctypes.c_float), int(cap))
+    if rc:
+        raise MemoryError("oracle allocation failed")
+    g = lambda f: np.array([getattr(r, f) for r in res])  # noqa: E731
+    return BatchResult(g("token").astype(np.int32), g("path"), g("n"), g("cutoff"),
+                       g("draw_index"), g("draw_margin"), g("topp_margin"),
+                       ids, vals, probs)
+
+
+def topk_slots(logits: np.ndarray, vocab: int, k: int, method: int = LITERAL):
+    ids = np.full(k, -1, np.int32)
+    vals = np.full(k, -np.inf, np.float32)
+    rc = lib().orc_topk_slots(_ptr(np.ascontiguousarray(logits, np.float32), ctypes.c_float),
+                              int(vocab), int(k), int(method),
+                              _ptr(ids, ctypes.c_int32), _ptr(vals, ctypes.c_float))
+    if rc:
+        raise MemoryError("oracle allocation failed")
+    return ids, vals
