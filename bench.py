@@ -1,0 +1,229 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 logits-to-token sampler.
+
+One step = one full sampling pass (penalties -> top-k select -> sort ->
+softmax -> min-p / top-p -> draw) over a batch of device-resident logit rows.
+Default workload: 256 rows x 151936 fp32 logits, top-k 40, top-p 0.9,
+repetition penalty 1.1 over a 64-token history, temperature 0.7.
+
+Prints one JSON line: rows/s (value), ms per step, the roofline of the
+dominant kernel (the chunk-select kernel: algorithmic bytes per launch over
+its average duration, timed with HIP events on the launch stream) and a CPU
+baseline (the JavaScript restatement of sampler.ts under Node on this host).
+
+  python bench.py [--steps K] [--warmup W] [--workload NAME] [--sets N]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "sampled rows/sec and HBM GB/s (% roofline) at B=256, V=151936 fp32"
+HBM_PEAK_GBPS = 8000.0   # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def write_workload_dir(wl, rows: int, path: str) -> None:
+    """Files read by oracle/cpu_bench.js (first `rows` rows)."""
+    os.makedirs(path, exist_ok=True)
+    wl.logits[:rows].tofile(os.path.join(path, "logits.f32"))
+    np.asarray(wl.uniforms[:rows], np.float64).tofile(os.path.join(path, "uniforms.f64"))
+    has_h = wl.hist_ids is not None
+    if has_h:
+        end = int(wl.hist_off[rows])
+        wl.hist_ids[:end].tofile(os.path.join(path, "hist_ids.i32"))
+        wl.hist_off[:rows + 1].astype(np.float64).tofile(os.path.join(path, "hist_off.f64"))
+
+    def js(v):
+        if isinstance(v, float) and not np.isfinite(v):
+            return "NaN" if np.isnan(v) else ("Infinity" if v > 0 else "-Infinity")
+        return v
+
+    meta = dict(rows=rows, vocab=wl.vocab, stride=wl.logits.shape[1], has_history=has_h,
+                configs=[{k: js(v) for k, v in c.items()} for c in wl.configs[:rows]])
+    with open(os.path.join(path, "meta.json"), "w") as f:
+        json.dump(meta, f)
+
+
+def cpu_baseline(wl, seconds: float, threads: int, rows: int) -> dict | None:
+    """Times oracle/sampler_port.js (sampler.ts restated) under Node: one row
+    of fresh logits per call, for `seconds` on 1 thread and on `threads`."""
+    node = "node"
+    try:
+        ver = subprocess.run([node, "--version"], capture_output=True, text=True, timeout=30)
+    except (OSError, subprocess.TimeoutExpired):
+        return None
+    if ver.returncode != 0:
+        return None
+    with tempfile.TemporaryDirectory(prefix="hs_cpu_") as d:
+        write_workload_dir(wl, rows, d)
+        cmd = [node, os.path.join(ROOT, "oracle", "cpu_bench.js"), "bench", d, str(seconds),
+               str(threads)]
+        log(f"[bench] cpu baseline: {' '.join(cmd[1:3])} ... {seconds}s x (1, {threads}) threads")
+        out = subprocess.run(cmd, capture_output=True, text=True, timeout=seconds * 4 + 120)
+    if out.returncode != 0:
+        log(f"[bench] cpu baseline failed: {out.stderr[-2000:]}")
+        return None
+    r = json.loads(out.stdout.strip().splitlines()[-1])
+    return dict(
+        value=round(r["rows_per_s_all"], 1), unit="rows/s", cores=r["threads"], kind="port",
+        value_1core=round(r["rows_per_s_1core"], 1),
+        sample=(f"oracle/sampler_port.js (sampler.ts restated, Node {r['node']}, {r['cpu']}): "
+                f"first {rows} rows of the workload, one fresh row per call, "
+                f"{seconds}s on 1 thread ({r['rows_1core']} rows) and {seconds}s on "
+                f"{r['threads']} worker threads ({r['rows_all']} rows); time inside the "
+                f"sampler only"))
+
+
+def oracle_parity(wl, tokens: np.ndarray) -> dict:
+    from oracle import pyoracle
+    ref = wl.logits.copy()
+    res = pyoracle.sample_batch(ref, wl.vocab, wl.hist_ids, wl.hist_off, wl.configs,
+                                wl.uniforms)
+    eq = tokens == res.token
+    boundary = int(((~eq) & ((res.draw_margin < 1e-6) | (res.topp_margin < 1e-6))).sum())
+    return dict(rows=int(eq.size), tokens_equal=int(eq.sum()), boundary_cases=boundary)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="headline")
+    ap.add_argument("--sets", type=int, default=3,
+                    help="input copies rotated per step so reads come from HBM, not MALL")
+    ap.add_argument("--cpu-seconds", type=float, default=6.0)
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, cpu count)")
+    ap.add_argument("--cpu-rows", type=int, default=64)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-parity", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (rows are "
+              "independent; a batch shards by rows with no communication). Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    from hachiue_amd import Sampler, hip, workloads
+    from hachiue_amd.sampler import make_configs
+
+    t_gen = time.time()
+    wl = workloads.make(args.workload, seed=0)
+    rows, vocab = wl.rows, wl.vocab
+    log(f"[bench] workload {wl.name}: {rows} x {vocab} (generated in {time.time() - t_gen:.1f}s)")
+
+    sampler = Sampler(0)
+    stream = hip.Stream()
+    cfgs = make_configs(wl.configs, rows)
+    sets = max(1, args.sets)
+    d_logits = [hip.DeviceArray.from_numpy(wl.logits) for _ in range(sets)]
+    d_ids = hip.DeviceArray.from_numpy(wl.hist_ids) if wl.hist_ids is not None else None
+    d_off = hip.DeviceArray.from_numpy(wl.hist_off) if wl.hist_off is not None else None
+    d_u = hip.DeviceArray.from_numpy(wl.uniforms)
+    d_tok = hip.DeviceArray(rows, np.int32)
+
+    def step(i: int) -> None:
+        sampler.sample_device(d_logits[i % sets].addr, rows, vocab, vocab,
+                              d_ids.addr if d_ids else None, d_off.addr if d_off else None,
+                              cfgs, d_u.addr, d_tok.addr, stream=stream)
+
+    parity = None
+    if not args.no_parity:
+        step(0)
+        stream.synchronize()
+        parity = oracle_parity(wl, d_tok.download())
+        log(f"[bench] parity vs oracle: {parity}")
+        d_logits[0].upload(wl.logits)
+
+    for i in range(args.warmup):
+        step(i)
+    stream.synchronize()
+    log(f"[bench] warmup {args.warmup} steps done")
+
+    sampler.set_timing(True)
+    sampler.kernel_times()
+    e0, e1 = hip.Event(), hip.Event()
+    hip.synchronize()
+    e0.record(stream)
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    e1.synchronize()
+    wall = time.perf_counter() - t0
+    hip.synchronize()
+    total_ms = e0.elapsed_ms(e1)
+    chunk_ms, fin_ms, calls = sampler.kernel_times()
+    sampler.set_timing(False)
+    log(f"[bench] timed {args.steps} steps: {total_ms:.3f} ms device, {wall * 1e3:.1f} ms wall")
+
+    ms_per_step = total_ms / args.steps
+    value = rows / (ms_per_step * 1e-3)
+    alg_step = wl.algorithmic_bytes()
+    alg_chunk = alg_step - 4 * rows          # the token writes belong to finalize
+    chunk_avg = chunk_ms / max(calls, 1)
+    fin_avg = fin_ms / max(calls, 1)
+    achieved = alg_chunk / (chunk_avg * 1e-3) / 1e9
+
+    cpu = None
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        cpu = cpu_baseline(wl, args.cpu_seconds, threads, min(args.cpu_rows, rows))
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"{wl.name}: {rows} rows x {vocab} fp32 logits; "
+                         + ("top-k 40, top-p 0.9, repetition 1.1 over a 64-token history, "
+                            "temperature 0.7" if wl.name == "headline" else "see workloads.py")),
+            "rows": rows, "vocab": vocab, "input_sets": sets,
+            "algorithmic_bytes_per_step": alg_step,
+        },
+        "hbm_gbps_step": round(alg_step / (ms_per_step * 1e-3) / 1e9, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "chunk_kernel",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "kernel_ms": round(chunk_avg, 5),
+            "finalize_ms": round(fin_avg, 5),
+        },
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(line), flush=True)
+    sampler.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

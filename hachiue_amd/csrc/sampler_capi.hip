@@ -80,6 +80,11 @@ struct hs_context {
   // host entry points
   DevBuf h_logits, h_hist, h_off, h_u, h_tok;
   hipStream_t stream = nullptr;
+  // per-kernel timing diagnostics
+  bool timing = false;
+  std::vector<hipEvent_t> ev_free, ev_used;   // used: groups of kTimedKernels + 1
+  double kernel_ms[hs::kTimedKernels] = {0, 0};
+  int64_t timed_calls = 0;
 };
 
 namespace {
@@ -249,7 +254,22 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   a.cand_count_out = d_cand_count;
   a.cutoff_out = d_cutoff;
   a.row_flags = d_row_flags;
-  hipError_t e = hs::launch_sample(a, ws, stream);
+  hipEvent_t ev[hs::kTimedKernels + 1];
+  bool timed = false;
+  if (ctx->timing) {
+    for (int i = 0; i <= hs::kTimedKernels; ++i) {
+      if (ctx->ev_free.empty()) {
+        hipEvent_t x;
+        HS_HIP(hipEventCreate(&x));
+        ctx->ev_free.push_back(x);
+      }
+      ev[i] = ctx->ev_free.back();
+      ctx->ev_free.pop_back();
+      ctx->ev_used.push_back(ev[i]);
+    }
+    timed = true;
+  }
+  hipError_t e = hs::launch_sample(a, ws, stream, timed ? ev : nullptr);
   if (e != hipSuccess) {
     (void)hipMemsetAsync(ctx->cand_count.p, 0, ctx->cand_count.bytes, stream);
     return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
@@ -308,11 +328,42 @@ int hs_context_create(int device, hs_context **out) {
   return HS_OK;
 }
 
+int hs_context_set_timing(hs_context *ctx, int enable) {
+  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  ctx->timing = enable != 0;
+  return HS_OK;
+}
+
+int hs_context_kernel_times(hs_context *ctx, double *ms, int32_t count, int64_t *calls) {
+  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  if (count < 0 || (count > 0 && !ms)) return fail(HS_ERR_INVALID_ARGUMENT, "bad output array");
+  DeviceGuard guard(ctx->device);
+  const size_t g = hs::kTimedKernels + 1;
+  for (size_t i = 0; i + g <= ctx->ev_used.size(); i += g) {
+    HS_HIP(hipEventSynchronize(ctx->ev_used[i + g - 1]));
+    for (int k = 0; k < hs::kTimedKernels; ++k) {
+      float t = 0;
+      HS_HIP(hipEventElapsedTime(&t, ctx->ev_used[i + k], ctx->ev_used[i + k + 1]));
+      ctx->kernel_ms[k] += t;
+    }
+    ++ctx->timed_calls;
+  }
+  for (hipEvent_t x : ctx->ev_used) ctx->ev_free.push_back(x);
+  ctx->ev_used.clear();
+  for (int k = 0; k < count; ++k) ms[k] = k < hs::kTimedKernels ? ctx->kernel_ms[k] : 0.0;
+  if (calls) *calls = ctx->timed_calls;
+  for (int k = 0; k < hs::kTimedKernels; ++k) ctx->kernel_ms[k] = 0;
+  ctx->timed_calls = 0;
+  return HS_OK;
+}
+
 int hs_context_destroy(hs_context *ctx) {
   if (!ctx) return HS_OK;
   {
     DeviceGuard guard(ctx->device);
     (void)hipDeviceSynchronize();
+    for (hipEvent_t x : ctx->ev_free) (void)hipEventDestroy(x);
+    for (hipEvent_t x : ctx->ev_used) (void)hipEventDestroy(x);
     ctx->plans.release();
     ctx->cand.release();
     ctx->cand_count.release();

@@ -93,7 +93,11 @@ struct LaunchArgs {
   uint32_t *row_flags;
 };
 
-hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream);
+// Launches the two kernels on `stream`.  When `ev` is not null, records
+// ev[0] before the chunk kernel, ev[1] between the kernels, ev[2] after.
+constexpr int kTimedKernels = 2;
+hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,
+                         hipEvent_t *ev);
 hipError_t prepare_kernels();   // per device, once: raise dynamic LDS limits
 size_t finalize_smem_bytes();
 

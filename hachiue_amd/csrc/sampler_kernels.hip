@@ -753,18 +753,25 @@ hipError_t prepare_kernels() {
                              (int)finalize_smem_bytes());
 }
 
-hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream) {
+hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,
+                         hipEvent_t *ev) {
   const size_t chunk_smem = (size_t)(2 * (kChunk / 32) + (a.any_pf ? kChunk : 0)) * 4;
   const dim3 grid((unsigned)(a.rows * a.chunks));
+  hipError_t e;
+  if (ev && (e = hipEventRecord(ev[0], stream)) != hipSuccess) return e;
   if (a.vec)
     hipLaunchKernelGGL(chunk_kernel<true>, grid, dim3(kThreads), chunk_smem, stream, a, ws);
   else
     hipLaunchKernelGGL(chunk_kernel<false>, grid, dim3(kThreads), chunk_smem, stream, a, ws);
-  hipError_t e = hipGetLastError();
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (ev && (e = hipEventRecord(ev[1], stream)) != hipSuccess) return e;
   hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)a.rows), dim3(kThreads),
                      finalize_smem_bytes(), stream, a, ws);
-  return hipGetLastError();
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (ev && (e = hipEventRecord(ev[2], stream)) != hipSuccess) return e;
+  return hipSuccess;
 }
 
 }  // namespace hs

@@ -34,7 +34,8 @@ ROW_GREEDY, ROW_REPLAYED, ROW_TIES, ROW_SINGLE = 0x1, 0x2, 0x4, 0x8
 # Every symbol include/hachiue_sampler.h declares.
 EXPORTS = ("hs_abi_version", "hs_last_error", "hs_config_default", "hs_context_create",
            "hs_context_destroy", "hs_sample_logits", "hs_sample_logits_batch",
-           "hs_sample_batch_device", "hs_sample_batch_device_ex")
+           "hs_sample_batch_device", "hs_sample_batch_device_ex", "hs_context_set_timing",
+           "hs_context_kernel_times")
 
 
 class SamplerError(RuntimeError):
@@ -102,6 +103,8 @@ def _load() -> ctypes.CDLL:
                                          vp, vp]
     L.hs_sample_batch_device_ex.argtypes = [vp, vp, i32, i64, i32, vp, vp, P(SampleConfigC),
                                             vp, vp, i32, vp, vp, vp, vp, vp, vp]
+    L.hs_context_set_timing.argtypes = [vp, ctypes.c_int]
+    L.hs_context_kernel_times.argtypes = [vp, P(dbl), i32, P(i64)]
     return L
 
 
@@ -182,6 +185,17 @@ class Sampler:
             self.close()
         except Exception:
             pass
+
+    # ---- diagnostics ---------------------------------------------------------
+    def set_timing(self, enable: bool) -> None:
+        _check(lib().hs_context_set_timing(self._ctx, 1 if enable else 0))
+
+    def kernel_times(self):
+        """(chunk_ms_total, finalize_ms_total, calls) since the last query."""
+        ms = (ctypes.c_double * 2)()
+        calls = ctypes.c_int64()
+        _check(lib().hs_context_kernel_times(self._ctx, ms, 2, ctypes.byref(calls)))
+        return float(ms[0]), float(ms[1]), int(calls.value)
 
     # ---- drop-in: one host row -------------------------------------------
     def sample_logits(self, logits: np.ndarray, vocab: int, history=(), config: dict | None = None,

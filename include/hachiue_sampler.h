@@ -118,6 +118,15 @@ int hs_sample_batch_device_ex(hs_context *ctx, float *d_logits, int32_t rows,
                               int32_t *d_cutoff, uint32_t *d_row_flags,
                               void *stream);
 
+/* Diagnostics (no counterpart in the reference, which has no GPU sampler):
+ * while enabled, every sampling call records HIP events on its stream around
+ * each of its two kernel launches.  hs_context_kernel_times() waits for the
+ * recorded calls, writes the summed device milliseconds per kernel
+ * (ms[0] = chunk select, ms[1] = finalize) and the number of timed calls, and
+ * resets the totals. */
+int hs_context_set_timing(hs_context *ctx, int enable);
+int hs_context_kernel_times(hs_context *ctx, double *ms, int32_t count, int64_t *calls);
+
 #ifdef __cplusplus
 }
 #endif
