@@ -4,6 +4,7 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <mutex>
@@ -73,8 +74,9 @@ struct hs_context {
   int64_t cand_count_rows = 0;     // rows whose counter is known to be zero
   // plan upload cache
   std::vector<hs::RowPlan> last_plans;
-  hs::RowPlan *plan_staging = nullptr;   // pinned
-  size_t plan_staging_rows = 0;
+  int last_vocab = -1;
+  void *plan_staging = nullptr;          // pinned
+  size_t plan_staging_bytes = 0;
   hipEvent_t plan_done = nullptr;
   bool plan_pending = false;
   // host entry points
@@ -83,7 +85,9 @@ struct hs_context {
   // per-kernel timing diagnostics
   bool timing = false;
   std::vector<hipEvent_t> ev_free, ev_used;   // used: groups of kTimedKernels + 1
-  double kernel_ms[hs::kTimedKernels] = {0, 0};
+  double kernel_ms[hs::kTimedKernels] = {};
+  // rows routed to the row kernel only when a call has at least this many
+  int row_min_rows = 1;
   int64_t timed_calls = 0;
 };
 
@@ -110,10 +114,17 @@ int64_t resolve_k(double top_k, int64_t vocab) {
   return (int64_t)floor(k);
 }
 
-int build_plans(const hs_sample_config *cfgs, int rows, int vocab, std::vector<hs::RowPlan> &out,
-                bool *any_pf) {
+// Routing of rows to kernels, uploaded next to the plans.
+struct Routing {
+  std::vector<int32_t> pf, row, chunk;
+};
+
+int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_rows,
+                std::vector<hs::RowPlan> &out, Routing &rt) {
   out.resize((size_t)rows);
-  *any_pf = false;
+  rt.pf.clear();
+  rt.row.clear();
+  rt.chunk.clear();
   for (int r = 0; r < rows; ++r) {
     const hs_sample_config &c = cfgs[r];
     hs::RowPlan p;
@@ -126,7 +137,6 @@ int build_plans(const hs_sample_config *cfgs, int rows, int vocab, std::vector<h
     p.freq = c.frequency_penalty;
     p.pen = (c.repetition_penalty != 1.0 ? hs::kPenRep : 0) |
             ((c.presence_penalty != 0.0 || c.frequency_penalty != 0.0) ? hs::kPenPF : 0);
-    if (p.pen & hs::kPenPF) *any_pf = true;
     if (c.temperature <= 0) {   // src/sampler.ts:36 (NaN is not <= 0)
       p.mode = hs::kModeGreedy;
       p.k = 1;
@@ -141,30 +151,43 @@ int build_plans(const hs_sample_config *cfgs, int rows, int vocab, std::vector<h
                     (long long)k, hs::kMaxK);
     }
     out[(size_t)r] = p;
+    if (p.pen & hs::kPenPF) rt.pf.push_back(r);
+    const bool row_kernel = (p.mode == hs::kModeGreedy || p.mode == hs::kModeSmall) &&
+                            vocab <= hs::kRowMaxVocab && rows >= row_min_rows;
+    (row_kernel ? rt.row : rt.chunk).push_back(r);
   }
   return HS_OK;
 }
 
-int upload_plans(hs_context *ctx, const std::vector<hs::RowPlan> &plans, hipStream_t stream) {
+// Uploads plans and routing lists (skipped when identical to the last call's).
+int upload_plans(hs_context *ctx, const std::vector<hs::RowPlan> &plans, const Routing &rt,
+                 int vocab, hipStream_t stream) {
   const size_t rows = plans.size();
-  const size_t bytes = rows * sizeof(hs::RowPlan);
-  if (ctx->last_plans.size() == rows && ctx->plans.bytes >= bytes &&
-      memcmp(ctx->last_plans.data(), plans.data(), bytes) == 0)
+  const size_t pbytes = rows * sizeof(hs::RowPlan);
+  const size_t lbytes = sizeof(int32_t) * (rt.pf.size() + rt.row.size() + rt.chunk.size());
+  const size_t bytes = pbytes + lbytes;
+  if (ctx->last_plans.size() == rows && ctx->last_vocab == vocab && ctx->plans.bytes >= bytes &&
+      memcmp(ctx->last_plans.data(), plans.data(), pbytes) == 0)
     return HS_OK;
   HS_HIP(ctx->plans.ensure(bytes));
   if (ctx->plan_pending) {   // the staging buffer may still be read by a copy
     HS_HIP(hipEventSynchronize(ctx->plan_done));
     ctx->plan_pending = false;
   }
-  if (ctx->plan_staging_rows < rows) {
+  if (ctx->plan_staging_bytes < bytes) {
     if (ctx->plan_staging) (void)hipHostFree(ctx->plan_staging);
     ctx->plan_staging = nullptr;
-    ctx->plan_staging_rows = 0;
-    HS_HIP(hipHostMalloc(reinterpret_cast<void **>(&ctx->plan_staging), bytes));
-    ctx->plan_staging_rows = rows;
+    ctx->plan_staging_bytes = 0;
+    HS_HIP(hipHostMalloc(&ctx->plan_staging, bytes));
+    ctx->plan_staging_bytes = bytes;
   }
-  memcpy(ctx->plan_staging, plans.data(), bytes);
-  HS_HIP(hipMemcpyAsync(ctx->plans.p, ctx->plan_staging, bytes, hipMemcpyHostToDevice, stream));
+  char *st = static_cast<char *>(ctx->plan_staging);
+  memcpy(st, plans.data(), pbytes);
+  int32_t *lists = reinterpret_cast<int32_t *>(st + pbytes);
+  memcpy(lists, rt.pf.data(), sizeof(int32_t) * rt.pf.size());
+  memcpy(lists + rt.pf.size(), rt.row.data(), sizeof(int32_t) * rt.row.size());
+  memcpy(lists + rt.pf.size() + rt.row.size(), rt.chunk.data(), sizeof(int32_t) * rt.chunk.size());
+  HS_HIP(hipMemcpyAsync(ctx->plans.p, st, bytes, hipMemcpyHostToDevice, stream));
   HS_HIP(hipEventRecord(ctx->plan_done, stream));
   ctx->plan_pending = true;
   try {
@@ -173,6 +196,7 @@ int upload_plans(hs_context *ctx, const std::vector<hs::RowPlan> &plans, hipStre
     ctx->last_plans.clear();
     return fail(HS_ERR_OUT_OF_MEMORY, "host allocation failed");
   }
+  ctx->last_vocab = vocab;
   return HS_OK;
 }
 
@@ -209,27 +233,33 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
     return fail(HS_ERR_UNSUPPORTED, "vocab %d x rows %d too large", vocab, rows);
 
   std::vector<hs::RowPlan> plans;
-  bool any_pf = false;
+  Routing rt;
   try {
-    int rc = build_plans(configs, rows, vocab, plans, &any_pf);
+    int rc = build_plans(configs, rows, vocab, ctx->row_min_rows, plans, rt);
     if (rc) return rc;
   } catch (const std::bad_alloc &) {
     return fail(HS_ERR_OUT_OF_MEMORY, "host allocation failed");
   }
+  const int n_pf = (int)rt.pf.size(), n_row = (int)rt.row.size(), n_chunk = (int)rt.chunk.size();
 
-  // workspace
-  const size_t cand_bytes = (size_t)rows * (size_t)S * hs::kChunkCap * sizeof(uint2);
-  HS_HIP(ctx->cand.ensure(cand_bytes));
-  HS_HIP(ctx->info.ensure((size_t)rows * (size_t)S * sizeof(hs::ChunkInfo)));
-  if (ctx->cand_count.bytes < sizeof(int32_t) * (size_t)rows) {
-    HS_HIP(ctx->cand_count.ensure(sizeof(int32_t) * (size_t)rows));
-    HS_HIP(hipMemset(ctx->cand_count.p, 0, ctx->cand_count.bytes));
+  // workspace (the chunk path only)
+  if (n_chunk > 0) {
+    HS_HIP(ctx->cand.ensure((size_t)n_chunk * (size_t)S * hs::kChunkCap * sizeof(uint2)));
+    HS_HIP(ctx->info.ensure((size_t)n_chunk * (size_t)S * sizeof(hs::ChunkInfo)));
+    if (ctx->cand_count.bytes < sizeof(int32_t) * (size_t)n_chunk) {
+      HS_HIP(ctx->cand_count.ensure(sizeof(int32_t) * (size_t)n_chunk));
+      HS_HIP(hipMemset(ctx->cand_count.p, 0, ctx->cand_count.bytes));
+    }
   }
-  int rc = upload_plans(ctx, plans, stream);
+  int rc = upload_plans(ctx, plans, rt, vocab, stream);
   if (rc) return rc;
 
   hs::Workspace ws;
   ws.plans = static_cast<hs::RowPlan *>(ctx->plans.p);
+  const int32_t *lists = reinterpret_cast<const int32_t *>(ws.plans + rows);
+  ws.pf_list = lists;
+  ws.row_list = lists + n_pf;
+  ws.chunk_list = lists + n_pf + n_row;
   ws.cand = static_cast<uint2 *>(ctx->cand.p);
   ws.cand_count = static_cast<int32_t *>(ctx->cand_count.p);
   ws.info = static_cast<hs::ChunkInfo *>(ctx->info.p);
@@ -242,8 +272,10 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   a.vocab = vocab;
   a.chunks = (int32_t)S;
   a.vec = ((reinterpret_cast<uintptr_t>(d_logits) & 15u) == 0 && (row_stride & 3) == 0) ? 1 : 0;
-  a.any_pf = any_pf ? 1 : 0;
   a.want_cands = (d_cand_ids || d_cand_probs) ? 1 : 0;
+  a.n_pf = n_pf;
+  a.n_row = n_row;
+  a.n_chunk = n_chunk;
   a.hist_ids = d_hist_ids;
   a.hist_off = d_hist_offsets;
   a.uniforms = d_uniforms;
@@ -271,7 +303,8 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   }
   hipError_t e = hs::launch_sample(a, ws, stream, timed ? ev : nullptr);
   if (e != hipSuccess) {
-    (void)hipMemsetAsync(ctx->cand_count.p, 0, ctx->cand_count.bytes, stream);
+    if (ctx->cand_count.p)
+      (void)hipMemsetAsync(ctx->cand_count.p, 0, ctx->cand_count.bytes, stream);
     return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
   }
   return HS_OK;
@@ -318,6 +351,7 @@ int hs_context_create(int device, hs_context **out) {
   hs_context *ctx = new (std::nothrow) hs_context();
   if (!ctx) return fail(HS_ERR_OUT_OF_MEMORY, "host allocation failed");
   ctx->device = device;
+  if (const char *env = getenv("HS_ROW_KERNEL_MIN_ROWS")) ctx->row_min_rows = atoi(env);
   e = hipEventCreateWithFlags(&ctx->plan_done, hipEventDisableTiming);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {

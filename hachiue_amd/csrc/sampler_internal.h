@@ -6,33 +6,38 @@
 
 namespace hs {
 
-// Workgroup geometry of the row-chunk kernel: 256 threads (4 wave64s); each
-// thread holds NV float4s, so one workgroup owns CHUNK consecutive logits of a
-// row and each wave a contiguous quarter of it.
+// ---- row kernel: one 1024-thread workgroup streams a whole row.  Each wave
+// takes 3072-logit spans (12 float4 per lane) round-robin.
+constexpr int kRowThreads = 1024;
+constexpr int kRowWaves = kRowThreads / 64;
+constexpr int kSpanNV = 12;                      // float4 per lane per span
+constexpr int kSpan = 64 * kSpanNV * 4;          // 3072 logits
+constexpr int kRowCandCap = 4096;                // streamed candidates per row
+constexpr int kRowMaxVocab = 1 << 19;            // LDS bitmap limit (64 KiB)
+
+// ---- chunk kernel: 256 threads own CHUNK consecutive logits of a row.
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kNV = 16;                        // float4 per thread
-constexpr int kChunk = kThreads * kNV * 4;     // 16384 logits per workgroup
-constexpr int kWaveSpan = kChunk / kWaves;     // 4096 logits per wave
+constexpr int kNV = 16;                          // float4 per thread
+constexpr int kChunk = kThreads * kNV * 4;       // 16384 logits per workgroup
+constexpr int kWaveSpan = kChunk / kWaves;       // 4096 logits per wave
+constexpr int kChunkCap = 2048;                  // candidates per chunk (row region S*cap)
 
-// Candidate capacity per chunk (two layouts share it): the k<=64 path writes
-// one list per wave at offsets w*kWaveCap; the k<=1024 path writes one list.
-constexpr int kChunkCap = 2048;
-constexpr int kWaveCap = kChunkCap / kWaves;   // 512
-constexpr int kSmallK = 64;                    // wave-select path
-constexpr int kMaxK = 1024;                    // largest k of the select paths
-constexpr int kFinalCap = 12288;               // finalize LDS entries (>= X_row)
+constexpr int kSmallK = 64;                      // wave-select paths
+constexpr int kMaxK = 1024;                      // largest k of the select paths
+constexpr int kFinalCap = 12288;                 // finalize: candidates >= X_row in LDS
+constexpr int kSortCap = 2048;                   // candidates >= T sorted in LDS
 
 enum RowMode : int32_t {
   kModeGreedy = 0,   // temperature <= 0 (src/sampler.ts:36-46)
   kModeSmall = 1,    // 1 <= k <= 64
   kModeGeneric = 2,  // 64 < k <= 1024
-  kModeLarge = 3,    // k > 1024 (nucleus over most of the row)
+  kModeLarge = 3,    // k > 1024
 };
 
 enum RowPen : int32_t {
   kPenRep = 1,       // repetition penalty active
-  kPenPF = 2,        // presence / frequency extension active
+  kPenPF = 2,        // presence / frequency extension active (pre-pass applies all)
 };
 
 // Host-resolved per-row sampling plan (64 bytes).
@@ -50,26 +55,24 @@ struct RowPlan {
 };
 static_assert(sizeof(RowPlan) == 64, "RowPlan layout");
 
-// Per (row, chunk) summary written by the chunk kernel.
+// Per (list position, chunk) summary written by the chunk kernel.
 struct ChunkInfo {
   unsigned long long best;  // greedy: (key << 32) | ~index, 0 = none
   uint32_t thr;             // lower bound key all chunk candidates satisfy
   int32_t finite;           // finite logits in the chunk, -1 if not counted
-  int32_t overflow;         // candidate lists truncated
+  int32_t overflow;         // candidate list truncated
   int32_t pad;
 };
 static_assert(sizeof(ChunkInfo) == 24, "ChunkInfo layout");
 
-// Large-k path: per-chunk histogram of probability mass over key buckets
-// below the row maximum.
-constexpr int kLargeBuckets = 512;
-constexpr int kLargeShift = 20;
-
 struct Workspace {
   RowPlan *plans;            // [rows]
-  uint2 *cand;               // [rows][S][kChunkCap] (key, index)
-  int32_t *cand_count;       // [rows][S][kWaves]
-  ChunkInfo *info;           // [rows][S]
+  const int32_t *pf_list;    // rows penalised by the pre-pass
+  const int32_t *row_list;   // rows of the row kernel
+  const int32_t *chunk_list; // rows of the chunk + finalize kernels
+  uint2 *cand;               // [n_chunk][S][kChunkCap] (key, index)
+  int32_t *cand_count;       // [n_chunk]
+  ChunkInfo *info;           // [n_chunk][S]
 };
 
 struct LaunchArgs {
@@ -79,8 +82,8 @@ struct LaunchArgs {
   int32_t vocab;
   int32_t chunks;            // S = ceil(vocab / kChunk)
   int32_t vec;               // float4 loads allowed (alignment)
-  int32_t any_pf;            // some row uses presence / frequency
   int32_t want_cands;        // exact candidate order must be produced
+  int32_t n_pf, n_row, n_chunk;
   const int32_t *hist_ids;
   const int64_t *hist_off;
   const double *uniforms;
@@ -93,12 +96,14 @@ struct LaunchArgs {
   uint32_t *row_flags;
 };
 
-// Launches the two kernels on `stream`.  When `ev` is not null, records
-// ev[0] before the chunk kernel, ev[1] between the kernels, ev[2] after.
-constexpr int kTimedKernels = 2;
+// Launches the kernels of one call on `stream`.  When `ev` is not null it
+// records ev[0] first and ev[i + 1] after kernel i: 0 penalty pre-pass,
+// 1 row kernel, 2 chunk kernel, 3 finalize (a kernel with no rows is
+// skipped and times ~0).
+constexpr int kTimedKernels = 4;
 hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,
                          hipEvent_t *ev);
 hipError_t prepare_kernels();   // per device, once: raise dynamic LDS limits
-size_t finalize_smem_bytes();
+size_t row_smem_bytes(int vocab);
 
 }  // namespace hs

@@ -190,12 +190,14 @@ class Sampler:
     def set_timing(self, enable: bool) -> None:
         _check(lib().hs_context_set_timing(self._ctx, 1 if enable else 0))
 
+    KERNELS = ("pen_kernel", "row_kernel", "chunk_kernel", "finalize_kernel")
+
     def kernel_times(self):
-        """(chunk_ms_total, finalize_ms_total, calls) since the last query."""
-        ms = (ctypes.c_double * 2)()
+        """({kernel: total device ms}, calls) since the last query."""
+        ms = (ctypes.c_double * len(self.KERNELS))()
         calls = ctypes.c_int64()
-        _check(lib().hs_context_kernel_times(self._ctx, ms, 2, ctypes.byref(calls)))
-        return float(ms[0]), float(ms[1]), int(calls.value)
+        _check(lib().hs_context_kernel_times(self._ctx, ms, len(self.KERNELS), ctypes.byref(calls)))
+        return {k: float(ms[i]) for i, k in enumerate(self.KERNELS)}, int(calls.value)
 
     # ---- drop-in: one host row -------------------------------------------
     def sample_logits(self, logits: np.ndarray, vocab: int, history=(), config: dict | None = None,

@@ -32,3 +32,27 @@ def sampler():
     s = Sampler(0)
     yield s
     s.close()
+
+
+@pytest.fixture(scope="session")
+def sampler_chunk():
+    """A context that routes every row to the chunk + finalize kernels (the
+    row kernel is used only for calls with at least HS_ROW_KERNEL_MIN_ROWS
+    rows, read at context creation)."""
+    from hachiue_amd import Sampler
+    old = os.environ.get("HS_ROW_KERNEL_MIN_ROWS")
+    os.environ["HS_ROW_KERNEL_MIN_ROWS"] = str(1 << 30)
+    try:
+        s = Sampler(0)
+    finally:
+        if old is None:
+            del os.environ["HS_ROW_KERNEL_MIN_ROWS"]
+        else:
+            os.environ["HS_ROW_KERNEL_MIN_ROWS"] = old
+    yield s
+    s.close()
+
+
+@pytest.fixture(params=["row", "chunk"])
+def any_sampler(request, sampler, sampler_chunk):
+    return sampler if request.param == "row" else sampler_chunk

@@ -87,9 +87,13 @@ def compare(got: GpuResult, want, want_logits, configs, vocab, cap, label=""):
                           f"{got.cand_ids[r, :8].tolist()} vs {want.cand_ids[r, :8].tolist()}")
         if n >= 2:
             gp, wp = got.cand_probs[r, :m].astype(np.float64), want.cand_probs[r, :m].astype(np.float64)
-            rel = np.abs(gp - wp) / np.maximum(np.abs(wp), np.finfo(np.float32).tiny)
-            if not (rel <= PROB_RTOL).all():
-                errors.append(f"row {r}: probs rel err {rel.max():.3g}")
+            with np.errstate(invalid="ignore"):
+                rel = np.abs(gp - wp) / np.maximum(np.abs(wp), np.finfo(np.float32).tiny)
+            # a +Infinity candidate makes every probability NaN in the
+            # reference too ((Inf - Inf) * invTemp, src/sampler.ts:84)
+            ok = (rel <= PROB_RTOL) | (np.isnan(gp) & np.isnan(wp))
+            if not ok.all():
+                errors.append(f"row {r}: probs rel err {np.nanmax(rel):.3g}")
         near_topp = want.topp_margin[r] < BOUNDARY
         if got.cutoff[r] != want.cutoff[r] and not near_topp:
             errors.append(f"row {r}: cutoff {got.cutoff[r]} != {want.cutoff[r]}")

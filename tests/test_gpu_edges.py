@@ -1,0 +1,168 @@
+"""GPU parity on the edge cases the reference's semantics single out
+(src/sampler.ts): signed zeros, NaN / +-Infinity, ties at and inside the
+top-k (slot-history order), k beyond the finite count, fractional / zero /
+negative / infinite topK, NaN options, penalties below 1 and on zeros,
+ragged vocab and stride, empty and out-of-range histories, extreme uniforms.
+Both kernel routes (row kernel, chunk + finalize) are checked."""
+import numpy as np
+import pytest
+
+from tests.gpu_util import compare, run_gpu, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _batch(cases, vocab, stride=None):
+    stride = stride or vocab
+    rows = len(cases)
+    logits = np.full((rows, stride), np.float32(np.nan), np.float32)
+    hists, configs, us = [], [], []
+    for r, (row, hist, cfg, u) in enumerate(cases):
+        row = np.asarray(row, np.float32)
+        logits[r, :row.size] = row
+        hists.append(np.asarray(hist, np.int32))
+        configs.append(cfg)
+        us.append(u)
+    off = np.zeros(rows + 1, np.int64)
+    for r, h in enumerate(hists):
+        off[r + 1] = off[r] + h.size
+    ids = np.concatenate(hists).astype(np.int32) if off[-1] else np.zeros(1, np.int32)
+    return logits, ids, off, configs, np.array(us, np.float64)
+
+
+def _run(sampler, cases, vocab, stride=None, cap=64, label="edges"):
+    logits, ids, off, configs, us = _batch(cases, vocab, stride)
+    got = run_gpu(sampler, logits, vocab, ids, off, configs, us, cap, stride=logits.shape[1])
+    want, want_logits = run_oracle(logits, vocab, ids, off, configs, us, cap)
+    compare(got, want, want_logits, configs, vocab, cap, label)
+    return got, want
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+SAMPLE = dict(temperature=0.7, topK=40, topP=0.9)
+
+
+def test_signed_zeros(any_sampler):
+    V = 3000
+    r = _rng(1)
+    a = np.where(r.random(V) < 0.5, np.float32(0.0), np.float32(-0.0)).astype(np.float32)
+    b = a.copy(); b[:5] = -1.0
+    c = -np.abs(r.standard_normal(V).astype(np.float32)); c[[7, 900, 2000]] = -0.0; c[50] = 0.0
+    cases = [(a, [], SAMPLE, 0.3), (b, [], dict(temperature=0.0), 0.5),
+             (c, [], dict(temperature=1.0, topK=3, topP=1.0), 0.9),
+             (a, [], dict(temperature=1.0, topK=1), 0.2)]
+    _run(any_sampler, cases, V)
+
+
+def test_nan_and_infinities(any_sampler):
+    V = 2000
+    r = _rng(2)
+    base = r.standard_normal(V).astype(np.float32)
+    one_inf = base.copy(); one_inf[123] = np.inf
+    two_inf = base.copy(); two_inf[[5, 1500]] = np.inf
+    nan0 = base.copy(); nan0[0] = np.nan
+    some_nan = base.copy(); some_nan[::7] = np.nan
+    all_nan = np.full(V, np.nan, np.float32)
+    all_ninf = np.full(V, -np.inf, np.float32)
+    one_finite = all_ninf.copy(); one_finite[777] = 3.0
+    ninf_mix = base.copy(); ninf_mix[::3] = -np.inf
+    cases = [(one_inf, [], SAMPLE, 0.5), (two_inf, [], SAMPLE, 0.5),
+             (nan0, [], dict(temperature=0.0), 0.1), (nan0, [], SAMPLE, 0.4),
+             (some_nan, [], SAMPLE, 0.6), (all_nan, [], SAMPLE, 0.5),
+             (all_nan, [], dict(temperature=0.0), 0.5), (all_ninf, [], SAMPLE, 0.5),
+             (all_ninf, [], dict(temperature=0.0), 0.5), (one_finite, [], SAMPLE, 0.5),
+             (ninf_mix, [], dict(temperature=0.9, topK=100, topP=0.95), 0.7)]
+    _run(any_sampler, cases, V)
+
+
+def test_ties(any_sampler):
+    V = 5000
+    r = _rng(3)
+    all_eq = np.ones(V, np.float32)
+    boundary = r.standard_normal(V).astype(np.float32)
+    boundary[r.choice(V, 60, replace=False)] = 4.0          # 60 equal values around the k-th
+    inside = r.standard_normal(V).astype(np.float32)
+    inside[r.choice(V, 6, replace=False)] = 9.0             # a tie group at the top
+    coarse = np.round(r.standard_normal(V) * 4).astype(np.float32)   # many duplicates
+    kmax_tie = r.standard_normal(V).astype(np.float32); kmax_tie[[10, 20, 4000]] = 7.5
+    cases = [(all_eq, [], SAMPLE, 0.5), (all_eq, [], dict(temperature=0.0), 0.5),
+             (boundary, [], SAMPLE, 0.99), (inside, [], SAMPLE, 0.01),
+             (inside, [], dict(temperature=1.0, topK=10, topP=1.0), 0.55),
+             (coarse, [], dict(temperature=1.3, topK=64, topP=1.0), 0.77),
+             (coarse, [], dict(temperature=1.3, topK=200, topP=1.0), 0.33),
+             (kmax_tie, [], dict(temperature=1.0, topK=1), 0.5),
+             (kmax_tie, [], dict(temperature=0.0), 0.5)]
+    for u in (0.0, 0.25, 0.5, 0.75, 1.0 - 2.0 ** -53):
+        cases.append((inside, [], dict(temperature=0.5, topK=8, topP=1.0), u))
+    _run(any_sampler, cases, V, cap=256)
+
+
+def test_k_beyond_finite_and_topk_forms(any_sampler):
+    V = 50
+    r = _rng(4)
+    row = np.round(r.standard_normal(V) * 2).astype(np.float32)
+    sparse = np.full(V, -np.inf, np.float32); sparse[[3, 9, 11, 30]] = [1.0, 2.0, 1.0, 2.0]
+    cases = [(row, [], dict(temperature=1.0, topK=64, topP=1.0), 0.42),
+             (row, [], dict(temperature=1.0, topK=float("inf"), topP=0.8), 0.42),
+             (row, [], dict(temperature=1.0, topK=0), 0.3),        # 0 -> 64
+             (row, [], dict(temperature=1.0, topK=-3), 0.3),       # negative -> 64
+             (row, [], dict(temperature=1.0, topK=2.7), 0.6),      # truncated to 2
+             (row, [], dict(temperature=1.0, topK=0.5), 0.6),      # max(1, 0.5) -> 1
+             (row, [], dict(temperature=1.0, topK=float("nan")), 0.6),   # NaN -> 64
+             (sparse, [], dict(temperature=1.0, topK=3, topP=1.0), 0.99),
+             (sparse, [], dict(temperature=1.0, topK=10, topP=1.0), 0.99),
+             (row, [], {}, 0.5)]                                   # reference defaults
+    _run(any_sampler, cases, V)
+
+
+def test_option_edge_values(any_sampler):
+    V = 4000
+    r = _rng(5)
+    row = (r.standard_normal(V) * 2.5).astype(np.float32)
+    cases = [(row, [], dict(temperature=float("nan")), 0.5),
+             (row, [], dict(temperature=0.7, topP=float("nan")), 0.5),
+             (row, [], dict(temperature=0.7, minP=float("nan")), 0.5),
+             (row, [], dict(temperature=0.7, minP=0.05), 0.8),
+             (row, [], dict(temperature=0.7, minP=1.0), 0.8),
+             (row, [], dict(temperature=0.7, minP=2.0), 0.8),
+             (row, [], dict(temperature=0.7, topP=0.0), 0.8),
+             (row, [], dict(temperature=1e-6, topK=40), 0.8),
+             (row, [], dict(temperature=1e6, topK=40, topP=0.5), 0.8),
+             (row, [], dict(temperature=-1.0), 0.8),
+             (row, [], dict(temperature=0.7, topK=40, topP=0.9), 0.0)]
+    _run(any_sampler, cases, V)
+
+
+def test_penalty_edges(any_sampler):
+    V = 6000
+    r = _rng(6)
+    row = (r.standard_normal(V) * 2).astype(np.float32)
+    row[[10, 11, 12]] = [0.0, -0.0, -3.0]
+    long_hist = [7] + list(r.integers(0, V, 128))                  # id 7 falls out of the last 128
+    cases = [(row, [10, 11, 12, 12, 12, -5, V, V + 3, 2**31 - 1], dict(repetitionPenalty=2.0, **SAMPLE), 0.4),
+             (row, [10, 11, 12], dict(repetitionPenalty=0.8, **SAMPLE), 0.4),
+             (row, [10, 11, 12, 100], dict(repetitionPenalty=0.0, **SAMPLE), 0.4),
+             (row, [10, 100], dict(repetitionPenalty=float("nan"), **SAMPLE), 0.4),
+             (row, long_hist, dict(repetitionPenalty=1.3, **SAMPLE), 0.4),
+             (row, [], dict(repetitionPenalty=1.3, **SAMPLE), 0.4),
+             (row, list(r.integers(0, 50, 300)), dict(repetitionPenalty=1.2, presencePenalty=0.5,
+                                                      frequencyPenalty=0.25, **SAMPLE), 0.4),
+             (row, [5, 5, 5, 9], dict(presencePenalty=-1.0, frequencyPenalty=0.0, **SAMPLE), 0.4),
+             (row, [5, 5, 5, 9], dict(temperature=0.0, repetitionPenalty=1.5), 0.4)]
+    _run(any_sampler, cases, V)
+
+
+@pytest.mark.parametrize("vocab,pad", [(151669, 0), (1001, 3), (4097, 1), (1, 0), (2, 5), (3, 0)])
+def test_ragged_vocab_and_stride(any_sampler, vocab, pad):
+    r = _rng(vocab + pad)
+    cases = []
+    for i in range(3):
+        row = (r.standard_normal(vocab) * 2).astype(np.float32)
+        hist = list(r.integers(0, vocab, 20))
+        cases.append((row, hist, dict(temperature=0.8, topK=40, topP=0.95, repetitionPenalty=1.1),
+                      float(r.random())))
+    cases.append((cases[0][0], [], dict(temperature=0.0), 0.5))
+    _run(any_sampler, cases, vocab, stride=vocab + pad)

@@ -21,31 +21,31 @@ def _check(sampler, wl, cap=CAP, label=None):
 
 
 @pytest.mark.parametrize("seed", [0, 1])
-def test_single_row(sampler, seed):
-    _check(sampler, workloads.make("single", seed))
+def test_single_row(any_sampler, seed):
+    _check(any_sampler, workloads.make("single", seed))
 
 
-def test_single_row_greedy(sampler):
-    _check(sampler, workloads.make("single", 3, greedy=True))
+def test_single_row_greedy(any_sampler):
+    _check(any_sampler, workloads.make("single", 3, greedy=True))
 
 
-def test_single_row_exact_spikes(sampler):
+def test_single_row_exact_spikes(any_sampler):
     # eight logits of exactly 12.0: ties inside the top-k, order by slot history
     wl = workloads.make("single", 4, exact_spikes=True)
-    _, got, _ = _check(sampler, wl)
+    _, got, _ = _check(any_sampler, wl)
 
 
-def test_batch64(sampler):
-    _check(sampler, workloads.make("batch64", 0))
+def test_batch64(any_sampler):
+    _check(any_sampler, workloads.make("batch64", 0))
 
 
-def test_headline_batch(sampler):
-    _check(sampler, workloads.make("headline", 0))
+def test_headline_batch(any_sampler):
+    _check(any_sampler, workloads.make("headline", 0))
 
 
-def test_perrow256(sampler):
-    _check(sampler, workloads.make("perrow256", 0), cap=1024)
+def test_perrow256(any_sampler):
+    _check(any_sampler, workloads.make("perrow256", 0), cap=1024)
 
 
-def test_v262k512(sampler):
-    _check(sampler, workloads.make("v262k512", 0), cap=128)
+def test_v262k512(any_sampler):
+    _check(any_sampler, workloads.make("v262k512", 0), cap=128)
