@@ -142,12 +142,75 @@ struct SelectSmem {
   int32_t digit, above, total;
 };
 
+// Inclusive prefix sum across a wave64 with DPP row shifts and row
+// broadcasts (no LDS traffic).
+__device__ __forceinline__ uint32_t wave_scan_incl(uint32_t x) {
+  // row_shr:n = 0x110 + n, row_bcast:15 = 0x142, row_bcast:31 = 0x143
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF, true);
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF, true);
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, true);
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF, true);
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xA, 0xF, false);
+  x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xC, 0xF, false);
+  return x;
+}
+
+// Exact k-th largest key of a block-wide multiset, four 8-bit digit passes.
+// All threads add their keys to a 256-bin LDS histogram; wave 0 alone finds
+// the digit (bins scanned from the top, four per lane) and clears the bins
+// for the next pass: two barriers per pass.  `hist_pass(shift, prefix, pass)`
+// adds this thread's keys (see hist_add).  Returns T, or 0 when fewer than k
+// keys participate; *total receives the participant count.
+template <int NT, typename HistPass>
+__device__ __forceinline__ uint32_t block_select_fast(int k, HistPass hist_pass, SelectSmem &sm,
+                                                      int *total) {
+  const int tid = threadIdx.x;
+  if (tid < 256) sm.hist[tid] = 0;
+  __syncthreads();
+  uint32_t prefix = 0;
+  int rem = k;
+  for (int pass = 0; pass < 4; ++pass) {
+    const int shift = 24 - 8 * pass;
+    hist_pass(shift, prefix, pass);
+    __syncthreads();
+    if (tid < 64) {
+      // lane l owns bins 255-4l .. 252-4l (descending digit order)
+      uint32_t c[4], part = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c[i] = sm.hist[255 - 4 * tid - i];
+        sm.hist[255 - 4 * tid - i] = 0;
+        part += c[i];
+      }
+      const uint32_t incl = wave_scan_incl(part);
+      if (pass == 0 && tid == 63) sm.total = (int)incl;
+      uint32_t run = incl - part;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (run < (uint32_t)rem && run + c[i] >= (uint32_t)rem) {
+          sm.digit = 255 - 4 * tid - i;
+          sm.above = (int)run;
+        }
+        run += c[i];
+      }
+    }
+    __syncthreads();
+    if (pass == 0) {
+      *total = sm.total;
+      if (sm.total < k) return 0u;
+    }
+    prefix |= (uint32_t)sm.digit << shift;
+    rem -= sm.above;
+  }
+  return prefix;
+}
+
 // Exact k-th largest key of a block-wide multiset: four 8-bit digit passes
 // over a 256-bin LDS histogram.  `hist_pass(shift, prefix, pass)` adds this
 // thread's keys (see hist_add).  Returns T, or 0 when fewer than k keys
 // participate; *total receives the participant count.
 template <int NT, typename HistPass>
-__device__ uint32_t block_select(int k, HistPass hist_pass, SelectSmem &sm, int *total) {
+__device__ __forceinline__ uint32_t block_select(int k, HistPass hist_pass, SelectSmem &sm, int *total) {
   const int tid = threadIdx.x;
   uint32_t prefix = 0;
   int rem = k;
@@ -281,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void pen_kernel(LaunchArgs a, Workspace w
 // row by one wave: slot j holds (sv[j], sid[j]); a logit enters iff it is
 // strictly greater than the current minimum, into the first slot holding that
 // minimum.  Logits are consumed in index order.
-__device__ void replay_row(const float *rowp, int vocab, int k, float *sv, int32_t *sid) {
+__device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, float *sv, int32_t *sid) {
   const int lane = lane_id();
   for (int j = lane; j < k; j += 64) { sv[j] = -INFINITY; sid[j] = -1; }
   float mv = -INFINITY;
@@ -484,7 +547,7 @@ __device__ void finish_row(const LaunchArgs &a, const RowPlan &P, int row, const
 
 // Writes the greedy result: first index of the maximum (src/sampler.ts:37-45);
 // `best` is the packed maximum over the row (0 = no non-NaN logit).
-__device__ void write_greedy(const LaunchArgs &a, int row, const float *rowp,
+__device__ __forceinline__ void write_greedy(const LaunchArgs &a, int row, const float *rowp,
                              unsigned long long best) {
   int token = best ? (int)cand_idx(best) : 0;
   if (isnan(rowp[0])) token = 0;   // bestVal = logits[0] = NaN: nothing is '>' it
@@ -503,7 +566,7 @@ __device__ int select_into(int n_ent, GetEnt get, uint32_t lo, int k, unsigned l
                            SelectSmem &sm, TailSmem &f, uint32_t *T_out) {
   const int tid = threadIdx.x;
   int total = 0;
-  const uint32_t T = block_select<NT>(
+  const uint32_t T = block_select_fast<NT>(
       k,
       [&](int shift, uint32_t prefix, int pass) {
         for (int p = tid; p < n_ent; p += NT) {
@@ -532,148 +595,469 @@ __device__ int select_into(int n_ent, GetEnt get, uint32_t lo, int k, unsigned l
 
 // ---------------------------------------------------------------- row kernel
 
+// One span of a row into registers: lane-coalesced float4 loads, NaN past
+// the vocabulary (NaN never becomes a candidate).  Spans wholly inside the
+// row take the branch-free path.
+template <bool VEC>
+__device__ __forceinline__ void load_span(float (&v)[kSpanNV][4], const float *rowp, int base,
+                                          int V, int lane) {
+  if (VEC && base + kSpan <= V) {
+#pragma unroll
+    for (int j = 0; j < kSpanNV; ++j) {
+      const int e = base + (j * 64 + lane) * 4;
+      const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(rowp + e));
+      v[j][0] = t[0]; v[j][1] = t[1]; v[j][2] = t[2]; v[j][3] = t[3];
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < kSpanNV; ++j) {
+    const int e = base + (j * 64 + lane) * 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[j][q] = (e + q < V) ? rowp[e + q] : __builtin_nanf("");
+  }
+}
+
+// Exclusive prefix over the wave of a per-lane count c < 64 (and the wave
+// total), from the six bit-slices of c: no LDS traffic.
+__device__ __forceinline__ uint32_t wave_excl_prefix(uint32_t c, uint32_t *total) {
+  uint32_t pre = 0, tot = 0;
+#pragma unroll
+  for (int b = 0; b < 6; ++b) {
+    const unsigned long long m = __ballot((c >> b) & 1u);
+    pre += lanes_below(m) << b;
+    tot += (uint32_t)__popcll(m) << b;
+  }
+  *total = tot;
+  return pre;
+}
+
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t x, int lane) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, lane);
+}
+__device__ __forceinline__ float readlane_f32(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+__device__ __forceinline__ double readlane_f64(double x, int lane) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(x);
+  const uint32_t lo = readlane_u32((uint32_t)b, lane), hi = readlane_u32((uint32_t)(b >> 32), lane);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// Sorts one packed candidate per lane (0 = none) descending among the first n
+// lanes by counting, for each lane, the larger packed values (readlane loop,
+// no shuffles), then scattering through `tmp` (64 entries of LDS).
+__device__ __forceinline__ unsigned long long wave_rank_sort(unsigned long long x, int n,
+                                                             unsigned long long *tmp) {
+  const int lane = lane_id();
+  int rank = 0;
+  for (int j = 0; j < n; ++j) {
+    const unsigned long long y =
+        ((unsigned long long)readlane_u32((uint32_t)(x >> 32), j) << 32) |
+        readlane_u32((uint32_t)x, j);
+    rank += y > x ? 1 : 0;
+  }
+  if (lane < n) tmp[rank] = x;   // packed values are distinct (index in the low word)
+  return lane < n ? tmp[lane] : 0ull;
+}
+
+// Tail of src/sampler.ts:76-117 for n <= 64 candidates held one per lane
+// (value keys `key`, sorted descending), by one wave.  Sequential sums run in
+// the reference's order through readlane, so every binary64 rounding matches.
+// Returns the picked position (-1 when n == 0) and writes the cutoff and each
+// lane's normalised probability.
+__device__ __forceinline__ int wave_tail(uint32_t key, int n, const RowPlan &P, double u, int *cutoff,
+                         float *prob_out) {
+  const int lane = lane_id();
+  if (n < 2) {
+    *cutoff = n;
+    *prob_out = 1.0f;
+    return n == 1 ? 0 : -1;
+  }
+  const double v = (double)key2f(key);
+  const double maxl = readlane_f64(v, 0);
+  const double inv_temp = 1.0 / P.temperature;
+  const double p = lane < n ? exp((v - maxl) * inv_temp) : 0.0;
+  double sum = 0;
+  for (int i = 0; i < n; ++i) sum += readlane_f64(p, i);   // unrounded, in order
+  const float prob = (float)((double)(float)p / sum);
+  *prob_out = prob;
+  const double thr = P.min_p * (double)readlane_f32(prob, 0);
+  double cum = 0;
+  int cut = n;
+  for (int i = 0; i < n; ++i) {
+    const double pi = (double)readlane_f32(prob, i);
+    if (i > 0 && pi < thr) { cut = i; break; }
+    cum += pi;
+    if (cum >= P.top_p) { cut = i + 1; break; }
+  }
+  double kept = 0;
+  for (int i = 0; i < cut; ++i) kept += (double)readlane_f32(prob, i);
+  double r = u * kept;
+  int pick = cut - 1;
+  for (int i = 0; i < cut; ++i) {
+    r -= (double)readlane_f32(prob, i);
+    if (r <= 0) { pick = i; break; }
+  }
+  *cutoff = cut;
+  return pick;
+}
+
+// Completes a row of the row kernel in wave 0 from F, the row's top-64 list
+// (sorted packed candidates, one per lane).  extra_ties: logits equal to the
+// k-th largest may exist beyond F.  Replays the reference's slot scan when an
+// equal-value group can change the token (or the candidate outputs), and
+// always when force_replay (the candidate list overflowed).
+__device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &P, int row, const float *rowp,
+                            unsigned long long F, bool extra_ties, bool force_replay, double u,
+                            float *rsv, int32_t *rsid) {
+  const int lane = lane_id();
+  const int k = P.k;
+  const uint32_t fkey = cand_key(F);
+  const unsigned long long Fk = __shfl(F, k - 1);
+  const uint32_t T = cand_key(Fk);           // 0: fewer than k candidates
+  const int n_sel = __popcll(__ballot(F != 0ull && fkey >= T));
+  int n = n_sel < k ? n_sel : k;
+  const bool boundary_tie = n_sel > k || (T != 0 && extra_ties);
+  const uint32_t next_key = __shfl_down(fkey, 1);
+  const bool internal_tie = __ballot(lane + 1 < n && next_key == fkey) != 0;
+
+  uint32_t key = fkey;
+  int32_t id = (int32_t)cand_idx(F);
+  int cut = 0;
+  float prob = 0.f;
+  int pick = force_replay ? -1 : wave_tail(key, n, P, u, &cut, &prob);
+  bool replayed = false;
+  if (boundary_tie || internal_tie || force_replay) {
+    // the order inside a group of equal values follows the slot history
+    bool need = a.want_cands != 0 || force_replay;
+    if (!need && pick >= 0) {
+      const uint32_t kp = readlane_u32(key, pick);
+      const uint32_t km = pick > 0 ? readlane_u32(key, pick - 1) : 0u;
+      const uint32_t kn = pick + 1 < n ? readlane_u32(key, pick + 1) : 0u;
+      need = (pick > 0 && km == kp) || (pick + 1 < n && kn == kp) || (boundary_tie && kp == T);
+    }
+    if (need) {
+      replay_row(rowp, a.vocab, k, rsv, rsid);
+      const bool filled = lane < k && rsid[lane] >= 0;
+      unsigned long long x = filled ? pack_cand(f2key(rsv[lane]), (uint32_t)lane) : 0ull;
+      x = wave_sort_desc64(x);   // value descending, slot ascending (stable sort)
+      n = __popcll(__ballot(filled));
+      key = cand_key(x);
+      id = lane < n ? rsid[cand_idx(x)] : -1;
+      pick = wave_tail(key, n, P, u, &cut, &prob);
+      replayed = true;
+    }
+  }
+  const int token = pick >= 0 ? __shfl(id, pick) : 0;
+  if (lane == 0) {
+    a.tokens[row] = token;
+    if (a.cand_count_out) a.cand_count_out[row] = n;
+    if (a.cutoff_out) a.cutoff_out[row] = cut;
+    if (a.row_flags) {
+      uint32_t fl = 0;
+      if (replayed) fl |= HS_ROW_REPLAYED;
+      if (boundary_tie || internal_tie) fl |= HS_ROW_TIES;
+      if (n < 2) fl |= HS_ROW_SINGLE;
+      a.row_flags[row] = fl;
+    }
+  }
+  const int cs = a.cand_stride;
+  if (lane < n && lane < cs) {
+    if (a.cand_ids) a.cand_ids[(int64_t)row * cs + lane] = id;
+    if (a.cand_probs) a.cand_probs[(int64_t)row * cs + lane] = prob;
+  }
+}
+
+// Selects, in one wave, the top-64 of n packed candidates at ent[0, n)
+// (n <= 512, LDS): T = exact k-th largest key by a binary search over the key
+// bits (up to eight entries per lane, ballot counts), then the entries with
+// key >= T gathered through `tmp` (64 entries) and sorted.  *extra is set
+// when more than 64 entries reach T (the tie group at T extends beyond).
+__device__ __forceinline__ unsigned long long wave_top64(const unsigned long long *ent, int n,
+                                                         int k, unsigned long long *tmp,
+                                                         bool *extra) {
+  const int lane = lane_id();
+  const int slots = (n + 63) >> 6;
+  uint32_t key[8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int i = lane + 64 * s;
+    key[s] = (s < slots && i < n) ? cand_key(ent[i]) : 0u;
+  }
+  uint32_t T = 0;
+  if (n >= k) {
+#pragma unroll 1
+    for (int b = 31; b >= 0; --b) {
+      const uint32_t c = T | (1u << b);
+      int cnt = 0;
+#pragma unroll
+      for (int s = 0; s < 8; ++s)
+        if (s < slots) cnt += __popcll(__ballot(key[s] >= c));
+      if (cnt >= k) T = c;
+    }
+  }
+  const uint32_t lo = T ? T : 1u;
+  int pos = 0;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    if (s < slots) {
+      const bool pass = key[s] >= lo;
+      const unsigned long long b = __ballot(pass);
+      const int p = pos + (int)lanes_below(b);
+      if (pass && p < 64) tmp[p] = ent[lane + 64 * s];
+      pos += __popcll(b);
+    }
+  }
+  *extra = pos > 64;
+  const int m = pos < 64 ? pos : 64;
+  const unsigned long long x = lane < m ? tmp[lane] : 0ull;
+  return wave_rank_sort(x, m, tmp);
+}
+
+// Appends the logits of v passing `xf` (and, with a repetition penalty, not
+// penalised) to cbuf: one LDS reservation per non-empty ballot.  For spans
+// after the bound is tight, where candidates are rare.
+template <bool REP>
+__device__ __forceinline__ void append_rare(const float (&v)[kSpanNV][4], int base, int lane,
+                                            float xf, const uint32_t *bitmap,
+                                            unsigned long long *cbuf, int *n_c) {
+#pragma unroll
+  for (int j = 0; j < kSpanNV; ++j) {
+    const int e = base + (j * 64 + lane) * 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      bool pass = v[j][q] >= xf;
+      if (__ballot(pass)) {
+        if (REP && pass) pass = !((bitmap[(e + q) >> 5] >> ((e + q) & 31)) & 1u);
+        const unsigned long long b = __ballot(pass);
+        if (b) {
+          int bp = 0;
+          if (lane_id() == (int)(__ffsll((long long)b) - 1)) bp = atomicAdd(n_c, __popcll(b));
+          bp = __shfl(bp, __ffsll((long long)b) - 1);
+          const int p = bp + (int)lanes_below(b);
+          if (pass && p < kRowCandCap) cbuf[p] = pack_cand(f2key(v[j][q]), (uint32_t)(e + q));
+        }
+      }
+    }
+  }
+}
+
+// Packed maximum (value, then lowest index) of a span, folded into `best`.
+__device__ __forceinline__ unsigned long long greedy_span(const float (&v)[kSpanNV][4], int base,
+                                                          int lane, unsigned long long best) {
+#pragma unroll
+  for (int j = 0; j < kSpanNV; ++j) {
+    const int e = base + (j * 64 + lane) * 4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t key = f2key(v[j][q]);
+      const unsigned long long c = key ? pack_cand(key, (uint32_t)(e + q)) : 0ull;
+      best = c > best ? c : best;
+    }
+  }
+  return best;
+}
+
+size_t row_smem_bytes(int vocab) {
+  const size_t words = ((size_t)vocab + 31) / 32;
+  return (size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + 64 * 8 + 128 * 8 +
+         (size_t)kSmallK * 8 + words * 4;
+}
+
 struct RowSmem {
   SelectSmem sel;
   TailSmem tail;
   unsigned long long best[kRowWaves];
+  double temperature, top_p, min_p, u;   // fetched at the start for the tail
   uint32_t theta;
-  int32_t n_c;
+  int32_t n_c, n_pen, n_keep;
 };
-
-size_t row_smem_bytes(int vocab) {
-  const size_t words = ((size_t)vocab + 31) / 32;
-  return (size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + (size_t)kSmallK * 8 +
-         (size_t)kSmallK * 4 * 5 + words * 4;
-}
 
 template <bool VEC>
 __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspace ws) {
   extern __shared__ unsigned long long rdyn[];
-  unsigned long long *cbuf = rdyn;                       // kRowCandCap
-  unsigned long long *srt = cbuf + kRowCandCap;          // kSortCap
-  RowScratch s;
-  s.sp = reinterpret_cast<double *>(srt + kSortCap);     // kSmallK each below
-  s.skey = reinterpret_cast<uint32_t *>(s.sp + kSmallK);
-  s.sids = reinterpret_cast<int32_t *>(s.skey + kSmallK);
-  s.sprob = reinterpret_cast<float *>(s.sids + kSmallK);
-  s.rsv = s.sprob + kSmallK;
-  s.rsid = reinterpret_cast<int32_t *>(s.rsv + kSmallK);
-  uint32_t *bitmap = reinterpret_cast<uint32_t *>(s.rsid + kSmallK);   // ceil(V/32)
+  unsigned long long *cbuf = rdyn;                         // kRowCandCap candidates
+  unsigned long long *srt = cbuf + kRowCandCap;            // kSortCap (fallback select)
+  unsigned long long *tmp = srt + kSortCap;                // 64
+  float *pen_val = reinterpret_cast<float *>(tmp + 64);    // 128 penalised values
+  int32_t *pen_id = reinterpret_cast<int32_t *>(pen_val + 128);   // 128 their ids
+  float *rsv = reinterpret_cast<float *>(pen_id + 128);    // kSmallK replay slots
+  int32_t *rsid = reinterpret_cast<int32_t *>(rsv + kSmallK);
+  uint32_t *bitmap = reinterpret_cast<uint32_t *>(rsid + kSmallK);   // ceil(V/32)
   __shared__ RowSmem rs;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row = ws.row_list[blockIdx.x];
-  const RowPlan P = ws.plans[row];
+  const RowPlan *plan = ws.plans + row;
   float *rowp = a.logits + (int64_t)row * a.stride;
   const int V = a.vocab;
-  const bool greedy = P.mode == kModeGreedy;
-  const int k = P.k;
+  // only what the streaming loop needs is read here; the tail rereads the plan
+  const bool greedy = plan->mode == kModeGreedy;
+  const int k = plan->k;
+  const int penbits = plan->pen;
   // presence / frequency rows were penalised in place by pen_kernel
-  const bool rep = (P.pen & kPenRep) && !(P.pen & kPenPF);
+  const bool rep = (penbits & kPenRep) && !(penbits & kPenPF);
+  const int nspan = (V + kSpan - 1) / kSpan;
 
-  if (tid == 0) { rs.theta = 0; rs.n_c = 0; }
+  if (tid == 0) {   // the tail's parameters, fetched before the stream starts
+    rs.temperature = plan->temperature;
+    rs.top_p = plan->top_p;
+    rs.min_p = plan->min_p;
+    rs.u = a.uniforms[row];
+  }
+  float v[kSpanNV][4];
+  // the first span's loads are in flight while the penalty set is built
+  if (wave < nspan) load_span<VEC>(v, rowp, wave * kSpan, V, lane);
+  if (tid == 0) { rs.theta = 0; rs.n_c = 0; rs.n_pen = 0; rs.n_keep = 0; }
   if (rep) {
+    // src/sampler.ts:24-33: the distinct ids of the last 128 history entries.
+    // Their logits leave the stream (bitmap) and join the selection with the
+    // penalised value; the in-place write-back waits until every read of the
+    // row is done.
     const int words = (V + 31) >> 5;
     for (int i = tid; i < words; i += kRowThreads) bitmap[i] = 0;
     __syncthreads();
     const int64_t h0 = a.hist_off ? a.hist_off[row] : 0;
     const int64_t hl = a.hist_off ? a.hist_off[row + 1] - h0 : 0;
     const int64_t last = hl < 128 ? hl : 128;   // history.slice(-128)
-    for (int64_t t = tid; t < last; t += kRowThreads) {
-      const int id = a.hist_ids[h0 + hl - last + t];
-      if (id >= 0 && id < V) atomicOr(&bitmap[id >> 5], 1u << (id & 31));
+    if (tid < last) {
+      const int id = a.hist_ids[h0 + hl - last + tid];
+      if (id >= 0 && id < V) {
+        const uint32_t bit = 1u << (id & 31);
+        if (!(atomicOr(&bitmap[id >> 5], bit) & bit)) {   // the first occurrence owns the id
+          RowPlan pr;
+          pr.rep = plan->rep;
+          pr.pen = kPenRep;
+          const int slot = atomicAdd(&rs.n_pen, 1);
+          pen_val[slot] = penalise(rowp[id], true, 0u, pr);
+          pen_id[slot] = id;
+        }
+      }
     }
   }
   __syncthreads();
 
-  unsigned long long best = 0;
-  const int nspan = (V + kSpan - 1) / kSpan;
-  for (int sp = wave; sp < nspan; sp += kRowWaves) {
-    const int base = sp * kSpan;
-    float v[kSpanNV][4];
+  // ---- round 0: span `wave`
+  const bool have0 = wave < nspan;
+  if (have0 && rep) {
 #pragma unroll
     for (int j = 0; j < kSpanNV; ++j) {
-      const int e = base + (j * 64 + lane) * 4;
-      if (VEC && e + 3 < V) {
-        const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(rowp + e));
-        v[j][0] = t[0]; v[j][1] = t[1]; v[j][2] = t[2]; v[j][3] = t[3];
-      } else {
+      const int e = wave * kSpan + (j * 64 + lane) * 4;
+      if (e < V) {
+        const uint32_t bits = (bitmap[e >> 5] >> (e & 31)) & 0xFu;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[j][q] = (e + q < V) ? rowp[e + q] : __builtin_nanf("");
+        for (int q = 0; q < 4; ++q)
+          if (bits & (1u << q)) v[j][q] = __builtin_nanf("");   // never selected
       }
     }
-    if (rep) {
-      // src/sampler.ts:24-33 on the ids of this span, written back in place
+  }
+  unsigned long long best = 0;   // greedy: packed maximum
+  if (have0) {
+    if (greedy) {
+      best = greedy_span(v, wave * kSpan, lane, best);
+    } else {
+      // The span's k-th largest lane maximum: k distinct logits reach it, so
+      // it bounds the row's k-th largest from below.
+      float lm = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < kSpanNV; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) lm = fmaxf(lm, v[j][q]);
+      const uint32_t M = wave_kth_largest(f2key(lm), k);
+      const float xf = key_floor(M ? M : 1u);
+      uint32_t cnt = 0;
+#pragma unroll
+      for (int j = 0; j < kSpanNV; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) cnt += (uint32_t)__popcll(__ballot(v[j][q] >= xf));
+      int bp = 0;
+      if (lane == 0 && cnt) bp = atomicAdd(&rs.n_c, (int)cnt);
+      bp = __shfl(bp, 0);
+      uint32_t pos = 0;
 #pragma unroll
       for (int j = 0; j < kSpanNV; ++j) {
-        const int e = base + (j * 64 + lane) * 4;
-        if (e < V) {
-          const uint32_t bits = (bitmap[e >> 5] >> (e & 31)) & 0xFu;
-          if (bits) {
+        const int e = wave * kSpan + (j * 64 + lane) * 4;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              if (bits & (1u << q)) {
-                const float nv = penalise(v[j][q], true, 0u, P);
-                v[j][q] = nv;
-                rowp[e + q] = nv;
-              }
-            }
+        for (int q = 0; q < 4; ++q) {
+          const bool pass = v[j][q] >= xf;
+          const unsigned long long b = __ballot(pass);
+          if (b) {
+            const int p = bp + (int)(pos + lanes_below(b));
+            if (pass && p < kRowCandCap) cbuf[p] = pack_cand(f2key(v[j][q]), (uint32_t)(e + q));
+            pos += (uint32_t)__popcll(b);
           }
         }
       }
     }
+  }
+
+  // prefetch round 1 while the bound is tightened
+  const int sp1 = wave + kRowWaves;
+  if (sp1 < nspan) load_span<VEC>(v, rowp, sp1 * kSpan, V, lane);
+
+  if (!greedy) {
+    // exact k-th largest of the round-0 candidates (the first 16 spans): a
+    // lower bound of the row's k-th largest; keep only candidates reaching it
+    __syncthreads();
+    const int n1 = min(rs.n_c, kRowCandCap);
+    int total = 0;
+    const uint32_t T1 = block_select_fast<kRowThreads>(
+        k,
+        [&](int shift, uint32_t prefix, int pass) {
+          for (int p = tid; p < n1; p += kRowThreads)
+            hist_add(rs.sel, cand_key(cbuf[p]), shift, prefix, pass);
+        },
+        rs.sel, &total);
+    unsigned long long keep[kRowCandCap / kRowThreads];
+#pragma unroll
+    for (int i = 0; i < kRowCandCap / kRowThreads; ++i) {
+      const int p = tid + i * kRowThreads;
+      keep[i] = (p < n1 && cand_key(cbuf[p]) >= T1) ? cbuf[p] : 0ull;
+    }
+    if (tid == 0) rs.theta = T1;
+    __syncthreads();
+    if (rs.n_c <= kRowCandCap) {
+#pragma unroll
+      for (int i = 0; i < kRowCandCap / kRowThreads; ++i)
+        if (keep[i]) cbuf[atomicAdd(&rs.n_keep, 1)] = keep[i];
+    }
+    __syncthreads();
+    if (tid == 0 && rs.n_c <= kRowCandCap) rs.n_c = rs.n_keep;
+    __syncthreads();
+  }
+
+  // ---- rounds >= 1: the bound is tight, candidates are rare
+  const uint32_t theta = rs.theta;
+  const float xft = key_floor(theta ? theta : 1u);
+  for (int sp = sp1; sp < nspan; sp += kRowWaves) {
+    if (sp != sp1) load_span<VEC>(v, rowp, sp * kSpan, V, lane);
+    const int base = sp * kSpan;
     if (greedy) {
+      if (rep) {
 #pragma unroll
-      for (int j = 0; j < kSpanNV; ++j) {
-        const int e = base + (j * 64 + lane) * 4;
+        for (int j = 0; j < kSpanNV; ++j) {
+          const int e = base + (j * 64 + lane) * 4;
+          if (e < V) {
+            const uint32_t bits = (bitmap[e >> 5] >> (e & 31)) & 0xFu;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t key = f2key(v[j][q]);
-          const unsigned long long c = key ? pack_cand(key, (uint32_t)(e + q)) : 0ull;
-          best = c > best ? c : best;
+            for (int q = 0; q < 4; ++q)
+              if (bits & (1u << q)) v[j][q] = __builtin_nanf("");
+          }
         }
       }
-      continue;
-    }
-    // k-th largest lane maximum of the span: a lower bound of the row's k-th
-    // largest logit (the k largest lane maxima are k distinct logits).
-    float lm = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kSpanNV; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) lm = fmaxf(lm, v[j][q]);
-    const uint32_t M = wave_kth_largest(f2key(lm), k);
-    uint32_t th = rs.theta;   // the best bound any wave has published
-    if (M > th) {
-      if (lane == 0) atomicMax(&rs.theta, M);
-      th = M;
-    }
-    const float xf = key_floor(th ? th : 1u);
-    uint32_t cnt = 0;
-#pragma unroll
-    for (int j = 0; j < kSpanNV; ++j)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) cnt += (uint32_t)__popcll(__ballot(v[j][q] >= xf));
-    if (cnt == 0) continue;
-    int basepos = 0;
-    if (lane == 0) basepos = atomicAdd(&rs.n_c, (int)cnt);
-    basepos = __shfl(basepos, 0);
-    uint32_t pos = 0;
-#pragma unroll
-    for (int j = 0; j < kSpanNV; ++j) {
-      const int e = base + (j * 64 + lane) * 4;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const bool pass = v[j][q] >= xf;
-        const unsigned long long b = __ballot(pass);
-        if (b) {
-          const int p = basepos + (int)(pos + lanes_below(b));
-          if (pass && p < kRowCandCap) cbuf[p] = pack_cand(f2key(v[j][q]), (uint32_t)(e + q));
-          pos += (uint32_t)__popcll(b);
-        }
-      }
+      best = greedy_span(v, base, lane, best);
+    } else if (rep) {
+      append_rare<true>(v, base, lane, xft, bitmap, cbuf, &rs.n_c);
+    } else {
+      append_rare<false>(v, base, lane, xft, bitmap, cbuf, &rs.n_c);
     }
   }
+
+  __syncthreads();
+  // every read of the row is done: the penalised logits go back in place
+  const int n_pen = rs.n_pen;
+  for (int i = tid; i < n_pen; i += kRowThreads) rowp[pen_id[i]] = pen_val[i];
 
   if (greedy) {
     best = wave_max64(best);
@@ -682,21 +1066,48 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     if (tid == 0) {
       unsigned long long b = rs.best[0];
       for (int w = 1; w < kRowWaves; ++w) b = rs.best[w] > b ? rs.best[w] : b;
+      for (int i = 0; i < n_pen; ++i) {
+        const uint32_t key = f2key(pen_val[i]);
+        const unsigned long long c = key ? pack_cand(key, (uint32_t)pen_id[i]) : 0ull;
+        b = c > b ? c : b;
+      }
       write_greedy(a, row, rowp, b);
     }
     return;
   }
 
+  // the penalised logits join the candidates
+  bool overflow = rs.n_c + n_pen > kRowCandCap;
+  if (!overflow) {
+    const int c0 = rs.n_c;
+    for (int i = tid; i < n_pen; i += kRowThreads)
+      cbuf[c0 + i] = pack_cand(f2key(pen_val[i]), (uint32_t)pen_id[i]);
+  }
   __syncthreads();
-  const int n_c = rs.n_c;
-  bool overflow = n_c > kRowCandCap;
-  const int n_ent = overflow ? 0 : n_c;
-  const uint32_t lo = rs.theta ? rs.theta : 1u;
-  uint32_t T = 0;
-  int n_sel = select_into<kRowThreads>(
-      n_ent, [&](int p) { return cbuf[p]; }, lo, k, srt, rs.sel, rs.tail, &T);
-  if (n_sel < 0) { overflow = true; n_sel = 0; }
-  finish_row<kRowThreads>(a, P, row, rowp, srt, n_sel, T, false, overflow, s, rs.tail);
+  const int n_all = overflow ? 0 : rs.n_c + n_pen;
+  unsigned long long F = 0;
+  bool extra = false;
+  if (n_all > 512) {
+    // rare: many candidates reach the bound (ties); select block-wide first
+    uint32_t T = 0;
+    const int n_sel = select_into<kRowThreads>(
+        n_all, [&](int p) { return cbuf[p]; }, 0u, k, srt, rs.sel, rs.tail, &T);
+    if (n_sel < 0) overflow = true;
+    if (wave != 0) return;
+    if (!overflow) {
+      F = lane < n_sel ? srt[lane] : 0ull;
+      extra = n_sel > 64;
+    }
+  } else {
+    if (wave != 0) return;
+    F = wave_top64(cbuf, n_all, k, tmp, &extra);
+  }
+  RowPlan P;
+  P.temperature = rs.temperature;
+  P.top_p = rs.top_p;
+  P.min_p = rs.min_p;
+  P.k = k;
+  finish_wave(a, P, row, rowp, F, extra, overflow, rs.u, rsv, rsid);
 }
 
 // ---------------------------------------------------------------- chunk kernel
