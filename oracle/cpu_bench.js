@@ -9,6 +9,7 @@
  *   uniforms.f64   rows float64
  *
  *   node cpu_bench.js check <dir> [cap]       one JSON line per row
+ *   node cpu_bench.js kat <cases.json>        the known-answer cases, one line each
  *   node cpu_bench.js bench <dir> <seconds> <threads> [max_rows]
  *
  * bench: like the engine (src/engine.ts:1642) each call gets one row of
@@ -70,6 +71,30 @@ function check(dir, cap) {
     }));
   }
   process.stdout.write(lines.join('\n') + '\n');
+}
+
+function special(x) {
+  if (x === 'NaN') return NaN;
+  if (x === 'Infinity') return Infinity;
+  if (x === '-Infinity') return -Infinity;
+  if (x === '-0') return -0;
+  return x;
+}
+
+function kat(file) {
+  const data = JSON.parse(fs.readFileSync(file, 'utf8'));
+  const out = [];
+  data.cases.forEach(function (c) {
+    const logits = new Float32Array(c.logits.map(special));
+    const cfg = {};
+    Object.keys(c.config).forEach(function (key) { cfg[key] = special(c.config[key]); });
+    const r = port.sampleDetailed(logits, c.vocab, c.history.slice(), cfg, c.u);
+    out.push(JSON.stringify({
+      name: c.name, token: r.token, n: r.n, cutoff: r.cutoff, ids: r.ids, probs: r.probs,
+      logits_bits: Array.from(new Uint32Array(logits.buffer)),
+    }));
+  });
+  process.stdout.write(out.join('\n') + '\n');
 }
 
 function runFor(w, seconds, first, step, maxRows) {
@@ -134,11 +159,12 @@ if (!wt.isMainThread) {
 } else if (require.main === module) {
   const mode = process.argv[2];
   if (mode === 'check') check(process.argv[3], Number(process.argv[4] || 64));
+  else if (mode === 'kat') kat(process.argv[3]);
   else if (mode === 'bench')
     bench(process.argv[3], Number(process.argv[4] || 5), Number(process.argv[5] || 1),
       Number(process.argv[6] || 0));
   else {
-    process.stderr.write('usage: cpu_bench.js check <dir> [cap] | bench <dir> <seconds> <threads> [max_rows]\n');
+    process.stderr.write('usage: cpu_bench.js check <dir> [cap] | kat <cases.json> | bench <dir> <seconds> <threads> [max_rows]\n');
     process.exit(2);
   }
 }
