@@ -1,0 +1,60 @@
+/**
+ * TypeScript surface of the MI355X sampler: the same call surface as
+ * hachiue's src/sampler.ts (SampleConfig, sampleLogits) plus batch entry
+ * points.  Implemented in index.js over the Node-API addon.
+ */
+
+/** src/sampler.ts:1-7, plus optional extensions that default to off. */
+export interface SampleConfig {
+  temperature?: number
+  topK?: number
+  topP?: number
+  minP?: number
+  repetitionPenalty?: number
+  /** extension: subtracted once from every logit whose id occurs in the history */
+  presencePenalty?: number
+  /** extension: subtracted n times, n = occurrences of the id in the history */
+  frequencyPenalty?: number
+  /** extension: value in [0, 1) used instead of Math.random() */
+  uniform?: number
+}
+
+/**
+ * Sample a token ID from logits with Repetition Penalty, Top-K, Top-P, Min-P
+ * and Temperature (src/sampler.ts:12-17).  `logits` is updated in place with
+ * the penalised values.
+ */
+export function sampleLogits(
+  logits: Float32Array,
+  vocab: number,
+  history: number[] | Int32Array,
+  config?: SampleConfig,
+): number
+
+export interface BatchShape {
+  rows?: number
+  /** floats between the starts of consecutive rows (default: vocab) */
+  stride?: number
+}
+
+/** Samples every row of a [rows, stride] Float32Array in one GPU call. */
+export function sampleLogitsBatch(
+  logits: Float32Array,
+  vocab: number,
+  histories: Array<number[] | Int32Array> | null,
+  configs: SampleConfig | SampleConfig[],
+  uniforms?: ArrayLike<number> | null,
+  shape?: BatchShape,
+): Int32Array
+
+export function sampleLogitsBatchAsync(
+  logits: Float32Array,
+  vocab: number,
+  histories: Array<number[] | Int32Array> | null,
+  configs: SampleConfig | SampleConfig[],
+  uniforms?: ArrayLike<number> | null,
+  shape?: BatchShape,
+): Promise<Int32Array>
+
+export const DEFAULTS: Readonly<Required<Pick<SampleConfig,
+  'temperature' | 'topK' | 'topP' | 'minP' | 'repetitionPenalty'>>>

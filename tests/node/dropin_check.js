@@ -1,0 +1,82 @@
+'use strict';
+// Drives hachiue_amd/js (the sampleLogits drop-in) for the tests:
+//   node dropin_check.js kat <cases.json>
+//   node dropin_check.js rows <workload dir>     sampleLogits row by row
+//   node dropin_check.js batch <workload dir>    sampleLogitsBatch (+ async)
+//   node dropin_check.js nogpu                   error behaviour without a GPU
+const fs = require('fs');
+const path = require('path');
+const hs = require(path.join(__dirname, '..', '..', 'hachiue_amd', 'js', 'index.js'));
+
+function special(x) {
+  return x === 'NaN' ? NaN : x === 'Infinity' ? Infinity : x === '-Infinity' ? -Infinity
+    : x === '-0' ? -0 : x;
+}
+function typed(file, Ctor) {
+  const buf = fs.readFileSync(file);
+  const ab = new ArrayBuffer(buf.length);
+  new Uint8Array(ab).set(buf);
+  return new Ctor(ab);
+}
+function load(dir) {
+  const meta = JSON.parse(fs.readFileSync(path.join(dir, 'meta.json'), 'utf8'));
+  const w = { meta: meta, logits: typed(path.join(dir, 'logits.f32'), Float32Array),
+    uniforms: typed(path.join(dir, 'uniforms.f64'), Float64Array) };
+  if (meta.has_history) {
+    w.ids = typed(path.join(dir, 'hist_ids.i32'), Int32Array);
+    w.off = typed(path.join(dir, 'hist_off.f64'), Float64Array);
+  }
+  w.configs = meta.configs.map(function (c) {
+    const o = {};
+    Object.keys(c).forEach(function (k) { o[k] = special(c[k]); });
+    return o;
+  });
+  w.history = function (r) { return w.ids ? Array.from(w.ids.subarray(w.off[r], w.off[r + 1])) : []; };
+  return w;
+}
+function bits(a) { return Array.from(new Uint32Array(a.buffer, a.byteOffset, a.length)); }
+
+const mode = process.argv[2];
+if (mode === 'kat') {
+  const data = JSON.parse(fs.readFileSync(process.argv[3], 'utf8'));
+  data.cases.forEach(function (c) {
+    const logits = new Float32Array(c.logits.map(special));
+    const cfg = { uniform: c.u };
+    Object.keys(c.config).forEach(function (k) { cfg[k] = special(c.config[k]); });
+    const token = hs.sampleLogits(logits, c.vocab, c.history.slice(), cfg);
+    console.log(JSON.stringify({ name: c.name, token: token, logits_bits: bits(logits) }));
+  });
+} else if (mode === 'rows') {
+  const w = load(process.argv[3]);
+  const s = w.meta.stride;
+  for (let r = 0; r < w.meta.rows; r++) {
+    const row = w.logits.slice(r * s, r * s + s);
+    const cfg = Object.assign({ uniform: w.uniforms[r] }, w.configs[r]);
+    const token = hs.sampleLogits(row, w.meta.vocab, w.history(r), cfg);
+    console.log(JSON.stringify({ row: r, token: token }));
+  }
+} else if (mode === 'batch') {
+  const w = load(process.argv[3]);
+  const hists = w.ids ? w.configs.map(function (_, r) { return w.history(r); }) : null;
+  const logits = w.logits.slice();
+  const tok = hs.sampleLogitsBatch(logits, w.meta.vocab, hists, w.configs, w.uniforms,
+    { rows: w.meta.rows, stride: w.meta.stride });
+  const logits2 = w.logits.slice();
+  hs.sampleLogitsBatchAsync(logits2, w.meta.vocab, hists, w.configs, w.uniforms,
+    { rows: w.meta.rows, stride: w.meta.stride }).then(function (tok2) {
+    console.log(JSON.stringify({ tokens: Array.from(tok), tokens_async: Array.from(tok2),
+      logits_same: bits(logits).join() === bits(logits2).join(),
+      penalised: bits(logits) }));
+  }, function (e) { console.error(e); process.exit(1); });
+} else if (mode === 'nogpu') {
+  const out = {};
+  out.vocab0 = hs.sampleLogits(new Float32Array([1, 2]), 0, [], {});
+  try {
+    hs.sampleLogits(new Float32Array([1, 2, 3]), 3, [0], { temperature: 1 });
+    out.error = null;
+  } catch (e) {
+    out.error = e.code || e.message;
+  }
+  try { hs.sampleLogits([1, 2, 3], 3, [], {}); } catch (e) { out.type_error = e instanceof TypeError; }
+  console.log(JSON.stringify(out));
+}
