@@ -84,7 +84,12 @@ struct hs_context {
   hipStream_t stream = nullptr;
   // per-kernel timing diagnostics
   bool timing = false;
-  std::vector<hipEvent_t> ev_free, ev_used;   // used: groups of kTimedKernels + 1
+  struct TimedCall {
+    unsigned mask;                         // launched_kernels() of the call
+    hipEvent_t ev[2 * hs::kTimedKernels];  // start/end per launched kernel
+  };
+  std::vector<hipEvent_t> ev_free;
+  std::vector<TimedCall> timed;
   double kernel_ms[hs::kTimedKernels] = {};
   // rows routed to the row kernel only when a call has at least this many
   int row_min_rows = 1;
@@ -275,6 +280,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   a.want_cands = (d_cand_ids || d_cand_probs) ? 1 : 0;
   a.n_pf = n_pf;
   a.n_row = n_row;
+  a.rows_direct = n_row == rows ? 1 : 0;
   a.n_chunk = n_chunk;
   a.hist_ids = d_hist_ids;
   a.hist_off = d_hist_offsets;
@@ -286,22 +292,23 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   a.cand_count_out = d_cand_count;
   a.cutoff_out = d_cutoff;
   a.row_flags = d_row_flags;
-  hipEvent_t ev[hs::kTimedKernels + 1];
-  bool timed = false;
-  if (ctx->timing) {
-    for (int i = 0; i <= hs::kTimedKernels; ++i) {
+  hs_context::TimedCall tc{};
+  const bool timed = ctx->timing;
+  if (timed) {
+    tc.mask = hs::launched_kernels(a);
+    for (int i = 0; i < 2 * hs::kTimedKernels; ++i) {
+      if (!(tc.mask >> (i / 2) & 1u)) continue;
       if (ctx->ev_free.empty()) {
         hipEvent_t x;
         HS_HIP(hipEventCreate(&x));
         ctx->ev_free.push_back(x);
       }
-      ev[i] = ctx->ev_free.back();
+      tc.ev[i] = ctx->ev_free.back();
       ctx->ev_free.pop_back();
-      ctx->ev_used.push_back(ev[i]);
     }
-    timed = true;
+    ctx->timed.push_back(tc);
   }
-  hipError_t e = hs::launch_sample(a, ws, stream, timed ? ev : nullptr);
+  hipError_t e = hs::launch_sample(a, ws, stream, timed ? tc.ev : nullptr);
   if (e != hipSuccess) {
     if (ctx->cand_count.p)
       (void)hipMemsetAsync(ctx->cand_count.p, 0, ctx->cand_count.bytes, stream);
@@ -372,18 +379,20 @@ int hs_context_kernel_times(hs_context *ctx, double *ms, int32_t count, int64_t 
   if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
   if (count < 0 || (count > 0 && !ms)) return fail(HS_ERR_INVALID_ARGUMENT, "bad output array");
   DeviceGuard guard(ctx->device);
-  const size_t g = hs::kTimedKernels + 1;
-  for (size_t i = 0; i + g <= ctx->ev_used.size(); i += g) {
-    HS_HIP(hipEventSynchronize(ctx->ev_used[i + g - 1]));
+  for (const hs_context::TimedCall &tc : ctx->timed) {
     for (int k = 0; k < hs::kTimedKernels; ++k) {
+      if (!(tc.mask >> k & 1u)) continue;
       float t = 0;
-      HS_HIP(hipEventElapsedTime(&t, ctx->ev_used[i + k], ctx->ev_used[i + k + 1]));
+      HS_HIP(hipEventSynchronize(tc.ev[2 * k + 1]));
+      HS_HIP(hipEventElapsedTime(&t, tc.ev[2 * k], tc.ev[2 * k + 1]));
       ctx->kernel_ms[k] += t;
     }
     ++ctx->timed_calls;
   }
-  for (hipEvent_t x : ctx->ev_used) ctx->ev_free.push_back(x);
-  ctx->ev_used.clear();
+  for (const hs_context::TimedCall &tc : ctx->timed)
+    for (int i = 0; i < 2 * hs::kTimedKernels; ++i)
+      if (tc.mask >> (i / 2) & 1u) ctx->ev_free.push_back(tc.ev[i]);
+  ctx->timed.clear();
   for (int k = 0; k < count; ++k) ms[k] = k < hs::kTimedKernels ? ctx->kernel_ms[k] : 0.0;
   if (calls) *calls = ctx->timed_calls;
   for (int k = 0; k < hs::kTimedKernels; ++k) ctx->kernel_ms[k] = 0;
@@ -397,7 +406,9 @@ int hs_context_destroy(hs_context *ctx) {
     DeviceGuard guard(ctx->device);
     (void)hipDeviceSynchronize();
     for (hipEvent_t x : ctx->ev_free) (void)hipEventDestroy(x);
-    for (hipEvent_t x : ctx->ev_used) (void)hipEventDestroy(x);
+    for (const hs_context::TimedCall &tc : ctx->timed)
+      for (int i = 0; i < 2 * hs::kTimedKernels; ++i)
+        if (tc.mask >> (i / 2) & 1u) (void)hipEventDestroy(tc.ev[i]);
     ctx->plans.release();
     ctx->cand.release();
     ctx->cand_count.release();

@@ -6,12 +6,12 @@
 
 namespace hs {
 
-// ---- row kernel: one 1024-thread workgroup streams a whole row.  Each wave
-// takes 3072-logit spans (12 float4 per lane) round-robin.
+// ---- row kernel: one 1024-thread workgroup streams a whole row in rounds of
+// 8 float4 per thread (32768 logits), two rounds in registers at a time.
 constexpr int kRowThreads = 1024;
 constexpr int kRowWaves = kRowThreads / 64;
-constexpr int kSpanNV = 12;                      // float4 per lane per span
-constexpr int kSpan = 64 * kSpanNV * 4;          // 3072 logits
+constexpr int kRowNV = 8;                        // float4 per thread per round
+constexpr int kRoundF4 = kRowThreads * kRowNV;   // float4 per round
 constexpr int kRowCandCap = 4096;                // streamed candidates per row
 constexpr int kRowMaxVocab = 1 << 19;            // LDS bitmap limit (64 KiB)
 
@@ -83,6 +83,7 @@ struct LaunchArgs {
   int32_t chunks;            // S = ceil(vocab / kChunk)
   int32_t vec;               // float4 loads allowed (alignment)
   int32_t want_cands;        // exact candidate order must be produced
+  int32_t rows_direct;       // the row kernel takes every row: row = block index
   int32_t n_pf, n_row, n_chunk;
   const int32_t *hist_ids;
   const int64_t *hist_off;
@@ -96,11 +97,14 @@ struct LaunchArgs {
   uint32_t *row_flags;
 };
 
-// Launches the kernels of one call on `stream`.  When `ev` is not null it
-// records ev[0] first and ev[i + 1] after kernel i: 0 penalty pre-pass,
-// 1 row kernel, 2 chunk kernel, 3 finalize (a kernel with no rows is
-// skipped and times ~0).
+// Launches the kernels of one call on `stream`.  When `ev` is not null,
+// ev[2i] and ev[2i + 1] receive the start and end of kernel i's dispatch
+// (0 penalty pre-pass, 1 row kernel, 2 chunk kernel, 3 finalize), for the
+// kernels that launch only: launched_kernels() says which.
 constexpr int kTimedKernels = 4;
+inline unsigned launched_kernels(const LaunchArgs &a) {
+  return (a.n_pf > 0 ? 1u : 0u) | (a.n_row > 0 ? 2u : 0u) | (a.n_chunk > 0 ? 12u : 0u);
+}
 hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,
                          hipEvent_t *ev);
 hipError_t prepare_kernels();   // per device, once: raise dynamic LDS limits

@@ -11,13 +11,13 @@
 //                    LDS and applies the repetition penalty (last 128 ids) and
 //                    the extension in place.
 //   row_kernel       greedy rows and rows with k <= 64, one 1024-thread
-//                    workgroup per row (the hot path).  Each wave streams
-//                    3072-logit spans from HBM into registers; a ballot binary
-//                    search gives the span's k-th largest lane maximum, a lower
-//                    bound of the row's k-th largest value; every logit at or
-//                    above the running bound is appended to an LDS candidate
-//                    list.  The workgroup then selects, sorts and samples the
-//                    row itself: one HBM pass, one launch.
+//                    workgroup per row (the hot path).  The row streams from
+//                    HBM in rounds of 32768 logits, two rounds in registers.
+//                    Round 0 fixes a lower bound of the row's k-th largest
+//                    value (the exact k-th largest of the 1024 lane maxima);
+//                    every logit at or above it is appended to an LDS
+//                    candidate list.  The workgroup then ranks, samples and
+//                    writes the row itself: one HBM pass, one launch.
 //   chunk_kernel     rows with 64 < k <= 1024 (and k <= 64 rows the row
 //                    kernel does not take), grid rows*S, 256 threads: a chunk
 //                    of 16384 logits in registers, exact chunk k-th largest by
@@ -28,6 +28,8 @@
 // depend on its slot history (src/sampler.ts:55-69); when such a group can
 // change the result, the exact replace-min scan is replayed over the row.
 #include "sampler_internal.h"
+
+#include <hip/hip_ext.h>
 
 #include <float.h>
 #include <math.h>
@@ -77,6 +79,18 @@ __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
 __device__ __forceinline__ uint32_t lanes_below(unsigned long long mask) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                    __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+}
+
+__device__ __forceinline__ uint32_t readlane_u32(uint32_t x, int lane) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, lane);
+}
+__device__ __forceinline__ float readlane_f32(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+__device__ __forceinline__ double readlane_f64(double x, int lane) {
+  const unsigned long long b = (unsigned long long)__double_as_longlong(x);
+  const uint32_t lo = readlane_u32((uint32_t)b, lane), hi = readlane_u32((uint32_t)(b >> 32), lane);
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
 }
 
 // Exact k-th largest of one key per lane (1 <= k <= 64) by a binary search
@@ -595,112 +609,336 @@ __device__ int select_into(int n_ent, GetEnt get, uint32_t lo, int k, unsigned l
 
 // ---------------------------------------------------------------- row kernel
 
-// One span of a row into registers: lane-coalesced float4 loads, NaN past
-// the vocabulary (NaN never becomes a candidate).  Spans wholly inside the
-// row take the branch-free path.
+// A row is read in rounds: in round r thread t holds the float4s
+// r * kRoundF4 + t + j * kRowThreads (j < kRowNV), so every wave reads 1 KiB
+// contiguous per load instruction and all waves finish a round together.
+// Two rounds are in registers at once: the next round's loads are in flight
+// while the current one is examined.
+
+// One round into registers; NaN past the vocabulary (never a candidate).
 template <bool VEC>
-__device__ __forceinline__ void load_span(float (&v)[kSpanNV][4], const float *rowp, int base,
-                                          int V, int lane) {
-  if (VEC && base + kSpan <= V) {
+__device__ __forceinline__ void load_round(float (&v)[kRowNV][4], const float *rowp, int r,
+                                           int V, int tid) {
+  const int f0 = r * kRoundF4 + tid;
+  const int nfull = V >> 2;   // float4 wholly inside the row
+  const f32x4 *p4 = reinterpret_cast<const f32x4 *>(rowp);
+  if (VEC && (r + 1) * kRoundF4 <= nfull) {
 #pragma unroll
-    for (int j = 0; j < kSpanNV; ++j) {
-      const int e = base + (j * 64 + lane) * 4;
-      const f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(rowp + e));
+    for (int j = 0; j < kRowNV; ++j) {
+      const f32x4 t = __builtin_nontemporal_load(p4 + f0 + j * kRowThreads);
       v[j][0] = t[0]; v[j][1] = t[1]; v[j][2] = t[2]; v[j][3] = t[3];
     }
     return;
   }
 #pragma unroll
-  for (int j = 0; j < kSpanNV; ++j) {
-    const int e = base + (j * 64 + lane) * 4;
+  for (int j = 0; j < kRowNV; ++j) {
+    const int f = f0 + j * kRowThreads;
+    if (VEC && f < nfull) {
+      const f32x4 t = __builtin_nontemporal_load(p4 + f);
+      v[j][0] = t[0]; v[j][1] = t[1]; v[j][2] = t[2]; v[j][3] = t[3];
+    } else {
+      const int e = 4 * f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) v[j][q] = (e + q < V) ? rowp[e + q] : __builtin_nanf("");
+      for (int q = 0; q < 4; ++q) v[j][q] = (e + q < V) ? rowp[e + q] : __builtin_nanf("");
+    }
   }
 }
 
-// Exclusive prefix over the wave of a per-lane count c < 64 (and the wave
-// total), from the six bit-slices of c: no LDS traffic.
-__device__ __forceinline__ uint32_t wave_excl_prefix(uint32_t c, uint32_t *total) {
-  uint32_t pre = 0, tot = 0;
+__device__ __forceinline__ int round_elem(int r, int tid, int j) {
+  return 4 * (r * kRoundF4 + tid + j * kRowThreads);
+}
+
+// Logits whose id is in the repetition set (bitmap) leave the stream: their
+// penalised values join the selection separately.
+__device__ __forceinline__ void mask_penalised(float (&v)[kRowNV][4], int r, int tid, int V,
+                                               const uint32_t *bitmap) {
 #pragma unroll
-  for (int b = 0; b < 6; ++b) {
-    const unsigned long long m = __ballot((c >> b) & 1u);
-    pre += lanes_below(m) << b;
-    tot += (uint32_t)__popcll(m) << b;
+  for (int j = 0; j < kRowNV; ++j) {
+    const int e = round_elem(r, tid, j);
+    if (e < V) {
+      const uint32_t bits = (bitmap[e >> 5] >> (e & 31)) & 0xFu;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (bits & (1u << q)) v[j][q] = __builtin_nanf("");
+    }
   }
-  *total = tot;
-  return pre;
 }
 
-__device__ __forceinline__ uint32_t readlane_u32(uint32_t x, int lane) {
-  return (uint32_t)__builtin_amdgcn_readlane((int)x, lane);
-}
-__device__ __forceinline__ float readlane_f32(float x, int lane) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
-}
-__device__ __forceinline__ double readlane_f64(double x, int lane) {
-  const unsigned long long b = (unsigned long long)__double_as_longlong(x);
-  const uint32_t lo = readlane_u32((uint32_t)b, lane), hi = readlane_u32((uint32_t)(b >> 32), lane);
-  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+// Appends every logit of the round at or above xf (and, with REP, outside the
+// repetition set) to cbuf: one LDS reservation per non-empty ballot.
+template <bool REP>
+__device__ __forceinline__ void append_round(const float (&v)[kRowNV][4], int r, int tid, float xf,
+                                             const uint32_t *bitmap, unsigned long long *cbuf,
+                                             int *n_c) {
+  const int lane = tid & 63;
+#pragma unroll
+  for (int j = 0; j < kRowNV; ++j) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      bool pass = v[j][q] >= xf;
+      if (__ballot(pass)) {
+        const int e = round_elem(r, tid, j) + q;
+        if (REP && pass) pass = !((bitmap[e >> 5] >> (e & 31)) & 1u);
+        const unsigned long long b = __ballot(pass);
+        if (b) {
+          const int leader = __ffsll((long long)b) - 1;
+          int bp = 0;
+          if (lane == leader) bp = atomicAdd(n_c, __popcll(b));
+          bp = __shfl(bp, leader);
+          const int p = bp + (int)lanes_below(b);
+          if (pass && p < kRowCandCap) cbuf[p] = pack_cand(f2key(v[j][q]), (uint32_t)e);
+        }
+      }
+    }
+  }
 }
 
-// Sorts one packed candidate per lane (0 = none) descending among the first n
-// lanes by counting, for each lane, the larger packed values (readlane loop,
-// no shuffles), then scattering through `tmp` (64 entries of LDS).
-__device__ __forceinline__ unsigned long long wave_rank_sort(unsigned long long x, int n,
-                                                             unsigned long long *tmp) {
+// Packed maximum (value, then lowest index) of a round, folded into `best`.
+__device__ __forceinline__ unsigned long long greedy_round(const float (&v)[kRowNV][4], int r,
+                                                           int tid, unsigned long long best) {
+#pragma unroll
+  for (int j = 0; j < kRowNV; ++j) {
+    const int e = round_elem(r, tid, j);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t key = f2key(v[j][q]);
+      const unsigned long long c = key ? pack_cand(key, (uint32_t)(e + q)) : 0ull;
+      best = c > best ? c : best;
+    }
+  }
+  return best;
+}
+
+__device__ __forceinline__ float round_max(const float (&v)[kRowNV][4]) {
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < kRowNV; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) m = fmaxf(m, v[j][q]);   // NaN is ignored
+  return m;
+}
+
+__device__ __forceinline__ int uniform_i32(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// Wave-uniform read of memory the kernel never writes, through the scalar
+// cache (constant address space): it completes independently of the vector
+// loads queued before it.
+template <typename T>
+__device__ __forceinline__ T load_scalar(const T *p) {
+  return *(const __attribute__((address_space(4))) T *)(p);
+}
+
+// Maximum of one key per lane over the wave (DPP row shifts and row
+// broadcasts, then lane 63), returned wave-uniform.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  // row_shr:n = 0x110 + n, row_bcast:15 = 0x142, row_bcast:31 = 0x143
+  uint32_t y;
+  y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x111, 0xF, 0xF, false); x = x > y ? x : y;
+  y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x112, 0xF, 0xF, false); x = x > y ? x : y;
+  y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x114, 0xF, 0xF, false); x = x > y ? x : y;
+  y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x118, 0xF, 0xF, false); x = x > y ? x : y;
+  y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x142, 0xA, 0xF, false); x = x > y ? x : y;
+  y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x143, 0xC, 0xF, false); x = x > y ? x : y;
+  return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+
+// The j-th largest of one key per lane (1 <= j <= 4, multiset order; 0 when
+// fewer than j lanes hold a non-zero key): j rounds of wave maximum, each
+// retiring one lane that holds it.
+__device__ __forceinline__ uint32_t wave_jth_largest(uint32_t key, int j) {
   const int lane = lane_id();
-  int rank = 0;
-  for (int j = 0; j < n; ++j) {
-    const unsigned long long y =
-        ((unsigned long long)readlane_u32((uint32_t)(x >> 32), j) << 32) |
-        readlane_u32((uint32_t)x, j);
-    rank += y > x ? 1 : 0;
+  uint32_t m = 0;
+  for (int t = 0; t < j; ++t) {
+    m = wave_max_u32(key);
+    const unsigned long long b = __ballot(key == m);
+    if (lane == (int)__ffsll((long long)b) - 1) key = 0;
   }
-  if (lane < n) tmp[rank] = x;   // packed values are distinct (index in the low word)
-  return lane < n ? tmp[lane] : 0ull;
+  return m;
 }
+
+// Largest t in [lo, hi] with at least k of the keys >= t: a ballot binary
+// search over the bits in which lo and hi differ (all others are shared).
+template <int SLOTS>
+__device__ __forceinline__ uint32_t wave_search(const uint32_t (&key)[SLOTS], int slots, int k,
+                                                uint32_t lo, uint32_t hi) {
+  const uint32_t diff = lo ^ hi;
+  if (!diff) return lo;
+  const int hb = 31 - __builtin_clz(diff);
+  uint32_t t = hb == 31 ? 0u : (lo & ~((2u << hb) - 1u));
+  for (int b = hb; b >= 0; --b) {
+    const uint32_t c = t | (1u << b);
+    int cnt = 0;
+#pragma unroll
+    for (int s = 0; s < SLOTS; ++s)
+      if (SLOTS <= 4 || s < slots) cnt += __popcll(__ballot(key[s] >= c));
+    if (cnt >= k) t = c;
+  }
+  return t;
+}
+
+// Exact k-th largest of n keys list[0, n) (n <= kRowThreads) by one wave,
+// given that at least k of them are >= lo.  0 when n < k.
+__device__ __forceinline__ uint32_t wave_kth_of_list(const uint32_t *list, int n, int k,
+                                                     uint32_t lo) {
+  n = uniform_i32(n);
+  lo = (uint32_t)uniform_i32((int)lo);
+  if (n < k) return 0u;
+  const int lane = lane_id();
+  if (n <= 128) {
+    uint32_t key[2];
+    key[0] = lane < n ? list[lane] : 0u;
+    key[1] = lane + 64 < n ? list[lane + 64] : 0u;
+    const uint32_t hi = wave_max_u32(key[0] > key[1] ? key[0] : key[1]);
+    return wave_search<2>(key, 2, k, lo, hi);
+  }
+  if (n <= 256) {
+    uint32_t key[4], hi = 0;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      key[s] = lane + 64 * s < n ? list[lane + 64 * s] : 0u;
+      hi = key[s] > hi ? key[s] : hi;
+    }
+    hi = wave_max_u32(hi);
+    return wave_search<4>(key, 4, k, lo, hi);
+  }
+  const int slots = (n + 63) >> 6;
+  uint32_t key[kRowWaves];
+  uint32_t hi = 0;
+#pragma unroll
+  for (int s = 0; s < kRowWaves; ++s) {
+    const int i = lane + 64 * s;
+    key[s] = (s < slots && i < n) ? list[i] : 0u;
+    hi = key[s] > hi ? key[s] : hi;
+  }
+  hi = wave_max_u32(hi);
+  return wave_search<kRowWaves>(key, slots, k, lo, hi);
+}
+
+// Tightens the bound mid-row, by one wave: T = the exact k-th largest key of
+// the n candidates cbuf[0, n) (k <= n <= 64 * SLOTS, all with a key >= lo),
+// a lower bound of the row's k-th largest; the candidates below T are
+// dropped in place.  Returns T and the number kept.
+template <int SLOTS>
+__device__ __forceinline__ uint32_t wave_refine(unsigned long long *cbuf, int n, int k, uint32_t lo,
+                                                int *kept) {
+  const int lane = lane_id();
+  unsigned long long c[SLOTS];
+  uint32_t key[SLOTS], hi = 0;
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    const int i = lane + 64 * s;
+    c[s] = i < n ? cbuf[i] : 0ull;
+    key[s] = cand_key(c[s]);
+    hi = key[s] > hi ? key[s] : hi;
+  }
+  hi = wave_max_u32(hi);
+  const uint32_t T = wave_search<SLOTS>(key, SLOTS, k, lo ? lo : 1u, hi);
+  int m = 0;   // every read above precedes the writes below (one wave, LDS in order)
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) {
+    const bool pass = key[s] >= T;
+    const unsigned long long b = __ballot(pass);
+    if (pass) cbuf[m + (int)lanes_below(b)] = c[s];
+    m += __popcll(b);
+  }
+  *kept = m;
+  return T;
+}
+
+// Sorted top-64 of n distinct packed candidates cbuf[0, n) (n <= kRowThreads)
+// by ranking: G threads per candidate count the larger ones, the candidate of
+// rank r < 64 lands in top[r]; the key of rank 64 goes to *key64 (0 if none).
+// top[] must hold zeros beforehand.  Ends with a barrier.
+__device__ __forceinline__ void rank_top64(const unsigned long long *cbuf, int n,
+                                           unsigned long long *top, uint32_t *key64) {
+  const int tid = threadIdx.x;
+  int G = 1;
+  while (G < 64 && 2 * G * n <= kRowThreads) G <<= 1;
+  const int i = tid / G, g = tid & (G - 1);
+  const unsigned long long x = i < n ? cbuf[i] : ~0ull;
+  int rank = 0;
+  if (i < n) {
+    int j = g;
+    for (; j + 3 * G < n; j += 4 * G) {
+      const unsigned long long y0 = cbuf[j], y1 = cbuf[j + G], y2 = cbuf[j + 2 * G],
+                               y3 = cbuf[j + 3 * G];
+      rank += (int)(y0 > x) + (int)(y1 > x) + (int)(y2 > x) + (int)(y3 > x);
+    }
+    for (; j < n; j += G) rank += (int)(cbuf[j] > x);
+  }
+  for (int m = 1; m < G; m <<= 1) rank += __shfl_xor(rank, m);
+  if (i < n && g == 0) {
+    if (rank < 64) top[rank] = x;
+    if (rank == 64) *key64 = cand_key(x);
+  }
+  __syncthreads();
+}
+
 
 // Tail of src/sampler.ts:76-117 for n <= 64 candidates held one per lane
-// (value keys `key`, sorted descending), by one wave.  Sequential sums run in
-// the reference's order through readlane, so every binary64 rounding matches.
-// Returns the picked position (-1 when n == 0) and writes the cutoff and each
-// lane's normalised probability.
+// (value keys `key`, sorted descending), by one wave.  The reference's three
+// sequential binary64 sums (sumProb, cumProb, the draw's r) are reproduced in
+// its order: the terms go through `sp` (64 doubles of LDS) and every lane
+// reads them back by broadcast and runs the chain itself, lane L stopping
+// at index L (later terms are replaced by +0, which leaves a running sum
+// unchanged), so lane L ends with the running value at its own index and
+// the loop exits become ballots.  Returns the picked position (-1 when
+// n == 0) and writes the cutoff and each lane's normalised probability.
 __device__ __forceinline__ int wave_tail(uint32_t key, int n, const RowPlan &P, double u, int *cutoff,
-                         float *prob_out) {
+                         float *prob_out, double *sp) {
   const int lane = lane_id();
   if (n < 2) {
     *cutoff = n;
     *prob_out = 1.0f;
     return n == 1 ? 0 : -1;
   }
+  n = uniform_i32(n);
+  const int n8 = (n + 7) & ~7;
   const double v = (double)key2f(key);
   const double maxl = readlane_f64(v, 0);
   const double inv_temp = 1.0 / P.temperature;
   const double p = lane < n ? exp((v - maxl) * inv_temp) : 0.0;
-  double sum = 0;
-  for (int i = 0; i < n; ++i) sum += readlane_f64(p, i);   // unrounded, in order
+  sp[lane] = p;   // a wave's LDS accesses complete in order
+  double sum = 0;   // src/sampler.ts:82-86: unrounded p, in order
+  for (int j = 0; j < n8; j += 8) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) sum += sp[j + q];
+  }
   const float prob = (float)((double)(float)p / sum);
   *prob_out = prob;
-  const double thr = P.min_p * (double)readlane_f32(prob, 0);
+  const double pd = lane < n ? (double)prob : 0.0;
+  sp[lane] = pd;
+  // src/sampler.ts:91-105: cumProb after index `lane`
   double cum = 0;
-  int cut = n;
-  for (int i = 0; i < n; ++i) {
-    const double pi = (double)readlane_f32(prob, i);
-    if (i > 0 && pi < thr) { cut = i; break; }
-    cum += pi;
-    if (cum >= P.top_p) { cut = i + 1; break; }
+  for (int j = 0; j < n8; j += 8) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const double t = sp[j + q];
+      cum += j + q <= lane ? t : 0.0;
+    }
   }
-  double kept = 0;
-  for (int i = 0; i < cut; ++i) kept += (double)readlane_f32(prob, i);
+  const double thr = P.min_p * readlane_f64(pd, 0);
+  const unsigned long long minp = __ballot(lane > 0 && lane < n && pd < thr);
+  const unsigned long long topp = __ballot(lane < n && cum >= P.top_p);
+  const int f1 = minp ? (int)__ffsll((long long)minp) - 1 : n;   // break before adding f1
+  const int f2 = topp ? (int)__ffsll((long long)topp) - 1 : n;   // break after adding f2
+  const int cut = f1 <= f2 ? f1 : f2 + 1;
+  // keptSum (src/sampler.ts:107-108) adds probs[0, cutoff) from 0 in the
+  // same order as cumProb: it equals cumProb at cutoff - 1
+  const double kept = readlane_f64(cum, cut - 1);
+  // src/sampler.ts:110-116: r after subtracting index `lane`
   double r = u * kept;
-  int pick = cut - 1;
-  for (int i = 0; i < cut; ++i) {
-    r -= (double)readlane_f32(prob, i);
-    if (r <= 0) { pick = i; break; }
+  const int c8 = (cut + 7) & ~7;
+  for (int j = 0; j < c8; j += 8) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const double t = sp[j + q];
+      r -= j + q <= lane ? t : 0.0;
+    }
   }
+  const unsigned long long hit = __ballot(lane < cut && r <= 0);
   *cutoff = cut;
-  return pick;
+  return hit ? (int)__ffsll((long long)hit) - 1 : cut - 1;
 }
 
 // Completes a row of the row kernel in wave 0 from F, the row's top-64 list
@@ -710,7 +948,7 @@ __device__ __forceinline__ int wave_tail(uint32_t key, int n, const RowPlan &P, 
 // always when force_replay (the candidate list overflowed).
 __device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &P, int row, const float *rowp,
                             unsigned long long F, bool extra_ties, bool force_replay, double u,
-                            float *rsv, int32_t *rsid) {
+                            float *rsv, int32_t *rsid, double *sp) {
   const int lane = lane_id();
   const int k = P.k;
   const uint32_t fkey = cand_key(F);
@@ -726,7 +964,7 @@ __device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &
   int32_t id = (int32_t)cand_idx(F);
   int cut = 0;
   float prob = 0.f;
-  int pick = force_replay ? -1 : wave_tail(key, n, P, u, &cut, &prob);
+  int pick = force_replay ? -1 : wave_tail(key, n, P, u, &cut, &prob, sp);
   bool replayed = false;
   if (boundary_tie || internal_tie || force_replay) {
     // the order inside a group of equal values follows the slot history
@@ -745,7 +983,7 @@ __device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &
       n = __popcll(__ballot(filled));
       key = cand_key(x);
       id = lane < n ? rsid[cand_idx(x)] : -1;
-      pick = wave_tail(key, n, P, u, &cut, &prob);
+      pick = wave_tail(key, n, P, u, &cut, &prob, sp);
       replayed = true;
     }
   }
@@ -769,109 +1007,18 @@ __device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &
   }
 }
 
-// Selects, in one wave, the top-64 of n packed candidates at ent[0, n)
-// (n <= 512, LDS): T = exact k-th largest key by a binary search over the key
-// bits (up to eight entries per lane, ballot counts), then the entries with
-// key >= T gathered through `tmp` (64 entries) and sorted.  *extra is set
-// when more than 64 entries reach T (the tie group at T extends beyond).
-__device__ __forceinline__ unsigned long long wave_top64(const unsigned long long *ent, int n,
-                                                         int k, unsigned long long *tmp,
-                                                         bool *extra) {
-  const int lane = lane_id();
-  const int slots = (n + 63) >> 6;
-  uint32_t key[8];
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    const int i = lane + 64 * s;
-    key[s] = (s < slots && i < n) ? cand_key(ent[i]) : 0u;
-  }
-  uint32_t T = 0;
-  if (n >= k) {
-#pragma unroll 1
-    for (int b = 31; b >= 0; --b) {
-      const uint32_t c = T | (1u << b);
-      int cnt = 0;
-#pragma unroll
-      for (int s = 0; s < 8; ++s)
-        if (s < slots) cnt += __popcll(__ballot(key[s] >= c));
-      if (cnt >= k) T = c;
-    }
-  }
-  const uint32_t lo = T ? T : 1u;
-  int pos = 0;
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    if (s < slots) {
-      const bool pass = key[s] >= lo;
-      const unsigned long long b = __ballot(pass);
-      const int p = pos + (int)lanes_below(b);
-      if (pass && p < 64) tmp[p] = ent[lane + 64 * s];
-      pos += __popcll(b);
-    }
-  }
-  *extra = pos > 64;
-  const int m = pos < 64 ? pos : 64;
-  const unsigned long long x = lane < m ? tmp[lane] : 0ull;
-  return wave_rank_sort(x, m, tmp);
-}
-
-// Appends the logits of v passing `xf` (and, with a repetition penalty, not
-// penalised) to cbuf: one LDS reservation per non-empty ballot.  For spans
-// after the bound is tight, where candidates are rare.
-template <bool REP>
-__device__ __forceinline__ void append_rare(const float (&v)[kSpanNV][4], int base, int lane,
-                                            float xf, const uint32_t *bitmap,
-                                            unsigned long long *cbuf, int *n_c) {
-#pragma unroll
-  for (int j = 0; j < kSpanNV; ++j) {
-    const int e = base + (j * 64 + lane) * 4;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      bool pass = v[j][q] >= xf;
-      if (__ballot(pass)) {
-        if (REP && pass) pass = !((bitmap[(e + q) >> 5] >> ((e + q) & 31)) & 1u);
-        const unsigned long long b = __ballot(pass);
-        if (b) {
-          int bp = 0;
-          if (lane_id() == (int)(__ffsll((long long)b) - 1)) bp = atomicAdd(n_c, __popcll(b));
-          bp = __shfl(bp, __ffsll((long long)b) - 1);
-          const int p = bp + (int)lanes_below(b);
-          if (pass && p < kRowCandCap) cbuf[p] = pack_cand(f2key(v[j][q]), (uint32_t)(e + q));
-        }
-      }
-    }
-  }
-}
-
-// Packed maximum (value, then lowest index) of a span, folded into `best`.
-__device__ __forceinline__ unsigned long long greedy_span(const float (&v)[kSpanNV][4], int base,
-                                                          int lane, unsigned long long best) {
-#pragma unroll
-  for (int j = 0; j < kSpanNV; ++j) {
-    const int e = base + (j * 64 + lane) * 4;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t key = f2key(v[j][q]);
-      const unsigned long long c = key ? pack_cand(key, (uint32_t)(e + q)) : 0ull;
-      best = c > best ? c : best;
-    }
-  }
-  return best;
-}
-
 size_t row_smem_bytes(int vocab) {
   const size_t words = ((size_t)vocab + 31) / 32;
-  return (size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + 64 * 8 + 128 * 8 +
-         (size_t)kSmallK * 8 + words * 4;
+  return (size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + 64 * 8 + (size_t)kSmallK * 8 +
+         words * 4;
 }
 
 struct RowSmem {
   SelectSmem sel;
   TailSmem tail;
   unsigned long long best[kRowWaves];
-  double temperature, top_p, min_p, u;   // fetched at the start for the tail
-  uint32_t theta;
-  int32_t n_c, n_pen, n_keep;
+  uint32_t t_min, theta, key64;
+  int32_t n_c, n_l;
 };
 
 template <bool VEC>
@@ -879,215 +1026,208 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   extern __shared__ unsigned long long rdyn[];
   unsigned long long *cbuf = rdyn;                         // kRowCandCap candidates
   unsigned long long *srt = cbuf + kRowCandCap;            // kSortCap (fallback select)
-  unsigned long long *tmp = srt + kSortCap;                // 64
-  float *pen_val = reinterpret_cast<float *>(tmp + 64);    // 128 penalised values
-  int32_t *pen_id = reinterpret_cast<int32_t *>(pen_val + 128);   // 128 their ids
-  float *rsv = reinterpret_cast<float *>(pen_id + 128);    // kSmallK replay slots
+  uint32_t *lmax = reinterpret_cast<uint32_t *>(srt);      // round-0 lane maxima (aliases srt)
+  unsigned long long *top = srt + kSortCap;                // 64: sorted top of the row
+  float *rsv = reinterpret_cast<float *>(top + 64);        // kSmallK replay slots
   int32_t *rsid = reinterpret_cast<int32_t *>(rsv + kSmallK);
   uint32_t *bitmap = reinterpret_cast<uint32_t *>(rsid + kSmallK);   // ceil(V/32)
   __shared__ RowSmem rs;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int row = ws.row_list[blockIdx.x];
-  const RowPlan *plan = ws.plans + row;
+  const int row = a.rows_direct ? (int)blockIdx.x : ws.row_list[blockIdx.x];
   float *rowp = a.logits + (int64_t)row * a.stride;
   const int V = a.vocab;
-  // only what the streaming loop needs is read here; the tail rereads the plan
-  const bool greedy = plan->mode == kModeGreedy;
-  const int k = plan->k;
-  const int penbits = plan->pen;
+  const int nr = (V + 4 * kRoundF4 - 1) / (4 * kRoundF4);   // rounds
+
+  // The last <= 128 history ids (one per thread of waves 0-1) are requested
+  // before the stream: a wave's vector loads complete in order, so a request
+  // queued behind two rounds would wait for both.
+  int hid = -1;
+  if (a.hist_off && wave < 2) {
+    const int64_t h0 = load_scalar(a.hist_off + row);
+    const int64_t hl = load_scalar(a.hist_off + row + 1) - h0;
+    const int64_t last = hl < 128 ? hl : 128;   // history.slice(-128)
+    if (tid < last) hid = a.hist_ids[h0 + hl - last + tid];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // Round 0 alone goes out first (32768 logits per row, enough to keep HBM
+  // busy); round 1 follows as soon as round 0 has arrived, so the bound
+  // below is computed while round 1 streams.
+  float va[kRowNV][4], vb[kRowNV][4];
+  load_round<VEC>(va, rowp, 0, V, tid);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // the row's plan through the scalar cache, which does not queue behind
+  // the vector loads
+  const RowPlan *plan = ws.plans + row;
+  const int mode = load_scalar(&plan->mode);
+  const int k = load_scalar(&plan->k);
+  const int penbits = load_scalar(&plan->pen);
+  const double prep = load_scalar(&plan->rep);
+  const double temperature = load_scalar(&plan->temperature);
+  const double top_p = load_scalar(&plan->top_p), min_p = load_scalar(&plan->min_p);
+  const double u = load_scalar(a.uniforms + row);
+  const bool greedy = mode == kModeGreedy;
   // presence / frequency rows were penalised in place by pen_kernel
   const bool rep = (penbits & kPenRep) && !(penbits & kPenPF);
-  const int nspan = (V + kSpan - 1) / kSpan;
-
-  if (tid == 0) {   // the tail's parameters, fetched before the stream starts
-    rs.temperature = plan->temperature;
-    rs.top_p = plan->top_p;
-    rs.min_p = plan->min_p;
-    rs.u = a.uniforms[row];
+  if (tid == 0) {
+    rs.t_min = 0xFFFFFFFFu; rs.theta = 0; rs.key64 = 0;
+    rs.n_c = 0; rs.n_l = 0;
   }
-  float v[kSpanNV][4];
-  // the first span's loads are in flight while the penalty set is built
-  if (wave < nspan) load_span<VEC>(v, rowp, wave * kSpan, V, lane);
-  if (tid == 0) { rs.theta = 0; rs.n_c = 0; rs.n_pen = 0; rs.n_keep = 0; }
+  if (tid < 64) top[tid] = 0ull;
+
+  // src/sampler.ts:24-33: the distinct ids of the last 128 history entries.
+  // Their logits leave the stream (bitmap); the thread holding the first
+  // occurrence of an id keeps its raw logit for the end of the row.
+  int pid = -1;
+  float pval = 0.f;
   if (rep) {
-    // src/sampler.ts:24-33: the distinct ids of the last 128 history entries.
-    // Their logits leave the stream (bitmap) and join the selection with the
-    // penalised value; the in-place write-back waits until every read of the
-    // row is done.
     const int words = (V + 31) >> 5;
     for (int i = tid; i < words; i += kRowThreads) bitmap[i] = 0;
     __syncthreads();
-    const int64_t h0 = a.hist_off ? a.hist_off[row] : 0;
-    const int64_t hl = a.hist_off ? a.hist_off[row + 1] - h0 : 0;
-    const int64_t last = hl < 128 ? hl : 128;   // history.slice(-128)
-    if (tid < last) {
-      const int id = a.hist_ids[h0 + hl - last + tid];
-      if (id >= 0 && id < V) {
-        const uint32_t bit = 1u << (id & 31);
-        if (!(atomicOr(&bitmap[id >> 5], bit) & bit)) {   // the first occurrence owns the id
-          RowPlan pr;
-          pr.rep = plan->rep;
-          pr.pen = kPenRep;
-          const int slot = atomicAdd(&rs.n_pen, 1);
-          pen_val[slot] = penalise(rowp[id], true, 0u, pr);
-          pen_id[slot] = id;
-        }
+    if (hid >= 0 && hid < V) {
+      const uint32_t bit = 1u << (hid & 31);
+      if (!(atomicOr(&bitmap[hid >> 5], bit) & bit)) {   // the first occurrence owns the id
+        pid = hid;
+        pval = rowp[hid];   // used after the stream: its latency hides behind it
       }
     }
   }
-  __syncthreads();
+  __syncthreads();   // bitmap complete
 
-  // ---- round 0: span `wave`
-  const bool have0 = wave < nspan;
-  if (have0 && rep) {
-#pragma unroll
-    for (int j = 0; j < kSpanNV; ++j) {
-      const int e = wave * kSpan + (j * 64 + lane) * 4;
-      if (e < V) {
-        const uint32_t bits = (bitmap[e >> 5] >> (e & 31)) & 0xFu;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (bits & (1u << q)) v[j][q] = __builtin_nanf("");   // never selected
-      }
-    }
-  }
+  // ---- round 0 fixes the bound: theta = the exact k-th largest of the 1024
+  // lane maxima (each a distinct logit outside the repetition set), a lower
+  // bound of the row's k-th largest value
+  if (rep) mask_penalised(va, 0, tid, V, bitmap);
   unsigned long long best = 0;   // greedy: packed maximum
-  if (have0) {
-    if (greedy) {
-      best = greedy_span(v, wave * kSpan, lane, best);
-    } else {
-      // The span's k-th largest lane maximum: k distinct logits reach it, so
-      // it bounds the row's k-th largest from below.
-      float lm = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < kSpanNV; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) lm = fmaxf(lm, v[j][q]);
-      const uint32_t M = wave_kth_largest(f2key(lm), k);
-      const float xf = key_floor(M ? M : 1u);
-      uint32_t cnt = 0;
-#pragma unroll
-      for (int j = 0; j < kSpanNV; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) cnt += (uint32_t)__popcll(__ballot(v[j][q] >= xf));
-      int bp = 0;
-      if (lane == 0 && cnt) bp = atomicAdd(&rs.n_c, (int)cnt);
-      bp = __shfl(bp, 0);
-      uint32_t pos = 0;
-#pragma unroll
-      for (int j = 0; j < kSpanNV; ++j) {
-        const int e = wave * kSpan + (j * 64 + lane) * 4;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const bool pass = v[j][q] >= xf;
-          const unsigned long long b = __ballot(pass);
-          if (b) {
-            const int p = bp + (int)(pos + lanes_below(b));
-            if (pass && p < kRowCandCap) cbuf[p] = pack_cand(f2key(v[j][q]), (uint32_t)(e + q));
-            pos += (uint32_t)__popcll(b);
-          }
-        }
-      }
-    }
-  }
-
-  // prefetch round 1 while the bound is tightened
-  const int sp1 = wave + kRowWaves;
-  if (sp1 < nspan) load_span<VEC>(v, rowp, sp1 * kSpan, V, lane);
-
+  uint32_t key = 0;              // lane maximum of round 0
+  if (greedy)
+    best = greedy_round(va, 0, tid, best);
+  else
+    key = f2key(round_max(va));
+  __builtin_amdgcn_sched_barrier(0);
+  if (nr > 1) load_round<VEC>(vb, rowp, 1, V, tid);
+  __builtin_amdgcn_sched_barrier(0);
+  float xf = -FLT_MAX;
+  uint32_t theta = 0;
   if (!greedy) {
-    // exact k-th largest of the round-0 candidates (the first 16 spans): a
-    // lower bound of the row's k-th largest; keep only candidates reaching it
+    // Each wave's j-th largest lane maximum, j = ceil(k/16): the 16 waves
+    // together hold at least 16j >= k lanes at or above the smallest of them.
+    const uint32_t mj = wave_jth_largest(key, (k + kRowWaves - 1) / kRowWaves);
+    if (lane == 0) atomicMin(&rs.t_min, mj);   // 0 when a wave has fewer such lanes
     __syncthreads();
-    const int n1 = min(rs.n_c, kRowCandCap);
-    int total = 0;
-    const uint32_t T1 = block_select_fast<kRowThreads>(
-        k,
-        [&](int shift, uint32_t prefix, int pass) {
-          for (int p = tid; p < n1; p += kRowThreads)
-            hist_add(rs.sel, cand_key(cbuf[p]), shift, prefix, pass);
-        },
-        rs.sel, &total);
-    unsigned long long keep[kRowCandCap / kRowThreads];
-#pragma unroll
-    for (int i = 0; i < kRowCandCap / kRowThreads; ++i) {
-      const int p = tid + i * kRowThreads;
-      keep[i] = (p < n1 && cand_key(cbuf[p]) >= T1) ? cbuf[p] : 0ull;
-    }
-    if (tid == 0) rs.theta = T1;
-    __syncthreads();
-    if (rs.n_c <= kRowCandCap) {
-#pragma unroll
-      for (int i = 0; i < kRowCandCap / kRowThreads; ++i)
-        if (keep[i]) cbuf[atomicAdd(&rs.n_keep, 1)] = keep[i];
+    const uint32_t lo0 = (uint32_t)uniform_i32((int)rs.t_min);
+    const uint32_t lo = lo0 ? lo0 : 1u;
+    const bool pass = key >= lo;
+    const unsigned long long b = __ballot(pass);
+    if (b) {
+      const int leader = __ffsll((long long)b) - 1;
+      int bp = 0;
+      if (lane == leader) bp = atomicAdd(&rs.n_l, __popcll(b));
+      bp = __shfl(bp, leader);
+      if (pass) lmax[bp + (int)lanes_below(b)] = key;
     }
     __syncthreads();
-    if (tid == 0 && rs.n_c <= kRowCandCap) rs.n_c = rs.n_keep;
+    if (wave == 0) {
+      const uint32_t th = wave_kth_of_list(lmax, rs.n_l, k, lo);
+      if (lane == 0) rs.theta = th;
+    }
     __syncthreads();
+    theta = (uint32_t)uniform_i32((int)rs.theta);
+    xf = key_floor(theta ? theta : 1u);
+    append_round<false>(va, 0, tid, xf, bitmap, cbuf, &rs.n_c);
   }
 
-  // ---- rounds >= 1: the bound is tight, candidates are rare
-  const uint32_t theta = rs.theta;
-  const float xft = key_floor(theta ? theta : 1u);
-  for (int sp = sp1; sp < nspan; sp += kRowWaves) {
-    if (sp != sp1) load_span<VEC>(v, rowp, sp * kSpan, V, lane);
-    const int base = sp * kSpan;
-    if (greedy) {
-      if (rep) {
-#pragma unroll
-        for (int j = 0; j < kSpanNV; ++j) {
-          const int e = base + (j * 64 + lane) * 4;
-          if (e < V) {
-            const uint32_t bits = (bitmap[e >> 5] >> (e & 31)) & 0xFu;
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              if (bits & (1u << q)) v[j][q] = __builtin_nanf("");
-          }
-        }
+  // ---- rounds >= 1: candidates are rare
+  for (int r = 1; r < nr; r += 2) {
+    if (r + 1 < nr) load_round<VEC>(va, rowp, r + 1, V, tid);
+    if (r == 3 && !greedy && r + 1 < nr) {
+      // Rounds 3 and 4 are in flight: tighten the bound to the exact k-th
+      // largest of the candidates of rounds 0-2 and drop those below it.
+      __syncthreads();
+      const int n1 = uniform_i32(rs.n_c);
+      if (wave == 0 && n1 >= k && n1 <= 256) {
+        int m = 0;
+        const uint32_t t2 = n1 <= 128 ? wave_refine<2>(cbuf, n1, k, theta, &m)
+                                      : wave_refine<4>(cbuf, n1, k, theta, &m);
+        if (lane == 0) { rs.theta = t2; rs.n_c = m; }
       }
-      best = greedy_span(v, base, lane, best);
+      __syncthreads();
+      theta = (uint32_t)uniform_i32((int)rs.theta);
+      xf = key_floor(theta ? theta : 1u);
+    }
+    if (greedy) {
+      if (rep) mask_penalised(vb, r, tid, V, bitmap);
+      best = greedy_round(vb, r, tid, best);
     } else if (rep) {
-      append_rare<true>(v, base, lane, xft, bitmap, cbuf, &rs.n_c);
+      append_round<true>(vb, r, tid, xf, bitmap, cbuf, &rs.n_c);
     } else {
-      append_rare<false>(v, base, lane, xft, bitmap, cbuf, &rs.n_c);
+      append_round<false>(vb, r, tid, xf, bitmap, cbuf, &rs.n_c);
+    }
+    if (r + 1 >= nr) break;
+    if (r + 2 < nr) load_round<VEC>(vb, rowp, r + 2, V, tid);
+    if (greedy) {
+      if (rep) mask_penalised(va, r + 1, tid, V, bitmap);
+      best = greedy_round(va, r + 1, tid, best);
+    } else if (rep) {
+      append_round<true>(va, r + 1, tid, xf, bitmap, cbuf, &rs.n_c);
+    } else {
+      append_round<false>(va, r + 1, tid, xf, bitmap, cbuf, &rs.n_c);
     }
   }
 
-  __syncthreads();
-  // every read of the row is done: the penalised logits go back in place
-  const int n_pen = rs.n_pen;
-  for (int i = tid; i < n_pen; i += kRowThreads) rowp[pen_id[i]] = pen_val[i];
+  __syncthreads();   // every read of the row is done
+  // the penalised logits go back in place and join the candidates
+  float pv = 0.f;
+  if (pid >= 0) {
+    RowPlan pr;
+    pr.rep = prep;
+    pr.pen = kPenRep;
+    pv = penalise(pval, true, 0u, pr);
+    rowp[pid] = pv;
+  }
 
   if (greedy) {
+    if (pid >= 0) {
+      const uint32_t key = f2key(pv);
+      const unsigned long long c = key ? pack_cand(key, (uint32_t)pid) : 0ull;
+      best = c > best ? c : best;
+    }
     best = wave_max64(best);
     if (lane == 0) rs.best[wave] = best;
     __syncthreads();
     if (tid == 0) {
-      unsigned long long b = rs.best[0];
-      for (int w = 1; w < kRowWaves; ++w) b = rs.best[w] > b ? rs.best[w] : b;
-      for (int i = 0; i < n_pen; ++i) {
-        const uint32_t key = f2key(pen_val[i]);
-        const unsigned long long c = key ? pack_cand(key, (uint32_t)pen_id[i]) : 0ull;
-        b = c > b ? c : b;
-      }
-      write_greedy(a, row, rowp, b);
+      unsigned long long bb = rs.best[0];
+      for (int w = 1; w < kRowWaves; ++w) bb = rs.best[w] > bb ? rs.best[w] : bb;
+      write_greedy(a, row, rowp, bb);
     }
     return;
   }
 
-  // the penalised logits join the candidates
-  bool overflow = rs.n_c + n_pen > kRowCandCap;
-  if (!overflow) {
-    const int c0 = rs.n_c;
-    for (int i = tid; i < n_pen; i += kRowThreads)
-      cbuf[c0 + i] = pack_cand(f2key(pen_val[i]), (uint32_t)pen_id[i]);
+  {
+    const bool pass = pid >= 0 && pv >= xf;
+    const unsigned long long b = __ballot(pass);
+    if (b) {
+      const int leader = __ffsll((long long)b) - 1;
+      int bp = 0;
+      if (lane == leader) bp = atomicAdd(&rs.n_c, __popcll(b));
+      bp = __shfl(bp, leader);
+      const int p = bp + (int)lanes_below(b);
+      if (pass && p < kRowCandCap) cbuf[p] = pack_cand(f2key(pv), (uint32_t)pid);
+    }
   }
   __syncthreads();
-  const int n_all = overflow ? 0 : rs.n_c + n_pen;
+  const int n_all = rs.n_c;
+  bool overflow = n_all > kRowCandCap;
   unsigned long long F = 0;
   bool extra = false;
-  if (n_all > 512) {
+  if (!overflow && n_all <= kRowThreads) {
+    rank_top64(cbuf, n_all, top, &rs.key64);
+    if (wave != 0) return;
+    F = top[lane];
+    const uint32_t Tk = cand_key(__shfl(F, k - 1));
+    extra = rs.key64 != 0u && rs.key64 == Tk;
+  } else if (!overflow) {
     // rare: many candidates reach the bound (ties); select block-wide first
     uint32_t T = 0;
     const int n_sel = select_into<kRowThreads>(
@@ -1098,16 +1238,16 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
       F = lane < n_sel ? srt[lane] : 0ull;
       extra = n_sel > 64;
     }
-  } else {
-    if (wave != 0) return;
-    F = wave_top64(cbuf, n_all, k, tmp, &extra);
+  } else if (wave != 0) {
+    return;
   }
   RowPlan P;
-  P.temperature = rs.temperature;
-  P.top_p = rs.top_p;
-  P.min_p = rs.min_p;
+  P.temperature = temperature;
+  P.top_p = top_p;
+  P.min_p = min_p;
   P.k = k;
-  finish_wave(a, P, row, rowp, F, extra, overflow, rs.u, rsv, rsid);
+  finish_wave(a, P, row, rowp, F, extra, overflow, u, rsv, rsid,
+              reinterpret_cast<double *>(top));   // top[] is read into F already
 }
 
 // ---------------------------------------------------------------- chunk kernel
@@ -1381,43 +1521,49 @@ hipError_t prepare_kernels() {
                              (int)finalize_smem_bytes());
 }
 
+namespace {
+
+// One launch; with events, hipExtLaunchKernelGGL stamps the start and end of
+// the kernel's own dispatch (no marker packets are added to the stream).
+template <typename K>
+hipError_t launch_one(K kernel, dim3 grid, dim3 block, size_t smem, hipStream_t stream,
+                      hipEvent_t *ev, int slot, const LaunchArgs &a, const Workspace &ws) {
+  if (ev)
+    hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t)smem, stream, ev[2 * slot],
+                          ev[2 * slot + 1], 0u, a, ws);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, smem, stream, a, ws);
+  return hipGetLastError();
+}
+
+}  // namespace
+
 hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,
                          hipEvent_t *ev) {
   hipError_t e;
-  auto mark = [&](int i) -> hipError_t { return ev ? hipEventRecord(ev[i], stream) : hipSuccess; };
-  if ((e = mark(0)) != hipSuccess) return e;
   if (a.n_pf > 0) {
-    hipLaunchKernelGGL(pen_kernel, dim3((unsigned)(a.n_pf * a.chunks)), dim3(kThreads),
-                       (size_t)(kChunk + kChunk / 32) * 4, stream, a, ws);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    e = launch_one(pen_kernel, dim3((unsigned)(a.n_pf * a.chunks)), dim3(kThreads),
+                   (size_t)(kChunk + kChunk / 32) * 4, stream, ev, 0, a, ws);
+    if (e != hipSuccess) return e;
   }
-  if ((e = mark(1)) != hipSuccess) return e;
   if (a.n_row > 0) {
     const size_t smem = row_smem_bytes(a.vocab);
-    if (a.vec)
-      hipLaunchKernelGGL(row_kernel<true>, dim3((unsigned)a.n_row), dim3(kRowThreads), smem,
-                         stream, a, ws);
-    else
-      hipLaunchKernelGGL(row_kernel<false>, dim3((unsigned)a.n_row), dim3(kRowThreads), smem,
-                         stream, a, ws);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    e = a.vec ? launch_one(row_kernel<true>, dim3((unsigned)a.n_row), dim3(kRowThreads), smem,
+                           stream, ev, 1, a, ws)
+              : launch_one(row_kernel<false>, dim3((unsigned)a.n_row), dim3(kRowThreads), smem,
+                           stream, ev, 1, a, ws);
+    if (e != hipSuccess) return e;
   }
-  if ((e = mark(2)) != hipSuccess) return e;
   if (a.n_chunk > 0) {
     const dim3 grid((unsigned)(a.n_chunk * a.chunks));
-    if (a.vec)
-      hipLaunchKernelGGL(chunk_kernel<true>, grid, dim3(kThreads), 0, stream, a, ws);
-    else
-      hipLaunchKernelGGL(chunk_kernel<false>, grid, dim3(kThreads), 0, stream, a, ws);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    e = a.vec ? launch_one(chunk_kernel<true>, grid, dim3(kThreads), 0, stream, ev, 2, a, ws)
+              : launch_one(chunk_kernel<false>, grid, dim3(kThreads), 0, stream, ev, 2, a, ws);
+    if (e != hipSuccess) return e;
+    e = launch_one(finalize_kernel, dim3((unsigned)a.n_chunk), dim3(kThreads),
+                   finalize_smem_bytes(), stream, ev, 3, a, ws);
+    if (e != hipSuccess) return e;
   }
-  if ((e = mark(3)) != hipSuccess) return e;
-  if (a.n_chunk > 0) {
-    hipLaunchKernelGGL(finalize_kernel, dim3((unsigned)a.n_chunk), dim3(kThreads),
-                       finalize_smem_bytes(), stream, a, ws);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-  }
-  return mark(4);
+  return hipSuccess;
 }
 
 }  // namespace hs

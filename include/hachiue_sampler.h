@@ -123,7 +123,7 @@ int hs_sample_batch_device_ex(hs_context *ctx, float *d_logits, int32_t rows,
  * each of its kernel launches.  hs_context_kernel_times() waits for the
  * recorded calls, writes the summed device milliseconds per kernel
  * (ms[0] presence/frequency pre-pass, ms[1] row kernel, ms[2] chunk kernel,
- * ms[3] finalize; a kernel a call did not need counts ~0) and the number of
+ * ms[3] finalize; a kernel a call did not launch adds 0) and the number of
  * timed calls, and resets the totals. */
 int hs_context_set_timing(hs_context *ctx, int enable);
 int hs_context_kernel_times(hs_context *ctx, double *ms, int32_t count, int64_t *calls);
