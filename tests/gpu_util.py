@@ -70,6 +70,7 @@ def compare(got: GpuResult, want, want_logits, configs, vocab, cap, label=""):
     bad = np.flatnonzero(~same.reshape(rows, -1).all(axis=1))
     assert bad.size == 0, f"{label}: penalised logits differ in rows {bad[:10]}"
     boundary = 0
+    probs_total = probs_exact = 0
     errors = []
     for r in range(rows):
         path = int(want.path[r])
@@ -92,6 +93,8 @@ def compare(got: GpuResult, want, want_logits, configs, vocab, cap, label=""):
             # a +Infinity candidate makes every probability NaN in the
             # reference too ((Inf - Inf) * invTemp, src/sampler.ts:84)
             ok = (rel <= PROB_RTOL) | (np.isnan(gp) & np.isnan(wp))
+            probs_total += m
+            probs_exact += int(((gp == wp) | (np.isnan(gp) & np.isnan(wp))).sum())
             if not ok.all():
                 errors.append(f"row {r}: probs rel err {np.nanmax(rel):.3g}")
         near_topp = want.topp_margin[r] < BOUNDARY
@@ -104,5 +107,6 @@ def compare(got: GpuResult, want, want_logits, configs, vocab, cap, label=""):
                 errors.append(f"row {r}: token {got.tokens[r]} != {want.token[r]} "
                               f"(draw margin {want.draw_margin[r]:.3g})")
     assert not errors, f"{label}: {len(errors)} mismatches: " + "; ".join(errors[:8])
-    print(f"[parity] {label}: {rows} rows ok, boundary cases {boundary}", file=sys.stderr)
+    print(f"[parity] {label}: {rows} rows ok, boundary cases {boundary}, "
+          f"probabilities bit-equal {probs_exact}/{probs_total}", file=sys.stderr)
     return boundary
