@@ -121,7 +121,7 @@ int64_t resolve_k(double top_k, int64_t vocab) {
 
 // Routing of rows to kernels, uploaded next to the plans.
 struct Routing {
-  std::vector<int32_t> pf, row, chunk;
+  std::vector<int32_t> pf, row, chunk, large;
 };
 
 int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_rows,
@@ -130,6 +130,7 @@ int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_r
   rt.pf.clear();
   rt.row.clear();
   rt.chunk.clear();
+  rt.large.clear();
   for (int r = 0; r < rows; ++r) {
     const hs_sample_config &c = cfgs[r];
     hs::RowPlan p;
@@ -150,13 +151,16 @@ int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_r
       p.k = (int32_t)k;
       if (k <= hs::kSmallK) p.mode = hs::kModeSmall;
       else if (k <= hs::kMaxK) p.mode = hs::kModeGeneric;
-      else
-        return fail(HS_ERR_UNSUPPORTED,
-                    "row %d: top-k %lld exceeds %d, the largest k this build selects", r,
-                    (long long)k, hs::kMaxK);
+      else p.mode = hs::kModeLarge;
     }
     out[(size_t)r] = p;
-    if (p.pen & hs::kPenPF) rt.pf.push_back(r);
+    // the large-k kernel takes penalised logits: its rows' penalties run in
+    // the pre-pass, like the presence / frequency rows of the other kernels
+    if ((p.pen & hs::kPenPF) || (p.pen && p.mode == hs::kModeLarge)) rt.pf.push_back(r);
+    if (p.mode == hs::kModeLarge) {
+      rt.large.push_back(r);
+      continue;
+    }
     const bool row_kernel = (p.mode == hs::kModeGreedy || p.mode == hs::kModeSmall) &&
                             vocab <= hs::kRowMaxVocab && rows >= row_min_rows;
     (row_kernel ? rt.row : rt.chunk).push_back(r);
@@ -169,7 +173,8 @@ int upload_plans(hs_context *ctx, const std::vector<hs::RowPlan> &plans, const R
                  int vocab, hipStream_t stream) {
   const size_t rows = plans.size();
   const size_t pbytes = rows * sizeof(hs::RowPlan);
-  const size_t lbytes = sizeof(int32_t) * (rt.pf.size() + rt.row.size() + rt.chunk.size());
+  const size_t lbytes =
+      sizeof(int32_t) * (rt.pf.size() + rt.row.size() + rt.chunk.size() + rt.large.size());
   const size_t bytes = pbytes + lbytes;
   if (ctx->last_plans.size() == rows && ctx->last_vocab == vocab && ctx->plans.bytes >= bytes &&
       memcmp(ctx->last_plans.data(), plans.data(), pbytes) == 0)
@@ -192,6 +197,8 @@ int upload_plans(hs_context *ctx, const std::vector<hs::RowPlan> &plans, const R
   memcpy(lists, rt.pf.data(), sizeof(int32_t) * rt.pf.size());
   memcpy(lists + rt.pf.size(), rt.row.data(), sizeof(int32_t) * rt.row.size());
   memcpy(lists + rt.pf.size() + rt.row.size(), rt.chunk.data(), sizeof(int32_t) * rt.chunk.size());
+  memcpy(lists + rt.pf.size() + rt.row.size() + rt.chunk.size(), rt.large.data(),
+         sizeof(int32_t) * rt.large.size());
   HS_HIP(hipMemcpyAsync(ctx->plans.p, st, bytes, hipMemcpyHostToDevice, stream));
   HS_HIP(hipEventRecord(ctx->plan_done, stream));
   ctx->plan_pending = true;
@@ -246,6 +253,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
     return fail(HS_ERR_OUT_OF_MEMORY, "host allocation failed");
   }
   const int n_pf = (int)rt.pf.size(), n_row = (int)rt.row.size(), n_chunk = (int)rt.chunk.size();
+  const int n_large = (int)rt.large.size();
 
   // workspace (the chunk path only)
   if (n_chunk > 0) {
@@ -265,6 +273,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   ws.pf_list = lists;
   ws.row_list = lists + n_pf;
   ws.chunk_list = lists + n_pf + n_row;
+  ws.large_list = lists + n_pf + n_row + n_chunk;
   ws.cand = static_cast<uint2 *>(ctx->cand.p);
   ws.cand_count = static_cast<int32_t *>(ctx->cand_count.p);
   ws.info = static_cast<hs::ChunkInfo *>(ctx->info.p);
@@ -282,6 +291,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   a.n_row = n_row;
   a.rows_direct = n_row == rows ? 1 : 0;
   a.n_chunk = n_chunk;
+  a.n_large = n_large;
   a.hist_ids = d_hist_ids;
   a.hist_off = d_hist_offsets;
   a.uniforms = d_uniforms;
@@ -508,6 +518,12 @@ int hs_sample_logits_batch(hs_context *ctx, float *logits, int32_t rows, int64_t
   if (penalised)   // the reference writes penalised values back (src/sampler.ts:30)
     HS_HIP(hipMemcpyAsync(logits, ctx->h_logits.p, lbytes, hipMemcpyDeviceToHost, st));
   HS_HIP(hipStreamSynchronize(st));
+  for (int r = 0; r < rows; ++r)
+    if (tokens_out[r] < 0)
+      return fail(HS_ERR_UNSUPPORTED,
+                  "row %d: top-k above 1024 with equal logits at the drawn position; the "
+                  "reference orders them by its slot history, which this build does not replay "
+                  "at that size", r);
   return HS_OK;
 }
 

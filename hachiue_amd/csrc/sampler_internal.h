@@ -32,7 +32,7 @@ enum RowMode : int32_t {
   kModeGreedy = 0,   // temperature <= 0 (src/sampler.ts:36-46)
   kModeSmall = 1,    // 1 <= k <= 64
   kModeGeneric = 2,  // 64 < k <= 1024
-  kModeLarge = 3,    // k > 1024
+  kModeLarge = 3,    // k > 1024 (large_kernel)
 };
 
 enum RowPen : int32_t {
@@ -70,6 +70,7 @@ struct Workspace {
   const int32_t *pf_list;    // rows penalised by the pre-pass
   const int32_t *row_list;   // rows of the row kernel
   const int32_t *chunk_list; // rows of the chunk + finalize kernels
+  const int32_t *large_list; // rows of the large-k kernel
   uint2 *cand;               // [n_chunk][S][kChunkCap] (key, index)
   int32_t *cand_count;       // [n_chunk]
   ChunkInfo *info;           // [n_chunk][S]
@@ -84,7 +85,7 @@ struct LaunchArgs {
   int32_t vec;               // float4 loads allowed (alignment)
   int32_t want_cands;        // exact candidate order must be produced
   int32_t rows_direct;       // the row kernel takes every row: row = block index
-  int32_t n_pf, n_row, n_chunk;
+  int32_t n_pf, n_row, n_chunk, n_large;
   const int32_t *hist_ids;
   const int64_t *hist_off;
   const double *uniforms;
@@ -99,11 +100,12 @@ struct LaunchArgs {
 
 // Launches the kernels of one call on `stream`.  When `ev` is not null,
 // ev[2i] and ev[2i + 1] receive the start and end of kernel i's dispatch
-// (0 penalty pre-pass, 1 row kernel, 2 chunk kernel, 3 finalize), for the
-// kernels that launch only: launched_kernels() says which.
-constexpr int kTimedKernels = 4;
+// (0 penalty pre-pass, 1 row kernel, 2 chunk kernel, 3 finalize, 4 large-k
+// kernel), for the kernels that launch only: launched_kernels() says which.
+constexpr int kTimedKernels = 5;
 inline unsigned launched_kernels(const LaunchArgs &a) {
-  return (a.n_pf > 0 ? 1u : 0u) | (a.n_row > 0 ? 2u : 0u) | (a.n_chunk > 0 ? 12u : 0u);
+  return (a.n_pf > 0 ? 1u : 0u) | (a.n_row > 0 ? 2u : 0u) | (a.n_chunk > 0 ? 12u : 0u) |
+         (a.n_large > 0 ? 16u : 0u);
 }
 hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,
                          hipEvent_t *ev);

@@ -24,6 +24,10 @@
 //                    block radix select, candidates to a per-row list.
 //   finalize_kernel  one workgroup per chunk-kernel row: exact select over the
 //                    row's candidates, then the shared row completion.
+//   large_kernel     rows with k > 1024: one 1024-thread workgroup per row,
+//                    several passes (radix select of the k-th value, softmax
+//                    normaliser, probability-mass histogram, positions located
+//                    by narrowing one bucket).
 // Row completion (finish_row): equal-value groups make the reference's order
 // depend on its slot history (src/sampler.ts:55-69); when such a group can
 // change the result, the exact replace-min scan is replayed over the row.
@@ -1501,6 +1505,577 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(LaunchArgs a, Worksp
   finish_row<kThreads>(a, P, row, rowp, srt, n_sel, T, closed_form, need_replay, s, f.tail);
 }
 
+// ---------------------------------------------------------------- large-k kernel
+
+// Rows with k > 1024 (up to topK = Infinity, src/sampler.ts:49): one
+// 1024-thread workgroup per row making several passes over the row.
+//   1. extremes: the packed maximum (value, lowest index), the smallest
+//      finite key and n_F, the number of logits that can become candidates;
+//   2. k < n_F only: T, the exact k-th largest key (12/12/8-bit radix
+//      select).  The candidates are the logits above T plus k - #(> T) of
+//      those equal to T.  With k >= n_F every such logit is a candidate and no
+//      slot is ever evicted, so the reference's order is value descending,
+//      index ascending (src/sampler.ts:50-73 with no replacement);
+//   3. the normaliser S and a 4096-bucket histogram of candidate counts and
+//      probability mass over the key range.  These binary64 sums run in
+//      another order than the reference's (src/sampler.ts:82-86, 97, 108),
+//      which moves probabilities by far less than the 1e-5 tolerance;
+//   4. each position the tail needs (the top-p crossing, cutoff - 1, the
+//      draw) is found from its bucket, narrowed by 1024-bucket passes until at
+//      most 2048 logits remain, which are gathered into LDS, sorted and
+//      walked in order.
+// With k < n_F a group of equal values is ordered by slot history: when the
+// drawn position falls in such a group the row reports HS_ROW_UNSUPPORTED
+// and token -1 instead of guessing.
+
+constexpr int kLT = 1024;      // threads per workgroup
+constexpr int kLBins = 4096;   // level-1 buckets
+constexpr int kLSub = 1024;    // refinement buckets
+constexpr int kLCap = 2048;    // logits gathered and sorted in LDS
+
+struct LargeSmem {
+  uint32_t cnt[kLBins];
+  double mass[kLBins];
+  uint32_t cnt2[kLSub];
+  double mass2[kLSub];
+  unsigned long long buf[kLCap];
+  double pbuf[kLCap];          // probability of buf[i] (binary64 of the f32 value)
+  unsigned long long ured[kLT / 64];
+  double dred[kLT / 64];
+  // located bucket / element, published by one thread
+  int32_t found, pos, id, tie, nbuf;
+  uint32_t key, b, ecnt;
+  double emass, cum;
+};
+
+size_t large_smem_bytes() { return sizeof(LargeSmem); }
+
+// Per-row constants of the large path (wave-uniform).
+struct LargeRow {
+  const float *rowp;
+  int V, vec;
+  uint32_t T;      // 0: every finite logit is a candidate; else keys > T plus `tin` equal to T
+  int tin, teq;    // candidates equal to T, logits equal to T
+  uint32_t lo, hi; // key range of the candidates
+  int s1;          // level-1 bucket shift
+  double m, inv_temp, S;
+};
+
+__device__ __forceinline__ bool large_cand(const LargeRow &L, uint32_t key) {
+  return key != 0u && key >= L.T;
+}
+
+// src/sampler.ts:83-89: probs[i] = f32(f32(exp((v - max) / T)) / S)
+__device__ __forceinline__ float large_prob(const LargeRow &L, float v) {
+  const double p = exp(((double)v - L.m) * L.inv_temp);
+  return (float)((double)(float)p / L.S);
+}
+
+// Calls f(index, value) for every logit of the row (float4 loads when aligned).
+template <typename F>
+__device__ __forceinline__ void large_pass(const LargeRow &L, F f) {
+  const int tid = threadIdx.x;
+  if (L.vec) {
+    const int nfull = L.V >> 2;
+    const f32x4 *p4 = reinterpret_cast<const f32x4 *>(L.rowp);
+    for (int i = tid; i < nfull; i += kLT) {
+      const f32x4 t = __builtin_nontemporal_load(p4 + i);
+      f(4 * i, t[0]); f(4 * i + 1, t[1]); f(4 * i + 2, t[2]); f(4 * i + 3, t[3]);
+    }
+    for (int e = 4 * nfull + tid; e < L.V; e += kLT) f(e, L.rowp[e]);
+  } else {
+    for (int e = tid; e < L.V; e += kLT) f(e, L.rowp[e]);
+  }
+}
+
+__device__ __forceinline__ double wave_sum_f64(double x) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) x += __shfl_xor(x, m);
+  return x;
+}
+
+__device__ __forceinline__ unsigned long long block_max_u64(unsigned long long x, LargeSmem &sm) {
+  x = wave_max64(x);
+  if (lane_id() == 0) sm.ured[threadIdx.x >> 6] = x;
+  __syncthreads();
+  unsigned long long r = 0;
+  for (int w = 0; w < kLT / 64; ++w) r = sm.ured[w] > r ? sm.ured[w] : r;
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ unsigned long long block_sum_u64(unsigned long long x, LargeSmem &sm) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) x += __shfl_xor(x, m);
+  if (lane_id() == 0) sm.ured[threadIdx.x >> 6] = x;
+  __syncthreads();
+  unsigned long long r = 0;
+  for (int w = 0; w < kLT / 64; ++w) r += sm.ured[w];
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ double block_sum_f64(double x, LargeSmem &sm) {
+  x = wave_sum_f64(x);
+  if (lane_id() == 0) sm.dred[threadIdx.x >> 6] = x;
+  __syncthreads();
+  double r = 0;
+  for (int w = 0; w < kLT / 64; ++w) r += sm.dred[w];
+  __syncthreads();
+  return r;
+}
+
+// Exclusive prefix over the threads of the workgroup, in thread order, of a
+// (count, mass) pair.
+__device__ __forceinline__ void block_excl_scan2(uint32_t c, double m, uint32_t *ec, double *em,
+                                                 LargeSmem &sm) {
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  uint32_t ic = c;
+  double im = m;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t tc = __shfl_up(ic, d);
+    const double tm = __shfl_up(im, d);
+    if (lane >= d) { ic += tc; im += tm; }
+  }
+  if (lane == 63) { sm.ured[wave] = ic; sm.dred[wave] = im; }
+  const uint32_t pc = __shfl_up(ic, 1);
+  const double pm = __shfl_up(im, 1);
+  __syncthreads();
+  uint32_t bc = 0;
+  double bm = 0;
+  for (int w = 0; w < wave; ++w) { bc += (uint32_t)sm.ured[w]; bm += sm.dred[w]; }
+  *ec = bc + (lane ? pc : 0u);
+  *em = bm + (lane ? pm : 0.0);
+  __syncthreads();
+}
+
+enum { kByMass = 0, kByPos = 1 };
+
+// Whether a bucket holding positions [ec, ec + c) with mass [em, em + m)
+// holds the located position.
+__device__ __forceinline__ bool large_hit(int mode, double target, uint32_t pos, uint32_t ec,
+                                          uint32_t c, double em, double m) {
+  if (c == 0) return false;
+  if (mode == kByPos) return ec <= pos && pos < ec + c;
+  return em < target && em + m >= target;
+}
+
+// Located element of the candidate order.
+struct LargeLoc {
+  bool found;
+  int pos, id;
+  uint32_t key;
+  bool tie;        // another candidate holds the same value
+  double cum;      // cumProb through this position
+};
+
+// The id of the j-th logit (index order) whose key equals `key`.
+__device__ int large_nth_equal(const LargeRow &L, uint32_t key, uint32_t j, LargeSmem &sm) {
+  const int tid = threadIdx.x;
+  const int span = (L.V + kLT - 1) / kLT;
+  const int b0 = tid * span, b1 = min(L.V, b0 + span);
+  uint32_t c = 0;
+  for (int e = b0; e < b1; ++e) c += f2key(L.rowp[e]) == key;
+  uint32_t ec;
+  double dummy;
+  block_excl_scan2(c, 0.0, &ec, &dummy, sm);
+  if (tid == 0) sm.id = -1;
+  __syncthreads();
+  if (ec <= j && j < ec + c) {
+    uint32_t seen = ec;
+    for (int e = b0; e < b1; ++e) {
+      if (f2key(L.rowp[e]) == key) {
+        if (seen == j) { sm.id = e; break; }
+        ++seen;
+      }
+    }
+  }
+  __syncthreads();
+  const int id = sm.id;
+  __syncthreads();
+  return id;
+}
+
+// Gathers the candidates with keys in [klo, khi] into sm.buf (sm.nbuf counts
+// them, possibly past kLCap).  When more logits equal T than slots remain
+// for them, which ones the reference keeps depends on its slot history: they
+// are represented by `tin` placeholder entries (key T, id 0) instead.
+__device__ void large_gather(const LargeRow &L, uint32_t klo, uint32_t khi, LargeSmem &sm) {
+  const bool btie = L.T != 0u && L.teq > L.tin;
+  if (threadIdx.x == 0) sm.nbuf = 0;
+  __syncthreads();
+  large_pass(L, [&](int e, float v) {
+    const uint32_t key = f2key(v);
+    if (large_cand(L, key) && key >= klo && key <= khi && !(btie && key == L.T)) {
+      const int p = atomicAdd(&sm.nbuf, 1);
+      if (p < kLCap) sm.buf[p] = pack_cand(key, (uint32_t)e);
+    }
+  });
+  __syncthreads();
+  if (threadIdx.x == 0 && btie && L.T >= klo && L.T <= khi) {
+    for (int i = 0; i < L.tin; ++i) {
+      const int p = sm.nbuf++;
+      if (p < kLCap) sm.buf[p] = pack_cand(L.T, 0u);
+    }
+  }
+  __syncthreads();
+}
+
+// Finds the first position whose cumProb reaches `target` (kByMass) or the
+// position `pos` (kByPos).  sm.cnt / sm.mass hold the level-1 histogram.
+__device__ LargeLoc large_locate(const LargeRow &L, int mode, double target, uint32_t pos,
+                                 LargeSmem &sm) {
+  const int tid = threadIdx.x;
+  LargeLoc r;
+  r.found = false; r.pos = -1; r.id = -1; r.key = 0; r.tie = false; r.cum = 0;
+  // level 1: thread t owns buckets 4095-4t .. 4092-4t (descending values)
+  {
+    uint32_t c[4], tc = 0;
+    double m[4], tm = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int b = kLBins - 1 - 4 * tid - i;
+      c[i] = sm.cnt[b]; m[i] = sm.mass[b];
+      tc += c[i]; tm += m[i];
+    }
+    uint32_t ec;
+    double em;
+    block_excl_scan2(tc, tm, &ec, &em, sm);
+    if (tid == 0) sm.found = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (large_hit(mode, target, pos, ec, c[i], em, m[i])) {
+        sm.found = 1; sm.b = (uint32_t)(kLBins - 1 - 4 * tid - i); sm.ecnt = ec; sm.emass = em;
+      }
+      ec += c[i]; em += m[i];
+    }
+    __syncthreads();
+  }
+  if (!sm.found) { __syncthreads(); return r; }
+  uint32_t klo = L.lo + (sm.b << L.s1);
+  uint32_t khi = (L.hi - klo) >> L.s1 ? klo + ((1u << L.s1) - 1u) : L.hi;
+  uint32_t count = sm.cnt[sm.b];
+  uint32_t Ec = sm.ecnt;
+  double Em = sm.emass;
+  __syncthreads();
+  // narrow the bucket while it holds more logits than LDS sorts
+  while (count > (uint32_t)kLCap && klo < khi) {
+    int s2 = 0;
+    while (((khi - klo) >> s2) >= (uint32_t)kLSub) ++s2;
+    sm.cnt2[tid] = 0;
+    sm.mass2[tid] = 0;
+    __syncthreads();
+    large_pass(L, [&](int, float v) {
+      const uint32_t key = f2key(v);
+      if (large_cand(L, key) && key >= klo && key <= khi) {
+        const uint32_t b = (key - klo) >> s2;
+        atomicAdd(&sm.cnt2[b], 1u);
+        atomicAdd(&sm.mass2[b], (double)large_prob(L, v));
+      }
+    });
+    __syncthreads();
+    if (tid == 0 && L.T && L.teq > L.tin && L.T >= klo && L.T <= khi) {
+      const uint32_t b = (L.T - klo) >> s2;   // only `tin` of the T-valued logits count
+      sm.cnt2[b] -= (uint32_t)(L.teq - L.tin);
+      sm.mass2[b] -= (double)(L.teq - L.tin) * (double)large_prob(L, key2f(L.T));
+    }
+    __syncthreads();
+    const int b = kLSub - 1 - tid;
+    const uint32_t c = sm.cnt2[b];
+    const double m = sm.mass2[b];
+    uint32_t ec;
+    double em;
+    block_excl_scan2(c, m, &ec, &em, sm);
+    ec += Ec; em += Em;
+    if (tid == 0) sm.found = 0;
+    __syncthreads();
+    if (large_hit(mode, target, pos, ec, c, em, m)) {
+      sm.found = 1; sm.b = (uint32_t)b; sm.ecnt = ec; sm.emass = em;
+    }
+    __syncthreads();
+    if (!sm.found) { __syncthreads(); return r; }
+    const uint32_t nlo = klo + (sm.b << s2);
+    khi = (khi - nlo) >> s2 ? nlo + ((1u << s2) - 1u) : khi;
+    klo = nlo;
+    count = sm.cnt2[sm.b];
+    Ec = sm.ecnt;
+    Em = sm.emass;
+    __syncthreads();
+  }
+  if (count > (uint32_t)kLCap) {
+    // one value held by more logits than LDS sorts: equal probabilities,
+    // index order (the reference's order when no slot was evicted)
+    const uint32_t key = klo;
+    const float pv = large_prob(L, key2f(key));
+    uint32_t j = 0;
+    double c = Em;
+    if (mode == kByPos) {
+      j = pos - Ec;
+      for (uint32_t i = 0; i <= j; ++i) c += (double)pv;
+    } else {
+      for (j = 0; j < count; ++j) {
+        c += (double)pv;
+        if (c >= target) break;
+      }
+      if (j == count) { j = count - 1; }
+    }
+    r.found = true; r.pos = (int)(Ec + j); r.key = key; r.tie = true; r.cum = c;
+    r.id = large_nth_equal(L, key, j, sm);
+    return r;
+  }
+  // gather the bucket's logits, sort them, walk them in order
+  large_gather(L, klo, khi, sm);
+  const int nb = min(sm.nbuf, kLCap);
+  int P2 = 1;
+  while (P2 < nb) P2 <<= 1;
+  for (int i = nb + tid; i < P2; i += kLT) sm.buf[i] = 0ull;
+  __syncthreads();
+  block_sort_desc<kLT>(sm.buf, P2);
+  for (int i = tid; i < nb; i += kLT) sm.pbuf[i] = (double)large_prob(L, key2f(cand_key(sm.buf[i])));
+  __syncthreads();
+  if (tid == 0) {
+    double c = Em;
+    int hit = -1, tseen = 0;
+    const int avail = (int)count;   // T-valued logits past `tin` are not candidates
+    int j = 0;
+    for (; j < nb && j < avail; ++j) {
+      const uint32_t key = cand_key(sm.buf[j]);
+      if (L.T && key == L.T && tseen++ >= L.tin) break;
+      c += sm.pbuf[j];
+      if (mode == kByPos ? Ec + (uint32_t)j == pos : c >= target) { hit = j; break; }
+    }
+    if (hit < 0) { hit = j > 0 ? j - 1 : 0; }   // rounding at a bucket edge: its last logit
+    const uint32_t key = cand_key(sm.buf[hit]);
+    sm.pos = (int)Ec + hit;
+    sm.id = (int)cand_idx(sm.buf[hit]);
+    sm.key = key;
+    sm.cum = c;
+    sm.tie = (hit > 0 && cand_key(sm.buf[hit - 1]) == key) ||
+             (hit + 1 < nb && cand_key(sm.buf[hit + 1]) == key);
+  }
+  __syncthreads();
+  r.found = true; r.pos = sm.pos; r.id = sm.id; r.key = sm.key; r.tie = sm.tie != 0; r.cum = sm.cum;
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(kLT) void large_kernel(LaunchArgs a, Workspace ws) {
+  extern __shared__ unsigned long long ldyn[];
+  LargeSmem &sm = *reinterpret_cast<LargeSmem *>(ldyn);
+  const int tid = threadIdx.x;
+  const int row = ws.large_list[blockIdx.x];
+  const RowPlan P = ws.plans[row];
+  LargeRow L;
+  L.rowp = a.logits + (int64_t)row * a.stride;
+  L.V = a.vocab;
+  L.vec = a.vec;
+  L.T = 1u;       // every finite logit, for the first passes
+  L.tin = L.teq = 0;
+
+  // 1. extremes and n_F
+  unsigned long long best = 0;
+  unsigned long long kmin_neg = 0;   // max of ~key = min key
+  unsigned long long nf = 0;
+  large_pass(L, [&](int e, float v) {
+    const uint32_t key = f2key(v);
+    if (key) {
+      const unsigned long long c = pack_cand(key, (uint32_t)e);
+      best = c > best ? c : best;
+      const unsigned long long nk = (unsigned long long)(~key);
+      kmin_neg = nk > kmin_neg ? nk : kmin_neg;
+      ++nf;
+    }
+  });
+  best = block_max_u64(best, sm);
+  const uint32_t kmin = ~(uint32_t)block_max_u64(kmin_neg, sm);
+  const int n_f = (int)block_sum_u64(nf, sm);
+  const int k = P.k;
+  const int n = k < n_f ? k : n_f;
+  const int cs = a.cand_stride;
+
+  if (n <= 1) {   // src/sampler.ts:76-77: no draw
+    if (tid == 0) {
+      a.tokens[row] = n == 1 ? (int)cand_idx(best) : 0;
+      if (a.cand_count_out) a.cand_count_out[row] = n;
+      if (a.cutoff_out) a.cutoff_out[row] = n;
+      if (a.row_flags) a.row_flags[row] = HS_ROW_SINGLE | HS_ROW_LARGE;
+      if (n == 1 && cs > 0) {
+        if (a.cand_ids) a.cand_ids[(int64_t)row * cs] = (int)cand_idx(best);
+        if (a.cand_probs) a.cand_probs[(int64_t)row * cs] = 1.0f;
+      }
+    }
+    return;
+  }
+
+  // 2. k < n_F: T = the exact k-th largest key
+  L.T = 0u;
+  if (k < n_f) {
+    uint32_t prefix = 0;
+    int rem = k;
+    for (int pass = 0; pass < 3; ++pass) {
+      const int sh = pass == 0 ? 20 : (pass == 1 ? 8 : 0);
+      const int nbits = pass == 2 ? 8 : 12;
+      const int nb = 1 << nbits, top = sh + nbits;
+      for (int i = tid; i < kLBins; i += kLT) sm.cnt[i] = 0;
+      __syncthreads();
+      large_pass(L, [&](int, float v) {
+        const uint32_t key = f2key(v);
+        if (key && (pass == 0 || (key >> top) == (prefix >> top)))
+          atomicAdd(&sm.cnt[(key >> sh) & (uint32_t)(nb - 1)], 1u);
+      });
+      __syncthreads();
+      // thread t owns digits nb-1-4t .. nb-4-4t (descending)
+      uint32_t c[4], tc = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = nb - 1 - 4 * tid - i;
+        c[i] = d >= 0 ? sm.cnt[d] : 0u;
+        tc += c[i];
+      }
+      uint32_t ec;
+      double dummy;
+      block_excl_scan2(tc, 0.0, &ec, &dummy, sm);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (ec < (uint32_t)rem && ec + c[i] >= (uint32_t)rem) {
+          sm.b = (uint32_t)(nb - 1 - 4 * tid - i);
+          sm.ecnt = ec;
+          sm.nbuf = (int)c[i];
+        }
+        ec += c[i];
+      }
+      __syncthreads();
+      prefix |= sm.b << sh;
+      rem -= (int)sm.ecnt;
+      L.teq = sm.nbuf;
+      __syncthreads();
+    }
+    L.T = prefix;
+    L.tin = rem;            // k - #(> T) slots left for the T-valued logits
+  }
+  L.lo = L.T ? L.T : kmin;
+  L.hi = cand_key(best);
+  L.s1 = 0;
+  while (((L.hi - L.lo) >> L.s1) >= (uint32_t)kLBins) ++L.s1;
+  L.m = (double)key2f(L.hi);
+  L.inv_temp = 1.0 / P.temperature;
+
+  // 3. normaliser and level-1 histogram
+  double s = 0;
+  large_pass(L, [&](int, float v) {
+    const uint32_t key = f2key(v);
+    if (key != 0u && key > L.T) s += exp(((double)v - L.m) * L.inv_temp);
+  });
+  L.S = block_sum_f64(s, sm);
+  if (L.T) L.S += (double)L.tin * exp(((double)key2f(L.T) - L.m) * L.inv_temp);
+  const float prob0 = large_prob(L, key2f(L.hi));
+  const double thr = P.min_p * (double)prob0;
+  for (int i = tid; i < kLBins; i += kLT) { sm.cnt[i] = 0; sm.mass[i] = 0; }
+  __syncthreads();
+  unsigned long long nlt = 0;   // candidates with !(prob < thr), src/sampler.ts:96
+  large_pass(L, [&](int, float v) {
+    const uint32_t key = f2key(v);
+    if (key != 0u && key > L.T) {
+      const float pr = large_prob(L, v);
+      const uint32_t b = (key - L.lo) >> L.s1;
+      atomicAdd(&sm.cnt[b], 1u);
+      atomicAdd(&sm.mass[b], (double)pr);
+      nlt += !((double)pr < thr);
+    }
+  });
+  nlt = block_sum_u64(nlt, sm);
+  if (L.T) {
+    const float pt = large_prob(L, key2f(L.T));
+    if (tid == 0) {
+      sm.cnt[0] += (uint32_t)L.tin;   // T is the lowest candidate key: bucket 0
+      sm.mass[0] += (double)L.tin * (double)pt;
+    }
+    nlt += !((double)pt < thr) ? (unsigned long long)L.tin : 0ull;
+  }
+  __syncthreads();
+
+  // 4. src/sampler.ts:93-105: min-p stop f1, top-p stop f2
+  int f1 = 1 + (int)nlt - (!((double)prob0 < thr) ? 1 : 0);
+  f1 = f1 < 1 ? 1 : (f1 > n ? n : f1);
+  int f2 = n;
+  if (P.top_p <= 0.0) {
+    f2 = 0;   // cumProb >= topP at the first index
+  } else {
+    const LargeLoc ltop = large_locate(L, kByMass, P.top_p, 0u, sm);
+    if (ltop.found) f2 = ltop.pos;
+  }
+  int cut = f1 <= f2 ? f1 : f2 + 1;
+  cut = cut > n ? n : cut;
+  // src/sampler.ts:107-116: keptSum = cumProb at cutoff - 1, then the draw
+  const LargeLoc lkept = large_locate(L, kByPos, 0.0, (uint32_t)(cut - 1), sm);
+  const double target = a.uniforms[row] * lkept.cum;
+  LargeLoc lpick = large_locate(L, kByMass, target, 0u, sm);
+  if (!lpick.found || lpick.pos >= cut) lpick = lkept;
+  if (!(target > 0.0) && target == target) {
+    // r = u * keptSum <= 0: the first subtraction already ends the walk
+    lpick = large_locate(L, kByPos, 0.0, 0u, sm);
+  }
+  const bool ambiguous = L.T != 0u && lpick.tie;   // slot history orders equal values
+  uint32_t flags = HS_ROW_LARGE;
+  if (ambiguous) flags |= HS_ROW_UNSUPPORTED | HS_ROW_TIES;
+  if (tid == 0) {
+    a.tokens[row] = ambiguous ? -1 : lpick.id;
+    if (a.cand_count_out) a.cand_count_out[row] = n;
+    if (a.cutoff_out) a.cutoff_out[row] = cut;
+  }
+
+  // candidate outputs: the first min(n, cand_stride) positions.  The values
+  // above the last position's value are gathered and sorted; the last value's
+  // group fills the rest in index order.
+  if (cs > 0 && (a.cand_ids || a.cand_probs)) {
+    const int mo = n < cs ? n : cs;
+    const LargeLoc lend = large_locate(L, kByPos, 0.0, (uint32_t)(mo - 1), sm);
+    const uint32_t kend = lend.key;
+    large_gather(L, kend + 1u, L.hi, sm);   // kend < hi or nothing lies above
+    int nb = kend < L.hi ? sm.nbuf : 0;     // < mo: they precede position mo - 1
+    const bool too_long = nb > kLCap;       // a list longer than LDS sorts
+    if (too_long) {
+      flags |= HS_ROW_UNSUPPORTED;
+      nb = 0;
+    }
+    int P2 = 1;
+    while (P2 < nb) P2 <<= 1;
+    for (int i = nb + tid; i < P2; i += kLT) sm.buf[i] = 0ull;
+    __syncthreads();
+    block_sort_desc<kLT>(sm.buf, P2);
+    int tie = 0;
+    for (int i = tid; i < nb; i += kLT) {
+      const unsigned long long c = sm.buf[i];
+      if (a.cand_ids) a.cand_ids[(int64_t)row * cs + i] = (int32_t)cand_idx(c);
+      if (a.cand_probs) a.cand_probs[(int64_t)row * cs + i] = large_prob(L, key2f(cand_key(c)));
+      if (i + 1 < nb && cand_key(sm.buf[i + 1]) == cand_key(c)) tie = 1;
+    }
+    // the group of the last listed value, in index order
+    const int rest = mo - nb;
+    const float pend = large_prob(L, key2f(kend));
+    const int span = (L.V + kLT - 1) / kLT;
+    const int b0 = tid * span, b1 = min(L.V, b0 + span);
+    uint32_t c = 0;
+    if (!too_long)
+      for (int e = b0; e < b1; ++e) c += f2key(L.rowp[e]) == kend;
+    uint32_t ec;
+    double dummy;
+    block_excl_scan2(c, 0.0, &ec, &dummy, sm);
+    for (int e = b0; e < b1 && ec < (uint32_t)rest; ++e) {
+      if (f2key(L.rowp[e]) == kend) {
+        const int i = nb + (int)ec++;
+        if (a.cand_ids) a.cand_ids[(int64_t)row * cs + i] = e;
+        if (a.cand_probs) a.cand_probs[(int64_t)row * cs + i] = pend;
+      }
+    }
+    if (rest > 1 || (kend == L.T && L.teq > L.tin)) tie = 1;
+    if (__syncthreads_or(tie) && L.T) flags |= HS_ROW_UNSUPPORTED | HS_ROW_TIES;
+  }
+  if (tid == 0 && a.row_flags) a.row_flags[row] = flags;
+}
+
 // ---------------------------------------------------------------- launch
 
 hipError_t prepare_kernels() {
@@ -1516,9 +2091,12 @@ hipError_t prepare_kernels() {
   if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&row_kernel<false>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, row_smem)) != hipSuccess)
     return e;
-  return hipFuncSetAttribute(reinterpret_cast<const void *>(&finalize_kernel),
-                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)finalize_smem_bytes());
+  if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&finalize_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)finalize_smem_bytes())) != hipSuccess)
+    return e;
+  return hipFuncSetAttribute(reinterpret_cast<const void *>(&large_kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)large_smem_bytes());
 }
 
 namespace {
@@ -1561,6 +2139,11 @@ hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t s
     if (e != hipSuccess) return e;
     e = launch_one(finalize_kernel, dim3((unsigned)a.n_chunk), dim3(kThreads),
                    finalize_smem_bytes(), stream, ev, 3, a, ws);
+    if (e != hipSuccess) return e;
+  }
+  if (a.n_large > 0) {
+    e = launch_one(large_kernel, dim3((unsigned)a.n_large), dim3(kLT), large_smem_bytes(), stream,
+                   ev, 4, a, ws);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

@@ -56,6 +56,13 @@ typedef struct hs_sample_config {
 #define HS_ROW_REPLAYED     0x2u /* exact replace-min replay was needed (ties) */
 #define HS_ROW_TIES         0x4u /* equal values among or at the candidates */
 #define HS_ROW_SINGLE       0x8u /* 0 or 1 candidate: no draw consumed */
+#define HS_ROW_UNSUPPORTED 0x10u /* top-k > 1024 below the finite count with a group of
+                                    equal values at the drawn position (or in the
+                                    candidate outputs): the reference orders it by
+                                    its slot history, which this build does not
+                                    replay at that size; token is -1 */
+#define HS_ROW_LARGE       0x20u /* top-k > 1024 path: binary64 sums in another order
+                                    than the reference's (probabilities within 1e-5) */
 
 typedef struct hs_context hs_context;
 
@@ -86,7 +93,8 @@ int hs_sample_logits(hs_context *ctx, float *logits, int32_t vocab,
 /* Batched host variant: `rows` rows of `row_stride` floats; row r's history
  * is hist_ids[hist_offsets[r] .. hist_offsets[r+1]) (hist_offsets has rows+1
  * entries; both may be NULL for no history); configs[r], uniforms[r].  Copies
- * in, samples, copies tokens and penalised logits back.  Blocks. */
+ * in, samples, copies tokens and penalised logits back.  Blocks.
+ * HS_ERR_UNSUPPORTED when a row ends with HS_ROW_UNSUPPORTED (see above). */
 int hs_sample_logits_batch(hs_context *ctx, float *logits, int32_t rows,
                            int64_t row_stride, int32_t vocab,
                            const int32_t *hist_ids, const int64_t *hist_offsets,
@@ -98,7 +106,8 @@ int hs_sample_logits_batch(hs_context *ctx, float *logits, int32_t rows,
  * HOST array of `rows` configs (staged to the device by the library, skipped
  * when identical to the previous call's).  Optional device outputs (each may
  * be NULL): the first `cand_stride` sorted candidates per row (ids, normalised
- * probabilities), the candidate count, the kept-prefix length and row flags. */
+ * probabilities), the candidate count, the kept-prefix length and row flags.
+ * A row with HS_ROW_UNSUPPORTED gets token -1. */
 int hs_sample_batch_device(hs_context *ctx, float *d_logits, int32_t rows,
                            int64_t row_stride, int32_t vocab,
                            const int32_t *d_hist_ids,
@@ -123,7 +132,8 @@ int hs_sample_batch_device_ex(hs_context *ctx, float *d_logits, int32_t rows,
  * each of its kernel launches.  hs_context_kernel_times() waits for the
  * recorded calls, writes the summed device milliseconds per kernel
  * (ms[0] presence/frequency pre-pass, ms[1] row kernel, ms[2] chunk kernel,
- * ms[3] finalize; a kernel a call did not launch adds 0) and the number of
+ * ms[3] finalize, ms[4] large-k kernel; a kernel a call did not launch adds 0)
+ * and the number of
  * timed calls, and resets the totals. */
 int hs_context_set_timing(hs_context *ctx, int enable);
 int hs_context_kernel_times(hs_context *ctx, double *ms, int32_t count, int64_t *calls);
