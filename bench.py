@@ -98,6 +98,19 @@ def oracle_parity(wl, tokens: np.ndarray) -> dict:
     return dict(rows=int(eq.size), tokens_equal=int(eq.sum()), boundary_cases=boundary)
 
 
+def load_traffic(workload: str, kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, each scaled by the same counter on a
+    device-to-device copy of known size), or None when there is none."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+        return int(t["traffic_bytes_per_launch"]), os.path.relpath(path, ROOT)
+    except (OSError, ValueError, KeyError):
+        return None, None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -111,6 +124,9 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="end with one device-to-device copy of one input set (the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -189,6 +205,13 @@ def main() -> int:
     # logits and history it streams); the other kernels move only the ids.
     achieved = alg_step / (kavg[dominant] * 1e-3) / 1e9
 
+    if args.copy_probe:
+        d_logits[1 % sets].copy_from(d_logits[0])
+        hip.synchronize()
+        log(f"[bench] copy probe: {d_logits[0].nbytes} bytes device to device")
+
+    traffic, traffic_note = load_traffic(wl.name, dominant)
+
     cpu = None
     if not args.no_cpu:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
@@ -222,7 +245,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_note,
             "kernel_ms": round(kavg[dominant], 5),
             "kernels_ms": {k: round(v, 5) for k, v in kavg.items() if v > 0.0005},
             "ms_per_step_instrumented": round(inst_ms / args.steps, 5),
