@@ -879,15 +879,47 @@ __device__ __forceinline__ void rank_top64(const unsigned long long *cbuf, int n
 }
 
 
+// Inclusive prefix sum of one binary64 value per lane over the wave (DPP row
+// shifts and row broadcasts on both halves of the value).
+__device__ __forceinline__ double wave_scan_incl_f64(double x) {
+  // row_shr:n = 0x110 + n (bound_ctrl: 0 where the source lane is outside the
+  // row), row_bcast:15 = 0x142 into rows 1 and 3, row_bcast:31 = 0x143 into
+  // rows 2 and 3 (other rows keep 0)
+#define HS_DPP_ADD(ctrl, rmask, bc)                                                        \
+  {                                                                                        \
+    const unsigned long long b = (unsigned long long)__double_as_longlong(x);              \
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, ctrl,   \
+                                                               rmask, 0xF, bc);            \
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), \
+                                                               ctrl, rmask, 0xF, bc);      \
+    x += __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));           \
+  }
+  HS_DPP_ADD(0x111, 0xF, true)
+  HS_DPP_ADD(0x112, 0xF, true)
+  HS_DPP_ADD(0x114, 0xF, true)
+  HS_DPP_ADD(0x118, 0xF, true)
+  HS_DPP_ADD(0x142, 0xA, false)
+  HS_DPP_ADD(0x143, 0xC, false)
+#undef HS_DPP_ADD
+  return x;
+}
+
 // Tail of src/sampler.ts:76-117 for n <= 64 candidates held one per lane
-// (value keys `key`, sorted descending), by one wave.  The reference's three
-// sequential binary64 sums (sumProb, cumProb, the draw's r) are reproduced in
-// its order: the terms go through `sp` (64 doubles of LDS) and every lane
-// reads them back by broadcast and runs the chain itself, lane L stopping
-// at index L (later terms are replaced by +0, which leaves a running sum
-// unchanged), so lane L ends with the running value at its own index and
-// the loop exits become ballots.  Returns the picked position (-1 when
-// n == 0) and writes the cutoff and each lane's normalised probability.
+// (value keys `key`, sorted descending), by one wave.
+//   sumProb (src/sampler.ts:82-86) adds unrounded binary64 terms, so it runs
+//   as a sequential chain in the reference's order: the terms go through `sp`
+//   (64 doubles of LDS) and are read back by broadcast.
+//   cumProb and the draw's r (src/sampler.ts:91-116) add and subtract the
+//   binary32 probabilities.  When every probability is 0 or in [2^-29, 1],
+//   each is a multiple of 2^-52, so every partial sum below 2 is exact in
+//   binary64 in any order; then cumProb is a wave prefix sum, and r stays
+//   exactly u*keptSum - cumProb until its sign flips (a rounded difference
+//   keeps the sign of the exact one), so the draw is the first index whose
+//   prefix reaches u*keptSum.  Otherwise the sums run as sequential chains
+//   through `sp` with every lane stopping at its own index (later terms are
+//   replaced by +0, which leaves a running sum unchanged).
+// Returns the picked position (-1 when n == 0) and writes the cutoff and each
+// lane's normalised probability.
 __device__ __forceinline__ int wave_tail(uint32_t key, int n, const RowPlan &P, double u, int *cutoff,
                          float *prob_out, double *sp) {
   const int lane = lane_id();
@@ -903,7 +935,7 @@ __device__ __forceinline__ int wave_tail(uint32_t key, int n, const RowPlan &P, 
   const double inv_temp = 1.0 / P.temperature;
   const double p = lane < n ? exp((v - maxl) * inv_temp) : 0.0;
   sp[lane] = p;   // a wave's LDS accesses complete in order
-  double sum = 0;   // src/sampler.ts:82-86: unrounded p, in order
+  double sum = 0;
   for (int j = 0; j < n8; j += 8) {
 #pragma unroll
     for (int q = 0; q < 8; ++q) sum += sp[j + q];
@@ -911,14 +943,21 @@ __device__ __forceinline__ int wave_tail(uint32_t key, int n, const RowPlan &P, 
   const float prob = (float)((double)(float)p / sum);
   *prob_out = prob;
   const double pd = lane < n ? (double)prob : 0.0;
-  sp[lane] = pd;
-  // src/sampler.ts:91-105: cumProb after index `lane`
+  bool exact = !__ballot(lane < n && !(pd == 0.0 || (pd >= 0x1p-29 && pd <= 1.0)));
   double cum = 0;
-  for (int j = 0; j < n8; j += 8) {
+  if (exact) {
+    cum = wave_scan_incl_f64(pd);
+    exact = readlane_f64(cum, 63) < 2.0;
+  }
+  if (!exact) {
+    sp[lane] = pd;
+    cum = 0;
+    for (int j = 0; j < n8; j += 8) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const double t = sp[j + q];
-      cum += j + q <= lane ? t : 0.0;
+      for (int q = 0; q < 8; ++q) {
+        const double t = sp[j + q];
+        cum += j + q <= lane ? t : 0.0;
+      }
     }
   }
   const double thr = P.min_p * readlane_f64(pd, 0);
@@ -930,17 +969,22 @@ __device__ __forceinline__ int wave_tail(uint32_t key, int n, const RowPlan &P, 
   // keptSum (src/sampler.ts:107-108) adds probs[0, cutoff) from 0 in the
   // same order as cumProb: it equals cumProb at cutoff - 1
   const double kept = readlane_f64(cum, cut - 1);
-  // src/sampler.ts:110-116: r after subtracting index `lane`
-  double r = u * kept;
-  const int c8 = (cut + 7) & ~7;
-  for (int j = 0; j < c8; j += 8) {
+  const double r0 = u * kept;
+  unsigned long long hit;
+  if (exact) {
+    hit = __ballot(lane < cut && cum >= r0);
+  } else {
+    double r = r0;   // r after subtracting index `lane`
+    const int c8 = (cut + 7) & ~7;
+    for (int j = 0; j < c8; j += 8) {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const double t = sp[j + q];
-      r -= j + q <= lane ? t : 0.0;
+      for (int q = 0; q < 8; ++q) {
+        const double t = sp[j + q];
+        r -= j + q <= lane ? t : 0.0;
+      }
     }
+    hit = __ballot(lane < cut && r <= 0);
   }
-  const unsigned long long hit = __ballot(lane < cut && r <= 0);
   *cutoff = cut;
   return hit ? (int)__ffsll((long long)hit) - 1 : cut - 1;
 }

@@ -132,7 +132,12 @@ def test_option_edge_values(any_sampler):
              (row, [], dict(temperature=1e-6, topK=40), 0.8),
              (row, [], dict(temperature=1e6, topK=40, topP=0.5), 0.8),
              (row, [], dict(temperature=-1.0), 0.8),
-             (row, [], dict(temperature=0.7, topK=40, topP=0.9), 0.0)]
+             (row, [], dict(temperature=0.7, topK=40, topP=0.9), 0.0),
+             # probabilities below 2^-29 among the candidates: the tail's
+             # cumulative sums take the sequential path
+             (row, [], dict(temperature=0.1, topK=60, topP=1.0), 0.9999999),
+             (row, [], dict(temperature=0.12, topK=64, topP=0.9999999), 0.999),
+             (row, [], dict(temperature=0.09, topK=64, topP=1.0, minP=1e-12), 0.5)]
     _run(any_sampler, cases, V)
 
 
