@@ -6,12 +6,15 @@
 
 namespace hs {
 
-// ---- row kernel: one 1024-thread workgroup streams a whole row in rounds of
-// 8 float4 per thread (32768 logits), two rounds in registers at a time.
+// ---- row kernel: one 1024-thread workgroup streams a whole row: round 0 of
+// 6 float4 per thread (24576 logits), then rounds of 8 float4 per thread
+// (32768 logits), two rounds in flight at a time.
 constexpr int kRowThreads = 1024;
 constexpr int kRowWaves = kRowThreads / 64;
-constexpr int kRowNV = 8;                        // float4 per thread per round
-constexpr int kRoundF4 = kRowThreads * kRowNV;   // float4 per round
+constexpr int kR0NV = 6;                         // float4 per thread in round 0
+constexpr int kR0F4 = kRowThreads * kR0NV;       // float4 of round 0
+constexpr int kRowNV = 8;                        // float4 per thread per later round
+constexpr int kRoundF4 = kRowThreads * kRowNV;   // float4 per later round
 constexpr int kRowCandCap = 4096;                // streamed candidates per row
 constexpr int kRowMaxVocab = 1 << 19;            // LDS bitmap limit (64 KiB)
 

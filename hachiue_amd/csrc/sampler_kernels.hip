@@ -613,52 +613,86 @@ __device__ int select_into(int n_ent, GetEnt get, uint32_t lo, int k, unsigned l
 
 // ---------------------------------------------------------------- row kernel
 
-// A row is read in rounds: in round r thread t holds the float4s
-// r * kRoundF4 + t + j * kRowThreads (j < kRowNV), so every wave reads 1 KiB
-// contiguous per load instruction and all waves finish a round together.
-// Two rounds are in registers at once: the next round's loads are in flight
-// while the current one is examined.
+// A row is read in rounds.  Round 0 holds kR0NV float4 per thread (24576
+// logits); every later round kRowNV (32768 logits).  In a round whose first
+// float4 is fb, thread t holds the float4s fb + t + j * kRowThreads, so every
+// wave reads 1 KiB contiguous per load instruction and all waves finish a
+// round together.  Round 0 is small so that the bound it fixes is ready
+// early, while rounds 1 and 2 are both in flight.
 
-// One round into registers; NaN past the vocabulary (never a candidate).
-template <bool VEC>
-__device__ __forceinline__ void load_round(float (&v)[kRowNV][4], const float *rowp, int r,
-                                           int V, int tid) {
-  const int f0 = r * kRoundF4 + tid;
-  const int nfull = V >> 2;   // float4 wholly inside the row
-  const f32x4 *p4 = reinterpret_cast<const f32x4 *>(rowp);
-  if (VEC && (r + 1) * kRoundF4 <= nfull) {
+__device__ __forceinline__ int round_base(int r) {
+  return r == 0 ? 0 : kR0F4 + (r - 1) * kRoundF4;
+}
+
+__device__ __forceinline__ int row_rounds(int V) {
+  const int nf4 = (V + 3) >> 2;
+  return nf4 <= kR0F4 ? 1 : 1 + (nf4 - kR0F4 + kRoundF4 - 1) / kRoundF4;
+}
+
+__device__ __forceinline__ int slot_elem(int fb, int tid, int j) {
+  return 4 * (fb + tid + j * kRowThreads);
+}
+
+// Row reads go through buffer resources.  A read at or past a resource's
+// num_records returns 0 and touches no memory, so no read of the row needs a
+// branch around it, and the compiler counts the reads in flight exactly: a
+// round is waited for only when it is used, never at a barrier or a branch.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kReadNT = 2;   // cache policy of a streamed read: nt
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)bytes, 0x00020000);
+}
+
+// The row as the rounds read it.  With VEC (16-byte aligned rows) x4 covers
+// the lim = 4 * floor(V / 4) logits of whole float4s, and the fewer than four
+// past them (the tail) are read apart; without VEC the rounds read the row by
+// element through x1 and lim = V.
+struct RowSrc {
+  rsrc_t x4, x1;
+  int lim;
+};
+
+// One round into registers.  Slots past lim read as 0 here; clip_rd turns
+// them into NaN (never a candidate) once the round has arrived.
+template <int NV, bool VEC>
+__device__ __forceinline__ void load_rd(float (&v)[NV][4], const RowSrc &src, int fb, int tid) {
 #pragma unroll
-    for (int j = 0; j < kRowNV; ++j) {
-      const f32x4 t = __builtin_nontemporal_load(p4 + f0 + j * kRowThreads);
-      v[j][0] = t[0]; v[j][1] = t[1]; v[j][2] = t[2]; v[j][3] = t[3];
-    }
-    return;
-  }
+  for (int j = 0; j < NV; ++j) {
+    const int f = fb + tid + j * kRowThreads;
+    if (VEC) {
+      const auto t = __builtin_amdgcn_raw_buffer_load_b128(src.x4, f * 16, 0, kReadNT);
 #pragma unroll
-  for (int j = 0; j < kRowNV; ++j) {
-    const int f = f0 + j * kRowThreads;
-    if (VEC && f < nfull) {
-      const f32x4 t = __builtin_nontemporal_load(p4 + f);
-      v[j][0] = t[0]; v[j][1] = t[1]; v[j][2] = t[2]; v[j][3] = t[3];
+      for (int q = 0; q < 4; ++q) v[j][q] = __uint_as_float(t[q]);
     } else {
-      const int e = 4 * f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) v[j][q] = (e + q < V) ? rowp[e + q] : __builtin_nanf("");
+      for (int q = 0; q < 4; ++q)
+        v[j][q] = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(src.x1, (4 * f + q) * 4, 0, kReadNT));
     }
   }
 }
 
-__device__ __forceinline__ int round_elem(int r, int tid, int j) {
-  return 4 * (r * kRoundF4 + tid + j * kRowThreads);
+template <int NV>
+__device__ __forceinline__ void clip_rd(float (&v)[NV][4], int fb, int tid, int lim) {
+  if (4 * (fb + NV * kRowThreads) <= lim) return;   // uniform: only a round reaching past lim
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int e = slot_elem(fb, tid, j);
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (e + q >= lim) v[j][q] = __builtin_nanf("");
+  }
 }
 
 // Logits whose id is in the repetition set (bitmap) leave the stream: their
 // penalised values join the selection separately.
-__device__ __forceinline__ void mask_penalised(float (&v)[kRowNV][4], int r, int tid, int V,
+template <int NV>
+__device__ __forceinline__ void mask_penalised(float (&v)[NV][4], int fb, int tid, int V,
                                                const uint32_t *bitmap) {
 #pragma unroll
-  for (int j = 0; j < kRowNV; ++j) {
-    const int e = round_elem(r, tid, j);
+  for (int j = 0; j < NV; ++j) {
+    const int e = slot_elem(fb, tid, j);
     if (e < V) {
       const uint32_t bits = (bitmap[e >> 5] >> (e & 31)) & 0xFu;
 #pragma unroll
@@ -670,18 +704,18 @@ __device__ __forceinline__ void mask_penalised(float (&v)[kRowNV][4], int r, int
 
 // Appends every logit of the round at or above xf (and, with REP, outside the
 // repetition set) to cbuf: one LDS reservation per non-empty ballot.
-template <bool REP>
-__device__ __forceinline__ void append_round(const float (&v)[kRowNV][4], int r, int tid, float xf,
-                                             const uint32_t *bitmap, unsigned long long *cbuf,
-                                             int *n_c) {
+template <int NV, bool REP>
+__device__ __forceinline__ void append_rd(const float (&v)[NV][4], int fb, int tid, float xf,
+                                          const uint32_t *bitmap, unsigned long long *cbuf,
+                                          int *n_c) {
   const int lane = tid & 63;
 #pragma unroll
-  for (int j = 0; j < kRowNV; ++j) {
+  for (int j = 0; j < NV; ++j) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       bool pass = v[j][q] >= xf;
       if (__ballot(pass)) {
-        const int e = round_elem(r, tid, j) + q;
+        const int e = slot_elem(fb, tid, j) + q;
         if (REP && pass) pass = !((bitmap[e >> 5] >> (e & 31)) & 1u);
         const unsigned long long b = __ballot(pass);
         if (b) {
@@ -698,11 +732,12 @@ __device__ __forceinline__ void append_round(const float (&v)[kRowNV][4], int r,
 }
 
 // Packed maximum (value, then lowest index) of a round, folded into `best`.
-__device__ __forceinline__ unsigned long long greedy_round(const float (&v)[kRowNV][4], int r,
-                                                           int tid, unsigned long long best) {
+template <int NV>
+__device__ __forceinline__ unsigned long long greedy_rd(const float (&v)[NV][4], int fb, int tid,
+                                                        unsigned long long best) {
 #pragma unroll
-  for (int j = 0; j < kRowNV; ++j) {
-    const int e = round_elem(r, tid, j);
+  for (int j = 0; j < NV; ++j) {
+    const int e = slot_elem(fb, tid, j);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const uint32_t key = f2key(v[j][q]);
@@ -713,10 +748,11 @@ __device__ __forceinline__ unsigned long long greedy_round(const float (&v)[kRow
   return best;
 }
 
-__device__ __forceinline__ float round_max(const float (&v)[kRowNV][4]) {
+template <int NV>
+__device__ __forceinline__ float rd_max(const float (&v)[NV][4]) {
   float m = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < kRowNV; ++j)
+  for (int j = 0; j < NV; ++j)
 #pragma unroll
     for (int q = 0; q < 4; ++q) m = fmaxf(m, v[j][q]);   // NaN is ignored
   return m;
@@ -847,6 +883,27 @@ __device__ __forceinline__ uint32_t wave_refine(unsigned long long *cbuf, int n,
   }
   *kept = m;
   return T;
+}
+
+// A bound from a snapshot of the candidate list, by one wave while the other
+// waves keep appending: the exact k-th largest of the keys of cbuf[0, n)
+// (n <= 256), where an entry reserved but not yet written reads as key 0.
+// Only the key word of each entry is read, so an entry is either absent or
+// whole.  A result above lo has at least k written keys at or above it.
+__device__ __forceinline__ uint32_t wave_snapshot_bound(const unsigned long long *cbuf, int n,
+                                                        int k, uint32_t lo) {
+  const int lane = lane_id();
+  const uint32_t *words = reinterpret_cast<const uint32_t *>(cbuf);
+  uint32_t key[4], hi = 0;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int i = lane + 64 * s;
+    key[s] = i < n ? __atomic_load_n(words + 2 * i + 1, __ATOMIC_RELAXED) : 0u;
+    hi = key[s] > hi ? key[s] : hi;
+  }
+  hi = wave_max_u32(hi);
+  if (hi <= lo) return lo;
+  return wave_search<4>(key, 4, k, lo ? lo : 1u, hi);
 }
 
 // Sorted top-64 of n distinct packed candidates cbuf[0, n) (n <= kRowThreads)
@@ -1066,7 +1123,8 @@ struct RowSmem {
   TailSmem tail;
   unsigned long long best[kRowWaves];
   uint32_t t_min, theta, key64;
-  int32_t n_c, n_l;
+  uint32_t theta2;   // refined bound, published by wave 0 mid-row
+  int32_t n_c, n_l, n_f;
 };
 
 template <bool VEC>
@@ -1085,24 +1143,40 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   const int row = a.rows_direct ? (int)blockIdx.x : ws.row_list[blockIdx.x];
   float *rowp = a.logits + (int64_t)row * a.stride;
   const int V = a.vocab;
-  const int nr = (V + 4 * kRoundF4 - 1) / (4 * kRoundF4);   // rounds
+  const int nr = row_rounds(V);
 
-  // The last <= 128 history ids (one per thread of waves 0-1) are requested
-  // before the stream: a wave's vector loads complete in order, so a request
-  // queued behind two rounds would wait for both.
-  int hid = -1;
-  if (a.hist_off && wave < 2) {
+  // The last <= 128 history ids, one per thread of waves 0-1, are requested
+  // before the stream: a wave's reads complete in order.  Threads past them
+  // read outside the resource (0, no memory touched).
+  const int32_t *hist_p = a.hist_ids;
+  int hist_n = 0;
+  if (a.hist_off) {
     const int64_t h0 = load_scalar(a.hist_off + row);
     const int64_t hl = load_scalar(a.hist_off + row + 1) - h0;
-    const int64_t last = hl < 128 ? hl : 128;   // history.slice(-128)
-    if (tid < last) hid = a.hist_ids[h0 + hl - last + tid];
+    hist_n = (int)(hl < 128 ? hl : 128);   // history.slice(-128)
+    hist_p = a.hist_ids + (h0 + hl - hist_n);
   }
-  __builtin_amdgcn_sched_barrier(0);
-  // Round 0 alone goes out first (32768 logits per row, enough to keep HBM
-  // busy); round 1 follows as soon as round 0 has arrived, so the bound
-  // below is computed while round 1 streams.
-  float va[kRowNV][4], vb[kRowNV][4];
-  load_round<VEC>(va, rowp, 0, V, tid);
+  const int hraw = (int)__builtin_amdgcn_raw_buffer_load_b32(make_rsrc(hist_p, 4u * hist_n),
+                                                             tid * 4, 0, 0);
+  RowSrc src;
+  src.lim = VEC ? (V & ~3) : V;
+  src.x4 = make_rsrc(rowp, 4u * (uint32_t)(V & ~3));
+  src.x1 = make_rsrc(rowp, 4u * (uint32_t)V);
+  // rounds 0 and 1 go out together; round 2 follows as soon as round 0 has
+  // arrived, so the bound below is computed while rounds 1 and 2 stream
+  float v0[kR0NV][4], va[kRowNV][4], vb[kRowNV][4];
+  load_rd<kR0NV, VEC>(v0, src, 0, tid);
+  load_rd<kRowNV, VEC>(vb, src, round_base(1), tid);   // past the row when nr == 1
+  // the logits past the last whole float4 (VEC only), read by thread 0
+  float tl[3] = {0.f, 0.f, 0.f};
+  if (VEC) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int e = src.lim + q;
+      tl[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          src.x1, (tid == 0 && e < V ? e : V) * 4, 0, 0));
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
 
   // the row's plan through the scalar cache, which does not queue behind
@@ -1115,46 +1189,50 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   const double temperature = load_scalar(&plan->temperature);
   const double top_p = load_scalar(&plan->top_p), min_p = load_scalar(&plan->min_p);
   const double u = load_scalar(a.uniforms + row);
+
   const bool greedy = mode == kModeGreedy;
   // presence / frequency rows were penalised in place by pen_kernel
   const bool rep = (penbits & kPenRep) && !(penbits & kPenPF);
   if (tid == 0) {
-    rs.t_min = 0xFFFFFFFFu; rs.theta = 0; rs.key64 = 0;
-    rs.n_c = 0; rs.n_l = 0;
+    rs.t_min = 0xFFFFFFFFu; rs.theta = 0; rs.theta2 = 0; rs.key64 = 0;
+    rs.n_c = 0; rs.n_l = 0; rs.n_f = 0;
   }
   if (tid < 64) top[tid] = 0ull;
+  // the mid-row snapshot reads entries not yet written as 0 (no candidate)
+  if (!greedy && tid < 256) cbuf[tid] = 0ull;
 
   // src/sampler.ts:24-33: the distinct ids of the last 128 history entries.
   // Their logits leave the stream (bitmap); the thread holding the first
   // occurrence of an id keeps its raw logit for the end of the row.
   int pid = -1;
-  float pval = 0.f;
   if (rep) {
     const int words = (V + 31) >> 5;
     for (int i = tid; i < words; i += kRowThreads) bitmap[i] = 0;
     __syncthreads();
+    const int hid = tid < hist_n ? hraw : -1;
     if (hid >= 0 && hid < V) {
       const uint32_t bit = 1u << (hid & 31);
-      if (!(atomicOr(&bitmap[hid >> 5], bit) & bit)) {   // the first occurrence owns the id
-        pid = hid;
-        pval = rowp[hid];   // used after the stream: its latency hides behind it
-      }
+      if (!(atomicOr(&bitmap[hid >> 5], bit) & bit)) pid = hid;   // the first occurrence owns the id
     }
   }
-  __syncthreads();   // bitmap complete
+  // the owner's raw logit, used after the stream (its latency hides behind it)
+  const float pval =
+      __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(src.x1, (pid >= 0 ? pid : V) * 4, 0, 0));
+  __syncthreads();   // bitmap complete, LDS cleared
 
   // ---- round 0 fixes the bound: theta = the exact k-th largest of the 1024
   // lane maxima (each a distinct logit outside the repetition set), a lower
   // bound of the row's k-th largest value
-  if (rep) mask_penalised(va, 0, tid, V, bitmap);
+  clip_rd<kR0NV>(v0, 0, tid, src.lim);
+  if (rep) mask_penalised<kR0NV>(v0, 0, tid, V, bitmap);
   unsigned long long best = 0;   // greedy: packed maximum
   uint32_t key = 0;              // lane maximum of round 0
   if (greedy)
-    best = greedy_round(va, 0, tid, best);
+    best = greedy_rd<kR0NV>(v0, 0, tid, best);
   else
-    key = f2key(round_max(va));
+    key = f2key(rd_max<kR0NV>(v0));
   __builtin_amdgcn_sched_barrier(0);
-  if (nr > 1) load_round<VEC>(vb, rowp, 1, V, tid);
+  load_rd<kRowNV, VEC>(va, src, round_base(2), tid);
   __builtin_amdgcn_sched_barrier(0);
   float xf = -FLT_MAX;
   uint32_t theta = 0;
@@ -1183,45 +1261,49 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     __syncthreads();
     theta = (uint32_t)uniform_i32((int)rs.theta);
     xf = key_floor(theta ? theta : 1u);
-    append_round<false>(va, 0, tid, xf, bitmap, cbuf, &rs.n_c);
+    append_rd<kR0NV, false>(v0, 0, tid, xf, bitmap, cbuf, &rs.n_c);   // masked already
   }
 
-  // ---- rounds >= 1: candidates are rare
+  // ---- rounds >= 1: candidates are rare.  vb holds the odd rounds, va the
+  // even ones.
   for (int r = 1; r < nr; r += 2) {
-    if (r + 1 < nr) load_round<VEC>(va, rowp, r + 1, V, tid);
-    if (r == 3 && !greedy && r + 1 < nr) {
-      // Rounds 3 and 4 are in flight: tighten the bound to the exact k-th
-      // largest of the candidates of rounds 0-2 and drop those below it.
-      __syncthreads();
-      const int n1 = uniform_i32(rs.n_c);
-      if (wave == 0 && n1 >= k && n1 <= 256) {
-        int m = 0;
-        const uint32_t t2 = n1 <= 128 ? wave_refine<2>(cbuf, n1, k, theta, &m)
-                                      : wave_refine<4>(cbuf, n1, k, theta, &m);
-        if (lane == 0) { rs.theta = t2; rs.n_c = m; }
+    if (!greedy) {
+      if (r == 3 && wave == 0) {
+        // Wave 0 alone tightens the bound to the exact k-th largest of the
+        // candidates appended so far (entries reserved but not yet written
+        // read as 0 and do not count); the other waves pick it up at their
+        // next round.  Any k appended logits bound the row's k-th largest.
+        const int n1 = uniform_i32(__atomic_load_n(&rs.n_c, __ATOMIC_RELAXED));
+        if (n1 >= k && n1 <= 256) {
+          const uint32_t t2 = wave_snapshot_bound(cbuf, n1, k, theta);
+          if (lane == 0 && t2 > theta) __atomic_store_n(&rs.theta2, t2, __ATOMIC_RELAXED);
+        }
       }
-      __syncthreads();
-      theta = (uint32_t)uniform_i32((int)rs.theta);
-      xf = key_floor(theta ? theta : 1u);
+      const uint32_t t2 =
+          (uint32_t)uniform_i32((int)__atomic_load_n(&rs.theta2, __ATOMIC_RELAXED));
+      if (t2 > theta) { theta = t2; xf = key_floor(theta); }
     }
+    clip_rd<kRowNV>(vb, round_base(r), tid, src.lim);
     if (greedy) {
-      if (rep) mask_penalised(vb, r, tid, V, bitmap);
-      best = greedy_round(vb, r, tid, best);
+      if (rep) mask_penalised<kRowNV>(vb, round_base(r), tid, V, bitmap);
+      best = greedy_rd<kRowNV>(vb, round_base(r), tid, best);
     } else if (rep) {
-      append_round<true>(vb, r, tid, xf, bitmap, cbuf, &rs.n_c);
+      append_rd<kRowNV, true>(vb, round_base(r), tid, xf, bitmap, cbuf, &rs.n_c);
     } else {
-      append_round<false>(vb, r, tid, xf, bitmap, cbuf, &rs.n_c);
+      append_rd<kRowNV, false>(vb, round_base(r), tid, xf, bitmap, cbuf, &rs.n_c);
     }
+    load_rd<kRowNV, VEC>(vb, src, round_base(r + 2), tid);   // past the row near its end
     if (r + 1 >= nr) break;
-    if (r + 2 < nr) load_round<VEC>(vb, rowp, r + 2, V, tid);
+    clip_rd<kRowNV>(va, round_base(r + 1), tid, src.lim);
     if (greedy) {
-      if (rep) mask_penalised(va, r + 1, tid, V, bitmap);
-      best = greedy_round(va, r + 1, tid, best);
+      if (rep) mask_penalised<kRowNV>(va, round_base(r + 1), tid, V, bitmap);
+      best = greedy_rd<kRowNV>(va, round_base(r + 1), tid, best);
     } else if (rep) {
-      append_round<true>(va, r + 1, tid, xf, bitmap, cbuf, &rs.n_c);
+      append_rd<kRowNV, true>(va, round_base(r + 1), tid, xf, bitmap, cbuf, &rs.n_c);
     } else {
-      append_round<false>(va, r + 1, tid, xf, bitmap, cbuf, &rs.n_c);
+      append_rd<kRowNV, false>(va, round_base(r + 1), tid, xf, bitmap, cbuf, &rs.n_c);
     }
+    load_rd<kRowNV, VEC>(va, src, round_base(r + 3), tid);
   }
 
   __syncthreads();   // every read of the row is done
@@ -1235,10 +1317,24 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     rowp[pid] = pv;
   }
 
+  // the tail logits (thread 0) outside the repetition set
+  bool tail_ok[3];
+#pragma unroll
+  for (int q = 0; q < 3; ++q) {
+    const int e = src.lim + q;
+    tail_ok[q] = VEC && tid == 0 && e < V && !(rep && ((bitmap[e >> 5] >> (e & 31)) & 1u));
+  }
+
   if (greedy) {
     if (pid >= 0) {
       const uint32_t key = f2key(pv);
       const unsigned long long c = key ? pack_cand(key, (uint32_t)pid) : 0ull;
+      best = c > best ? c : best;
+    }
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const uint32_t key = tail_ok[q] ? f2key(tl[q]) : 0u;
+      const unsigned long long c = key ? pack_cand(key, (uint32_t)(src.lim + q)) : 0ull;
       best = c > best ? c : best;
     }
     best = wave_max64(best);
@@ -1252,8 +1348,12 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     return;
   }
 
-  {
-    const bool pass = pid >= 0 && pv >= xf;
+  // the final bound: the round-0 bound or the refined one (pv and the list
+  // entries below it cannot be in the top k)
+  theta = (uint32_t)uniform_i32((int)rs.theta2) > theta ? (uint32_t)uniform_i32((int)rs.theta2)
+                                                         : theta;
+  xf = key_floor(theta ? theta : 1u);
+  auto join = [&](bool pass, float v, int id) {
     const unsigned long long b = __ballot(pass);
     if (b) {
       const int leader = __ffsll((long long)b) - 1;
@@ -1261,16 +1361,39 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
       if (lane == leader) bp = atomicAdd(&rs.n_c, __popcll(b));
       bp = __shfl(bp, leader);
       const int p = bp + (int)lanes_below(b);
-      if (pass && p < kRowCandCap) cbuf[p] = pack_cand(f2key(pv), (uint32_t)pid);
+      if (pass && p < kRowCandCap) cbuf[p] = pack_cand(f2key(v), (uint32_t)id);
+    }
+  };
+  join(pid >= 0 && pv >= xf, pv, pid);
+  if (VEC && src.lim < V) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) join(tail_ok[q] && tl[q] >= xf, tl[q], src.lim + q);
+  }
+  __syncthreads();
+  const int n_c = rs.n_c;
+  bool overflow = n_c > kRowCandCap;
+  // keep the entries at or above the final bound (in srt)
+  if (!overflow) {
+    for (int i = tid; i < n_c; i += kRowThreads) {
+      const unsigned long long c = cbuf[i];
+      const bool pass = cand_key(c) >= (theta ? theta : 1u);
+      const unsigned long long b = __ballot(pass);
+      if (b) {
+        const int leader = __ffsll((long long)b) - 1;
+        int bp = 0;
+        if (lane == leader) bp = atomicAdd(&rs.n_f, __popcll(b));
+        bp = __shfl(bp, leader);
+        const int p = bp + (int)lanes_below(b);
+        if (pass && p < kSortCap) srt[p] = c;
+      }
     }
   }
   __syncthreads();
-  const int n_all = rs.n_c;
-  bool overflow = n_all > kRowCandCap;
+  const int n_all = rs.n_f;
   unsigned long long F = 0;
   bool extra = false;
   if (!overflow && n_all <= kRowThreads) {
-    rank_top64(cbuf, n_all, top, &rs.key64);
+    rank_top64(srt, n_all, top, &rs.key64);
     if (wave != 0) return;
     F = top[lane];
     const uint32_t Tk = cand_key(__shfl(F, k - 1));
@@ -1279,7 +1402,7 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     // rare: many candidates reach the bound (ties); select block-wide first
     uint32_t T = 0;
     const int n_sel = select_into<kRowThreads>(
-        n_all, [&](int p) { return cbuf[p]; }, 0u, k, srt, rs.sel, rs.tail, &T);
+        n_c, [&](int p) { return cbuf[p]; }, theta ? theta : 1u, k, srt, rs.sel, rs.tail, &T);
     if (n_sel < 0) overflow = true;
     if (wave != 0) return;
     if (!overflow) {

@@ -160,8 +160,13 @@ def test_penalty_edges(any_sampler):
     _run(any_sampler, cases, V)
 
 
-@pytest.mark.parametrize("vocab,pad", [(151669, 0), (1001, 3), (4097, 1), (1, 0), (2, 5), (3, 0)])
+@pytest.mark.parametrize("vocab,pad", [(151669, 0), (1001, 3), (4097, 1), (1, 0), (2, 5), (3, 0),
+                                       (151937, 3), (50257, 3), (32003, 1), (6, 2), (7, 1)])
 def test_ragged_vocab_and_stride(any_sampler, vocab, pad):
+    """Rows whose length is not a multiple of four, with 16-byte aligned
+    strides (the last logits lie past the last whole float4) and unaligned
+    ones.  The last logits of some rows are planted as the largest, one of
+    them also in the repetition history."""
     r = _rng(vocab + pad)
     cases = []
     for i in range(3):
@@ -170,4 +175,10 @@ def test_ragged_vocab_and_stride(any_sampler, vocab, pad):
         cases.append((row, hist, dict(temperature=0.8, topK=40, topP=0.95, repetitionPenalty=1.1),
                       float(r.random())))
     cases.append((cases[0][0], [], dict(temperature=0.0), 0.5))
+    top = (r.standard_normal(vocab) * 2).astype(np.float32)
+    top[-3:] = np.float32([9.0, 9.5, 10.0])[-min(3, vocab):]
+    cases.append((top, [], dict(temperature=0.0), 0.5))
+    cases.append((top, [vocab - 1], dict(temperature=1.0, topK=5, topP=1.0,
+                                         repetitionPenalty=1.5), 0.999))
+    cases.append((top, [vocab - 1], dict(temperature=0.0, repetitionPenalty=100.0), 0.5))
     _run(any_sampler, cases, vocab, stride=vocab + pad)
