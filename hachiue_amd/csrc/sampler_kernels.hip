@@ -633,6 +633,8 @@ __device__ __forceinline__ int slot_elem(int fb, int tid, int j) {
   return 4 * (fb + tid + j * kRowThreads);
 }
 
+__device__ __forceinline__ int uniform_i32(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
 // Row reads go through buffer resources.  A read at or past a resource's
 // num_records returns 0 and touches no memory, so no read of the row needs a
 // branch around it, and the compiler counts the reads in flight exactly: a
@@ -702,30 +704,25 @@ __device__ __forceinline__ void mask_penalised(float (&v)[NV][4], int fb, int ti
   }
 }
 
-// Appends every logit of the round at or above xf (and, with REP, outside the
-// repetition set) to cbuf: one LDS reservation per non-empty ballot.
-template <int NV, bool REP>
+// Appends every logit of the round at or above xf to the wave's own segment
+// of the candidate list; cnt (wave-uniform) counts them, also past kSegCap,
+// where they are no longer stored.  No LDS round trip: a position is the
+// count so far plus the lanes below in the ballot.  Logits in the repetition
+// set are appended with their raw values and dropped at the end of the row.
+template <int NV>
 __device__ __forceinline__ void append_rd(const float (&v)[NV][4], int fb, int tid, float xf,
-                                          const uint32_t *bitmap, unsigned long long *cbuf,
-                                          int *n_c) {
-  const int lane = tid & 63;
+                                          unsigned long long *seg, int &cnt) {
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      bool pass = v[j][q] >= xf;
-      if (__ballot(pass)) {
-        const int e = slot_elem(fb, tid, j) + q;
-        if (REP && pass) pass = !((bitmap[e >> 5] >> (e & 31)) & 1u);
-        const unsigned long long b = __ballot(pass);
-        if (b) {
-          const int leader = __ffsll((long long)b) - 1;
-          int bp = 0;
-          if (lane == leader) bp = atomicAdd(n_c, __popcll(b));
-          bp = __shfl(bp, leader);
-          const int p = bp + (int)lanes_below(b);
-          if (pass && p < kRowCandCap) cbuf[p] = pack_cand(f2key(v[j][q]), (uint32_t)e);
-        }
+      const bool pass = v[j][q] >= xf;
+      const unsigned long long b = __ballot(pass);
+      if (b) {
+        const int p = cnt + (int)lanes_below(b);
+        if (pass && p < kSegCap)
+          seg[p] = pack_cand(f2key(v[j][q]), (uint32_t)(slot_elem(fb, tid, j) + q));
+        cnt = uniform_i32(cnt + __popcll(b));
       }
     }
   }
@@ -758,7 +755,6 @@ __device__ __forceinline__ float rd_max(const float (&v)[NV][4]) {
   return m;
 }
 
-__device__ __forceinline__ int uniform_i32(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 // Wave-uniform read of memory the kernel never writes, through the scalar
 // cache (constant address space): it completes independently of the vector
@@ -885,25 +881,46 @@ __device__ __forceinline__ uint32_t wave_refine(unsigned long long *cbuf, int n,
   return T;
 }
 
-// A bound from a snapshot of the candidate list, by one wave while the other
-// waves keep appending: the exact k-th largest of the keys of cbuf[0, n)
-// (n <= 256), where an entry reserved but not yet written reads as key 0.
-// Only the key word of each entry is read, so an entry is either absent or
-// whole.  A result above lo has at least k written keys at or above it.
-__device__ __forceinline__ uint32_t wave_snapshot_bound(const unsigned long long *cbuf, int n,
-                                                        int k, uint32_t lo) {
+// A bound from a snapshot of the candidate segments, by one wave while the
+// other waves keep appending: the exact k-th largest key among the entries
+// published so far (wcnt[w] of segment w, at most 32 each), leaving out the
+// logits of the repetition set.  A wave writes its entries before it
+// publishes their count and a wave's LDS accesses complete in order, so every
+// entry below a published count is whole.  A result above lo has at least k
+// such keys at or above it; lo is returned when the snapshot does not fit.
+__device__ __forceinline__ uint32_t wave_snapshot_bound(const unsigned long long *cbuf,
+                                                        const int32_t *wcnt, int k, uint32_t lo,
+                                                        const uint32_t *bitmap, bool rep) {
   const int lane = lane_id();
-  const uint32_t *words = reinterpret_cast<const uint32_t *>(cbuf);
-  uint32_t key[4], hi = 0;
+  const int c = lane < kRowWaves ? __atomic_load_n(wcnt + lane, __ATOMIC_RELAXED) : 0;
+  int tot = c, cmax = c;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const int i = lane + 64 * s;
-    key[s] = i < n ? __atomic_load_n(words + 2 * i + 1, __ATOMIC_RELAXED) : 0u;
-    hi = key[s] > hi ? key[s] : hi;
+  for (int m = 1; m < kRowWaves; m <<= 1) {
+    tot += __shfl_xor(tot, m);
+    const int o = __shfl_xor(cmax, m);
+    cmax = o > cmax ? o : cmax;
+  }
+  tot = uniform_i32(tot);
+  cmax = uniform_i32(cmax);
+  if (cmax > 32 || tot < k) return lo;
+  const int w = lane & (kRowWaves - 1);
+  const int cw = __shfl(c, w);
+  uint32_t key[8], hi = 0;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const int q = (lane >> 4) + 4 * t;
+    uint32_t kk = 0;
+    if (q < cw) {
+      const unsigned long long e = cbuf[w * kSegCap + q];
+      const uint32_t id = cand_idx(e);
+      kk = (rep && ((bitmap[id >> 5] >> (id & 31)) & 1u)) ? 0u : cand_key(e);
+    }
+    key[t] = kk;
+    hi = kk > hi ? kk : hi;
   }
   hi = wave_max_u32(hi);
   if (hi <= lo) return lo;
-  return wave_search<4>(key, 4, k, lo ? lo : 1u, hi);
+  return wave_search<8>(key, 8, k, lo ? lo : 1u, hi);
 }
 
 // Sorted top-64 of n distinct packed candidates cbuf[0, n) (n <= kRowThreads)
@@ -1114,8 +1131,8 @@ __device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &
 
 size_t row_smem_bytes(int vocab) {
   const size_t words = ((size_t)vocab + 31) / 32;
-  return (size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + 64 * 8 + (size_t)kSmallK * 8 +
-         words * 4;
+  return (size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + 64 * 8 + (size_t)kPenCap * 8 +
+         (size_t)kSmallK * 8 + words * 4;
 }
 
 struct RowSmem {
@@ -1123,8 +1140,9 @@ struct RowSmem {
   TailSmem tail;
   unsigned long long best[kRowWaves];
   uint32_t t_min, theta, key64;
-  uint32_t theta2;   // refined bound, published by wave 0 mid-row
-  int32_t n_c, n_l, n_f;
+  uint32_t theta2;             // refined bound, published by wave 0 mid-row
+  int32_t wcnt[kRowWaves];     // candidates each wave has appended (published)
+  int32_t n_l, n_f, n_p;
 };
 
 template <bool VEC>
@@ -1134,12 +1152,13 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   unsigned long long *srt = cbuf + kRowCandCap;            // kSortCap (fallback select)
   uint32_t *lmax = reinterpret_cast<uint32_t *>(srt);      // round-0 lane maxima (aliases srt)
   unsigned long long *top = srt + kSortCap;                // 64: sorted top of the row
-  float *rsv = reinterpret_cast<float *>(top + 64);        // kSmallK replay slots
+  unsigned long long *pbuf = top + 64;                     // kPenCap: joined at the end
+  float *rsv = reinterpret_cast<float *>(pbuf + kPenCap);  // kSmallK replay slots
   int32_t *rsid = reinterpret_cast<int32_t *>(rsv + kSmallK);
   uint32_t *bitmap = reinterpret_cast<uint32_t *>(rsid + kSmallK);   // ceil(V/32)
   __shared__ RowSmem rs;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform_i32(tid >> 6);
   const int row = a.rows_direct ? (int)blockIdx.x : ws.row_list[blockIdx.x];
   float *rowp = a.logits + (int64_t)row * a.stride;
   const int V = a.vocab;
@@ -1195,11 +1214,16 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   const bool rep = (penbits & kPenRep) && !(penbits & kPenPF);
   if (tid == 0) {
     rs.t_min = 0xFFFFFFFFu; rs.theta = 0; rs.theta2 = 0; rs.key64 = 0;
-    rs.n_c = 0; rs.n_l = 0; rs.n_f = 0;
+    rs.n_l = 0; rs.n_f = 0; rs.n_p = 0;
   }
+  if (tid < kRowWaves) rs.wcnt[tid] = 0;
   if (tid < 64) top[tid] = 0ull;
-  // the mid-row snapshot reads entries not yet written as 0 (no candidate)
-  if (!greedy && tid < 256) cbuf[tid] = 0ull;
+  // this wave's segment of the candidate list and its count (wave-uniform)
+  unsigned long long *seg = cbuf + wave * kSegCap;
+  int cnt = 0;
+  auto publish = [&]() {
+    if (lane == 0) __atomic_store_n(&rs.wcnt[wave], cnt, __ATOMIC_RELAXED);
+  };
 
   // src/sampler.ts:24-33: the distinct ids of the last 128 history entries.
   // Their logits leave the stream (bitmap); the thread holding the first
@@ -1261,7 +1285,8 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     __syncthreads();
     theta = (uint32_t)uniform_i32((int)rs.theta);
     xf = key_floor(theta ? theta : 1u);
-    append_rd<kR0NV, false>(v0, 0, tid, xf, bitmap, cbuf, &rs.n_c);   // masked already
+    append_rd<kR0NV>(v0, 0, tid, xf, seg, cnt);   // masked already
+    publish();
   }
 
   // ---- rounds >= 1: candidates are rare.  vb holds the odd rounds, va the
@@ -1270,14 +1295,11 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     if (!greedy) {
       if (r == 3 && wave == 0) {
         // Wave 0 alone tightens the bound to the exact k-th largest of the
-        // candidates appended so far (entries reserved but not yet written
-        // read as 0 and do not count); the other waves pick it up at their
-        // next round.  Any k appended logits bound the row's k-th largest.
-        const int n1 = uniform_i32(__atomic_load_n(&rs.n_c, __ATOMIC_RELAXED));
-        if (n1 >= k && n1 <= 256) {
-          const uint32_t t2 = wave_snapshot_bound(cbuf, n1, k, theta);
-          if (lane == 0 && t2 > theta) __atomic_store_n(&rs.theta2, t2, __ATOMIC_RELAXED);
-        }
+        // candidates published so far; the other waves pick it up at their
+        // next round.  Any k of the row's logits outside the repetition set
+        // bound its k-th largest.
+        const uint32_t t2 = wave_snapshot_bound(cbuf, rs.wcnt, k, theta, bitmap, rep);
+        if (lane == 0 && t2 > theta) __atomic_store_n(&rs.theta2, t2, __ATOMIC_RELAXED);
       }
       const uint32_t t2 =
           (uint32_t)uniform_i32((int)__atomic_load_n(&rs.theta2, __ATOMIC_RELAXED));
@@ -1287,10 +1309,9 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     if (greedy) {
       if (rep) mask_penalised<kRowNV>(vb, round_base(r), tid, V, bitmap);
       best = greedy_rd<kRowNV>(vb, round_base(r), tid, best);
-    } else if (rep) {
-      append_rd<kRowNV, true>(vb, round_base(r), tid, xf, bitmap, cbuf, &rs.n_c);
     } else {
-      append_rd<kRowNV, false>(vb, round_base(r), tid, xf, bitmap, cbuf, &rs.n_c);
+      append_rd<kRowNV>(vb, round_base(r), tid, xf, seg, cnt);
+      publish();
     }
     load_rd<kRowNV, VEC>(vb, src, round_base(r + 2), tid);   // past the row near its end
     if (r + 1 >= nr) break;
@@ -1298,10 +1319,9 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     if (greedy) {
       if (rep) mask_penalised<kRowNV>(va, round_base(r + 1), tid, V, bitmap);
       best = greedy_rd<kRowNV>(va, round_base(r + 1), tid, best);
-    } else if (rep) {
-      append_rd<kRowNV, true>(va, round_base(r + 1), tid, xf, bitmap, cbuf, &rs.n_c);
     } else {
-      append_rd<kRowNV, false>(va, round_base(r + 1), tid, xf, bitmap, cbuf, &rs.n_c);
+      append_rd<kRowNV>(va, round_base(r + 1), tid, xf, seg, cnt);
+      publish();
     }
     load_rd<kRowNV, VEC>(va, src, round_base(r + 3), tid);
   }
@@ -1353,43 +1373,49 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   theta = (uint32_t)uniform_i32((int)rs.theta2) > theta ? (uint32_t)uniform_i32((int)rs.theta2)
                                                          : theta;
   xf = key_floor(theta ? theta : 1u);
-  auto join = [&](bool pass, float v, int id) {
+  // appends to the list `list` of `cap` entries counted by *n (a ballot per call)
+  auto join = [&](bool pass, unsigned long long c, unsigned long long *list, int32_t *n, int cap) {
     const unsigned long long b = __ballot(pass);
     if (b) {
       const int leader = __ffsll((long long)b) - 1;
       int bp = 0;
-      if (lane == leader) bp = atomicAdd(&rs.n_c, __popcll(b));
+      if (lane == leader) bp = atomicAdd(n, __popcll(b));
       bp = __shfl(bp, leader);
       const int p = bp + (int)lanes_below(b);
-      if (pass && p < kRowCandCap) cbuf[p] = pack_cand(f2key(v), (uint32_t)id);
+      if (pass && p < cap) list[p] = c;
     }
   };
-  join(pid >= 0 && pv >= xf, pv, pid);
+  // the penalised logits and the tail join pbuf (at most 128 + 3 entries)
+  join(pid >= 0 && pv >= xf, pack_cand(f2key(pv), (uint32_t)pid), pbuf, &rs.n_p, kPenCap);
   if (VEC && src.lim < V) {
 #pragma unroll
-    for (int q = 0; q < 3; ++q) join(tail_ok[q] && tl[q] >= xf, tl[q], src.lim + q);
+    for (int q = 0; q < 3; ++q)
+      join(tail_ok[q] && tl[q] >= xf, pack_cand(f2key(tl[q]), (uint32_t)(src.lim + q)), pbuf,
+           &rs.n_p, kPenCap);
   }
   __syncthreads();
-  const int n_c = rs.n_c;
-  bool overflow = n_c > kRowCandCap;
-  // keep the entries at or above the final bound (in srt)
+  // a segment that filled up has lost candidates: replay the row
+  const unsigned long long full = __ballot(lane < kRowWaves && rs.wcnt[lane] > kSegCap);
+  bool overflow = full != 0;
+  // keep the entries at or above the final bound (in srt): each wave its own
+  // segment, leaving out the raw logits of the repetition set; wave 0 also pbuf
+  const uint32_t lo = theta ? theta : 1u;
   if (!overflow) {
-    for (int i = tid; i < n_c; i += kRowThreads) {
-      const unsigned long long c = cbuf[i];
-      const bool pass = cand_key(c) >= (theta ? theta : 1u);
-      const unsigned long long b = __ballot(pass);
-      if (b) {
-        const int leader = __ffsll((long long)b) - 1;
-        int bp = 0;
-        if (lane == leader) bp = atomicAdd(&rs.n_f, __popcll(b));
-        bp = __shfl(bp, leader);
-        const int p = bp + (int)lanes_below(b);
-        if (pass && p < kSortCap) srt[p] = c;
-      }
+    const int n_seg = cnt < kSegCap ? cnt : kSegCap;
+    for (int i = lane; i < n_seg; i += 64) {
+      const unsigned long long c = seg[i];
+      const uint32_t id = cand_idx(c);
+      join(cand_key(c) >= lo && !(rep && ((bitmap[id >> 5] >> (id & 31)) & 1u)), c, srt, &rs.n_f,
+           kSortCap);
+    }
+    if (wave == 0) {
+      const int n_p = rs.n_p < kPenCap ? rs.n_p : kPenCap;
+      for (int i = lane; i < n_p; i += 64) join(cand_key(pbuf[i]) >= lo, pbuf[i], srt, &rs.n_f, kSortCap);
     }
   }
   __syncthreads();
   const int n_all = rs.n_f;
+  overflow = overflow || n_all > kSortCap;
   unsigned long long F = 0;
   bool extra = false;
   if (!overflow && n_all <= kRowThreads) {
@@ -1399,14 +1425,15 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     const uint32_t Tk = cand_key(__shfl(F, k - 1));
     extra = rs.key64 != 0u && rs.key64 == Tk;
   } else if (!overflow) {
-    // rare: many candidates reach the bound (ties); select block-wide first
+    // rare: many candidates reach the bound (ties); select block-wide first,
+    // from srt into cbuf (the segments are no longer needed)
     uint32_t T = 0;
     const int n_sel = select_into<kRowThreads>(
-        n_c, [&](int p) { return cbuf[p]; }, theta ? theta : 1u, k, srt, rs.sel, rs.tail, &T);
+        n_all, [&](int p) { return srt[p]; }, lo, k, cbuf, rs.sel, rs.tail, &T);
     if (n_sel < 0) overflow = true;
     if (wave != 0) return;
     if (!overflow) {
-      F = lane < n_sel ? srt[lane] : 0ull;
+      F = lane < n_sel ? cbuf[lane] : 0ull;
       extra = n_sel > 64;
     }
   } else if (wave != 0) {
