@@ -17,7 +17,6 @@ constexpr int kRowNV = 8;                        // float4 per thread per later 
 constexpr int kRoundF4 = kRowThreads * kRowNV;   // float4 per later round
 constexpr int kRowCandCap = 4096;                // streamed candidates per row
 constexpr int kSegCap = kRowCandCap / kRowWaves; // of them per wave (its own segment)
-constexpr int kPenCap = 256;                     // penalised + tail logits joined at the end
 constexpr int kRowMaxVocab = 1 << 19;            // LDS bitmap limit (64 KiB)
 
 // ---- chunk kernel: 256 threads own CHUNK consecutive logits of a row.

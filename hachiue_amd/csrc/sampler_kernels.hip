@@ -714,6 +714,9 @@ __device__ __forceinline__ void append_rd(const float (&v)[NV][4], int fb, int t
                                           unsigned long long *seg, int &cnt) {
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
+    // one ballot per float4 first: most hold no candidate (NaN is ignored)
+    const float m = fmaxf(fmaxf(v[j][0], v[j][1]), fmaxf(v[j][2], v[j][3]));
+    if (!__ballot(m >= xf)) continue;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const bool pass = v[j][q] >= xf;
@@ -1131,8 +1134,8 @@ __device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &
 
 size_t row_smem_bytes(int vocab) {
   const size_t words = ((size_t)vocab + 31) / 32;
-  return (size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + 64 * 8 + (size_t)kPenCap * 8 +
-         (size_t)kSmallK * 8 + words * 4;
+  return (size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + 64 * 8 + (size_t)kSmallK * 8 +
+         words * 4;
 }
 
 struct RowSmem {
@@ -1142,7 +1145,7 @@ struct RowSmem {
   uint32_t t_min, theta, key64;
   uint32_t theta2;             // refined bound, published by wave 0 mid-row
   int32_t wcnt[kRowWaves];     // candidates each wave has appended (published)
-  int32_t n_l, n_f, n_p;
+  int32_t n_l, n_f, ovf;
 };
 
 template <bool VEC>
@@ -1152,8 +1155,7 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   unsigned long long *srt = cbuf + kRowCandCap;            // kSortCap (fallback select)
   uint32_t *lmax = reinterpret_cast<uint32_t *>(srt);      // round-0 lane maxima (aliases srt)
   unsigned long long *top = srt + kSortCap;                // 64: sorted top of the row
-  unsigned long long *pbuf = top + 64;                     // kPenCap: joined at the end
-  float *rsv = reinterpret_cast<float *>(pbuf + kPenCap);  // kSmallK replay slots
+  float *rsv = reinterpret_cast<float *>(top + 64);        // kSmallK replay slots
   int32_t *rsid = reinterpret_cast<int32_t *>(rsv + kSmallK);
   uint32_t *bitmap = reinterpret_cast<uint32_t *>(rsid + kSmallK);   // ceil(V/32)
   __shared__ RowSmem rs;
@@ -1214,7 +1216,7 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   const bool rep = (penbits & kPenRep) && !(penbits & kPenPF);
   if (tid == 0) {
     rs.t_min = 0xFFFFFFFFu; rs.theta = 0; rs.theta2 = 0; rs.key64 = 0;
-    rs.n_l = 0; rs.n_f = 0; rs.n_p = 0;
+    rs.n_l = 0; rs.n_f = 0; rs.ovf = 0;
   }
   if (tid < kRowWaves) rs.wcnt[tid] = 0;
   if (tid < 64) top[tid] = 0ull;
@@ -1326,8 +1328,9 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     load_rd<kRowNV, VEC>(va, src, round_base(r + 3), tid);
   }
 
-  __syncthreads();   // every read of the row is done
-  // the penalised logits go back in place and join the candidates
+  // The penalised logits go back in place.  No barrier is needed first:
+  // whatever a wave still streaming reads at these ids is left out (masked,
+  // or dropped with the repetition set at the end).
   float pv = 0.f;
   if (pid >= 0) {
     RowPlan pr;
@@ -1368,54 +1371,47 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     return;
   }
 
-  // the final bound: the round-0 bound or the refined one (pv and the list
-  // entries below it cannot be in the top k)
-  theta = (uint32_t)uniform_i32((int)rs.theta2) > theta ? (uint32_t)uniform_i32((int)rs.theta2)
-                                                         : theta;
-  xf = key_floor(theta ? theta : 1u);
-  // appends to the list `list` of `cap` entries counted by *n (a ballot per call)
-  auto join = [&](bool pass, unsigned long long c, unsigned long long *list, int32_t *n, int cap) {
+  // As soon as its stream ends, each wave moves into srt the entries of its
+  // segment at or above its bound (the refined one once it has seen it),
+  // leaving out the raw logits of the repetition set, and its penalised and
+  // tail logits at or above the bound.  Every wave's bound is a lower bound
+  // of the row's k-th largest, so srt holds every logit at or above the
+  // largest of them: the row's top k and all logits equal to the k-th.
+  {
+    const uint32_t t2 = (uint32_t)uniform_i32((int)__atomic_load_n(&rs.theta2, __ATOMIC_RELAXED));
+    if (t2 > theta) theta = t2;
+  }
+  const uint32_t lo = theta ? theta : 1u;
+  xf = key_floor(lo);
+  auto join = [&](bool pass, unsigned long long c) {
     const unsigned long long b = __ballot(pass);
     if (b) {
       const int leader = __ffsll((long long)b) - 1;
       int bp = 0;
-      if (lane == leader) bp = atomicAdd(n, __popcll(b));
+      if (lane == leader) bp = atomicAdd(&rs.n_f, __popcll(b));
       bp = __shfl(bp, leader);
       const int p = bp + (int)lanes_below(b);
-      if (pass && p < cap) list[p] = c;
+      if (pass && p < kSortCap) srt[p] = c;
     }
   };
-  // the penalised logits and the tail join pbuf (at most 128 + 3 entries)
-  join(pid >= 0 && pv >= xf, pack_cand(f2key(pv), (uint32_t)pid), pbuf, &rs.n_p, kPenCap);
+  if (cnt > kSegCap) {   // the segment filled up and lost candidates: replay the row
+    if (lane == 0) rs.ovf = 1;
+  } else {
+    for (int i = lane; i < cnt; i += 64) {
+      const unsigned long long c = seg[i];
+      const uint32_t id = cand_idx(c);
+      join(cand_key(c) >= lo && !(rep && ((bitmap[id >> 5] >> (id & 31)) & 1u)), c);
+    }
+  }
+  join(pid >= 0 && pv >= xf, pack_cand(f2key(pv), (uint32_t)pid));
   if (VEC && src.lim < V) {
 #pragma unroll
     for (int q = 0; q < 3; ++q)
-      join(tail_ok[q] && tl[q] >= xf, pack_cand(f2key(tl[q]), (uint32_t)(src.lim + q)), pbuf,
-           &rs.n_p, kPenCap);
-  }
-  __syncthreads();
-  // a segment that filled up has lost candidates: replay the row
-  const unsigned long long full = __ballot(lane < kRowWaves && rs.wcnt[lane] > kSegCap);
-  bool overflow = full != 0;
-  // keep the entries at or above the final bound (in srt): each wave its own
-  // segment, leaving out the raw logits of the repetition set; wave 0 also pbuf
-  const uint32_t lo = theta ? theta : 1u;
-  if (!overflow) {
-    const int n_seg = cnt < kSegCap ? cnt : kSegCap;
-    for (int i = lane; i < n_seg; i += 64) {
-      const unsigned long long c = seg[i];
-      const uint32_t id = cand_idx(c);
-      join(cand_key(c) >= lo && !(rep && ((bitmap[id >> 5] >> (id & 31)) & 1u)), c, srt, &rs.n_f,
-           kSortCap);
-    }
-    if (wave == 0) {
-      const int n_p = rs.n_p < kPenCap ? rs.n_p : kPenCap;
-      for (int i = lane; i < n_p; i += 64) join(cand_key(pbuf[i]) >= lo, pbuf[i], srt, &rs.n_f, kSortCap);
-    }
+      join(tail_ok[q] && tl[q] >= xf, pack_cand(f2key(tl[q]), (uint32_t)(src.lim + q)));
   }
   __syncthreads();
   const int n_all = rs.n_f;
-  overflow = overflow || n_all > kSortCap;
+  bool overflow = rs.ovf != 0 || n_all > kSortCap;
   unsigned long long F = 0;
   bool extra = false;
   if (!overflow && n_all <= kRowThreads) {
@@ -1429,7 +1425,7 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     // from srt into cbuf (the segments are no longer needed)
     uint32_t T = 0;
     const int n_sel = select_into<kRowThreads>(
-        n_all, [&](int p) { return srt[p]; }, lo, k, cbuf, rs.sel, rs.tail, &T);
+        n_all, [&](int p) { return srt[p]; }, 1u, k, cbuf, rs.sel, rs.tail, &T);
     if (n_sel < 0) overflow = true;
     if (wave != 0) return;
     if (!overflow) {
