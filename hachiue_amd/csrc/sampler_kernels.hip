@@ -1145,7 +1145,7 @@ struct RowSmem {
   uint32_t t_min, theta, key64;
   uint32_t theta2;             // refined bound, published by wave 0 mid-row
   int32_t wcnt[kRowWaves];     // candidates each wave has appended (published)
-  int32_t n_l, n_f, ovf;
+  int32_t n_l, n_f, ovf, done;
 };
 
 template <bool VEC>
@@ -1216,7 +1216,7 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   const bool rep = (penbits & kPenRep) && !(penbits & kPenPF);
   if (tid == 0) {
     rs.t_min = 0xFFFFFFFFu; rs.theta = 0; rs.theta2 = 0; rs.key64 = 0;
-    rs.n_l = 0; rs.n_f = 0; rs.ovf = 0;
+    rs.n_l = 0; rs.n_f = 0; rs.ovf = 0; rs.done = 0;
   }
   if (tid < kRowWaves) rs.wcnt[tid] = 0;
   if (tid < 64) top[tid] = 0ull;
@@ -1371,14 +1371,24 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     return;
   }
 
-  // As soon as its stream ends, each wave moves into srt the entries of its
-  // segment at or above its bound (the refined one once it has seen it),
-  // leaving out the raw logits of the repetition set, and its penalised and
-  // tail logits at or above the bound.  Every wave's bound is a lower bound
-  // of the row's k-th largest, so srt holds every logit at or above the
-  // largest of them: the row's top k and all logits equal to the k-th.
+  // The first wave to end its stream tightens the bound once more, from the
+  // entries published so far (every wave has published all but at most its
+  // last round).  After the barrier every wave moves into srt the entries of
+  // its segment at or above the final bound, leaving out the raw logits of
+  // the repetition set, and its penalised and tail logits at or above it.
   {
-    const uint32_t t2 = (uint32_t)uniform_i32((int)__atomic_load_n(&rs.theta2, __ATOMIC_RELAXED));
+    int first = 0;
+    if (lane == 0) first = atomicAdd(&rs.done, 1) == 0;
+    if (uniform_i32(first)) {
+      const uint32_t t0 = (uint32_t)uniform_i32((int)__atomic_load_n(&rs.theta2, __ATOMIC_RELAXED));
+      const uint32_t cur = t0 > theta ? t0 : theta;
+      const uint32_t t2 = wave_snapshot_bound(cbuf, rs.wcnt, k, cur, bitmap, rep);
+      if (lane == 0 && t2 > cur) atomicMax(&rs.theta2, t2);
+    }
+  }
+  __syncthreads();
+  {
+    const uint32_t t2 = (uint32_t)uniform_i32((int)rs.theta2);
     if (t2 > theta) theta = t2;
   }
   const uint32_t lo = theta ? theta : 1u;
