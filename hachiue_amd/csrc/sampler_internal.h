@@ -27,6 +27,14 @@ constexpr int kChunk = kThreads * kNV * 4;       // 16384 logits per workgroup
 constexpr int kWaveSpan = kChunk / kWaves;       // 4096 logits per wave
 constexpr int kChunkCap = 2048;                  // candidates per chunk (row region S*cap)
 
+// ---- pen_kernel: one workgroup per row, an LDS hash table of the history's
+// distinct ids.
+constexpr int kPenThreads = 1024;
+constexpr int kPenBits = 13;
+constexpr int kPenSlots = 1 << kPenBits;         // table slots (64 KiB with the counts)
+constexpr int kPenProbe = 64;                    // probes per insert before the range fallback
+constexpr int kPenRange = 16384;                 // ids per range of the fallback
+
 constexpr int kSmallK = 64;                      // wave-select paths
 constexpr int kMaxK = 1024;                      // largest k of the select paths
 constexpr int kFinalCap = 12288;                 // finalize: candidates >= X_row in LDS

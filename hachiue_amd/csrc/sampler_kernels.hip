@@ -6,10 +6,11 @@
 // file must be compiled with -ffp-contract=off so no multiply-add is fused.
 //
 // Kernels of one call (rows are routed by the host):
-//   pen_kernel       rows with presence / frequency penalties, grid rows*S,
-//                    256 threads: per 16384-id chunk, counts the history in
-//                    LDS and applies the repetition penalty (last 128 ids) and
-//                    the extension in place.
+//   pen_kernel       rows with presence / frequency penalties, one
+//                    1024-thread workgroup per row: counts the history's
+//                    distinct ids in an LDS hash table and applies the
+//                    repetition penalty (last 128 ids) and the extension in
+//                    place.
 //   row_kernel       greedy rows and rows with k <= 64, one 1024-thread
 //                    workgroup per row (the hot path).  The row streams from
 //                    HBM in rounds of 32768 logits, two rounds in registers.
@@ -316,44 +317,92 @@ __device__ __forceinline__ float penalise(float v, bool rep, uint32_t count, con
   return (float)x;
 }
 
-// Penalty pre-pass for rows with presence / frequency penalties: chunk
-// `chunk` of row pf_list[pos].  LDS: per-id counts of the chunk's id range and
-// the repetition bits.  Logits are read and written only where penalised.
-__global__ __launch_bounds__(kThreads) void pen_kernel(LaunchArgs a, Workspace ws) {
+// Penalty pre-pass for rows with presence / frequency penalties (and, on
+// the large-k path, any penalty): one workgroup per row of pf_list.  The
+// row's full history is counted into an LDS hash table of distinct ids (open
+// addressing; the count word's top bit marks the ids of the last 128 entries),
+// then every distinct id's logit is rewritten in place once.  A row whose
+// distinct ids do not fit the table (kPenSlots, at most kPenProbe probes per
+// insert) is counted instead by id ranges of kPenRange ids, one range at a
+// time.  Logits are read and written only where penalised.
+__device__ __forceinline__ uint32_t pen_hash(int id) {
+  return ((uint32_t)id * 2654435761u) >> (32 - kPenBits);
+}
+
+__global__ __launch_bounds__(kPenThreads) void pen_kernel(LaunchArgs a, Workspace ws) {
   extern __shared__ uint32_t pdyn[];
-  uint32_t *counts = pdyn;                  // kChunk
-  uint32_t *repbits = pdyn + kChunk;        // kChunk / 32
+  int32_t *keys = reinterpret_cast<int32_t *>(pdyn);   // kPenSlots ids (-1: empty)
+  uint32_t *cnts = pdyn + kPenSlots;                    // kPenSlots counts | rep bit
+  __shared__ int32_t full;
   const int tid = threadIdx.x;
-  const int S = a.chunks;
-  const int pos = blockIdx.x / S;
-  const int chunk = blockIdx.x - pos * S;
-  const int row = ws.pf_list[pos];
+  const int row = ws.pf_list[blockIdx.x];
   const RowPlan P = ws.plans[row];
   float *rowp = a.logits + (int64_t)row * a.stride;
-  const int lo = chunk * kChunk;
-  const int hi = min(lo + kChunk, a.vocab);
-  for (int i = tid; i < kChunk; i += kThreads) counts[i] = 0;
-  for (int i = tid; i < kChunk / 32; i += kThreads) repbits[i] = 0;
-  __syncthreads();
+  const int V = a.vocab;
   const int64_t h0 = a.hist_off ? a.hist_off[row] : 0;
   const int64_t hl = a.hist_off ? a.hist_off[row + 1] - h0 : 0;
-  if (P.pen & kPenRep) {
-    const int64_t last = hl < 128 ? hl : 128;   // history.slice(-128)
-    for (int64_t t = tid; t < last; t += kThreads) {
-      const int id = a.hist_ids[h0 + hl - last + t];
-      if (id >= lo && id < hi) atomicOr(&repbits[(id - lo) >> 5], 1u << ((id - lo) & 31));
-    }
-  }
-  for (int64_t t = tid; t < hl; t += kThreads) {
+  const int64_t rep0 = (P.pen & kPenRep) ? hl - (hl < 128 ? hl : 128) : hl;   // history.slice(-128)
+  const bool pf = (P.pen & kPenPF) != 0;
+  for (int i = tid; i < kPenSlots; i += kPenThreads) { keys[i] = -1; cnts[i] = 0; }
+  if (tid == 0) full = 0;
+  __syncthreads();
+  // the repetition-only entries (before rep0 without presence / frequency)
+  // are not counted: their count is not used
+  for (int64_t t = pf ? tid : rep0 + tid; t < hl; t += kPenThreads) {
     const int id = a.hist_ids[h0 + t];
-    if (id >= lo && id < hi) atomicAdd(&counts[id - lo], 1u);
+    if (id < 0 || id >= V) continue;
+    uint32_t h = pen_hash(id);
+    int probe = 0;
+    for (; probe < kPenProbe; ++probe) {
+      const int old = atomicCAS(&keys[h], -1, id);
+      if (old == -1 || old == id) break;
+      h = (h + 1) & (kPenSlots - 1);
+    }
+    if (probe == kPenProbe) {
+      full = 1;
+      break;
+    }
+    atomicAdd(&cnts[h], 1u);
+    if (t >= rep0) atomicOr(&cnts[h], 0x80000000u);
   }
   __syncthreads();
-  for (int o = tid; o < hi - lo; o += kThreads) {
-    const uint32_t n = counts[o];
-    const bool rep = (repbits[o >> 5] >> (o & 31)) & 1u;
-    if (n || rep) rowp[lo + o] = penalise(rowp[lo + o], rep, n, P);
+  if (!full) {
+    for (int i = tid; i < kPenSlots; i += kPenThreads) {
+      const int id = keys[i];
+      if (id < 0) continue;
+      const uint32_t c = cnts[i];
+      rowp[id] = penalise(rowp[id], (c >> 31) != 0, pf ? (c & 0x7FFFFFFFu) : 0u, P);
+    }
+    return;
   }
+  // too many distinct ids: count by id ranges (the table's LDS reused)
+  uint32_t *counts = pdyn;                  // kPenRange
+  uint32_t *repbits = pdyn + kPenRange;     // kPenRange / 32
+  for (int lo = 0; lo < V; lo += kPenRange) {
+    const int hi = min(lo + kPenRange, V);
+    __syncthreads();
+    for (int i = tid; i < kPenRange; i += kPenThreads) counts[i] = 0;
+    for (int i = tid; i < kPenRange / 32; i += kPenThreads) repbits[i] = 0;
+    __syncthreads();
+    for (int64_t t = pf ? tid : rep0 + tid; t < hl; t += kPenThreads) {
+      const int id = a.hist_ids[h0 + t];
+      if (id < lo || id >= hi) continue;
+      atomicAdd(&counts[id - lo], 1u);
+      if (t >= rep0) atomicOr(&repbits[(id - lo) >> 5], 1u << ((id - lo) & 31));
+    }
+    __syncthreads();
+    for (int o = tid; o < hi - lo; o += kPenThreads) {
+      const uint32_t n = counts[o];
+      const bool rep = (repbits[o >> 5] >> (o & 31)) & 1u;
+      if (n) rowp[lo + o] = penalise(rowp[lo + o], rep, pf ? n : 0u, P);
+    }
+  }
+}
+
+size_t pen_smem_bytes() {
+  const size_t table = (size_t)kPenSlots * 8;
+  const size_t ranges = (size_t)(kPenRange + kPenRange / 32) * 4;
+  return table > ranges ? table : ranges;
 }
 
 // ---------------------------------------------------------------- replay
@@ -2279,7 +2328,7 @@ __global__ __launch_bounds__(kLT) void large_kernel(LaunchArgs a, Workspace ws) 
 // ---------------------------------------------------------------- launch
 
 hipError_t prepare_kernels() {
-  const int pen_smem = (kChunk + kChunk / 32) * 4;
+  const int pen_smem = (int)pen_smem_bytes();
   const int row_smem = (int)row_smem_bytes(kRowMaxVocab);
   hipError_t e;
   if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&pen_kernel),
@@ -2320,8 +2369,8 @@ hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t s
                          hipEvent_t *ev) {
   hipError_t e;
   if (a.n_pf > 0) {
-    e = launch_one(pen_kernel, dim3((unsigned)(a.n_pf * a.chunks)), dim3(kThreads),
-                   (size_t)(kChunk + kChunk / 32) * 4, stream, ev, 0, a, ws);
+    e = launch_one(pen_kernel, dim3((unsigned)a.n_pf), dim3(kPenThreads), pen_smem_bytes(),
+                   stream, ev, 0, a, ws);
     if (e != hipSuccess) return e;
   }
   if (a.n_row > 0) {

@@ -160,6 +160,24 @@ def test_penalty_edges(any_sampler):
     _run(any_sampler, cases, V)
 
 
+def test_penalty_history_beyond_the_table(any_sampler):
+    """Histories whose distinct ids exceed the pre-pass's LDS hash table
+    (8192 slots) are counted by id ranges instead; one with few distinct ids
+    but long, and one hot id repeated thousands of times."""
+    V = 40000
+    r = _rng(8)
+    row = (r.standard_normal(V) * 2).astype(np.float32)
+    many = list(r.integers(0, V, 20000))                   # ~15k distinct ids
+    hot = [123] * 3000 + list(r.integers(0, 64, 3000))     # few distinct, long
+    pf = dict(presencePenalty=0.4, frequencyPenalty=0.05, **SAMPLE)
+    cases = [(row, many, dict(repetitionPenalty=1.2, **pf), 0.3),
+             (row, many, pf, 0.6),
+             (row, hot, dict(repetitionPenalty=1.1, **pf), 0.5),
+             (row, many, dict(temperature=1.0, topK=5000, topP=0.9, repetitionPenalty=1.3), 0.7),
+             (row, many, dict(temperature=0.0, presencePenalty=0.3), 0.5)]
+    _run(any_sampler, cases, V)
+
+
 @pytest.mark.parametrize("vocab,pad", [(151669, 0), (1001, 3), (4097, 1), (1, 0), (2, 5), (3, 0),
                                        (151937, 3), (50257, 3), (32003, 1), (6, 2), (7, 1)])
 def test_ragged_vocab_and_stride(any_sampler, vocab, pad):
