@@ -174,6 +174,31 @@ __device__ __forceinline__ uint32_t wave_scan_incl(uint32_t x) {
   return x;
 }
 
+// Inclusive prefix sum of one binary64 value per lane over the wave (DPP row
+// shifts and row broadcasts on both halves of the value).
+__device__ __forceinline__ double wave_scan_incl_f64(double x) {
+  // row_shr:n = 0x110 + n (bound_ctrl: 0 where the source lane is outside the
+  // row), row_bcast:15 = 0x142 into rows 1 and 3, row_bcast:31 = 0x143 into
+  // rows 2 and 3 (other rows keep 0)
+#define HS_DPP_ADD(ctrl, rmask, bc)                                                        \
+  {                                                                                        \
+    const unsigned long long b = (unsigned long long)__double_as_longlong(x);              \
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, ctrl,   \
+                                                               rmask, 0xF, bc);            \
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), \
+                                                               ctrl, rmask, 0xF, bc);      \
+    x += __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));           \
+  }
+  HS_DPP_ADD(0x111, 0xF, true)
+  HS_DPP_ADD(0x112, 0xF, true)
+  HS_DPP_ADD(0x114, 0xF, true)
+  HS_DPP_ADD(0x118, 0xF, true)
+  HS_DPP_ADD(0x142, 0xA, false)
+  HS_DPP_ADD(0x143, 0xC, false)
+#undef HS_DPP_ADD
+  return x;
+}
+
 // Exact k-th largest key of a block-wide multiset, four 8-bit digit passes.
 // All threads add their keys to a 256-bin LDS histogram; wave 0 alone finds
 // the digit (bins scanned from the top, four per lane) and clears the bins
@@ -461,7 +486,9 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
 
 struct TailSmem {
   int32_t n_sel, replay, cutoff, pick;
+  int32_t m, f1, f2, hit;
   double sum;
+  double wtot[16];
 };
 
 struct RowScratch {          // LDS arrays of at least k entries each
@@ -472,6 +499,114 @@ struct RowScratch {          // LDS arrays of at least k entries each
   float *rsv;
   int32_t *rsid;
 };
+
+// Block-parallel tail of src/sampler.ts:79-117 over n >= 2 sorted candidate
+// keys s.skey[0, n) (descending), by NT threads.  Leaves the probabilities in
+// s.sprob and f.cutoff, f.pick.
+//   sumProb is a block sum in tree order, not the reference's sequential
+//   order: the difference is a few binary64 ulps, far inside the binary32
+//   rounding of the probabilities.
+//   cumProb and the draw's r are exact, as in wave_tail: over the prefix of
+//   probabilities that are 0 or in [2^-29, 1] (the probabilities descend, so
+//   the others form a suffix starting at m) every partial sum below 2 is
+//   exact in any order, so cumProb is a block prefix sum there and the draw
+//   is the first index whose prefix reaches u*keptSum.  Past m, one thread
+//   continues the reference's sequential loops.
+template <int NT>
+__device__ void tail_block(int n, const RowPlan &P, double u, RowScratch s, TailSmem &f) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int NW = NT / 64;
+  const double maxl = (double)key2f(s.skey[0]);
+  const double inv_temp = 1.0 / P.temperature;
+  double local = 0;
+  for (int i = tid; i < n; i += NT) {
+    const double p = exp(((double)key2f(s.skey[i]) - maxl) * inv_temp);
+    s.sp[i] = p;
+    local += p;
+  }
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) local += __shfl_xor(local, d);
+  if (lane == 0) f.wtot[wave] = local;
+  if (tid == 0) { f.m = n; f.f1 = n; f.f2 = n; f.hit = n; }
+  __syncthreads();
+  double sum = 0;
+  for (int w = 0; w < NW; ++w) sum += f.wtot[w];
+  for (int i = tid; i < n; i += NT) {
+    const float prob = (float)((double)(float)s.sp[i] / sum);
+    s.sprob[i] = prob;
+    const double pd = (double)prob;
+    if (!(pd == 0.0 || (pd >= 0x1p-29 && pd <= 1.0))) atomicMin(&f.m, i);
+  }
+  __syncthreads();
+  const double thr = P.min_p * (double)s.sprob[0];
+  for (int i = tid; i < n; i += NT)
+    if (i > 0 && (double)s.sprob[i] < thr) atomicMin(&f.f1, i);
+  const int m = f.m;
+  // exact prefix sums over [0, m), into s.sp
+  double carry = 0;
+  bool exact = true;
+  for (int base = 0; base < m; base += NT) {
+    const int i = base + tid;
+    double c = wave_scan_incl_f64(i < m ? (double)s.sprob[i] : 0.0);
+    __syncthreads();   // the previous page's totals are read
+    if (lane == 63) f.wtot[wave] = c;
+    __syncthreads();
+    double add = carry, tot = carry;
+    for (int w = 0; w < NW; ++w) {
+      if (w < wave) add += f.wtot[w];
+      tot += f.wtot[w];
+    }
+    c += add;
+    if (i < m) {
+      s.sp[i] = c;
+      if (c >= P.top_p) atomicMin(&f.f2, i);
+    }
+    carry = tot;
+    exact = exact && tot < 2.0;
+  }
+  __syncthreads();
+  if (!exact) {   // partial sums reached 2: the sequential loops from the start
+    if (tid == 0) f.m = 0;
+    __syncthreads();
+  }
+  const int mm = f.m;
+  if (tid == 0) {
+    int f1 = f.f1, f2 = f.f2 < mm ? f.f2 : n;
+    int cut;
+    if (f1 <= f2 && f1 <= mm) cut = f1;          // a min-p break at or before m
+    else if (f2 < mm) cut = f2 + 1;              // a top-p break before m
+    else {                                       // the reference's loop from m on
+      double cum = mm > 0 ? s.sp[mm - 1] : 0.0;
+      cut = n;
+      for (int i = mm; i < n; ++i) {
+        if (i > 0 && (double)s.sprob[i] < thr) { cut = i; break; }
+        cum += (double)s.sprob[i];
+        s.sp[i] = cum;
+        if (cum >= P.top_p) { cut = i + 1; break; }
+      }
+    }
+    f.cutoff = cut;
+  }
+  __syncthreads();
+  const int cut = f.cutoff;
+  const double kept = s.sp[cut - 1];   // keptSum equals cumProb at cutoff - 1
+  const double r0 = u * kept;
+  if (cut <= mm) {
+    for (int i = tid; i < cut; i += NT)
+      if (s.sp[i] >= r0) atomicMin(&f.hit, i);
+    __syncthreads();
+    if (tid == 0) f.pick = f.hit < cut ? f.hit : cut - 1;
+  } else if (tid == 0) {
+    double r = r0;
+    int pick = cut - 1;
+    for (int i = 0; i < cut; ++i) {
+      r -= (double)s.sprob[i];
+      if (r <= 0) { pick = i; break; }
+    }
+    f.pick = pick;
+  }
+  __syncthreads();
+}
 
 // Completes a top-k row.  `srt` holds n_sel packed candidates, every logit
 // with key >= T (the exact k-th largest key; all candidates when fewer than
@@ -532,44 +667,7 @@ __device__ void finish_row(const LaunchArgs &a, const RowPlan &P, int row, const
     }
 
     if (n >= 2) {
-      const double maxl = (double)key2f(s.skey[0]);
-      const double inv_temp = 1.0 / P.temperature;
-      for (int i = tid; i < n; i += NT) {
-        const double p = exp(((double)key2f(s.skey[i]) - maxl) * inv_temp);
-        s.sp[i] = p;
-        s.sprob[i] = (float)p;
-      }
-      __syncthreads();
-      if (tid == 0) {
-        double sum = 0;
-        for (int i = 0; i < n; ++i) sum += s.sp[i];   // unrounded, in order
-        f.sum = sum;
-      }
-      __syncthreads();
-      const double sum = f.sum;
-      for (int i = tid; i < n; i += NT) s.sprob[i] = (float)((double)s.sprob[i] / sum);
-      __syncthreads();
-      if (tid == 0) {
-        const double thr = P.min_p * (double)s.sprob[0];
-        double cum = 0;
-        int cut = n;
-        for (int i = 0; i < n; ++i) {
-          if (i > 0 && (double)s.sprob[i] < thr) { cut = i; break; }
-          cum += (double)s.sprob[i];
-          if (cum >= P.top_p) { cut = i + 1; break; }
-        }
-        double kept = 0;
-        for (int i = 0; i < cut; ++i) kept += (double)s.sprob[i];
-        double r = u * kept;
-        int pick = cut - 1;
-        for (int i = 0; i < cut; ++i) {
-          r -= (double)s.sprob[i];
-          if (r <= 0) { pick = i; break; }
-        }
-        f.cutoff = cut;
-        f.pick = pick;
-      }
-      __syncthreads();
+      tail_block<NT>(n, P, u, s, f);
     } else {
       if (tid == 0) { f.cutoff = n; f.pick = n == 1 ? 0 : -1; }
       __syncthreads();
@@ -1004,31 +1102,6 @@ __device__ __forceinline__ void rank_top64(const unsigned long long *cbuf, int n
   __syncthreads();
 }
 
-
-// Inclusive prefix sum of one binary64 value per lane over the wave (DPP row
-// shifts and row broadcasts on both halves of the value).
-__device__ __forceinline__ double wave_scan_incl_f64(double x) {
-  // row_shr:n = 0x110 + n (bound_ctrl: 0 where the source lane is outside the
-  // row), row_bcast:15 = 0x142 into rows 1 and 3, row_bcast:31 = 0x143 into
-  // rows 2 and 3 (other rows keep 0)
-#define HS_DPP_ADD(ctrl, rmask, bc)                                                        \
-  {                                                                                        \
-    const unsigned long long b = (unsigned long long)__double_as_longlong(x);              \
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)b, ctrl,   \
-                                                               rmask, 0xF, bc);            \
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(b >> 32), \
-                                                               ctrl, rmask, 0xF, bc);      \
-    x += __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));           \
-  }
-  HS_DPP_ADD(0x111, 0xF, true)
-  HS_DPP_ADD(0x112, 0xF, true)
-  HS_DPP_ADD(0x114, 0xF, true)
-  HS_DPP_ADD(0x118, 0xF, true)
-  HS_DPP_ADD(0x142, 0xA, false)
-  HS_DPP_ADD(0x143, 0xC, false)
-#undef HS_DPP_ADD
-  return x;
-}
 
 // Tail of src/sampler.ts:76-117 for n <= 64 candidates held one per lane
 // (value keys `key`, sorted descending), by one wave.
