@@ -121,7 +121,7 @@ int64_t resolve_k(double top_k, int64_t vocab) {
 
 // Routing of rows to kernels, uploaded next to the plans.
 struct Routing {
-  std::vector<int32_t> pf, row, chunk, large;
+  std::vector<int32_t> pf, row, chunk, large, mid;
 };
 
 int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_rows,
@@ -131,6 +131,7 @@ int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_r
   rt.row.clear();
   rt.chunk.clear();
   rt.large.clear();
+  rt.mid.clear();
   for (int r = 0; r < rows; ++r) {
     const hs_sample_config &c = cfgs[r];
     hs::RowPlan p;
@@ -161,9 +162,10 @@ int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_r
       rt.large.push_back(r);
       continue;
     }
-    const bool row_kernel = (p.mode == hs::kModeGreedy || p.mode == hs::kModeSmall) &&
-                            vocab <= hs::kRowMaxVocab && rows >= row_min_rows;
-    (row_kernel ? rt.row : rt.chunk).push_back(r);
+    const bool one_pass = vocab <= hs::kRowMaxVocab && rows >= row_min_rows;
+    if (one_pass && p.mode == hs::kModeGeneric) rt.mid.push_back(r);
+    else if (one_pass) rt.row.push_back(r);
+    else rt.chunk.push_back(r);
   }
   return HS_OK;
 }
@@ -174,7 +176,8 @@ int upload_plans(hs_context *ctx, const std::vector<hs::RowPlan> &plans, const R
   const size_t rows = plans.size();
   const size_t pbytes = rows * sizeof(hs::RowPlan);
   const size_t lbytes =
-      sizeof(int32_t) * (rt.pf.size() + rt.row.size() + rt.chunk.size() + rt.large.size());
+      sizeof(int32_t) *
+      (rt.pf.size() + rt.row.size() + rt.chunk.size() + rt.large.size() + rt.mid.size());
   const size_t bytes = pbytes + lbytes;
   if (ctx->last_plans.size() == rows && ctx->last_vocab == vocab && ctx->plans.bytes >= bytes &&
       memcmp(ctx->last_plans.data(), plans.data(), pbytes) == 0)
@@ -199,6 +202,8 @@ int upload_plans(hs_context *ctx, const std::vector<hs::RowPlan> &plans, const R
   memcpy(lists + rt.pf.size() + rt.row.size(), rt.chunk.data(), sizeof(int32_t) * rt.chunk.size());
   memcpy(lists + rt.pf.size() + rt.row.size() + rt.chunk.size(), rt.large.data(),
          sizeof(int32_t) * rt.large.size());
+  memcpy(lists + rt.pf.size() + rt.row.size() + rt.chunk.size() + rt.large.size(), rt.mid.data(),
+         sizeof(int32_t) * rt.mid.size());
   HS_HIP(hipMemcpyAsync(ctx->plans.p, st, bytes, hipMemcpyHostToDevice, stream));
   HS_HIP(hipEventRecord(ctx->plan_done, stream));
   ctx->plan_pending = true;
@@ -253,7 +258,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
     return fail(HS_ERR_OUT_OF_MEMORY, "host allocation failed");
   }
   const int n_pf = (int)rt.pf.size(), n_row = (int)rt.row.size(), n_chunk = (int)rt.chunk.size();
-  const int n_large = (int)rt.large.size();
+  const int n_large = (int)rt.large.size(), n_mid = (int)rt.mid.size();
 
   // workspace (the chunk path only)
   if (n_chunk > 0) {
@@ -274,6 +279,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   ws.row_list = lists + n_pf;
   ws.chunk_list = lists + n_pf + n_row;
   ws.large_list = lists + n_pf + n_row + n_chunk;
+  ws.mid_list = lists + n_pf + n_row + n_chunk + n_large;
   ws.cand = static_cast<uint2 *>(ctx->cand.p);
   ws.cand_count = static_cast<int32_t *>(ctx->cand_count.p);
   ws.info = static_cast<hs::ChunkInfo *>(ctx->info.p);
@@ -292,6 +298,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   a.rows_direct = n_row == rows ? 1 : 0;
   a.n_chunk = n_chunk;
   a.n_large = n_large;
+  a.n_mid = n_mid;
   a.hist_ids = d_hist_ids;
   a.hist_off = d_hist_offsets;
   a.uniforms = d_uniforms;

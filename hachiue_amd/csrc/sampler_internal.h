@@ -19,6 +19,11 @@ constexpr int kRowCandCap = 4096;                // streamed candidates per row
 constexpr int kSegCap = kRowCandCap / kRowWaves; // of them per wave (its own segment)
 constexpr int kRowMaxVocab = 1 << 19;            // LDS bitmap limit (64 KiB)
 
+// ---- mid kernel (64 < k <= 1024): the row kernel's stream with a key
+// histogram of kMidBins bins (the top 13 key bits: 1/16 octave) for the bound.
+constexpr int kMidShift = 19;
+constexpr int kMidBins = 1 << (32 - kMidShift);
+
 // ---- chunk kernel: 256 threads own CHUNK consecutive logits of a row.
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
@@ -83,6 +88,7 @@ struct Workspace {
   const int32_t *row_list;   // rows of the row kernel
   const int32_t *chunk_list; // rows of the chunk + finalize kernels
   const int32_t *large_list; // rows of the large-k kernel
+  const int32_t *mid_list;   // rows of the mid kernel
   uint2 *cand;               // [n_chunk][S][kChunkCap] (key, index)
   int32_t *cand_count;       // [n_chunk]
   ChunkInfo *info;           // [n_chunk][S]
@@ -97,7 +103,7 @@ struct LaunchArgs {
   int32_t vec;               // float4 loads allowed (alignment)
   int32_t want_cands;        // exact candidate order must be produced
   int32_t rows_direct;       // the row kernel takes every row: row = block index
-  int32_t n_pf, n_row, n_chunk, n_large;
+  int32_t n_pf, n_row, n_chunk, n_large, n_mid;
   const int32_t *hist_ids;
   const int64_t *hist_off;
   const double *uniforms;
@@ -113,15 +119,17 @@ struct LaunchArgs {
 // Launches the kernels of one call on `stream`.  When `ev` is not null,
 // ev[2i] and ev[2i + 1] receive the start and end of kernel i's dispatch
 // (0 penalty pre-pass, 1 row kernel, 2 chunk kernel, 3 finalize, 4 large-k
-// kernel), for the kernels that launch only: launched_kernels() says which.
-constexpr int kTimedKernels = 5;
+// kernel, 5 mid kernel), for the kernels that launch only: launched_kernels()
+// says which.
+constexpr int kTimedKernels = 6;
 inline unsigned launched_kernels(const LaunchArgs &a) {
   return (a.n_pf > 0 ? 1u : 0u) | (a.n_row > 0 ? 2u : 0u) | (a.n_chunk > 0 ? 12u : 0u) |
-         (a.n_large > 0 ? 16u : 0u);
+         (a.n_large > 0 ? 16u : 0u) | (a.n_mid > 0 ? 32u : 0u);
 }
 hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,
                          hipEvent_t *ev);
 hipError_t prepare_kernels();   // per device, once: raise dynamic LDS limits
 size_t row_smem_bytes(int vocab);
+size_t mid_smem_bytes(int vocab);
 
 }  // namespace hs

@@ -513,7 +513,7 @@ struct RowScratch {          // LDS arrays of at least k entries each
 //   is the first index whose prefix reaches u*keptSum.  Past m, one thread
 //   continues the reference's sequential loops.
 template <int NT>
-__device__ void tail_block(int n, const RowPlan &P, double u, RowScratch s, TailSmem &f) {
+__device__ __forceinline__ void tail_block(int n, const RowPlan &P, double u, RowScratch s, TailSmem &f) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   constexpr int NW = NT / 64;
   const double maxl = (double)key2f(s.skey[0]);
@@ -615,7 +615,7 @@ __device__ void tail_block(int n, const RowPlan &P, double u, RowScratch s, Tail
 // need_replay: the candidates are not trustworthy (a list overflowed).
 // Writes the token and the optional outputs of `row`.
 template <int NT>
-__device__ void finish_row(const LaunchArgs &a, const RowPlan &P, int row, const float *rowp,
+__device__ __forceinline__ void finish_row(const LaunchArgs &a, const RowPlan &P, int row, const float *rowp,
                            unsigned long long *srt, int n_sel, uint32_t T, bool closed_form,
                            bool need_replay, RowScratch s, TailSmem &f) {
   const int tid = threadIdx.x;
@@ -1576,6 +1576,329 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
               reinterpret_cast<double *>(top));   // top[] is read into F already
 }
 
+// ---------------------------------------------------------------- mid kernel
+
+// Rows with 64 < k <= 1024: the row kernel's stream, with the bound taken
+// from an LDS histogram of keys (kMidBins bins of the top key bits).  Round 0
+// is counted whole; from then on only the logits at or above the bound are
+// counted (they are the candidates), which keeps every bin at or above any
+// later bound exact.  Each wave recomputes the bound from the histogram at
+// every round and drops the entries of its segment that fell below it.  At
+// the end the candidates at or above the final bound (about k plus one bin)
+// are sorted and finish_row completes the row.
+
+// Turns a round into keys and counts every finite one; returns the largest.
+template <int NV>
+__device__ __forceinline__ uint32_t hist_keys(const float (&v)[NV][4], uint32_t (&kk)[NV][4],
+                                              uint32_t *hist) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int j = 0; j < NV; ++j)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t key = f2key(v[j][q]);
+      kk[j][q] = key;
+      if (key) atomicAdd(&hist[key >> kMidShift], 1u);
+      m = key > m ? key : m;
+    }
+  return m;
+}
+
+// Appends every key >= lo (lo >= 1) of a round to the wave's segment.
+template <int NV>
+__device__ __forceinline__ void append_keys(const uint32_t (&kk)[NV][4], int fb, int tid,
+                                            uint32_t lo, unsigned long long *seg, int &cnt) {
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const uint32_t mx = max(max(kk[j][0], kk[j][1]), max(kk[j][2], kk[j][3]));
+    if (!__ballot(mx >= lo)) continue;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool pass = kk[j][q] >= lo;
+      const unsigned long long b = __ballot(pass);
+      if (b) {
+        const int p = cnt + (int)lanes_below(b);
+        if (pass && p < kSegCap)
+          seg[p] = pack_cand(kk[j][q], (uint32_t)(slot_elem(fb, tid, j) + q));
+        cnt = uniform_i32(cnt + __popcll(b));
+      }
+    }
+  }
+}
+
+// append_rd that also counts every appended logit; returns the largest key
+// appended.
+template <int NV>
+__device__ __forceinline__ uint32_t append_hist_rd(const float (&v)[NV][4], int fb, int tid, float xf,
+                                                   unsigned long long *seg, int &cnt,
+                                                   uint32_t *hist) {
+  uint32_t m = 0;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const float mx = fmaxf(fmaxf(v[j][0], v[j][1]), fmaxf(v[j][2], v[j][3]));
+    if (!__ballot(mx >= xf)) continue;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool pass = v[j][q] >= xf;
+      const unsigned long long b = __ballot(pass);
+      if (b) {
+        const int p = cnt + (int)lanes_below(b);
+        if (pass) {
+          const uint32_t key = f2key(v[j][q]);
+          if (p < kSegCap) seg[p] = pack_cand(key, (uint32_t)(slot_elem(fb, tid, j) + q));
+          atomicAdd(&hist[key >> kMidShift], 1u);
+          m = key > m ? key : m;
+        }
+        cnt = uniform_i32(cnt + __popcll(b));
+      }
+    }
+  }
+  return m;
+}
+
+// The largest bin edge t with at least k counted keys >= t, searching down
+// from the bin of `top` (the largest counted key); 0 when fewer than k are
+// counted.  Counts read while other waves still add are lower bounds of the
+// final ones, so the result is a lower bound of the row's k-th largest.
+__device__ __forceinline__ uint32_t hist_bound(const uint32_t *hist, uint32_t top, int k) {
+  const int lane = lane_id();
+  uint32_t cum = 0;
+  for (int base = (int)(top >> kMidShift); base >= 0; base -= 64) {
+    const int b = base - lane;
+    const uint32_t c = b >= 0 ? __atomic_load_n(hist + b, __ATOMIC_RELAXED) : 0u;
+    const uint32_t incl = wave_scan_incl(c);   // lane 0 holds the highest bin
+    const uint32_t tot = readlane_u32(incl, 63);
+    if (cum + tot >= (uint32_t)k) {
+      const unsigned long long mk = __ballot(cum + incl >= (uint32_t)k);
+      const int L = __ffsll((long long)mk) - 1;
+      return (uint32_t)(base - L) << kMidShift;
+    }
+    cum += tot;
+  }
+  return 0u;
+}
+
+// Drops the stored entries of a segment below lo (in place, order kept).
+__device__ __forceinline__ void compact_seg(unsigned long long *seg, int &cnt, uint32_t lo) {
+  const int lane = lane_id();
+  const int n = cnt < kSegCap ? cnt : kSegCap;
+  int m = 0;
+  for (int base = 0; base < n; base += 64) {
+    const int i = base + lane;
+    const unsigned long long c = i < n ? seg[i] : 0ull;
+    const bool keep = i < n && cand_key(c) >= lo;
+    const unsigned long long b = __ballot(keep);
+    if (keep) seg[m + (int)lanes_below(b)] = c;   // m <= base: entries not yet read stay
+    m += __popcll(b);
+  }
+  cnt = uniform_i32(m);
+}
+
+// One round of the mid kernel: the bound from the histogram (dropping the
+// segment's entries below it when it rose), then the round's candidates.
+__device__ __forceinline__ void mid_step(float (&v)[kRowNV][4], int fb, int tid, int lim, int V,
+                                         int k, bool rep, const uint32_t *bitmap, uint32_t *hist,
+                                         uint32_t *top_key, unsigned long long *seg, int &cnt,
+                                         uint32_t &theta, float &xf, bool &lost) {
+  const uint32_t t =
+      hist_bound(hist, (uint32_t)uniform_i32((int)__atomic_load_n(top_key, __ATOMIC_RELAXED)), k);
+  if (t > theta) {
+    theta = t;
+    xf = key_floor(theta);
+    lost = lost || cnt > kSegCap;
+    compact_seg(seg, cnt, theta);
+  }
+  clip_rd<kRowNV>(v, fb, tid, lim);
+  if (rep) mask_penalised<kRowNV>(v, fb, tid, V, bitmap);
+  const uint32_t m = wave_max_u32(append_hist_rd<kRowNV>(v, fb, tid, xf, seg, cnt, hist));
+  if ((tid & 63) == 0 && m) atomicMax(top_key, m);
+}
+
+size_t mid_smem_bytes(int vocab) {
+  const size_t words = ((size_t)vocab + 31) / 32;
+  return (size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + (size_t)kMidBins * 4 + words * 4;
+}
+
+struct MidSmem {
+  TailSmem tail;
+  uint32_t top_key;
+  int32_t n_f, ovf, n_sel;
+};
+
+template <bool VEC>
+__global__ __launch_bounds__(kRowThreads) void mid_kernel(LaunchArgs a, Workspace ws) {
+  extern __shared__ unsigned long long mdyn[];
+  unsigned long long *cbuf = mdyn;                                  // kRowCandCap
+  unsigned long long *srt = cbuf + kRowCandCap;                     // kSortCap
+  uint32_t *hist = reinterpret_cast<uint32_t *>(srt + kSortCap);    // kMidBins
+  uint32_t *bitmap = hist + kMidBins;                               // ceil(V/32)
+  __shared__ MidSmem ms;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform_i32(tid >> 6);
+  const int row = ws.mid_list[blockIdx.x];
+  float *rowp = a.logits + (int64_t)row * a.stride;
+  const int V = a.vocab;
+  const int nr = row_rounds(V);
+
+  // history ids first, then rounds 0 and 1 (as in row_kernel)
+  const int32_t *hist_p = a.hist_ids;
+  int hist_n = 0;
+  if (a.hist_off) {
+    const int64_t h0 = load_scalar(a.hist_off + row);
+    const int64_t hl = load_scalar(a.hist_off + row + 1) - h0;
+    hist_n = (int)(hl < 128 ? hl : 128);   // history.slice(-128)
+    hist_p = a.hist_ids + (h0 + hl - hist_n);
+  }
+  const int hraw = (int)__builtin_amdgcn_raw_buffer_load_b32(make_rsrc(hist_p, 4u * hist_n),
+                                                             tid * 4, 0, 0);
+  RowSrc src;
+  src.lim = VEC ? (V & ~3) : V;
+  src.x4 = make_rsrc(rowp, 4u * (uint32_t)(V & ~3));
+  src.x1 = make_rsrc(rowp, 4u * (uint32_t)V);
+  float v0[kR0NV][4], va[kRowNV][4], vb[kRowNV][4];
+  load_rd<kR0NV, VEC>(v0, src, 0, tid);
+  load_rd<kRowNV, VEC>(vb, src, round_base(1), tid);
+  float tl[3] = {0.f, 0.f, 0.f};
+  if (VEC) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int e = src.lim + q;
+      tl[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          src.x1, (tid == 0 && e < V ? e : V) * 4, 0, 0));
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  const RowPlan *plan = ws.plans + row;
+  const int k = load_scalar(&plan->k);
+  const int penbits = load_scalar(&plan->pen);
+  const double prep = load_scalar(&plan->rep);
+  // presence / frequency rows were penalised in place by pen_kernel
+  const bool rep = (penbits & kPenRep) && !(penbits & kPenPF);
+  if (tid == 0) { ms.top_key = 0; ms.n_f = 0; ms.ovf = 0; ms.n_sel = 0; }
+  for (int i = tid; i < kMidBins; i += kRowThreads) hist[i] = 0;
+  unsigned long long *seg = cbuf + wave * kSegCap;
+  int cnt = 0;
+  bool lost = false;
+
+  int pid = -1;
+  if (rep) {
+    const int words = (V + 31) >> 5;
+    for (int i = tid; i < words; i += kRowThreads) bitmap[i] = 0;
+    __syncthreads();
+    const int hid = tid < hist_n ? hraw : -1;
+    if (hid >= 0 && hid < V) {
+      const uint32_t bit = 1u << (hid & 31);
+      if (!(atomicOr(&bitmap[hid >> 5], bit) & bit)) pid = hid;
+    }
+  }
+  const float pval =
+      __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(src.x1, (pid >= 0 ? pid : V) * 4, 0, 0));
+  __syncthreads();   // bitmap complete, histogram cleared
+
+  // ---- round 0 is counted whole; the bound follows from the histogram
+  clip_rd<kR0NV>(v0, 0, tid, src.lim);
+  if (rep) mask_penalised<kR0NV>(v0, 0, tid, V, bitmap);
+  uint32_t k0[kR0NV][4];
+  {
+    const uint32_t m0 = wave_max_u32(hist_keys<kR0NV>(v0, k0, hist));
+    if (lane == 0) atomicMax(&ms.top_key, m0);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  load_rd<kRowNV, VEC>(va, src, round_base(2), tid);
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();   // round 0 counted
+  uint32_t theta = hist_bound(hist, ms.top_key, k);
+  float xf = key_floor(theta ? theta : 1u);
+  append_keys<kR0NV>(k0, 0, tid, theta ? theta : 1u, seg, cnt);
+
+  // ---- rounds >= 1
+  for (int r = 1; r < nr; r += 2) {
+    mid_step(vb, round_base(r), tid, src.lim, V, k, rep, bitmap, hist, &ms.top_key, seg, cnt,
+             theta, xf, lost);
+    load_rd<kRowNV, VEC>(vb, src, round_base(r + 2), tid);   // past the row near its end
+    if (r + 1 >= nr) break;
+    mid_step(va, round_base(r + 1), tid, src.lim, V, k, rep, bitmap, hist, &ms.top_key, seg, cnt,
+             theta, xf, lost);
+    load_rd<kRowNV, VEC>(va, src, round_base(r + 3), tid);
+  }
+  lost = lost || cnt > kSegCap;
+
+  // ---- end: penalised logits back in place (as in row_kernel)
+  float pv = 0.f;
+  if (pid >= 0) {
+    RowPlan pr;
+    pr.rep = prep;
+    pr.pen = kPenRep;
+    pv = penalise(pval, true, 0u, pr);
+    rowp[pid] = pv;
+  }
+  __syncthreads();   // every wave's counts are in
+  theta = hist_bound(hist, ms.top_key, k);
+  const uint32_t lo = theta ? theta : 1u;
+  xf = key_floor(lo);
+  auto join = [&](bool pass, unsigned long long c) {
+    const unsigned long long b = __ballot(pass);
+    if (b) {
+      const int leader = __ffsll((long long)b) - 1;
+      int bp = 0;
+      if (lane == leader) bp = atomicAdd(&ms.n_f, __popcll(b));
+      bp = __shfl(bp, leader);
+      const int p = bp + (int)lanes_below(b);
+      if (pass && p < kSortCap) srt[p] = c;
+    }
+  };
+  if (lost) {
+    if (lane == 0) ms.ovf = 1;
+  } else {
+    for (int i = lane; i < cnt; i += 64) join(cand_key(seg[i]) >= lo, seg[i]);
+  }
+  join(pid >= 0 && pv >= xf, pack_cand(f2key(pv), (uint32_t)pid));
+  if (VEC && src.lim < V) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int e = src.lim + q;
+      const bool ok = tid == 0 && e < V && !(rep && ((bitmap[e >> 5] >> (e & 31)) & 1u));
+      join(ok && tl[q] >= xf, pack_cand(f2key(tl[q]), (uint32_t)e));
+    }
+  }
+  __syncthreads();
+  const int n = ms.n_f;
+  const bool overflow = ms.ovf != 0 || n > kSortCap;
+  uint32_t T = 0;
+  int n_sel = 0;
+  if (!overflow) {
+    sort_packed<kRowThreads>(srt, n);   // ends with a barrier
+    if (n >= k) {
+      T = cand_key(srt[k - 1]);
+      if (tid == 0) ms.n_sel = k;
+      __syncthreads();
+      for (int i = k + tid; i < n; i += kRowThreads)   // the last entry equal to T
+        if (cand_key(srt[i]) == T && (i + 1 == n || cand_key(srt[i + 1]) != T)) ms.n_sel = i + 1;
+      __syncthreads();
+      n_sel = ms.n_sel;
+    } else {
+      n_sel = n;
+    }
+  }
+  RowPlan P;
+  P.temperature = load_scalar(&plan->temperature);
+  P.top_p = load_scalar(&plan->top_p);
+  P.min_p = load_scalar(&plan->min_p);
+  P.k = k;
+  // the histogram's LDS becomes the tail's scratch
+  RowScratch sc;
+  sc.skey = hist;
+  sc.sids = reinterpret_cast<int32_t *>(hist + kMaxK);
+  sc.sprob = reinterpret_cast<float *>(hist + 2 * kMaxK);
+  sc.sp = reinterpret_cast<double *>(hist + 3 * kMaxK);
+  sc.rsv = reinterpret_cast<float *>(hist + 5 * kMaxK);
+  sc.rsid = reinterpret_cast<int32_t *>(hist + 6 * kMaxK);
+  // closed form: all finite logits are candidates and there are at most k
+  finish_row<kRowThreads>(a, P, row, rowp, srt, n_sel, T, theta == 0 && n <= k, overflow, sc,
+                          ms.tail);
+}
+
 // ---------------------------------------------------------------- chunk kernel
 
 template <bool VEC>
@@ -2413,6 +2736,13 @@ hipError_t prepare_kernels() {
   if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&row_kernel<false>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, row_smem)) != hipSuccess)
     return e;
+  const int mid_smem = (int)mid_smem_bytes(kRowMaxVocab);
+  if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mid_kernel<true>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, mid_smem)) != hipSuccess)
+    return e;
+  if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mid_kernel<false>),
+                               hipFuncAttributeMaxDynamicSharedMemorySize, mid_smem)) != hipSuccess)
+    return e;
   if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&finalize_kernel),
                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)finalize_smem_bytes())) != hipSuccess)
@@ -2452,6 +2782,14 @@ hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t s
                            stream, ev, 1, a, ws)
               : launch_one(row_kernel<false>, dim3((unsigned)a.n_row), dim3(kRowThreads), smem,
                            stream, ev, 1, a, ws);
+    if (e != hipSuccess) return e;
+  }
+  if (a.n_mid > 0) {
+    const size_t smem = mid_smem_bytes(a.vocab);
+    e = a.vec ? launch_one(mid_kernel<true>, dim3((unsigned)a.n_mid), dim3(kRowThreads), smem,
+                           stream, ev, 5, a, ws)
+              : launch_one(mid_kernel<false>, dim3((unsigned)a.n_mid), dim3(kRowThreads), smem,
+                           stream, ev, 5, a, ws);
     if (e != hipSuccess) return e;
   }
   if (a.n_chunk > 0) {

@@ -190,7 +190,8 @@ class Sampler:
     def set_timing(self, enable: bool) -> None:
         _check(lib().hs_context_set_timing(self._ctx, 1 if enable else 0))
 
-    KERNELS = ("pen_kernel", "row_kernel", "chunk_kernel", "finalize_kernel", "large_kernel")
+    KERNELS = ("pen_kernel", "row_kernel", "chunk_kernel", "finalize_kernel", "large_kernel",
+               "mid_kernel")
 
     def kernel_times(self):
         """({kernel: total device ms}, calls) since the last query."""

@@ -132,7 +132,8 @@ int hs_sample_batch_device_ex(hs_context *ctx, float *d_logits, int32_t rows,
  * each of its kernel launches.  hs_context_kernel_times() waits for the
  * recorded calls, writes the summed device milliseconds per kernel
  * (ms[0] presence/frequency pre-pass, ms[1] row kernel, ms[2] chunk kernel,
- * ms[3] finalize, ms[4] large-k kernel; a kernel a call did not launch adds 0)
+ * ms[3] finalize, ms[4] large-k kernel, ms[5] mid-k kernel; a kernel a call did
+ * not launch adds 0)
  * and the number of
  * timed calls, and resets the totals. */
 int hs_context_set_timing(hs_context *ctx, int enable);
