@@ -167,6 +167,14 @@ int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_r
     else if (one_pass) rt.row.push_back(r);
     else rt.chunk.push_back(r);
   }
+  // In a call that launches the mid kernel anyway, its rows with k <= 64 join
+  // it: one launch over all of them instead of two in sequence, each filling
+  // only part of the GPU.  Greedy rows stay with the row kernel.
+  if (!rt.mid.empty() && !rt.row.empty()) {
+    std::vector<int32_t> keep;
+    for (int32_t r : rt.row) (out[(size_t)r].mode == hs::kModeSmall ? rt.mid : keep).push_back(r);
+    rt.row.swap(keep);
+  }
   return HS_OK;
 }
 

@@ -308,6 +308,74 @@ __device__ void block_sort_desc(unsigned long long *a, int P) {
   }
 }
 
+// Bitonic sort of P2 (a power of two, at most NT * E) packed candidates held
+// in registers, E per thread at indices tid + NT * e, descending.  Partners
+// closer than 64 are exchanged by lane shuffles, partners in other waves
+// through LDS (two barriers), partners NT or more apart within the thread.
+// `a` holds the input on entry (written before a barrier) and the result on
+// return (after a barrier).
+template <int NT, int E>
+__device__ void bitonic_reg(unsigned long long *a, int P2) {
+  const int tid = threadIdx.x;
+  unsigned long long x[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = tid + NT * e;
+    x[e] = i < P2 ? a[i] : 0ull;
+  }
+  for (int size = 2; size <= P2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      if (stride >= NT) {
+        // es = stride / NT, a power of two below E: one unrolled case each so
+        // that every register index is a constant
+#pragma unroll
+        for (int es = 1; es < E; es <<= 1) {
+          if (stride != NT * es) continue;
+#pragma unroll
+          for (int e = 0; e < E; ++e) {
+            if (e & es) continue;
+            const int i = tid + NT * e;
+            const bool desc = (i & size) == 0;
+            const unsigned long long lo = x[e], hi = x[e | es];
+            if ((lo < hi) == desc) { x[e] = hi; x[e | es] = lo; }
+          }
+        }
+      } else if (stride >= 64) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int i = tid + NT * e;
+          if (i < P2) a[i] = x[e];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int i = tid + NT * e;
+          if (i < P2) {
+            const unsigned long long y = a[i ^ stride];
+            const bool keep_max = ((i & stride) == 0) == ((i & size) == 0);
+            x[e] = keep_max ? (y > x[e] ? y : x[e]) : (y < x[e] ? y : x[e]);
+          }
+        }
+        __syncthreads();
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+          const int i = tid + NT * e;
+          const unsigned long long y = __shfl_xor(x[e], stride);
+          const bool keep_max = ((i & stride) == 0) == ((i & size) == 0);
+          x[e] = keep_max ? (y > x[e] ? y : x[e]) : (y < x[e] ? y : x[e]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = tid + NT * e;
+    if (i < P2) a[i] = x[e];
+  }
+  __syncthreads();
+}
+
 // Sorts the first n packed candidates of `a` descending (n <= kSortCap).
 template <int NT>
 __device__ void sort_packed(unsigned long long *a, int n) {
@@ -324,7 +392,8 @@ __device__ void sort_packed(unsigned long long *a, int n) {
     }
     __syncthreads();
   } else {
-    block_sort_desc<NT>(a, P2);
+    static_assert(kSortCap % NT == 0, "sort_packed: kSortCap must be a multiple of NT");
+    bitonic_reg<NT, kSortCap / NT>(a, P2);
   }
 }
 
