@@ -30,9 +30,10 @@ def _batch(cases, vocab, stride=None):
     return logits, ids, off, configs, np.array(us, np.float64)
 
 
-def _run(sampler, cases, vocab, stride=None, cap=64, label="edges"):
+def _run(sampler, cases, vocab, stride=None, cap=64, label="edges", want_cands=True):
     logits, ids, off, configs, us = _batch(cases, vocab, stride)
-    got = run_gpu(sampler, logits, vocab, ids, off, configs, us, cap, stride=logits.shape[1])
+    got = run_gpu(sampler, logits, vocab, ids, off, configs, us, cap, stride=logits.shape[1],
+                  want_cands=want_cands)
     want, want_logits = run_oracle(logits, vocab, ids, off, configs, us, cap)
     compare(got, want, want_logits, configs, vocab, cap, label)
     return got, want
@@ -200,3 +201,32 @@ def test_ragged_vocab_and_stride(any_sampler, vocab, pad):
                                          repetitionPenalty=1.5), 0.999))
     cases.append((top, [vocab - 1], dict(temperature=0.0, repetitionPenalty=100.0), 0.5))
     _run(any_sampler, cases, vocab, stride=vocab + pad)
+
+
+def test_mid_k_tail_without_candidate_outputs(any_sampler):
+    """Rows with 64 < k <= 1024 and no candidate outputs: the sort-free tail
+    (positions by probability-weighted selects) and its fallbacks (ties at or
+    inside the top k, probabilities below 2^-29, u = 0, min-p and top-p
+    edges, an infinite logit)."""
+    V = 30000
+    r = _rng(12)
+    base = (r.standard_normal(V) * 2.5).astype(np.float32)
+    ties = base.copy()
+    top = np.argsort(-base)[:300]
+    ties[top[10:20]] = ties[top[10]]          # a tie group inside the top k
+    ties[top[199:230]] = ties[top[199]]       # a group at the k-th value (k = 200)
+    inf = base.copy(); inf[777] = np.inf
+    cases = [(base, [], dict(temperature=0.8, topK=300, topP=0.9), 0.37),
+             (base, [], dict(temperature=1.5, topK=1024, topP=0.99), 0.61),
+             (base, [], dict(temperature=0.05, topK=500, topP=0.95), 0.5),    # tiny probabilities
+             (base, [], dict(temperature=1.0, topK=100, topP=0.0), 0.5),
+             (base, [], dict(temperature=1.0, topK=100, topP=1.0), 0.999),
+             (base, [], dict(temperature=1.0, topK=100, topP=0.9, minP=0.3), 0.7),
+             (base, [], dict(temperature=1.0, topK=100, topP=0.9, minP=1.0), 0.7),
+             (base, [], dict(temperature=1.0, topK=100, topP=0.9), 0.0),
+             (ties, [], dict(temperature=1.0, topK=200, topP=0.95), 0.42),
+             (ties, [], dict(temperature=3.0, topK=200, topP=1.0), 0.999999),
+             (inf, [], dict(temperature=1.0, topK=100, topP=0.9), 0.5),
+             (base, list(r.integers(0, V, 100)), dict(temperature=0.9, topK=80, topP=0.9,
+                                                     repetitionPenalty=1.2), 0.25)]
+    _run(any_sampler, cases, V, cap=1024, label="mid-k tokens only", want_cands=False)

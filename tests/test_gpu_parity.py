@@ -12,9 +12,9 @@ pytestmark = pytest.mark.gpu
 CAP = 64
 
 
-def _check(sampler, wl, cap=CAP, label=None):
+def _check(sampler, wl, cap=CAP, label=None, want_cands=True):
     got = run_gpu(sampler, wl.logits, wl.vocab, wl.hist_ids, wl.hist_off, wl.configs,
-                  wl.uniforms, cap)
+                  wl.uniforms, cap, want_cands=want_cands)
     want, want_logits = run_oracle(wl.logits, wl.vocab, wl.hist_ids, wl.hist_off, wl.configs,
                                    wl.uniforms, cap)
     return compare(got, want, want_logits, wl.configs, wl.vocab, cap, label or wl.name), got, want
@@ -49,3 +49,13 @@ def test_perrow256(any_sampler):
 
 def test_v262k512(any_sampler):
     _check(any_sampler, workloads.make("v262k512", 0), cap=128)
+
+
+# Without candidate outputs the kernels for 64 < k <= 1024 complete most rows
+# without ordering the candidate list (radix selects weighted by probability);
+# tokens, counts and cutoffs must still match the oracle.
+@pytest.mark.parametrize("name,seed", [("perrow256", 0), ("perrow256", 1), ("v262k512", 0),
+                                       ("batch64", 0), ("headline", 0)])
+def test_tokens_only(any_sampler, name, seed):
+    wl = workloads.make(name, seed)
+    _check(any_sampler, wl, cap=1024, label=f"{name} tokens only", want_cands=False)
