@@ -2246,6 +2246,7 @@ constexpr int kLT = 1024;      // threads per workgroup
 constexpr int kLBins = 4096;   // level-1 buckets
 constexpr int kLSub = 1024;    // refinement buckets
 constexpr int kLCap = 2048;    // logits gathered and sorted in LDS
+constexpr int kLWalk = 64;     // a bucket with more candidates is split once more
 
 struct LargeSmem {
   uint32_t cnt[kLBins];
@@ -2257,7 +2258,7 @@ struct LargeSmem {
   unsigned long long ured[kLT / 64];
   double dred[kLT / 64];
   // located bucket / element, published by one thread
-  int32_t found, pos, id, tie, nbuf;
+  int32_t found, pos, id, tie, nbuf, hit;
   uint32_t key, b, ecnt;
   double emass, cum;
 };
@@ -2272,7 +2273,7 @@ struct LargeRow {
   int tin, teq;    // candidates equal to T, logits equal to T
   uint32_t lo, hi; // key range of the candidates
   int s1;          // level-1 bucket shift
-  double m, inv_temp, S;
+  double m, inv_temp, S, inv_S;
 };
 
 __device__ __forceinline__ bool large_cand(const LargeRow &L, uint32_t key) {
@@ -2285,20 +2286,69 @@ __device__ __forceinline__ float large_prob(const LargeRow &L, float v) {
   return (float)((double)(float)p / L.S);
 }
 
-// Calls f(index, value) for every logit of the row (float4 loads when aligned).
+// exp(x) to about 1e-7 relative, for the passes over whole rows of the large
+// path: x * log2(e) is split in binary64 into an integer n and r in
+// [-1/2, 1/2]; 2^r comes from the hardware's binary32 exp2 and is scaled by
+// 2^n.  Its results feed the normaliser and the positions (cumProb) of rows
+// whose sums already run in another order than the reference's.
+__device__ __forceinline__ double exp_fast(double x) {
+  const double y = x * 1.4426950408889634074;   // log2(e)
+  if (!(y > -2000.0)) return y != y ? y : 0.0;   // NaN stays NaN; far below: 0
+  const double n = rint(y);
+  const float r = (float)(y - n);
+  return ldexp((double)__builtin_amdgcn_exp2f(r), (int)n);
+}
+
+// large_prob with exp_fast and a multiplication by 1/S: the probabilities
+// the large path locates with.
+__device__ __forceinline__ float large_pfast(const LargeRow &L, float v) {
+  const double p = exp_fast(((double)v - L.m) * L.inv_temp);
+  return (float)((double)(float)p * L.inv_S);
+}
+
+// Calls f(index, value) for every logit of the row.  Eight float4 (or, for
+// unaligned rows, eight logits) per thread are requested before any is used,
+// through a buffer resource: reads past the row return 0 and are skipped.
+// The reads are cached (not non-temporal): the path makes several passes
+// over a row, and the rows the GPU holds at once (607 KB each at V = 151936)
+// fit the last-level cache, so the passes after the first are served there.
 template <typename F>
 __device__ __forceinline__ void large_pass(const LargeRow &L, F f) {
+  constexpr int U = 8;
   const int tid = threadIdx.x;
   if (L.vec) {
     const int nfull = L.V >> 2;
-    const f32x4 *p4 = reinterpret_cast<const f32x4 *>(L.rowp);
-    for (int i = tid; i < nfull; i += kLT) {
-      const f32x4 t = __builtin_nontemporal_load(p4 + i);
-      f(4 * i, t[0]); f(4 * i + 1, t[1]); f(4 * i + 2, t[2]); f(4 * i + 3, t[3]);
+    const rsrc_t r4 = make_rsrc(L.rowp, 16u * (uint32_t)nfull);
+    for (int i0 = tid; i0 < nfull; i0 += U * kLT) {
+      f32x4 t[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const auto x = __builtin_amdgcn_raw_buffer_load_b128(r4, (i0 + u * kLT) * 16, 0, 0);
+        t[u] = f32x4{__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]),
+                     __uint_as_float(x[3])};
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * kLT;
+        if (i < nfull) {
+          f(4 * i, t[u][0]); f(4 * i + 1, t[u][1]); f(4 * i + 2, t[u][2]); f(4 * i + 3, t[u][3]);
+        }
+      }
     }
     for (int e = 4 * nfull + tid; e < L.V; e += kLT) f(e, L.rowp[e]);
   } else {
-    for (int e = tid; e < L.V; e += kLT) f(e, L.rowp[e]);
+    const rsrc_t r1 = make_rsrc(L.rowp, 4u * (uint32_t)L.V);
+    for (int e0 = tid; e0 < L.V; e0 += U * kLT) {
+      float t[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        t[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r1, (e0 + u * kLT) * 4, 0, 0));
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int e = e0 + u * kLT;
+        if (e < L.V) f(e, t[u]);
+      }
+    }
   }
 }
 
@@ -2385,7 +2435,7 @@ struct LargeLoc {
 };
 
 // The id of the j-th logit (index order) whose key equals `key`.
-__device__ int large_nth_equal(const LargeRow &L, uint32_t key, uint32_t j, LargeSmem &sm) {
+__device__ __forceinline__ int large_nth_equal(const LargeRow &L, uint32_t key, uint32_t j, LargeSmem &sm) {
   const int tid = threadIdx.x;
   const int span = (L.V + kLT - 1) / kLT;
   const int b0 = tid * span, b1 = min(L.V, b0 + span);
@@ -2414,16 +2464,32 @@ __device__ int large_nth_equal(const LargeRow &L, uint32_t key, uint32_t j, Larg
 // Gathers the candidates with keys in [klo, khi] into sm.buf (sm.nbuf counts
 // them, possibly past kLCap).  When more logits equal T than slots remain
 // for them, which ones the reference keeps depends on its slot history: they
-// are represented by `tin` placeholder entries (key T, id 0) instead.
-__device__ void large_gather(const LargeRow &L, uint32_t klo, uint32_t khi, LargeSmem &sm) {
+// are represented by `tin` placeholder entries (key T, id 0) instead.  With
+// s2 >= 0 the same pass also fills the sub-histogram sm.cnt2 / sm.mass2 of
+// the range by (key - klo) >> s2 (which must be cleared beforehand).
+__device__ __forceinline__ void large_gather(const LargeRow &L, uint32_t klo, uint32_t khi, LargeSmem &sm,
+                             int s2 = -1) {
   const bool btie = L.T != 0u && L.teq > L.tin;
   if (threadIdx.x == 0) sm.nbuf = 0;
   __syncthreads();
+  // [klo, khi] as a value range (klo >= lo >= T, so its logits are all
+  // candidates): two comparisons per logit, the key only for those inside.
+  // The value range holds the key range (at most also +-0 when an end key is
+  // the unused one below +0's), so the key is checked as well.
+  const float flo = key_floor(klo), fhi = key2f(khi);
   large_pass(L, [&](int e, float v) {
-    const uint32_t key = f2key(v);
-    if (large_cand(L, key) && key >= klo && key <= khi && !(btie && key == L.T)) {
-      const int p = atomicAdd(&sm.nbuf, 1);
-      if (p < kLCap) sm.buf[p] = pack_cand(key, (uint32_t)e);
+    if (v >= flo && v <= fhi) {
+      const uint32_t key = f2key(v);
+      if (key < klo || key > khi) return;
+      if (s2 >= 0) {
+        const uint32_t b = (key - klo) >> s2;
+        atomicAdd(&sm.cnt2[b], 1u);
+        atomicAdd(&sm.mass2[b], (double)large_pfast(L, v));
+      }
+      if (!(btie && key == L.T)) {
+        const int p = atomicAdd(&sm.nbuf, 1);
+        if (p < kLCap) sm.buf[p] = pack_cand(key, (uint32_t)e);
+      }
     }
   });
   __syncthreads();
@@ -2438,7 +2504,7 @@ __device__ void large_gather(const LargeRow &L, uint32_t klo, uint32_t khi, Larg
 
 // Finds the first position whose cumProb reaches `target` (kByMass) or the
 // position `pos` (kByPos).  sm.cnt / sm.mass hold the level-1 histogram.
-__device__ LargeLoc large_locate(const LargeRow &L, int mode, double target, uint32_t pos,
+__device__ __forceinline__ LargeLoc large_locate(const LargeRow &L, int mode, double target, uint32_t pos,
                                  LargeSmem &sm) {
   const int tid = threadIdx.x;
   LargeLoc r;
@@ -2481,19 +2547,21 @@ __device__ LargeLoc large_locate(const LargeRow &L, int mode, double target, uin
     sm.cnt2[tid] = 0;
     sm.mass2[tid] = 0;
     __syncthreads();
+    const float flo = key_floor(klo), fhi = key2f(khi);   // as in large_gather
     large_pass(L, [&](int, float v) {
-      const uint32_t key = f2key(v);
-      if (large_cand(L, key) && key >= klo && key <= khi) {
+      if (v >= flo && v <= fhi) {
+        const uint32_t key = f2key(v);
+        if (key < klo || key > khi) return;
         const uint32_t b = (key - klo) >> s2;
         atomicAdd(&sm.cnt2[b], 1u);
-        atomicAdd(&sm.mass2[b], (double)large_prob(L, v));
+        atomicAdd(&sm.mass2[b], (double)large_pfast(L, v));
       }
     });
     __syncthreads();
     if (tid == 0 && L.T && L.teq > L.tin && L.T >= klo && L.T <= khi) {
       const uint32_t b = (L.T - klo) >> s2;   // only `tin` of the T-valued logits count
       sm.cnt2[b] -= (uint32_t)(L.teq - L.tin);
-      sm.mass2[b] -= (double)(L.teq - L.tin) * (double)large_prob(L, key2f(L.T));
+      sm.mass2[b] -= (double)(L.teq - L.tin) * (double)large_pfast(L, key2f(L.T));
     }
     __syncthreads();
     const int b = kLSub - 1 - tid;
@@ -2522,7 +2590,7 @@ __device__ LargeLoc large_locate(const LargeRow &L, int mode, double target, uin
     // one value held by more logits than LDS sorts: equal probabilities,
     // index order (the reference's order when no slot was evicted)
     const uint32_t key = klo;
-    const float pv = large_prob(L, key2f(key));
+    const float pv = large_pfast(L, key2f(key));
     uint32_t j = 0;
     double c = Em;
     if (mode == kByPos) {
@@ -2539,17 +2607,109 @@ __device__ LargeLoc large_locate(const LargeRow &L, int mode, double target, uin
     r.id = large_nth_equal(L, key, j, sm);
     return r;
   }
-  // gather the bucket's logits, sort them, walk them in order
-  large_gather(L, klo, khi, sm);
+  // Gather the bucket's logits.  When it spans several keys and holds more
+  // than kLWalk candidates, the same pass builds its sub-histogram; only the
+  // sub-bucket holding the position is then kept, sorted and walked.
+  if (count > (uint32_t)kLWalk && klo < khi) {
+    int s2 = 0;
+    while (((khi - klo) >> s2) >= (uint32_t)kLSub) ++s2;
+    sm.cnt2[tid] = 0;
+    sm.mass2[tid] = 0;
+    __syncthreads();
+    large_gather(L, klo, khi, sm, s2);
+    if (tid == 0 && L.T && L.teq > L.tin && L.T >= klo && L.T <= khi) {
+      const uint32_t b = (L.T - klo) >> s2;   // only `tin` of the T-valued logits count
+      sm.cnt2[b] -= (uint32_t)(L.teq - L.tin);
+      sm.mass2[b] -= (double)(L.teq - L.tin) * (double)large_pfast(L, key2f(L.T));
+    }
+    __syncthreads();
+    const int b = kLSub - 1 - tid;
+    const uint32_t c = sm.cnt2[b];
+    const double m = sm.mass2[b];
+    uint32_t ec;
+    double em;
+    block_excl_scan2(c, m, &ec, &em, sm);
+    ec += Ec; em += Em;
+    if (tid == 0) sm.found = 0;
+    __syncthreads();
+    if (large_hit(mode, target, pos, ec, c, em, m)) {
+      sm.found = 1; sm.b = (uint32_t)b; sm.ecnt = ec; sm.emass = em;
+    }
+    __syncthreads();
+    if (sm.found) {   // else: rounding at the bucket's edge, walk it whole
+      const uint32_t nlo = klo + (sm.b << s2);
+      khi = (khi - nlo) >> s2 ? nlo + ((1u << s2) - 1u) : khi;
+      klo = nlo;
+      count = sm.cnt2[sm.b];
+      Ec = sm.ecnt;
+      Em = sm.emass;
+      // keep the gathered entries of the sub-bucket (through pbuf's storage)
+      unsigned long long *tmp = reinterpret_cast<unsigned long long *>(sm.pbuf);
+      const int nall = min(sm.nbuf, kLCap);
+      __syncthreads();
+      if (tid == 0) sm.hit = 0;
+      __syncthreads();
+      for (int i = tid; i < nall; i += kLT) {
+        const unsigned long long e = sm.buf[i];
+        const uint32_t key = cand_key(e);
+        if (key >= klo && key <= khi) tmp[atomicAdd(&sm.hit, 1)] = e;
+      }
+      __syncthreads();
+      const int nk = sm.hit;
+      for (int i = tid; i < nk; i += kLT) sm.buf[i] = tmp[i];
+      if (tid == 0) sm.nbuf = nk;
+      __syncthreads();
+    }
+  } else {
+    large_gather(L, klo, khi, sm);
+  }
   const int nb = min(sm.nbuf, kLCap);
-  int P2 = 1;
-  while (P2 < nb) P2 <<= 1;
-  for (int i = nb + tid; i < P2; i += kLT) sm.buf[i] = 0ull;
-  __syncthreads();
-  block_sort_desc<kLT>(sm.buf, P2);
-  for (int i = tid; i < nb; i += kLT) sm.pbuf[i] = (double)large_prob(L, key2f(cand_key(sm.buf[i])));
-  __syncthreads();
-  if (tid == 0) {
+  sort_packed<kLT>(sm.buf, nb);
+  // T-valued logits past `tin` are not candidates (the list holds at most tin)
+  const int nv = nb < (int)count ? nb : (int)count;
+  if (tid == 0) sm.hit = nv;
+  int bad = 0;
+  for (int i = tid; i < nv; i += kLT) {
+    const float pf = large_pfast(L, key2f(cand_key(sm.buf[i])));
+    sm.pbuf[i] = (double)pf;
+    bad |= !((double)pf == 0.0 || ((double)pf >= 0x1p-29 && (double)pf <= 1.0));
+  }
+  if (!__syncthreads_or(bad)) {
+    // Every probability is a multiple of 2^-52: the prefix sums are exact in
+    // any order (see wave_tail), so the walk is a block prefix sum; pbuf[i]
+    // becomes cumProb through position Ec + i.
+    const int lane = tid & 63, wave = tid >> 6;
+    double carry = Em;
+    for (int base = 0; base < nv; base += kLT) {
+      const int i = base + tid;
+      double c = wave_scan_incl_f64(i < nv ? sm.pbuf[i] : 0.0);
+      __syncthreads();
+      if (lane == 63) sm.dred[wave] = c;
+      __syncthreads();
+      double add = carry, tot = carry;
+      for (int w = 0; w < kLT / 64; ++w) {
+        if (w < wave) add += sm.dred[w];
+        tot += sm.dred[w];
+      }
+      c += add;
+      if (i < nv) {
+        sm.pbuf[i] = c;
+        if (mode == kByPos ? Ec + (uint32_t)i == pos : c >= target) atomicMin(&sm.hit, i);
+      }
+      carry = tot;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      const int hit = sm.hit < nv ? sm.hit : (nv > 0 ? nv - 1 : 0);   // past the end: its last logit
+      const uint32_t key = cand_key(sm.buf[hit]);
+      sm.pos = (int)Ec + hit;
+      sm.id = (int)cand_idx(sm.buf[hit]);
+      sm.key = key;
+      sm.cum = nv > 0 ? sm.pbuf[hit] : Em;
+      sm.tie = (hit > 0 && cand_key(sm.buf[hit - 1]) == key) ||
+               (hit + 1 < nb && cand_key(sm.buf[hit + 1]) == key);
+    }
+  } else if (tid == 0) {
     double c = Em;
     int hit = -1, tseen = 0;
     const int avail = (int)count;   // T-valued logits past `tin` are not candidates
@@ -2588,22 +2748,20 @@ __global__ __launch_bounds__(kLT) void large_kernel(LaunchArgs a, Workspace ws) 
   L.T = 1u;       // every finite logit, for the first passes
   L.tin = L.teq = 0;
 
-  // 1. extremes and n_F
-  unsigned long long best = 0;
-  unsigned long long kmin_neg = 0;   // max of ~key = min key
-  unsigned long long nf = 0;
+  // 1. extremes and n_F.  A thread meets its logits in index order, so its
+  // first maximum is kept by the strict comparison.
+  uint32_t bkey = 0, bidx = 0, kmin = 0xFFFFFFFFu, nf = 0;
   large_pass(L, [&](int e, float v) {
     const uint32_t key = f2key(v);
-    if (key) {
-      const unsigned long long c = pack_cand(key, (uint32_t)e);
-      best = c > best ? c : best;
-      const unsigned long long nk = (unsigned long long)(~key);
-      kmin_neg = nk > kmin_neg ? nk : kmin_neg;
-      ++nf;
-    }
+    const bool gt = key > bkey;
+    bkey = gt ? key : bkey;
+    bidx = gt ? (uint32_t)e : bidx;
+    const uint32_t km = key ? key : 0xFFFFFFFFu;
+    kmin = km < kmin ? km : kmin;
+    nf += key != 0u;
   });
-  best = block_max_u64(best, sm);
-  const uint32_t kmin = ~(uint32_t)block_max_u64(kmin_neg, sm);
+  const unsigned long long best = block_max_u64(bkey ? pack_cand(bkey, bidx) : 0ull, sm);
+  const uint32_t kmin_all = ~(uint32_t)block_max_u64((unsigned long long)(~kmin), sm);
   const int n_f = (int)block_sum_u64(nf, sm);
   const int k = P.k;
   const int n = k < n_f ? k : n_f;
@@ -2669,44 +2827,51 @@ __global__ __launch_bounds__(kLT) void large_kernel(LaunchArgs a, Workspace ws) 
     L.T = prefix;
     L.tin = rem;            // k - #(> T) slots left for the T-valued logits
   }
-  L.lo = L.T ? L.T : kmin;
+  L.lo = L.T ? L.T : kmin_all;
   L.hi = cand_key(best);
   L.s1 = 0;
   while (((L.hi - L.lo) >> L.s1) >= (uint32_t)kLBins) ++L.s1;
   L.m = (double)key2f(L.hi);
   L.inv_temp = 1.0 / P.temperature;
 
-  // 3. normaliser and level-1 histogram
+  // 3. normaliser and level-1 histogram in one pass.  A bucket sums the
+  // binary32-rounded exp values and is divided by S afterwards: its mass then
+  // differs from the sum of its binary32 probabilities by their rounding only.
+  for (int i = tid; i < kLBins; i += kLT) { sm.cnt[i] = 0; sm.mass[i] = 0; }
+  __syncthreads();
   double s = 0;
   large_pass(L, [&](int, float v) {
     const uint32_t key = f2key(v);
-    if (key != 0u && key > L.T) s += exp(((double)v - L.m) * L.inv_temp);
-  });
-  L.S = block_sum_f64(s, sm);
-  if (L.T) L.S += (double)L.tin * exp(((double)key2f(L.T) - L.m) * L.inv_temp);
-  const float prob0 = large_prob(L, key2f(L.hi));
-  const double thr = P.min_p * (double)prob0;
-  for (int i = tid; i < kLBins; i += kLT) { sm.cnt[i] = 0; sm.mass[i] = 0; }
-  __syncthreads();
-  unsigned long long nlt = 0;   // candidates with !(prob < thr), src/sampler.ts:96
-  large_pass(L, [&](int, float v) {
-    const uint32_t key = f2key(v);
     if (key != 0u && key > L.T) {
-      const float pr = large_prob(L, v);
+      const double p = exp_fast(((double)v - L.m) * L.inv_temp);
+      s += p;
       const uint32_t b = (key - L.lo) >> L.s1;
       atomicAdd(&sm.cnt[b], 1u);
-      atomicAdd(&sm.mass[b], (double)pr);
-      nlt += !((double)pr < thr);
+      atomicAdd(&sm.mass[b], (double)(float)p);
     }
   });
-  nlt = block_sum_u64(nlt, sm);
-  if (L.T) {
-    const float pt = large_prob(L, key2f(L.T));
-    if (tid == 0) {
-      sm.cnt[0] += (uint32_t)L.tin;   // T is the lowest candidate key: bucket 0
-      sm.mass[0] += (double)L.tin * (double)pt;
-    }
-    nlt += !((double)pt < thr) ? (unsigned long long)L.tin : 0ull;
+  const double pT = L.T ? exp_fast(((double)key2f(L.T) - L.m) * L.inv_temp) : 0.0;
+  L.S = block_sum_f64(s, sm) + (double)L.tin * pT;   // ends with a barrier
+  L.inv_S = 1.0 / L.S;
+  if (tid == 0 && L.T) {
+    sm.cnt[0] += (uint32_t)L.tin;   // T is the lowest candidate key: bucket 0
+    sm.mass[0] += (double)L.tin * (double)(float)pT;
+  }
+  __syncthreads();
+  for (int i = tid; i < kLBins; i += kLT) sm.mass[i] *= L.inv_S;
+  const float prob0 = large_pfast(L, key2f(L.hi));
+  const double thr = P.min_p * (double)prob0;
+  // candidates with !(prob < thr) (src/sampler.ts:96): all of them unless
+  // thr > 0, which needs one more pass
+  unsigned long long nlt = (unsigned long long)n;
+  if (thr > 0.0) {
+    nlt = 0;
+    large_pass(L, [&](int, float v) {
+      const uint32_t key = f2key(v);
+      if (key != 0u && key > L.T) nlt += !((double)large_pfast(L, v) < thr);
+    });
+    nlt = block_sum_u64(nlt, sm);
+    if (L.T) nlt += !((double)large_pfast(L, key2f(L.T)) < thr) ? (unsigned long long)L.tin : 0ull;
   }
   __syncthreads();
 
@@ -2714,16 +2879,21 @@ __global__ __launch_bounds__(kLT) void large_kernel(LaunchArgs a, Workspace ws) 
   int f1 = 1 + (int)nlt - (!((double)prob0 < thr) ? 1 : 0);
   f1 = f1 < 1 ? 1 : (f1 > n ? n : f1);
   int f2 = n;
+  LargeLoc f2_loc;
+  f2_loc.found = false;
   if (P.top_p <= 0.0) {
     f2 = 0;   // cumProb >= topP at the first index
   } else {
-    const LargeLoc ltop = large_locate(L, kByMass, P.top_p, 0u, sm);
-    if (ltop.found) f2 = ltop.pos;
+    f2_loc = large_locate(L, kByMass, P.top_p, 0u, sm);
+    if (f2_loc.found) f2 = f2_loc.pos;
   }
   int cut = f1 <= f2 ? f1 : f2 + 1;
   cut = cut > n ? n : cut;
-  // src/sampler.ts:107-116: keptSum = cumProb at cutoff - 1, then the draw
-  const LargeLoc lkept = large_locate(L, kByPos, 0.0, (uint32_t)(cut - 1), sm);
+  // src/sampler.ts:107-116: keptSum = cumProb at cutoff - 1 (the top-p
+  // position itself when the top-p stop sets the cutoff), then the draw
+  const LargeLoc lkept = cut == f2 + 1 && f2_loc.found
+                             ? f2_loc
+                             : large_locate(L, kByPos, 0.0, (uint32_t)(cut - 1), sm);
   const double target = a.uniforms[row] * lkept.cum;
   LargeLoc lpick = large_locate(L, kByMass, target, 0u, sm);
   if (!lpick.found || lpick.pos >= cut) lpick = lkept;
