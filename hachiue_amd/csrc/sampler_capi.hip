@@ -7,6 +7,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <new>
 #include <string>
@@ -71,6 +72,7 @@ struct hs_context {
   int device = 0;
   // workspace
   DevBuf plans, cand, cand_count, info;
+  DevBuf split_list, split_meta, split_cnt;   // split rows (split_cnt: zero between calls)
   int64_t cand_count_rows = 0;     // rows whose counter is known to be zero
   // plan upload cache
   std::vector<hs::RowPlan> last_plans;
@@ -93,6 +95,8 @@ struct hs_context {
   double kernel_ms[hs::kTimedKernels] = {};
   // rows routed to the row kernel only when a call has at least this many
   int row_min_rows = 1;
+  // workgroups per row of the row kernel: 0 chooses by batch size
+  int row_split = 0;
   int64_t timed_calls = 0;
 };
 
@@ -277,6 +281,27 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
       HS_HIP(hipMemset(ctx->cand_count.p, 0, ctx->cand_count.bytes));
     }
   }
+  // Small batches split each row of the row kernel over several workgroups
+  // (parts of whole float4s), so that the launch fills the CUs.
+  // HS_ROW_SPLIT (read at context creation) forces the count, whatever the
+  // part size.  Every part holds at least one float4.
+  int split = 1;
+  if (n_row > 0) {
+    split = ctx->row_split > 0 ? ctx->row_split
+                               : std::min(hs::kSplitCUs / n_row, vocab / hs::kSplitMinPart);
+    const int nf4 = (vocab + 3) / 4;
+    split = std::max(1, std::min(split, std::min(hs::kSplitMax, nf4)));
+    while (split > 1 && (split - 1) * ((nf4 + split - 1) / split) >= nf4) --split;
+  }
+  if (split > 1) {
+    const size_t parts = (size_t)n_row * (size_t)split;
+    HS_HIP(ctx->split_list.ensure(parts * hs::kPartCap * sizeof(unsigned long long)));
+    HS_HIP(ctx->split_meta.ensure(parts * sizeof(hs::SplitMeta)));
+    if (ctx->split_cnt.bytes < sizeof(uint32_t) * (size_t)n_row) {
+      HS_HIP(ctx->split_cnt.ensure(sizeof(uint32_t) * (size_t)n_row));
+      HS_HIP(hipMemset(ctx->split_cnt.p, 0, ctx->split_cnt.bytes));
+    }
+  }
   int rc = upload_plans(ctx, plans, rt, vocab, stream);
   if (rc) return rc;
 
@@ -291,6 +316,9 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   ws.cand = static_cast<uint2 *>(ctx->cand.p);
   ws.cand_count = static_cast<int32_t *>(ctx->cand_count.p);
   ws.info = static_cast<hs::ChunkInfo *>(ctx->info.p);
+  ws.split_list = static_cast<unsigned long long *>(ctx->split_list.p);
+  ws.split_meta = static_cast<hs::SplitMeta *>(ctx->split_meta.p);
+  ws.split_cnt = static_cast<uint32_t *>(ctx->split_cnt.p);
 
   hs::LaunchArgs a;
   memset(&a, 0, sizeof a);
@@ -303,6 +331,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   a.want_cands = (d_cand_ids || d_cand_probs) ? 1 : 0;
   a.n_pf = n_pf;
   a.n_row = n_row;
+  a.split = split;
   a.rows_direct = n_row == rows ? 1 : 0;
   a.n_chunk = n_chunk;
   a.n_large = n_large;
@@ -337,6 +366,8 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   if (e != hipSuccess) {
     if (ctx->cand_count.p)
       (void)hipMemsetAsync(ctx->cand_count.p, 0, ctx->cand_count.bytes, stream);
+    if (ctx->split_cnt.p)
+      (void)hipMemsetAsync(ctx->split_cnt.p, 0, ctx->split_cnt.bytes, stream);
     return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
   }
   return HS_OK;
@@ -384,6 +415,7 @@ int hs_context_create(int device, hs_context **out) {
   if (!ctx) return fail(HS_ERR_OUT_OF_MEMORY, "host allocation failed");
   ctx->device = device;
   if (const char *env = getenv("HS_ROW_KERNEL_MIN_ROWS")) ctx->row_min_rows = atoi(env);
+  if (const char *env = getenv("HS_ROW_SPLIT")) ctx->row_split = atoi(env);
   e = hipEventCreateWithFlags(&ctx->plan_done, hipEventDisableTiming);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
@@ -438,6 +470,9 @@ int hs_context_destroy(hs_context *ctx) {
     ctx->cand.release();
     ctx->cand_count.release();
     ctx->info.release();
+    ctx->split_list.release();
+    ctx->split_meta.release();
+    ctx->split_cnt.release();
     ctx->h_logits.release();
     ctx->h_hist.release();
     ctx->h_off.release();

@@ -18,6 +18,12 @@ constexpr int kRoundF4 = kRowThreads * kRowNV;   // float4 per later round
 constexpr int kRowCandCap = 4096;                // streamed candidates per row
 constexpr int kSegCap = kRowCandCap / kRowWaves; // of them per wave (its own segment)
 constexpr int kRowMaxVocab = 1 << 19;            // LDS bitmap limit (64 KiB)
+// Small batches split each row over kSplitMax workgroups at most (parts of at
+// least kSplitMinPart logits), so that the batch fills the GPU's CUs.
+constexpr int kSplitMax = 16;
+constexpr int kSplitMinPart = 16384;
+constexpr int kSplitCUs = 256;                   // workgroups a split call aims at
+constexpr int kPartCap = 64;                     // candidates a part hands over (its top 64)
 
 // ---- mid kernel (64 < k <= 1024): the row kernel's stream with a key
 // histogram of kMidBins bins (the top 13 key bits: 1/16 octave) for the bound.
@@ -82,6 +88,16 @@ struct ChunkInfo {
 };
 static_assert(sizeof(ChunkInfo) == 24, "ChunkInfo layout");
 
+// What a part of a split row hands over to the part that completes the row.
+struct SplitMeta {
+  unsigned long long best;   // greedy: packed maximum (global index), 0 = none
+  int32_t count;             // candidates in the part's list, -1: overflowed
+  uint32_t theta;            // their lower bound (a bound of the row's k-th largest)
+  uint32_t key64;            // key of the part's 65th largest candidate (0: none)
+  uint32_t pad;
+};
+static_assert(sizeof(SplitMeta) == 24, "SplitMeta layout");
+
 struct Workspace {
   RowPlan *plans;            // [rows]
   const int32_t *pf_list;    // rows penalised by the pre-pass
@@ -92,6 +108,9 @@ struct Workspace {
   uint2 *cand;               // [n_chunk][S][kChunkCap] (key, index)
   int32_t *cand_count;       // [n_chunk]
   ChunkInfo *info;           // [n_chunk][S]
+  unsigned long long *split_list;   // [n_row][split][kPartCap] packed candidates
+  SplitMeta *split_meta;            // [n_row][split]
+  uint32_t *split_cnt;              // [n_row] parts arrived (0 between calls)
 };
 
 struct LaunchArgs {
@@ -104,6 +123,7 @@ struct LaunchArgs {
   int32_t want_cands;        // exact candidate order must be produced
   int32_t rows_direct;       // the row kernel takes every row: row = block index
   int32_t n_pf, n_row, n_chunk, n_large, n_mid;
+  int32_t split;             // row kernel: workgroups per row (1: whole rows)
   const int32_t *hist_ids;
   const int64_t *hist_off;
   const double *uniforms;

@@ -18,11 +18,17 @@
 //                    value (the exact k-th largest of the 1024 lane maxima);
 //                    every logit at or above it is appended to an LDS
 //                    candidate list.  The workgroup then ranks, samples and
-//                    writes the row itself: one HBM pass, one launch.
-//   chunk_kernel     rows with 64 < k <= 1024 (and k <= 64 rows the row
-//                    kernel does not take), grid rows*S, 256 threads: a chunk
-//                    of 16384 logits in registers, exact chunk k-th largest by
-//                    block radix select, candidates to a per-row list.
+//                    writes the row itself: one HBM pass, one launch.  Small
+//                    batches split each row over up to 16 workgroups; the
+//                    last part to finish merges the parts' top-64 lists.
+//   mid_kernel       rows with 64 < k <= 1024 (and, in calls that launch it,
+//                    the k <= 64 rows): the row kernel's stream with the
+//                    bound from an LDS key histogram.
+//   chunk_kernel     rows of vocabularies above 512K (and calls below the
+//                    row kernel's minimum batch), grid rows*S, 256 threads: a
+//                    chunk of 16384 logits in registers, exact chunk k-th
+//                    largest by block radix select, candidates to a per-row
+//                    list.
 //   finalize_kernel  one workgroup per chunk-kernel row: exact select over the
 //                    row's candidates, then the shared row completion.
 //   large_kernel     rows with k > 1024: one 1024-thread workgroup per row,
@@ -781,10 +787,11 @@ __device__ __forceinline__ void finish_row(const LaunchArgs &a, const RowPlan &P
 
 // Writes the greedy result: first index of the maximum (src/sampler.ts:37-45);
 // `best` is the packed maximum over the row (0 = no non-NaN logit).
-__device__ __forceinline__ void write_greedy(const LaunchArgs &a, int row, const float *rowp,
+// x0: the row's (penalised) logit 0.
+__device__ __forceinline__ void write_greedy(const LaunchArgs &a, int row, float x0,
                              unsigned long long best) {
   int token = best ? (int)cand_idx(best) : 0;
-  if (isnan(rowp[0])) token = 0;   // bestVal = logits[0] = NaN: nothing is '>' it
+  if (isnan(x0)) token = 0;   // bestVal = logits[0] = NaN: nothing is '>' it
   a.tokens[row] = token;
   if (a.cand_count_out) a.cand_count_out[row] = 0;
   if (a.cutoff_out) a.cutoff_out[row] = 0;
@@ -1262,9 +1269,11 @@ __device__ __forceinline__ int wave_tail(uint32_t key, int n, const RowPlan &P, 
 // k-th largest may exist beyond F.  Replays the reference's slot scan when an
 // equal-value group can change the token (or the candidate outputs), and
 // always when force_replay (the candidate list overflowed).
+// acquire_replay: other workgroups wrote parts of the row (split rows), so a
+// replay first acquires their stores at agent scope.
 __device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &P, int row, const float *rowp,
                             unsigned long long F, bool extra_ties, bool force_replay, double u,
-                            float *rsv, int32_t *rsid, double *sp) {
+                            float *rsv, int32_t *rsid, double *sp, bool acquire_replay = false) {
   const int lane = lane_id();
   const int k = P.k;
   const uint32_t fkey = cand_key(F);
@@ -1292,6 +1301,7 @@ __device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &
       need = (pick > 0 && km == kp) || (pick + 1 < n && kn == kp) || (boundary_tie && kp == T);
     }
     if (need) {
+      if (acquire_replay) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       replay_row(rowp, a.vocab, k, rsv, rsid);
       const bool filled = lane < k && rsid[lane] >= 0;
       unsigned long long x = filled ? pack_cand(f2key(rsv[lane]), (uint32_t)lane) : 0ull;
@@ -1329,6 +1339,72 @@ size_t row_smem_bytes(int vocab) {
          words * 4;
 }
 
+// ---- split rows: a part's hand-over
+//
+// A part publishes its list (candidates with global indices) and meta data
+// with agent-scope stores, which write through to the point where every XCD
+// sees them, waits until its own stores have completed, and only then counts
+// itself in.  The part that counts S reads the others' data after an
+// agent-scope acquire and completes the row; no workgroup ever waits for
+// another.  The last part also resets the counter for the next call.
+__device__ __forceinline__ void store_agent(unsigned long long *p, unsigned long long v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(uint32_t *p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(int32_t *p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T>
+__device__ __forceinline__ T load_agent(const T *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Counts the calling part in (after its published stores completed); true
+// in the part that completes the row.  That part reads what the others
+// published with agent-scope loads, issued only after the count returned,
+// so they observe every store completed before the others counted
+// themselves in.  (No acquire fence: on this GPU it invalidates the XCD's
+// L2, which stalls every workgroup there; plain loads of shared data need
+// it, as before a replay of the row.)  `last` is LDS.  Every thread of the
+// workgroup calls it.
+__device__ __forceinline__ bool split_arrive(const Workspace &ws, int slot, int S, int32_t *last) {
+  __builtin_amdgcn_s_waitcnt(0);   // this thread's stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t old =
+        __hip_atomic_fetch_add(ws.split_cnt + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *last = old == (uint32_t)(S - 1);
+    if (*last) store_agent(ws.split_cnt + slot, 0u);   // for the next call
+  }
+  __syncthreads();
+  return *last != 0;
+}
+
+// Top 64 of two descending lists of 64 packed candidates (one per lane), by
+// one wave: the elementwise maximum of a and b reversed is bitonic and holds
+// the 64 largest, a half-cleaner cascade sorts it.  `disc` keeps the largest
+// key left out (per lane).
+__device__ __forceinline__ unsigned long long merge_top64(unsigned long long a, unsigned long long b,
+                                                          uint32_t &disc) {
+  const int lane = lane_id();
+  const unsigned long long br = __shfl(b, 63 - lane);
+  unsigned long long c = a > br ? a : br;
+  const uint32_t dk = cand_key(a > br ? br : a);
+  disc = dk > disc ? dk : disc;
+#pragma unroll
+  for (int j = 32; j >= 1; j >>= 1) {
+    const unsigned long long o = __shfl_xor(c, j);
+    c = (lane & j) ? (o < c ? o : c) : (o > c ? o : c);
+  }
+  return c;
+}
+
 struct RowSmem {
   SelectSmem sel;
   TailSmem tail;
@@ -1336,10 +1412,13 @@ struct RowSmem {
   uint32_t t_min, theta, key64;
   uint32_t theta2;             // refined bound, published by wave 0 mid-row
   int32_t wcnt[kRowWaves];     // candidates each wave has appended (published)
-  int32_t n_l, n_f, ovf, done;
+  int32_t n_l, n_f, ovf, done, last;
 };
 
-template <bool VEC>
+// SPLIT: a.split workgroups share a row, each streaming one part of it (a
+// run of whole float4s) as if it were a row of its own; the last part to
+// finish merges the parts' candidates and completes the row.
+template <bool VEC, bool SPLIT>
 __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspace ws) {
   extern __shared__ unsigned long long rdyn[];
   unsigned long long *cbuf = rdyn;                         // kRowCandCap candidates
@@ -1352,9 +1431,19 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   __shared__ RowSmem rs;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = uniform_i32(tid >> 6);
-  const int row = a.rows_direct ? (int)blockIdx.x : ws.row_list[blockIdx.x];
-  float *rowp = a.logits + (int64_t)row * a.stride;
-  const int V = a.vocab;
+  int slot = (int)blockIdx.x, part = 0, eoff = 0, V = a.vocab;
+  if (SPLIT) {   // this part: logits [eoff, eoff + V) of the row
+    const int S = a.split;
+    slot = (int)blockIdx.x / S;
+    part = (int)blockIdx.x - slot * S;
+    const int nf4 = (a.vocab + 3) >> 2, per = (nf4 + S - 1) / S;
+    const int f0 = min(nf4, part * per), f1 = min(nf4, f0 + per);
+    eoff = 4 * f0;
+    V = min(a.vocab, 4 * f1) - eoff;
+  }
+  const int row = a.rows_direct ? slot : ws.row_list[slot];
+  float *const rowfull = a.logits + (int64_t)row * a.stride;
+  float *rowp = rowfull + eoff;
   const int nr = row_rounds(V);
 
   // The last <= 128 history ids, one per thread of waves 0-1, are requested
@@ -1426,7 +1515,7 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     const int words = (V + 31) >> 5;
     for (int i = tid; i < words; i += kRowThreads) bitmap[i] = 0;
     __syncthreads();
-    const int hid = tid < hist_n ? hraw : -1;
+    const int hid = tid < hist_n ? hraw - eoff : -1;   // relative to the part
     if (hid >= 0 && hid < V) {
       const uint32_t bit = 1u << (hid & 31);
       if (!(atomicOr(&bitmap[hid >> 5], bit) & bit)) pid = hid;   // the first occurrence owns the id
@@ -1528,7 +1617,10 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     pr.rep = prep;
     pr.pen = kPenRep;
     pv = penalise(pval, true, 0u, pr);
-    rowp[pid] = pv;
+    if (SPLIT)
+      store_agent(rowp + pid, pv);   // read by the part that completes the row
+    else
+      rowp[pid] = pv;
   }
 
   // the tail logits (thread 0) outside the repetition set
@@ -1557,7 +1649,18 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     if (tid == 0) {
       unsigned long long bb = rs.best[0];
       for (int w = 1; w < kRowWaves; ++w) bb = rs.best[w] > bb ? rs.best[w] : bb;
-      write_greedy(a, row, rowp, bb);
+      if (SPLIT)   // the same packed form with the row's index (no borrow: idx + eoff < 2^32)
+        store_agent(&ws.split_meta[blockIdx.x].best, bb ? bb - (unsigned long long)eoff : 0ull);
+      else
+        write_greedy(a, row, rowp[0], bb);
+    }
+    if (SPLIT && split_arrive(ws, slot, a.split, &rs.last) && tid == 0) {
+      unsigned long long bb = 0;
+      for (int p = 0; p < a.split; ++p) {
+        const unsigned long long b = load_agent(&ws.split_meta[slot * a.split + p].best);
+        bb = b > bb ? b : bb;
+      }
+      write_greedy(a, row, load_agent(rowfull), bb);
     }
     return;
   }
@@ -1615,6 +1718,80 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   bool overflow = rs.ovf != 0 || n_all > kSortCap;
   unsigned long long F = 0;
   bool extra = false;
+  if (SPLIT) {
+    // The part hands over its top 64 (every logit of the row's top k, k <= 64,
+    // is among the top k of its part) and the key of its 65th, which flags
+    // values equal to the row's k-th largest left out of the list.
+    const int S = a.split;
+    overflow = overflow || n_all > kRowThreads;   // ties beyond the ranking's reach: replay
+    if (!overflow) rank_top64(srt, n_all, top, &rs.key64);
+    if (wave == 0) {
+      SplitMeta *m = ws.split_meta + blockIdx.x;
+      const unsigned long long c = top[lane];
+      if (!overflow && lane < n_all)
+        store_agent(ws.split_list + (int64_t)blockIdx.x * kPartCap + lane, c - (unsigned long long)eoff);
+      if (lane == 0) {
+        store_agent(&m->count, overflow ? -1 : min(n_all, kPartCap));
+        store_agent(&m->theta, lo);
+        store_agent(&m->key64, rs.key64);
+      }
+    }
+    if (!split_arrive(ws, slot, S, &rs.last)) return;
+    // The last part: the top 64 of the union of the parts' lists, by a tree
+    // of pairwise merges (wave w merges lists 2w and 2w + 1).  The parts'
+    // meta data and the first level's lists are requested together.
+    const SplitMeta *m0 = ws.split_meta + (int64_t)slot * S;
+    const unsigned long long *l0 = ws.split_list + (int64_t)slot * S * kPartCap;
+    int cntp = 0;
+    uint32_t k64 = 0;
+    if (lane < S) {
+      cntp = load_agent(&m0[lane].count);
+      k64 = load_agent(&m0[lane].key64);
+    }
+    unsigned long long ea = 0, eb = 0;
+    if (2 * wave < S) ea = load_agent(l0 + (2 * wave) * kPartCap + lane);
+    if (2 * wave + 1 < S) eb = load_agent(l0 + (2 * wave + 1) * kPartCap + lane);
+    overflow = __ballot(cntp < 0) != 0;   // a part's list is incomplete: replay
+    if (lane >= __shfl(cntp, (2 * wave) & 63)) ea = 0ull;        // entries past a count are stale
+    if (lane >= __shfl(cntp, (2 * wave + 1) & 63)) eb = 0ull;
+    uint32_t disc = 0;
+    unsigned long long c = 0;
+    int L = (S + 1) / 2;   // lists after this level
+    if (2 * wave < S) c = merge_top64(ea, eb, disc);
+    for (int lvl = 0; L > 1; ++lvl) {
+      unsigned long long *buf = srt + (lvl & 1) * (kSortCap / 2);   // 16 lists of 64 each
+      if (wave < L) buf[wave * 64 + lane] = c;
+      __syncthreads();
+      const int L2 = (L + 1) / 2;
+      if (wave < L2) {
+        const unsigned long long x = buf[(2 * wave) * 64 + lane];
+        const unsigned long long y = 2 * wave + 1 < L ? buf[(2 * wave + 1) * 64 + lane] : 0ull;
+        c = merge_top64(x, y, disc);
+      }
+      L = L2;
+    }
+    disc = wave_max_u32(disc);
+    if (tid == 0) rs.key64 = 0;
+    __syncthreads();
+    if (lane == 0 && disc) atomicMax(&rs.key64, disc);
+    __syncthreads();
+    if (wave != 0) return;
+    if (!overflow) {
+      F = c;
+      const uint32_t Tk = cand_key(__shfl(F, k - 1));
+      // the union's 65th, or a part's own 65th, equal to the row's k-th
+      // largest: more values equal to it may exist beyond F
+      extra = Tk != 0u && (rs.key64 == Tk || __ballot(lane < S && k64 == Tk) != 0);
+    }
+    RowPlan P;
+    P.temperature = temperature;
+    P.top_p = top_p;
+    P.min_p = min_p;
+    P.k = k;
+    finish_wave(a, P, row, rowfull, F, extra, overflow, u, rsv, rsid,
+                reinterpret_cast<double *>(top), true);
+    return;
+  }
   if (!overflow && n_all <= kRowThreads) {
     rank_top64(srt, n_all, top, &rs.key64);
     if (wave != 0) return;
@@ -2172,7 +2349,7 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(LaunchArgs a, Worksp
     if (tid == 0) {
       unsigned long long b = f.red[0];
       for (int w = 1; w < kWaves; ++w) b = f.red[w] > b ? f.red[w] : b;
-      write_greedy(a, row, rowp, b);
+      write_greedy(a, row, rowp[0], b);
     }
     return;
   }
@@ -2969,12 +3146,14 @@ hipError_t prepare_kernels() {
   if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&pen_kernel),
                                hipFuncAttributeMaxDynamicSharedMemorySize, pen_smem)) != hipSuccess)
     return e;
-  if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&row_kernel<true>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, row_smem)) != hipSuccess)
-    return e;
-  if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&row_kernel<false>),
-                               hipFuncAttributeMaxDynamicSharedMemorySize, row_smem)) != hipSuccess)
-    return e;
+  const void *row_k[4] = {reinterpret_cast<const void *>(&row_kernel<true, false>),
+                          reinterpret_cast<const void *>(&row_kernel<false, false>),
+                          reinterpret_cast<const void *>(&row_kernel<true, true>),
+                          reinterpret_cast<const void *>(&row_kernel<false, true>)};
+  for (const void *f : row_k)
+    if ((e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, row_smem)) !=
+        hipSuccess)
+      return e;
   const int mid_smem = (int)mid_smem_bytes(kRowMaxVocab);
   if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mid_kernel<true>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, mid_smem)) != hipSuccess)
@@ -3017,10 +3196,15 @@ hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t s
   }
   if (a.n_row > 0) {
     const size_t smem = row_smem_bytes(a.vocab);
-    e = a.vec ? launch_one(row_kernel<true>, dim3((unsigned)a.n_row), dim3(kRowThreads), smem,
-                           stream, ev, 1, a, ws)
-              : launch_one(row_kernel<false>, dim3((unsigned)a.n_row), dim3(kRowThreads), smem,
-                           stream, ev, 1, a, ws);
+    if (a.split > 1) {
+      const dim3 grid((unsigned)(a.n_row * a.split));
+      e = a.vec ? launch_one(row_kernel<true, true>, grid, dim3(kRowThreads), smem, stream, ev, 1, a, ws)
+                : launch_one(row_kernel<false, true>, grid, dim3(kRowThreads), smem, stream, ev, 1, a, ws);
+    } else {
+      const dim3 grid((unsigned)a.n_row);
+      e = a.vec ? launch_one(row_kernel<true, false>, grid, dim3(kRowThreads), smem, stream, ev, 1, a, ws)
+                : launch_one(row_kernel<false, false>, grid, dim3(kRowThreads), smem, stream, ev, 1, a, ws);
+    }
     if (e != hipSuccess) return e;
   }
   if (a.n_mid > 0) {
