@@ -229,6 +229,70 @@ int upload_plans(hs_context *ctx, const std::vector<hs::RowPlan> &plans, const R
   return HS_OK;
 }
 
+// Workgroups per row for `rows` rows streamed one workgroup per part: small
+// batches split each row (parts of whole float4s) so that the launch fills the
+// CUs.  HS_ROW_SPLIT (read at context creation) forces the count, whatever
+// the part size.  Every part holds at least one float4.
+int choose_split(const hs_context *ctx, int rows, int vocab) {
+  if (rows <= 0) return 1;
+  int split = ctx->row_split > 0 ? ctx->row_split
+                                 : std::min(hs::kSplitCUs / rows, vocab / hs::kSplitMinPart);
+  const int nf4 = (vocab + 3) / 4;
+  split = std::max(1, std::min(split, std::min(hs::kSplitMax, nf4)));
+  while (split > 1 && (split - 1) * ((nf4 + split - 1) / split) >= nf4) --split;
+  return split;
+}
+
+// The split rows' hand-over buffers for rows x split parts.
+int ensure_split(hs_context *ctx, int rows, int split) {
+  if (split <= 1) return HS_OK;
+  const size_t parts = (size_t)rows * (size_t)split;
+  HS_HIP(ctx->split_list.ensure(parts * hs::kPartCap * sizeof(unsigned long long)));
+  HS_HIP(ctx->split_meta.ensure(parts * sizeof(hs::SplitMeta)));
+  if (ctx->split_cnt.bytes < sizeof(uint32_t) * (size_t)rows) {
+    HS_HIP(ctx->split_cnt.ensure(sizeof(uint32_t) * (size_t)rows));
+    HS_HIP(hipMemset(ctx->split_cnt.p, 0, ctx->split_cnt.bytes));
+  }
+  return HS_OK;
+}
+
+hs::Workspace split_workspace(const hs_context *ctx) {
+  hs::Workspace ws;
+  memset(&ws, 0, sizeof ws);
+  ws.split_list = static_cast<unsigned long long *>(ctx->split_list.p);
+  ws.split_meta = static_cast<hs::SplitMeta *>(ctx->split_meta.p);
+  ws.split_cnt = static_cast<uint32_t *>(ctx->split_cnt.p);
+  return ws;
+}
+
+// With timing on, takes start/end events for every kernel the call launches.
+int begin_timed(hs_context *ctx, const hs::LaunchArgs &a, hipEvent_t **ev) {
+  *ev = nullptr;
+  if (!ctx->timing) return HS_OK;
+  hs_context::TimedCall tc{};
+  tc.mask = hs::launched_kernels(a);
+  for (int i = 0; i < 2 * hs::kTimedKernels; ++i) {
+    if (!(tc.mask >> (i / 2) & 1u)) continue;
+    if (ctx->ev_free.empty()) {
+      hipEvent_t x;
+      HS_HIP(hipEventCreate(&x));
+      ctx->ev_free.push_back(x);
+    }
+    tc.ev[i] = ctx->ev_free.back();
+    ctx->ev_free.pop_back();
+  }
+  ctx->timed.push_back(tc);
+  *ev = ctx->timed.back().ev;
+  return HS_OK;
+}
+
+// A failed launch may have left counters of earlier kernels of the call
+// raised: clear them for the next call.
+void reset_counters(hs_context *ctx, hipStream_t stream) {
+  if (ctx->cand_count.p) (void)hipMemsetAsync(ctx->cand_count.p, 0, ctx->cand_count.bytes, stream);
+  if (ctx->split_cnt.p) (void)hipMemsetAsync(ctx->split_cnt.p, 0, ctx->split_cnt.bytes, stream);
+}
+
 int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_stride,
                   int32_t vocab, const int32_t *d_hist_ids, const int64_t *d_hist_offsets,
                   const hs_sample_config *configs, const double *d_uniforms, int32_t *d_tokens,
@@ -281,31 +345,14 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
       HS_HIP(hipMemset(ctx->cand_count.p, 0, ctx->cand_count.bytes));
     }
   }
-  // Small batches split each row of the row kernel over several workgroups
-  // (parts of whole float4s), so that the launch fills the CUs.
-  // HS_ROW_SPLIT (read at context creation) forces the count, whatever the
-  // part size.  Every part holds at least one float4.
-  int split = 1;
-  if (n_row > 0) {
-    split = ctx->row_split > 0 ? ctx->row_split
-                               : std::min(hs::kSplitCUs / n_row, vocab / hs::kSplitMinPart);
-    const int nf4 = (vocab + 3) / 4;
-    split = std::max(1, std::min(split, std::min(hs::kSplitMax, nf4)));
-    while (split > 1 && (split - 1) * ((nf4 + split - 1) / split) >= nf4) --split;
-  }
-  if (split > 1) {
-    const size_t parts = (size_t)n_row * (size_t)split;
-    HS_HIP(ctx->split_list.ensure(parts * hs::kPartCap * sizeof(unsigned long long)));
-    HS_HIP(ctx->split_meta.ensure(parts * sizeof(hs::SplitMeta)));
-    if (ctx->split_cnt.bytes < sizeof(uint32_t) * (size_t)n_row) {
-      HS_HIP(ctx->split_cnt.ensure(sizeof(uint32_t) * (size_t)n_row));
-      HS_HIP(hipMemset(ctx->split_cnt.p, 0, ctx->split_cnt.bytes));
-    }
-  }
-  int rc = upload_plans(ctx, plans, rt, vocab, stream);
+  // small batches split each row of the row kernel over several workgroups
+  const int split = choose_split(ctx, n_row, vocab);
+  int rc = ensure_split(ctx, n_row, split);
+  if (rc) return rc;
+  rc = upload_plans(ctx, plans, rt, vocab, stream);
   if (rc) return rc;
 
-  hs::Workspace ws;
+  hs::Workspace ws = split_workspace(ctx);
   ws.plans = static_cast<hs::RowPlan *>(ctx->plans.p);
   const int32_t *lists = reinterpret_cast<const int32_t *>(ws.plans + rows);
   ws.pf_list = lists;
@@ -316,9 +363,6 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   ws.cand = static_cast<uint2 *>(ctx->cand.p);
   ws.cand_count = static_cast<int32_t *>(ctx->cand_count.p);
   ws.info = static_cast<hs::ChunkInfo *>(ctx->info.p);
-  ws.split_list = static_cast<unsigned long long *>(ctx->split_list.p);
-  ws.split_meta = static_cast<hs::SplitMeta *>(ctx->split_meta.p);
-  ws.split_cnt = static_cast<uint32_t *>(ctx->split_cnt.p);
 
   hs::LaunchArgs a;
   memset(&a, 0, sizeof a);
@@ -346,28 +390,57 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   a.cand_count_out = d_cand_count;
   a.cutoff_out = d_cutoff;
   a.row_flags = d_row_flags;
-  hs_context::TimedCall tc{};
-  const bool timed = ctx->timing;
-  if (timed) {
-    tc.mask = hs::launched_kernels(a);
-    for (int i = 0; i < 2 * hs::kTimedKernels; ++i) {
-      if (!(tc.mask >> (i / 2) & 1u)) continue;
-      if (ctx->ev_free.empty()) {
-        hipEvent_t x;
-        HS_HIP(hipEventCreate(&x));
-        ctx->ev_free.push_back(x);
-      }
-      tc.ev[i] = ctx->ev_free.back();
-      ctx->ev_free.pop_back();
-    }
-    ctx->timed.push_back(tc);
-  }
-  hipError_t e = hs::launch_sample(a, ws, stream, timed ? tc.ev : nullptr);
+  hipEvent_t *ev = nullptr;
+  rc = begin_timed(ctx, a, &ev);
+  if (rc) return rc;
+  hipError_t e = hs::launch_sample(a, ws, stream, ev);
   if (e != hipSuccess) {
-    if (ctx->cand_count.p)
-      (void)hipMemsetAsync(ctx->cand_count.p, 0, ctx->cand_count.bytes, stream);
-    if (ctx->split_cnt.p)
-      (void)hipMemsetAsync(ctx->split_cnt.p, 0, ctx->split_cnt.bytes, stream);
+    reset_counters(ctx, stream);
+    return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  }
+  return HS_OK;
+}
+
+// src/kernels.ts:1613-1654 (the argmax pipeline of the engine's greedy route).
+int argmax_device(hs_context *ctx, const float *d_logits, int32_t rows, int64_t row_stride,
+                  int32_t vocab, int32_t *d_tokens, hipStream_t stream) {
+  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  if (rows < 0) return fail(HS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %d)", rows);
+  if (rows == 0) return HS_OK;
+  if (!d_tokens) return fail(HS_ERR_INVALID_ARGUMENT, "tokens must not be null");
+  DeviceGuard guard(ctx->device);
+  if (vocab <= 0) {   // no invocation scans an id: every slot keeps id 0
+    HS_HIP(hipMemsetAsync(d_tokens, 0, sizeof(int32_t) * (size_t)rows, stream));
+    return HS_OK;
+  }
+  if (!d_logits) return fail(HS_ERR_INVALID_ARGUMENT, "logits must not be null");
+  if (row_stride < vocab)
+    return fail(HS_ERR_INVALID_ARGUMENT, "row_stride %lld < vocab %d", (long long)row_stride, vocab);
+  if (vocab > hs::kArgmaxMaxVocab)
+    return fail(HS_ERR_UNSUPPORTED, "vocab %d above %d", vocab, hs::kArgmaxMaxVocab);
+  const int split = choose_split(ctx, rows, vocab);
+  if ((int64_t)rows * split > 0x7FFFFFFF)
+    return fail(HS_ERR_UNSUPPORTED, "rows %d too many", rows);
+  int rc = ensure_split(ctx, rows, split);
+  if (rc) return rc;
+  hs::Workspace ws = split_workspace(ctx);
+  hs::LaunchArgs a;
+  memset(&a, 0, sizeof a);
+  a.logits = const_cast<float *>(d_logits);   // read only
+  a.stride = row_stride;
+  a.rows = rows;
+  a.vocab = vocab;
+  a.vec = ((reinterpret_cast<uintptr_t>(d_logits) & 15u) == 0 && (row_stride & 3) == 0) ? 1 : 0;
+  a.n_argmax = rows;
+  a.split = split;
+  a.rows_direct = 1;
+  a.tokens = d_tokens;
+  hipEvent_t *ev = nullptr;
+  rc = begin_timed(ctx, a, &ev);
+  if (rc) return rc;
+  hipError_t e = hs::launch_sample(a, ws, stream, ev);
+  if (e != hipSuccess) {
+    reset_counters(ctx, stream);
     return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
   }
   return HS_OK;
@@ -504,6 +577,44 @@ int hs_sample_batch_device(hs_context *ctx, float *d_logits, int32_t rows, int64
   return sample_device(ctx, d_logits, rows, row_stride, vocab, d_hist_ids, d_hist_offsets, configs,
                        d_uniforms, d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr,
                        static_cast<hipStream_t>(stream));
+}
+
+int hs_argmax_device(hs_context *ctx, const float *d_logits, int32_t rows, int64_t row_stride,
+                     int32_t vocab, int32_t *d_tokens, void *stream) {
+  return argmax_device(ctx, d_logits, rows, row_stride, vocab, d_tokens,
+                       static_cast<hipStream_t>(stream));
+}
+
+int hs_argmax(hs_context *ctx, const float *logits, int32_t rows, int64_t row_stride,
+              int32_t vocab, int32_t *tokens_out) {
+  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  if (rows < 0) return fail(HS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %d)", rows);
+  if (rows == 0) return HS_OK;
+  if (!tokens_out) return fail(HS_ERR_INVALID_ARGUMENT, "tokens_out must not be null");
+  if (vocab <= 0) {
+    for (int r = 0; r < rows; ++r) tokens_out[r] = 0;
+    return HS_OK;
+  }
+  if (!logits) return fail(HS_ERR_INVALID_ARGUMENT, "logits must not be null");
+  if (row_stride < vocab)
+    return fail(HS_ERR_INVALID_ARGUMENT, "row_stride %lld < vocab %d", (long long)row_stride, vocab);
+  if (vocab > hs::kArgmaxMaxVocab)
+    return fail(HS_ERR_UNSUPPORTED, "vocab %d above %d", vocab, hs::kArgmaxMaxVocab);
+  DeviceGuard guard(ctx->device);
+  hipStream_t st = ctx->stream;
+  const size_t lbytes = sizeof(float) * ((size_t)(rows - 1) * (size_t)row_stride + (size_t)vocab);
+  HS_HIP(ctx->h_logits.ensure(lbytes));
+  HS_HIP(ctx->h_tok.ensure(sizeof(int32_t) * rows));
+  HS_HIP(hipMemcpyAsync(ctx->h_logits.p, logits, lbytes, hipMemcpyHostToDevice, st));
+  int rc = argmax_device(ctx, static_cast<float *>(ctx->h_logits.p), rows, row_stride, vocab,
+                         static_cast<int32_t *>(ctx->h_tok.p), st);
+  if (rc) {
+    (void)hipStreamSynchronize(st);
+    return rc;
+  }
+  HS_HIP(hipMemcpyAsync(tokens_out, ctx->h_tok.p, sizeof(int32_t) * rows, hipMemcpyDeviceToHost, st));
+  HS_HIP(hipStreamSynchronize(st));
+  return HS_OK;
 }
 
 int hs_sample_logits_batch(hs_context *ctx, float *logits, int32_t rows, int64_t row_stride,

@@ -123,7 +123,8 @@ struct LaunchArgs {
   int32_t want_cands;        // exact candidate order must be produced
   int32_t rows_direct;       // the row kernel takes every row: row = block index
   int32_t n_pf, n_row, n_chunk, n_large, n_mid;
-  int32_t split;             // row kernel: workgroups per row (1: whole rows)
+  int32_t n_argmax;          // rows of the GPU greedy route (a call of its own)
+  int32_t split;             // row / argmax kernel: workgroups per row (1: whole rows)
   const int32_t *hist_ids;
   const int64_t *hist_off;
   const double *uniforms;
@@ -139,13 +140,16 @@ struct LaunchArgs {
 // Launches the kernels of one call on `stream`.  When `ev` is not null,
 // ev[2i] and ev[2i + 1] receive the start and end of kernel i's dispatch
 // (0 penalty pre-pass, 1 row kernel, 2 chunk kernel, 3 finalize, 4 large-k
-// kernel, 5 mid kernel), for the kernels that launch only: launched_kernels()
-// says which.
-constexpr int kTimedKernels = 6;
+// kernel, 5 mid kernel, 6 GPU greedy-route argmax), for the kernels that
+// launch only: launched_kernels() says which.
+constexpr int kTimedKernels = 7;
 inline unsigned launched_kernels(const LaunchArgs &a) {
   return (a.n_pf > 0 ? 1u : 0u) | (a.n_row > 0 ? 2u : 0u) | (a.n_chunk > 0 ? 12u : 0u) |
-         (a.n_large > 0 ? 16u : 0u) | (a.n_mid > 0 ? 32u : 0u);
+         (a.n_large > 0 ? 16u : 0u) | (a.n_mid > 0 ? 32u : 0u) | (a.n_argmax > 0 ? 64u : 0u);
 }
+// Largest vocabulary of the GPU greedy route (byte offsets of a row stay
+// below 2^31).
+constexpr int kArgmaxMaxVocab = 1 << 28;
 hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,
                          hipEvent_t *ev);
 hipError_t prepare_kernels();   // per device, once: raise dynamic LDS limits

@@ -3137,6 +3137,127 @@ __global__ __launch_bounds__(kLT) void large_kernel(LaunchArgs a, Workspace ws) 
   if (tid == 0 && a.row_flags) a.row_flags[row] = flags;
 }
 
+// ---------------------------------------------------------------- GPU greedy route
+
+// The engine sends greedy decoding without a repetition penalty
+// (src/engine.ts:1600-1601) to the WGSL argmax (src/kernels.ts:1613-1654)
+// instead of sampleLogits.  There, 256 invocations each keep the first id of
+// their maximum over ids t, t + 256, ... (strict '>' from f32(-1e30)), and a
+// tree reduction (stride 128 down to 1) keeps slot t against slot t + s on a
+// tie.  Among equal maxima the winner is therefore the id whose low byte,
+// bit-reversed, is smallest (the tree decides bit 7 of the invocation first
+// and bit 0 last), then the smallest id; NaN and values at or below
+// f32(-1e30) never win, and the result is 0 when no value exceeds it.  The
+// kernel streams each row once, folding packed (value key, preference) maxima:
+// no reduction tree, one comparison per logit.
+__device__ __forceinline__ unsigned long long wgsl_cand(float v, uint32_t id) {
+  const uint32_t pref = (__builtin_bitreverse32(id) & 0xFF000000u) | (id >> 8);
+  return v > -1e30f ? ((unsigned long long)f2key(v) << 32) | (0xFFFFFFFFu - pref) : 0ull;
+}
+
+__device__ __forceinline__ int32_t wgsl_id(unsigned long long c) {
+  if (!c) return 0;
+  const uint32_t pref = 0xFFFFFFFFu - (uint32_t)c;
+  return (int32_t)(((pref & 0x00FFFFFFu) << 8) | (__builtin_bitreverse32(pref) & 0xFFu));
+}
+
+// Thread tid reads the ids 4 (s + tid) + q of its part, s = fb + j * 1024,
+// in increasing order; every id of one q lies in one WGSL invocation's
+// stride class (4 s is a multiple of 256).  So each q keeps the first
+// maximum of its ids (strict '>', as the invocation) and the slot s where it
+// lies, which is wave-uniform: a compare and two selects per logit.
+template <int NV>
+__device__ __forceinline__ void wgsl_rd(const float (&v)[NV][4], int fb, float (&bv)[4],
+                                        int (&bs)[4]) {
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int s = fb + j * kRowThreads;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const bool take = v[j][q] > bv[q];   // NaN never
+      bv[q] = take ? v[j][q] : bv[q];
+      bs[q] = take ? s : bs[q];
+    }
+  }
+}
+
+// One 1024-thread workgroup per part of a row (a.split parts, as split rows
+// of the row kernel; the last part to finish combines the parts' maxima).
+template <bool VEC>
+__global__ __launch_bounds__(kRowThreads) void argmax_kernel(LaunchArgs a, Workspace ws) {
+  __shared__ unsigned long long wbest[kRowWaves];
+  __shared__ int32_t last;
+  const int tid = threadIdx.x, lane = tid & 63, wave = uniform_i32(tid >> 6);
+  const int S = a.split;
+  const int row = (int)blockIdx.x / S, part = (int)blockIdx.x - row * S;
+  const int nf4r = (a.vocab + 3) >> 2, per = (nf4r + S - 1) / S;
+  const int f0 = min(nf4r, part * per), f1 = min(nf4r, f0 + per);
+  const int eoff = 4 * f0, V = min(a.vocab, 4 * f1) - eoff;
+  const float *rowp = a.logits + (int64_t)row * a.stride + eoff;
+  RowSrc src;
+  src.lim = VEC ? (V & ~3) : V;
+  src.x4 = make_rsrc(rowp, 4u * (uint32_t)(V & ~3));
+  src.x1 = make_rsrc(rowp, 4u * (uint32_t)V);
+  const int nf4 = (V + 3) >> 2;
+  float va[kRowNV][4], vb[kRowNV][4];
+  load_rd<kRowNV, VEC>(va, src, 0, tid);
+  load_rd<kRowNV, VEC>(vb, src, kRoundF4, tid);
+  float tl[3] = {0.f, 0.f, 0.f};   // logits past the last whole float4 (VEC), thread 0
+  if (VEC) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int e = src.lim + q;
+      tl[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+          src.x1, (tid == 0 && e < V ? e : V) * 4, 0, 0));
+    }
+  }
+  float bv[4] = {-1e30f, -1e30f, -1e30f, -1e30f};   // as the invocation's initial value
+  int bs[4] = {0, 0, 0, 0};
+  for (int fb = 0; fb < nf4; fb += 2 * kRoundF4) {
+    clip_rd<kRowNV>(va, fb, tid, src.lim);
+    wgsl_rd<kRowNV>(va, fb, bv, bs);
+    load_rd<kRowNV, VEC>(va, src, fb + 2 * kRoundF4, tid);   // past the part near its end
+    if (fb + kRoundF4 >= nf4) break;
+    clip_rd<kRowNV>(vb, fb + kRoundF4, tid, src.lim);
+    wgsl_rd<kRowNV>(vb, fb + kRoundF4, bv, bs);
+    load_rd<kRowNV, VEC>(vb, src, fb + 3 * kRoundF4, tid);
+  }
+  unsigned long long best = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const unsigned long long c = wgsl_cand(bv[q], (uint32_t)(eoff + 4 * (bs[q] + tid) + q));
+    best = c > best ? c : best;
+  }
+  // the logits past the last whole float4 lie in other classes: candidates
+  // of their own
+  if (VEC && tid == 0) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      const int e = src.lim + q;
+      const unsigned long long c = e < V ? wgsl_cand(tl[q], (uint32_t)(eoff + e)) : 0ull;
+      best = c > best ? c : best;
+    }
+  }
+  best = wave_max64(best);
+  if (lane == 0) wbest[wave] = best;
+  __syncthreads();
+  unsigned long long bb = 0;
+  if (tid == 0)
+    for (int w = 0; w < kRowWaves; ++w) bb = wbest[w] > bb ? wbest[w] : bb;
+  if (S == 1) {
+    if (tid == 0) a.tokens[row] = wgsl_id(bb);
+    return;
+  }
+  if (tid == 0) store_agent(&ws.split_meta[blockIdx.x].best, bb);
+  if (split_arrive(ws, row, S, &last) && tid == 0) {
+    for (int p = 0; p < S; ++p) {
+      const unsigned long long b = load_agent(&ws.split_meta[row * S + p].best);
+      bb = b > bb ? b : bb;
+    }
+    a.tokens[row] = wgsl_id(bb);
+  }
+}
+
 // ---------------------------------------------------------------- launch
 
 hipError_t prepare_kernels() {
@@ -3227,6 +3348,12 @@ hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t s
   if (a.n_large > 0) {
     e = launch_one(large_kernel, dim3((unsigned)a.n_large), dim3(kLT), large_smem_bytes(), stream,
                    ev, 4, a, ws);
+    if (e != hipSuccess) return e;
+  }
+  if (a.n_argmax > 0) {
+    const dim3 grid((unsigned)(a.n_argmax * a.split));
+    e = a.vec ? launch_one(argmax_kernel<true>, grid, dim3(kRowThreads), 0, stream, ev, 6, a, ws)
+              : launch_one(argmax_kernel<false>, grid, dim3(kRowThreads), 0, stream, ev, 6, a, ws);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

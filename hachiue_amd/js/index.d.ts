@@ -56,5 +56,30 @@ export function sampleLogitsBatchAsync(
   shape?: BatchShape,
 ): Promise<Int32Array>
 
+/** src/engine.ts:1600-1601: temperature <= 0 and no repetition penalty. */
+export function isGreedyRoute(options?: SampleConfig): boolean
+
+/**
+ * The engine's GPU greedy route: the WGSL argmax of src/kernels.ts:1613-1654
+ * with its tie order (equal maxima: smallest bit-reversed low byte, then the
+ * smallest id; NaN and values <= -1e30 never taken).  Logits are read only.
+ */
+export function argmaxLogits(logits: Float32Array, vocab: number): number
+
+export function argmaxLogitsBatch(
+  logits: Float32Array,
+  vocab: number,
+  shape?: BatchShape,
+): Int32Array
+
+/** The engine's choice (src/engine.ts:1616-1620, :1642-1646): argmaxLogits on
+ * the greedy route, sampleLogits otherwise. */
+export function nextToken(
+  logits: Float32Array,
+  vocab: number,
+  history: number[] | Int32Array,
+  options?: SampleConfig,
+): number
+
 export const DEFAULTS: Readonly<Required<Pick<SampleConfig,
   'temperature' | 'topK' | 'topP' | 'minP' | 'repetitionPenalty'>>>

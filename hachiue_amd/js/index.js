@@ -13,6 +13,14 @@
  *   config.presencePenalty / config.frequencyPenalty  (x - freq*n) - pres
  *   config.uniform   the value in [0, 1) used instead of Math.random()
  *   sampleLogitsBatch / sampleLogitsBatchAsync        many rows per call
+ *
+ * The engine's greedy route (src/engine.ts:1600-1601): with temperature <= 0
+ * and no repetition penalty the engine takes the token from the WGSL argmax
+ * of its forward pass (src/kernels.ts:1613-1654), not from sampleLogits.
+ *   isGreedyRoute(options)               that decision
+ *   argmaxLogits / argmaxLogitsBatch     that argmax, with its tie order
+ *   nextToken(logits, vocab, history, options)   the engine's choice between
+ *                                        the two (src/engine.ts:1616-1620, :1642-1646)
  */
 const path = require('path');
 
@@ -101,6 +109,49 @@ function sampleLogits(logits, vocab, history, config) {
   return token;
 }
 
+/**
+ * src/engine.ts:1600-1601: greedy decoding without a repetition penalty takes
+ * the GPU argmax instead of sampleLogits.
+ * @param {object} [options]
+ * @returns {boolean}
+ */
+function isGreedyRoute(options) {
+  const o = options || {};
+  return option(o.temperature, 0.6) <= 0 &&
+    (o.repetitionPenalty === undefined || o.repetitionPenalty === 1.0);
+}
+
+/**
+ * The WGSL argmax of src/kernels.ts:1613-1654 over `rows` rows of `stride`
+ * floats (default: one row, stride = vocab).  Its tie order differs from
+ * sampleLogits' greedy path: among equal maxima the id whose low byte,
+ * bit-reversed, is smallest wins, then the smallest id; NaN and values at or
+ * below -1e30 are never taken (0 when nothing else is).  Logits are read only.
+ * @returns {Int32Array} ids
+ */
+function argmaxLogitsBatch(logits, vocab, shape) {
+  if (!(logits instanceof Float32Array)) throw new TypeError('logits must be a Float32Array');
+  if (!Number.isInteger(vocab) || vocab < 0) throw new RangeError('vocab must be a non-negative integer');
+  const stride = (shape && shape.stride) || vocab;
+  const rows = (shape && shape.rows !== undefined) ? shape.rows
+    : (stride > 0 ? Math.floor(logits.length / stride) : 0);
+  return native().argmax(context(), logits, rows, stride, vocab);
+}
+
+/** One row of argmaxLogitsBatch: the engine's greedy token. */
+function argmaxLogits(logits, vocab) {
+  return argmaxLogitsBatch(logits, vocab, { rows: 1, stride: vocab })[0];
+}
+
+/**
+ * The engine's next token (src/engine.ts:1616-1620, :1642-1646): the GPU
+ * argmax on its greedy route, sampleLogits otherwise.
+ */
+function nextToken(logits, vocab, history, options) {
+  return isGreedyRoute(options) ? argmaxLogits(logits, vocab)
+    : sampleLogits(logits, vocab, history, options);
+}
+
 function batchArgs(logits, vocab, histories, configs, uniforms, shape) {
   if (!(logits instanceof Float32Array)) throw new TypeError('logits must be a Float32Array');
   if (!Number.isInteger(vocab) || vocab < 0) throw new RangeError('vocab must be a non-negative integer');
@@ -155,6 +206,10 @@ module.exports = {
   sampleLogits: sampleLogits,
   sampleLogitsBatch: sampleLogitsBatch,
   sampleLogitsBatchAsync: sampleLogitsBatchAsync,
+  isGreedyRoute: isGreedyRoute,
+  argmaxLogits: argmaxLogits,
+  argmaxLogitsBatch: argmaxLogitsBatch,
+  nextToken: nextToken,
   DEFAULTS: Object.freeze({
     temperature: 0.6, topK: 20, topP: 0.95, minP: 0.0, repetitionPenalty: 1.0,
   }),

@@ -7,6 +7,7 @@
 //   sampleBatch(ctx, logits, rows, stride, vocab, histIds, histOffsets,
 //               configs, uniforms)                      -> Int32Array (sync)
 //   sampleBatchAsync(...same...)                        -> Promise<Int32Array>
+//   argmax(ctx, logits, rows, stride, vocab)            -> Int32Array (sync)
 //   lastError()                                         -> string
 // `config` / `configs` are Float64Arrays of 7 numbers per row in
 // hs_sample_config field order.  Logits are Float32Arrays updated in place.
@@ -333,6 +334,45 @@ napi_value SampleBatchAsync(napi_env env, napi_callback_info info) {
   return promise;
 }
 
+// argmax(ctx, logits: Float32Array, rows, stride, vocab): the engine's GPU
+// greedy route (the WGSL argmax of src/kernels.ts:1613-1654); logits are
+// read only.
+napi_value Argmax(napi_env env, napi_callback_info info) {
+  size_t argc = 5;
+  napi_value argv[5];
+  NAPI_OK(env, napi_get_cb_info(env, info, &argc, argv, nullptr, nullptr));
+  if (argc < 5) {
+    napi_throw_type_error(env, nullptr, "argmax needs 5 arguments");
+    return nullptr;
+  }
+  hs_context *ctx;
+  if (!get_ctx(env, argv[0], &ctx)) return nullptr;
+  float *logits;
+  size_t nl;
+  if (!get_typed(env, argv[1], napi_float32_array, &logits, &nl, false, "logits")) return nullptr;
+  double rows_d, stride_d, vocab_d;
+  if (!get_double(env, argv[2], &rows_d, "rows") || !get_double(env, argv[3], &stride_d, "stride") ||
+      !get_double(env, argv[4], &vocab_d, "vocab"))
+    return nullptr;
+  const int32_t rows = (int32_t)rows_d, vocab = (int32_t)vocab_d;
+  const int64_t stride = (int64_t)stride_d;
+  if (rows < 0 || (rows > 0 && vocab > 0 && (size_t)((int64_t)(rows - 1) * stride + vocab) > nl)) {
+    napi_throw_range_error(env, nullptr, "logits shorter than rows * stride");
+    return nullptr;
+  }
+  napi_value ab, tokens;
+  void *tok = nullptr;
+  if (napi_create_arraybuffer(env, sizeof(int32_t) * (size_t)(rows > 0 ? rows : 1), &tok, &ab) !=
+          napi_ok ||
+      napi_create_typedarray(env, napi_int32_array, (size_t)rows, ab, 0, &tokens) != napi_ok) {
+    napi_throw_error(env, nullptr, "cannot allocate the token array");
+    return nullptr;
+  }
+  const int st = hs_argmax(ctx, logits, rows, stride, vocab, static_cast<int32_t *>(tok));
+  if (st != HS_OK) return throw_status(env, st);
+  return tokens;
+}
+
 napi_value Init(napi_env env, napi_value exports) {
   napi_property_descriptor props[] = {
       {"createContext", nullptr, CreateContext, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
@@ -340,6 +380,7 @@ napi_value Init(napi_env env, napi_value exports) {
       {"sampleBatch", nullptr, SampleBatch, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"sampleBatchAsync", nullptr, SampleBatchAsync, nullptr, nullptr, nullptr, napi_enumerable,
        nullptr},
+      {"argmax", nullptr, Argmax, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
       {"lastError", nullptr, LastError, nullptr, nullptr, nullptr, napi_enumerable, nullptr},
   };
   napi_define_properties(env, exports, sizeof(props) / sizeof(props[0]), props);

@@ -34,8 +34,8 @@ ROW_GREEDY, ROW_REPLAYED, ROW_TIES, ROW_SINGLE = 0x1, 0x2, 0x4, 0x8
 # Every symbol include/hachiue_sampler.h declares.
 EXPORTS = ("hs_abi_version", "hs_last_error", "hs_config_default", "hs_context_create",
            "hs_context_destroy", "hs_sample_logits", "hs_sample_logits_batch",
-           "hs_sample_batch_device", "hs_sample_batch_device_ex", "hs_context_set_timing",
-           "hs_context_kernel_times")
+           "hs_sample_batch_device", "hs_sample_batch_device_ex", "hs_argmax_device",
+           "hs_argmax", "hs_context_set_timing", "hs_context_kernel_times")
 
 
 class SamplerError(RuntimeError):
@@ -103,6 +103,8 @@ def _load() -> ctypes.CDLL:
                                          vp, vp]
     L.hs_sample_batch_device_ex.argtypes = [vp, vp, i32, i64, i32, vp, vp, P(SampleConfigC),
                                             vp, vp, i32, vp, vp, vp, vp, vp, vp]
+    L.hs_argmax_device.argtypes = [vp, vp, i32, i64, i32, vp, vp]
+    L.hs_argmax.argtypes = [vp, P(ctypes.c_float), i32, i64, i32, P(i32)]
     L.hs_context_set_timing.argtypes = [vp, ctypes.c_int]
     L.hs_context_kernel_times.argtypes = [vp, P(dbl), i32, P(i64)]
     return L
@@ -191,7 +193,7 @@ class Sampler:
         _check(lib().hs_context_set_timing(self._ctx, 1 if enable else 0))
 
     KERNELS = ("pen_kernel", "row_kernel", "chunk_kernel", "finalize_kernel", "large_kernel",
-               "mid_kernel")
+               "mid_kernel", "argmax_kernel")
 
     def kernel_times(self):
         """({kernel: total device ms}, calls) since the last query."""
@@ -248,6 +250,32 @@ class Sampler:
             cfgs, u.ctypes.data_as(P(ctypes.c_double)), tok.ctypes.data_as(P(ctypes.c_int32))))
         return tok
 
+    # ---- the engine's GPU greedy route -----------------------------------------
+    def argmax(self, logits: np.ndarray, vocab: int | None = None) -> np.ndarray:
+        """The WGSL argmax of src/kernels.ts:1613-1654 (the engine's greedy
+        route without a repetition penalty, src/engine.ts:1600-1601) over the
+        rows of a 1-D or 2-D float32 array; logits are read only."""
+        if not (isinstance(logits, np.ndarray) and logits.dtype == np.float32
+                and logits.flags.c_contiguous):
+            raise TypeError("logits must be a contiguous float32 numpy array")
+        x = logits.reshape(1, -1) if logits.ndim == 1 else logits
+        rows, stride = x.shape
+        vocab = stride if vocab is None else int(vocab)
+        if vocab > stride:
+            raise ValueError("vocab exceeds the row length")
+        tok = np.zeros(rows, np.int32)
+        _check(lib().hs_argmax(self._ctx, _f32p(x), rows, stride, vocab,
+                               tok.ctypes.data_as(ctypes.POINTER(ctypes.c_int32))))
+        return tok
+
+    def argmax_device(self, d_logits: int, rows: int, row_stride: int, vocab: int,
+                      d_tokens: int, stream=None) -> None:
+        """Enqueue the greedy-route argmax on device buffers (addresses as ints)."""
+        vp = ctypes.c_void_p
+        st = stream.handle if isinstance(stream, hip.Stream) else stream
+        _check(lib().hs_argmax_device(self._ctx, vp(d_logits), int(rows), int(row_stride),
+                                      int(vocab), vp(d_tokens), st))
+
     # ---- device-resident batch ----------------------------------------------
     def sample_device(self, d_logits: int, rows: int, row_stride: int, vocab: int,
                       d_hist_ids: int | None, d_hist_off: int | None, configs,
@@ -274,6 +302,16 @@ def _configs(configs, rows: int):
     if len(configs) != rows:
         raise ValueError("one config per row is required")
     return (SampleConfigC * rows)(*[resolve_config(c) for c in configs])
+
+
+def greedy_route(options: dict | None) -> bool:
+    """src/engine.ts:1600-1601: the engine decodes with the GPU argmax instead
+    of sampleLogits when (temperature ?? 0.6) <= 0 and no repetition penalty
+    other than 1.0 is given."""
+    o = options or {}
+    t = o.get("temperature")
+    rp = o.get("repetitionPenalty")
+    return (0.6 if t is None else t) <= 0 and (rp is None or rp == 1.0)
 
 
 def make_configs(configs, rows: int):

@@ -127,13 +127,34 @@ int hs_sample_batch_device_ex(hs_context *ctx, float *d_logits, int32_t rows,
                               int32_t *d_cutoff, uint32_t *d_row_flags,
                               void *stream);
 
+/* The engine's GPU greedy route.  hachiue's engine decodes greedily without
+ * sampleLogits when temperature <= 0 and no repetition penalty is set
+ * (src/engine.ts:1600-1601): the forward pass ends in the WGSL argmax
+ * pipeline (src/kernels.ts:1613-1654, one 256-invocation workgroup per row,
+ * output u32 outToken).  These entry points replace that pipeline with its
+ * exact tie order, which differs from sampleLogits' greedy argmax
+ * (src/sampler.ts:36-46) on equal maxima, NaN and values at or below
+ * -1e30: invocation t keeps the first id of its maximum over ids t, t+256, ...
+ * (strict '>' from f32(-1e30)) and the tree reduction keeps slot t against
+ * slot t+s on a tie, so among equal maxima the id whose low byte, bit-reversed,
+ * is smallest wins, then the smallest id; no value above f32(-1e30) gives 0.
+ * Logits are read only.  `rows` rows of `row_stride` floats (the reference's
+ * rowOffset * vocab addressing is row_stride == vocab); vocab up to 2^28.
+ * hs_argmax_device is asynchronous on `stream` (device pointers);
+ * hs_argmax copies host rows in and the ids out, and blocks. */
+int hs_argmax_device(hs_context *ctx, const float *d_logits, int32_t rows,
+                     int64_t row_stride, int32_t vocab, int32_t *d_tokens,
+                     void *stream);
+int hs_argmax(hs_context *ctx, const float *logits, int32_t rows,
+              int64_t row_stride, int32_t vocab, int32_t *tokens_out);
+
 /* Diagnostics (no counterpart in the reference, which has no GPU sampler):
  * while enabled, every sampling call records HIP events on its stream around
  * each of its kernel launches.  hs_context_kernel_times() waits for the
  * recorded calls, writes the summed device milliseconds per kernel
  * (ms[0] presence/frequency pre-pass, ms[1] row kernel, ms[2] chunk kernel,
- * ms[3] finalize, ms[4] large-k kernel, ms[5] mid-k kernel; a kernel a call did
- * not launch adds 0)
+ * ms[3] finalize, ms[4] large-k kernel, ms[5] mid-k kernel, ms[6] greedy-route
+ * argmax; a kernel a call did not launch adds 0)
  * and the number of
  * timed calls, and resets the totals. */
 int hs_context_set_timing(hs_context *ctx, int enable);

@@ -114,6 +114,9 @@ def lib() -> ctypes.CDLL:
                                        ctypes.c_int, P(OrcResult),
                                        P(ctypes.c_int32), P(ctypes.c_float),
                                        P(ctypes.c_float), ctypes.c_int64]
+        L.orc_wgsl_argmax.restype = None
+        L.orc_wgsl_argmax.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int64,
+                                      ctypes.c_int64, P(ctypes.c_int32)]
         L.orc_topk_slots.restype = ctypes.c_int
         L.orc_topk_slots.argtypes = [P(ctypes.c_float), ctypes.c_int64,
                                      ctypes.c_int64, ctypes.c_int,
@@ -239,3 +242,18 @@ def topk_slots(logits: np.ndarray, vocab: int, k: int, method: int = LITERAL):
     if rc:
         raise MemoryError("oracle allocation failed")
     return ids, vals
+
+
+def wgsl_argmax(logits: np.ndarray, vocab: int, rows: int | None = None,
+                stride: int | None = None) -> np.ndarray:
+    """The engine's GPU greedy route (src/engine.ts:1600-1601): the WGSL
+    argmax of src/kernels.ts:1613-1654, one id per row."""
+    x = np.ascontiguousarray(logits, np.float32)
+    if x.ndim == 1:
+        x = x.reshape(1, -1)
+    rows = x.shape[0] if rows is None else rows
+    stride = x.shape[1] if stride is None else stride
+    out = np.zeros(rows, np.int32)
+    lib().orc_wgsl_argmax(_ptr(x, ctypes.c_float), rows, stride, vocab,
+                          _ptr(out, ctypes.c_int32))
+    return out

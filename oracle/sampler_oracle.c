@@ -316,3 +316,37 @@ int orc_sample_batch(float *logits, int64_t rows, int64_t stride, int64_t vocab,
   }
   return 0;
 }
+
+/* src/kernels.ts:1616-1654, invocation by invocation.  `-1e30` is a WGSL
+ * abstract float converted to f32 (src/kernels.ts:1629). */
+void orc_wgsl_argmax(const float *logits, int64_t rows, int64_t stride, int64_t vocab,
+                     int32_t *tokens) {
+  enum { WG = 256 };
+  float smax[WG];
+  uint32_t sidx[WG];
+  for (int64_t r = 0; r < rows; ++r) {
+    const float *row = logits + r * stride;
+    for (uint32_t tid = 0; tid < WG; ++tid) {   /* src/kernels.ts:1628-1640 */
+      float best_val = (float)-1e30;
+      uint32_t best_idx = 0;
+      for (int64_t i = tid; i < vocab; i += WG) {
+        const float v = row[i];
+        if (v > best_val) {
+          best_val = v;
+          best_idx = (uint32_t)i;
+        }
+      }
+      smax[tid] = best_val;
+      sidx[tid] = best_idx;
+    }
+    for (uint32_t s = WG / 2; s > 0; s >>= 1) {   /* src/kernels.ts:1641-1649 */
+      for (uint32_t tid = 0; tid < s; ++tid) {
+        if (smax[tid + s] > smax[tid]) {
+          smax[tid] = smax[tid + s];
+          sidx[tid] = sidx[tid + s];
+        }
+      }
+    }
+    tokens[r] = (int32_t)sidx[0];   /* src/kernels.ts:1650-1652 */
+  }
+}

@@ -81,6 +81,17 @@ int orc_sample_batch(float *logits, int64_t rows, int64_t stride, int64_t vocab,
 int orc_topk_slots(const float *logits, int64_t vocab, int64_t k, int method,
                    int32_t *slot_ids, float *slot_vals);
 
+/* The engine's GPU greedy route (src/engine.ts:1600-1601: temperature <= 0
+ * and no repetition penalty) takes the WGSL argmax pipeline
+ * (src/kernels.ts:1613-1654) instead of sampleLogits, simulated here step by
+ * step: 256 invocations, invocation t scans ids t, t+256, ... with a strict
+ * '>' from -1e30 (as binary32), then a shared-memory tree reduction with
+ * stride 128, 64, ..., 1 in which slot t takes slot t+s only when strictly
+ * greater.  Each row is `vocab` floats from logits + r*stride.  Writes one
+ * id per row. */
+void orc_wgsl_argmax(const float *logits, int64_t rows, int64_t stride, int64_t vocab,
+                     int32_t *tokens);
+
 #ifdef __cplusplus
 }
 #endif

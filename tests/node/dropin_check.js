@@ -3,6 +3,8 @@
 //   node dropin_check.js kat <cases.json>
 //   node dropin_check.js rows <workload dir>     sampleLogits row by row
 //   node dropin_check.js batch <workload dir>    sampleLogitsBatch (+ async)
+//   node dropin_check.js argmax <workload dir>   argmaxLogits / argmaxLogitsBatch / nextToken
+//   node dropin_check.js route                   isGreedyRoute on option objects
 //   node dropin_check.js nogpu                   error behaviour without a GPU
 const fs = require('fs');
 const path = require('path');
@@ -68,6 +70,25 @@ if (mode === 'kat') {
       logits_same: bits(logits).join() === bits(logits2).join(),
       penalised: bits(logits) }));
   }, function (e) { console.error(e); process.exit(1); });
+} else if (mode === 'argmax') {
+  const w = load(process.argv[3]);
+  const s = w.meta.stride;
+  const before = bits(w.logits).join();
+  const batch = hs.argmaxLogitsBatch(w.logits, w.meta.vocab, { rows: w.meta.rows, stride: s });
+  const rows = [];
+  const next = [];
+  for (let r = 0; r < w.meta.rows; r++) {
+    const row = w.logits.slice(r * s, r * s + w.meta.vocab);
+    rows.push(hs.argmaxLogits(row, w.meta.vocab));
+    next.push(hs.nextToken(row, w.meta.vocab, [], { temperature: 0 }));
+  }
+  console.log(JSON.stringify({ batch: Array.from(batch), rows: rows, next: next,
+    unchanged: bits(w.logits).join() === before }));
+} else if (mode === 'route') {
+  const cases = [undefined, {}, { temperature: 0 }, { temperature: -1 }, { temperature: null },
+    { temperature: 0, repetitionPenalty: 1.0 }, { temperature: 0, repetitionPenalty: 1.1 },
+    { temperature: 0, repetitionPenalty: null }, { temperature: 0.5 }, { temperature: NaN }];
+  console.log(JSON.stringify(cases.map(hs.isGreedyRoute)));
 } else if (mode === 'nogpu') {
   const out = {};
   out.vocab0 = hs.sampleLogits(new Float32Array([1, 2]), 0, [], {});

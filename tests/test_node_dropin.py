@@ -91,3 +91,27 @@ def test_dropin_batch_and_async_match_oracle():
     assert out["tokens"] == out["tokens_async"]
     assert out["logits_same"]
     assert np.array_equal(np.array(out["penalised"], np.uint32), ref.reshape(-1).view(np.uint32))
+
+
+@needs_node
+def test_greedy_route_decision():
+    # src/engine.ts:1600-1601 evaluated by hand on each option object:
+    # (temperature ?? 0.6) <= 0 && (repetitionPenalty === undefined || === 1.0)
+    want = [False, False, True, True, False, True, False, False, False, False]
+    assert _node("route")[0] == want
+
+
+@needs_node
+@pytest.mark.gpu
+def test_dropin_argmax_matches_oracle():
+    # eight logits of exactly 12.0 per row: the maximum ties, so the WGSL
+    # reduction order decides
+    wl = workloads.make("headline", 6, rows=8, exact_spikes=True)
+    with tempfile.TemporaryDirectory() as d:
+        _workload_dir(wl, d)
+        out = _node("argmax", d)[0]
+    want = pyoracle.wgsl_argmax(wl.logits, wl.vocab).tolist()
+    assert out["batch"] == want
+    assert out["rows"] == want
+    assert out["next"] == want          # nextToken on the greedy route
+    assert out["unchanged"]             # the argmax reads the logits only
