@@ -798,13 +798,20 @@ __device__ __forceinline__ void write_greedy(const LaunchArgs &a, int row, float
   if (a.row_flags) a.row_flags[row] = HS_ROW_GREEDY;
 }
 
+struct SelResult {
+  int n_sel;
+  uint32_t T;
+};
+
 // Gathers the entries get(0 .. n_ent) with key >= lo into srt after selecting
 // the exact k-th largest key T among them (all of them when fewer than k).
-// Returns n_sel (entries with key >= T) sorted descending in srt, or -1 when
-// more than kSortCap entries lie at or above T.
+// Returns T and n_sel (entries with key >= T) sorted descending in srt, or
+// n_sel = -1 when more than kSortCap entries lie at or above T.  (Not inlined:
+// a rare path.  Its arguments and result travel in registers, so the callers
+// need no scratch memory.)
 template <int NT, typename GetEnt>
-__device__ int select_into(int n_ent, GetEnt get, uint32_t lo, int k, unsigned long long *srt,
-                           SelectSmem &sm, TailSmem &f, uint32_t *T_out) {
+__device__ SelResult select_into(int n_ent, GetEnt get, uint32_t lo, int k,
+                                 unsigned long long *srt, SelectSmem &sm, TailSmem &f) {
   const int tid = threadIdx.x;
   int total = 0;
   const uint32_t T = block_select_fast<NT>(
@@ -828,10 +835,9 @@ __device__ int select_into(int n_ent, GetEnt get, uint32_t lo, int k, unsigned l
   }
   __syncthreads();
   const int n_sel = f.n_sel;
-  *T_out = T;
-  if (n_sel > kSortCap) return -1;
+  if (n_sel > kSortCap) return {-1, T};
   sort_packed<NT>(srt, n_sel);
-  return n_sel;
+  return {n_sel, T};
 }
 
 // ---------------------------------------------------------------- row kernel
@@ -1801,9 +1807,9 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   } else if (!overflow) {
     // rare: many candidates reach the bound (ties); select block-wide first,
     // from srt into cbuf (the segments are no longer needed)
-    uint32_t T = 0;
-    const int n_sel = select_into<kRowThreads>(
-        n_all, [&](int p) { return srt[p]; }, 1u, k, cbuf, rs.sel, rs.tail, &T);
+    const SelResult sel = select_into<kRowThreads>(
+        n_all, [srt](int p) { return srt[p]; }, 1u, k, cbuf, rs.sel, rs.tail);
+    const int n_sel = sel.n_sel;
     if (n_sel < 0) overflow = true;
     if (wave != 0) return;
     if (!overflow) {
@@ -2388,8 +2394,10 @@ __global__ __launch_bounds__(kThreads) void finalize_kernel(LaunchArgs a, Worksp
   uint32_t T = 0;
   if (!need_replay) {
     const int n_all = f.n_all;
-    n_sel = select_into<kThreads>(
-        n_all, [&](int p) { return ent[p]; }, 0u, k, srt, f.sel, f.tail, &T);
+    const SelResult sel = select_into<kThreads>(
+        n_all, [ent](int p) { return ent[p]; }, 0u, k, srt, f.sel, f.tail);
+    n_sel = sel.n_sel;
+    T = sel.T;
     if (n_sel < 0) { need_replay = true; n_sel = 0; }
   }
   if (tid == 0) ws.cand_count[pos] = 0;   // ready for the next call
