@@ -114,6 +114,23 @@ def lib() -> ctypes.CDLL:
                                        ctypes.c_int, P(OrcResult),
                                        P(ctypes.c_int32), P(ctypes.c_float),
                                        P(ctypes.c_float), ctypes.c_int64]
+        L.orc_block_weights.restype = ctypes.c_int
+        L.orc_block_weights.argtypes = [ctypes.c_int]
+        L.orc_block_bytes.restype = ctypes.c_int
+        L.orc_block_bytes.argtypes = [ctypes.c_int]
+        L.orc_fp16.restype = ctypes.c_float
+        L.orc_fp16.argtypes = [ctypes.c_uint16]
+        L.orc_dequant_row.restype = ctypes.c_int
+        L.orc_dequant_row.argtypes = [ctypes.c_int, P(ctypes.c_uint8), ctypes.c_int64,
+                                      P(ctypes.c_float)]
+        L.orc_gemv_exact.restype = ctypes.c_int
+        L.orc_gemv_exact.argtypes = [ctypes.c_int, P(ctypes.c_float), ctypes.c_int64,
+                                     ctypes.c_int64, P(ctypes.c_uint8), ctypes.c_int64,
+                                     P(ctypes.c_double), P(ctypes.c_double)]
+        L.orc_gemv_ref.restype = ctypes.c_int
+        L.orc_gemv_ref.argtypes = [ctypes.c_int, P(ctypes.c_float), ctypes.c_int64,
+                                   ctypes.c_int64, P(ctypes.c_uint8), ctypes.c_int64,
+                                   P(ctypes.c_float)]
         L.orc_wgsl_argmax.restype = None
         L.orc_wgsl_argmax.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int64,
                                       ctypes.c_int64, P(ctypes.c_int32)]
@@ -257,3 +274,52 @@ def wgsl_argmax(logits: np.ndarray, vocab: int, rows: int | None = None,
     lib().orc_wgsl_argmax(_ptr(x, ctypes.c_float), rows, stride, vocab,
                           _ptr(out, ctypes.c_int32))
     return out
+
+
+# ---- lm_head GEMV (oracle/lmhead_oracle.h) ----------------------------------
+W_F32, W_Q4_0, W_Q4_1, W_Q4_K, W_Q6_K = 0, 2, 3, 12, 14
+
+
+def block_spec(wtype: int) -> tuple[int, int]:
+    """(weights per block, bytes per block) of a GGML type (src/gguf.ts getBlockSpec)."""
+    return lib().orc_block_weights(wtype), lib().orc_block_bytes(wtype)
+
+
+def fp16(h: int) -> float:
+    return float(lib().orc_fp16(h))
+
+
+def dequant_row(wtype: int, row: np.ndarray, K: int) -> np.ndarray:
+    """One row of W dequantised as src/gguf.ts:149-230 does (binary32)."""
+    row = np.ascontiguousarray(row, np.uint8)
+    out = np.zeros(K, np.float32)
+    if lib().orc_dequant_row(wtype, _ptr(row, ctypes.c_uint8), K, _ptr(out, ctypes.c_float)):
+        raise ValueError("bad type or K")
+    return out
+
+
+def gemv_exact(wtype: int, x: np.ndarray, w: np.ndarray, N: int):
+    """(y, mag): y = x W^T in binary64 from the exact weights, mag = sum |x w|."""
+    x = np.ascontiguousarray(x, np.float32)
+    x2 = x.reshape(-1, x.shape[-1])
+    M, K = x2.shape
+    w = np.ascontiguousarray(w, np.uint8)
+    y = np.zeros((M, N), np.float64)
+    mag = np.zeros((M, N), np.float64)
+    if lib().orc_gemv_exact(wtype, _ptr(x2, ctypes.c_float), M, K, _ptr(w, ctypes.c_uint8), N,
+                            _ptr(y, ctypes.c_double), _ptr(mag, ctypes.c_double)):
+        raise ValueError("bad type or K")
+    return y, mag
+
+
+def gemv_ref(wtype: int, x: np.ndarray, w: np.ndarray, N: int) -> np.ndarray:
+    """The reference's binary32 GEMV result in its own summation order."""
+    x = np.ascontiguousarray(x, np.float32)
+    x2 = x.reshape(-1, x.shape[-1])
+    M, K = x2.shape
+    w = np.ascontiguousarray(w, np.uint8)
+    y = np.zeros((M, N), np.float32)
+    if lib().orc_gemv_ref(wtype, _ptr(x2, ctypes.c_float), M, K, _ptr(w, ctypes.c_uint8), N,
+                          _ptr(y, ctypes.c_float)):
+        raise ValueError("bad type or K")
+    return y
