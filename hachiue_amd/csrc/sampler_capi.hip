@@ -446,6 +446,79 @@ int argmax_device(hs_context *ctx, const float *d_logits, int32_t rows, int64_t 
   return HS_OK;
 }
 
+// src/engine.ts:1493-1515 (the lm_head GEMV; see lmhead_kernels.hip).
+int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32_t K,
+                const void *d_w, int32_t w_type, int32_t N, float *d_y, int64_t ldy,
+                hipStream_t stream) {
+  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  if (M < 0 || N < 0 || K <= 0)
+    return fail(HS_ERR_INVALID_ARGUMENT, "need M >= 0, N >= 0, K > 0 (got %d, %d, %d)", M, N, K);
+  if (M == 0 || N == 0) return HS_OK;
+  if (!d_x || !d_w || !d_y) return fail(HS_ERR_INVALID_ARGUMENT, "x, w and y must not be null");
+  if (ldx < K || ldy < N)
+    return fail(HS_ERR_INVALID_ARGUMENT, "ldx %lld < K or ldy %lld < N", (long long)ldx, (long long)ldy);
+  int bw = 0, bb = 0;
+  switch (w_type) {
+    case hs::kW_F32: bw = 32; bb = 128; break;   // as 32-weight units
+    case hs::kW_Q4_0: bw = 32; bb = 18; break;
+    case hs::kW_Q4_1: bw = 32; bb = 20; break;
+    case hs::kW_Q4_K: bw = 256; bb = 144; break;
+    case hs::kW_Q6_K: bw = 256; bb = 210; break;
+    default: return fail(HS_ERR_UNSUPPORTED, "weight type %d is not supported", w_type);
+  }
+  if (K % bw)
+    return fail(HS_ERR_INVALID_ARGUMENT, "K %d is not a multiple of the block size %d", K, bw);
+  if (K > hs::kGemvMaxK) return fail(HS_ERR_UNSUPPORTED, "K %d above %d", K, hs::kGemvMaxK);
+  if ((reinterpret_cast<uintptr_t>(d_w) & 15u) || (reinterpret_cast<uintptr_t>(d_x) & 3u))
+    return fail(HS_ERR_INVALID_ARGUMENT, "w must be 16-byte and x 4-byte aligned");
+  const int64_t row_bytes = (int64_t)(K / bw) * bb;
+  if ((int64_t)N * row_bytes > 0xFFFFFF00LL)
+    return fail(HS_ERR_UNSUPPORTED, "weights of %lld bytes above 4 GiB", (long long)(N * row_bytes));
+  hs::GemvArgs g;
+  memset(&g, 0, sizeof g);
+  g.x = d_x;
+  g.ldx = ldx;
+  g.w = d_w;
+  g.w_bytes = (uint32_t)(N * row_bytes);
+  g.row_bytes = (uint32_t)row_bytes;
+  g.y = d_y;
+  g.ldy = ldy;
+  g.N = N;
+  g.K = K;
+  g.M = M;
+  g.type = w_type;
+  g.units = w_type == hs::kW_Q6_K ? K / 64 : K / 32;
+  g.nru = g.units <= 64 ? 1 : 2;
+  int seg = 1;
+  while (seg < g.units && seg < 64) seg <<= 1;
+  g.seg = g.nru == 1 ? seg : 64;
+  const int64_t steps = ((int64_t)N + 64 / g.seg - 1) / (64 / g.seg);
+  // at most one wave per row step (the launch caps it at the resident workgroups)
+  const int64_t wpb = hs::kGemvThreads / 64;
+  g.blocks = (int32_t)std::min<int64_t>((steps + wpb - 1) / wpb, 1 << 20);
+  if (M > 65535) return fail(HS_ERR_UNSUPPORTED, "M %d above 65535", M);
+  DeviceGuard guard(ctx->device);
+  hipEvent_t *ev = nullptr;
+  if (ctx->timing) {
+    hs_context::TimedCall tc{};
+    tc.mask = 1u << hs::kGemvTimedSlot;
+    for (int i = 0; i < 2; ++i) {
+      if (ctx->ev_free.empty()) {
+        hipEvent_t x;
+        HS_HIP(hipEventCreate(&x));
+        ctx->ev_free.push_back(x);
+      }
+      tc.ev[2 * hs::kGemvTimedSlot + i] = ctx->ev_free.back();
+      ctx->ev_free.pop_back();
+    }
+    ctx->timed.push_back(tc);
+    ev = ctx->timed.back().ev + 2 * hs::kGemvTimedSlot;
+  }
+  const hipError_t e = hs::launch_gemv(g, stream, ev);
+  if (e != hipSuccess) return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return HS_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -583,6 +656,25 @@ int hs_argmax_device(hs_context *ctx, const float *d_logits, int32_t rows, int64
                      int32_t vocab, int32_t *d_tokens, void *stream) {
   return argmax_device(ctx, d_logits, rows, row_stride, vocab, d_tokens,
                        static_cast<hipStream_t>(stream));
+}
+
+int hs_gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32_t K,
+                   const void *d_w, int32_t w_type, int32_t N, float *d_y, int64_t ldy,
+                   void *stream) {
+  return gemv_device(ctx, d_x, M, ldx, K, d_w, w_type, N, d_y, ldy,
+                     static_cast<hipStream_t>(stream));
+}
+
+int hs_lm_head_sample_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32_t K,
+                             const void *d_w, int32_t w_type, int32_t N, float *d_logits,
+                             int64_t ldl, const int32_t *d_hist_ids, const int64_t *d_hist_offsets,
+                             const hs_sample_config *configs, const double *d_uniforms,
+                             int32_t *d_tokens, void *stream) {
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = gemv_device(ctx, d_x, M, ldx, K, d_w, w_type, N, d_logits, ldl, st);
+  if (rc) return rc;
+  return sample_device(ctx, d_logits, M, ldl, N, d_hist_ids, d_hist_offsets, configs, d_uniforms,
+                       d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr, st);
 }
 
 int hs_argmax(hs_context *ctx, const float *logits, int32_t rows, int64_t row_stride,

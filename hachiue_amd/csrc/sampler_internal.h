@@ -140,9 +140,10 @@ struct LaunchArgs {
 // Launches the kernels of one call on `stream`.  When `ev` is not null,
 // ev[2i] and ev[2i + 1] receive the start and end of kernel i's dispatch
 // (0 penalty pre-pass, 1 row kernel, 2 chunk kernel, 3 finalize, 4 large-k
-// kernel, 5 mid kernel, 6 GPU greedy-route argmax), for the kernels that
-// launch only: launched_kernels() says which.
-constexpr int kTimedKernels = 7;
+// kernel, 5 mid kernel, 6 GPU greedy-route argmax; 7 is the lm_head GEMV,
+// launched apart), for the kernels that launch only: launched_kernels() says
+// which.
+constexpr int kTimedKernels = 8;
 inline unsigned launched_kernels(const LaunchArgs &a) {
   return (a.n_pf > 0 ? 1u : 0u) | (a.n_row > 0 ? 2u : 0u) | (a.n_chunk > 0 ? 12u : 0u) |
          (a.n_large > 0 ? 16u : 0u) | (a.n_mid > 0 ? 32u : 0u) | (a.n_argmax > 0 ? 64u : 0u);
@@ -150,6 +151,38 @@ inline unsigned launched_kernels(const LaunchArgs &a) {
 // Largest vocabulary of the GPU greedy route (byte offsets of a row stay
 // below 2^31).
 constexpr int kArgmaxMaxVocab = 1 << 28;
+
+// ---- lm_head GEMV (lmhead_kernels.hip)
+// GGML type ids of the weight formats (src/types.ts:4-15).
+constexpr int kW_F32 = 0, kW_Q4_0 = 2, kW_Q4_1 = 3, kW_Q4_K = 12, kW_Q6_K = 14;
+constexpr int kGemvThreads = 256;
+constexpr int kGemvMaxK = 4096;       // x slices live in registers
+constexpr int kGemvTimedSlot = 7;     // its start/end events in a timed call
+struct GemvArgs {
+  const float *x;            // [M][ldx]
+  int64_t ldx;
+  const void *w;             // N rows of row_bytes, GGML blocks
+  uint32_t w_bytes, row_bytes;
+  float *y;                  // [M][ldy]
+  int64_t ldy;
+  int32_t N, K, M, type;
+  int32_t units;             // lane units per row
+  int32_t seg;               // lanes per row (power of two, <= 64) when nru == 1
+  int32_t nru;               // units per lane: 1, or 2 (a row takes all 64 lanes)
+  int32_t blocks;            // workgroups per activation row
+};
+// Block formats go through LDS in batches of row steps (a step: the rows of
+// one wave pass, 64 units): steps per batch and 16-byte reads per lane that
+// hold a batch (its bytes plus the alignment of its start).
+constexpr int gemv_batch_steps(int type) { return type == kW_Q6_K ? 2 : 4; }
+constexpr int gemv_unit_bytes2(int type) {   // twice a unit's bytes
+  return type == kW_Q6_K ? 105 : type == kW_Q4_1 ? 40 : 36;
+}
+constexpr int gemv_batch_chunks(int type) {
+  return (gemv_batch_steps(type) * 32 * gemv_unit_bytes2(type) + 32 + 1023) / 1024;
+}
+constexpr int gemv_lds_bytes(int type) { return (kGemvThreads / 64) * gemv_batch_chunks(type) * 1024; }
+hipError_t launch_gemv(const GemvArgs &g, hipStream_t stream, hipEvent_t *ev);
 hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,
                          hipEvent_t *ev);
 hipError_t prepare_kernels();   // per device, once: raise dynamic LDS limits

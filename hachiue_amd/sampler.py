@@ -35,7 +35,8 @@ ROW_GREEDY, ROW_REPLAYED, ROW_TIES, ROW_SINGLE = 0x1, 0x2, 0x4, 0x8
 EXPORTS = ("hs_abi_version", "hs_last_error", "hs_config_default", "hs_context_create",
            "hs_context_destroy", "hs_sample_logits", "hs_sample_logits_batch",
            "hs_sample_batch_device", "hs_sample_batch_device_ex", "hs_argmax_device",
-           "hs_argmax", "hs_context_set_timing", "hs_context_kernel_times")
+           "hs_argmax", "hs_gemv_device", "hs_lm_head_sample_device", "hs_context_set_timing",
+           "hs_context_kernel_times")
 
 
 class SamplerError(RuntimeError):
@@ -105,6 +106,9 @@ def _load() -> ctypes.CDLL:
                                             vp, vp, i32, vp, vp, vp, vp, vp, vp]
     L.hs_argmax_device.argtypes = [vp, vp, i32, i64, i32, vp, vp]
     L.hs_argmax.argtypes = [vp, P(ctypes.c_float), i32, i64, i32, P(i32)]
+    L.hs_gemv_device.argtypes = [vp, vp, i32, i64, i32, vp, i32, i32, vp, i64, vp]
+    L.hs_lm_head_sample_device.argtypes = [vp, vp, i32, i64, i32, vp, i32, i32, vp, i64, vp, vp,
+                                           P(SampleConfigC), vp, vp, vp]
     L.hs_context_set_timing.argtypes = [vp, ctypes.c_int]
     L.hs_context_kernel_times.argtypes = [vp, P(dbl), i32, P(i64)]
     return L
@@ -193,7 +197,7 @@ class Sampler:
         _check(lib().hs_context_set_timing(self._ctx, 1 if enable else 0))
 
     KERNELS = ("pen_kernel", "row_kernel", "chunk_kernel", "finalize_kernel", "large_kernel",
-               "mid_kernel", "argmax_kernel")
+               "mid_kernel", "argmax_kernel", "gemv_kernel")
 
     def kernel_times(self):
         """({kernel: total device ms}, calls) since the last query."""
@@ -275,6 +279,27 @@ class Sampler:
         st = stream.handle if isinstance(stream, hip.Stream) else stream
         _check(lib().hs_argmax_device(self._ctx, vp(d_logits), int(rows), int(row_stride),
                                       int(vocab), vp(d_tokens), st))
+
+    # ---- lm_head GEMV -----------------------------------------------------------
+    def gemv_device(self, d_x: int, M: int, ldx: int, K: int, d_w: int, w_type: int, N: int,
+                    d_y: int, ldy: int, stream=None) -> None:
+        """y = x W^T on device buffers (addresses as ints); W in GGML blocks."""
+        vp = ctypes.c_void_p
+        st = stream.handle if isinstance(stream, hip.Stream) else stream
+        _check(lib().hs_gemv_device(self._ctx, vp(d_x), int(M), int(ldx), int(K), vp(d_w),
+                                    int(w_type), int(N), vp(d_y), int(ldy), st))
+
+    def lm_head_sample_device(self, d_x: int, M: int, ldx: int, K: int, d_w: int, w_type: int,
+                              N: int, d_logits: int, ldl: int, d_hist_ids, d_hist_off, configs,
+                              d_uniforms: int, d_tokens: int, stream=None) -> None:
+        """The lm_head GEMV into d_logits, then sampling of its M rows."""
+        cfgs = configs if isinstance(configs, ctypes.Array) else _configs(configs, M)
+        vp = ctypes.c_void_p
+        st = stream.handle if isinstance(stream, hip.Stream) else stream
+        _check(lib().hs_lm_head_sample_device(
+            self._ctx, vp(d_x), int(M), int(ldx), int(K), vp(d_w), int(w_type), int(N),
+            vp(d_logits), int(ldl), vp(d_hist_ids or 0), vp(d_hist_off or 0), cfgs,
+            vp(d_uniforms), vp(d_tokens), st))
 
     # ---- device-resident batch ----------------------------------------------
     def sample_device(self, d_logits: int, rows: int, row_stride: int, vocab: int,

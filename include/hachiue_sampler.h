@@ -148,13 +148,40 @@ int hs_argmax_device(hs_context *ctx, const float *d_logits, int32_t rows,
 int hs_argmax(hs_context *ctx, const float *logits, int32_t rows,
               int64_t row_stride, int32_t vocab, int32_t *tokens_out);
 
+/* The logits producer in front of the sampler: hachiue's lm_head GEMV
+ * (src/engine.ts:1493-1515, runMatmul of output.weight; WGSL pipelines
+ * gemv_f32 / gemv_q4_0 / gemv_q4_1 / gemv_q4_k / gemv_q6_k,
+ * src/kernels.ts:244-290, :717-1090).  y[m][n] = sum_k x[m][k] W[n][k] for
+ * m < M, n < N; x is [M][ldx] binary32, y is [M][ldy] binary32, W is the
+ * GGUF tensor's raw blocks of `w_type` (GGML ids: 0 F32, 2 Q4_0, 3 Q4_1,
+ * 12 Q4_K, 14 Q6_K), N rows of K weights back to back, as the reference
+ * uploads them (src/engine.ts:772-800).  K a multiple of the block size,
+ * K <= 4096, W at most 4 GiB and 16-byte aligned.  Results differ from the
+ * reference's binary32 sums by rounding only.  Asynchronous on `stream`. */
+int hs_gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx,
+                   int32_t K, const void *d_w, int32_t w_type, int32_t N,
+                   float *d_y, int64_t ldy, void *stream);
+
+/* lm_head and sampler in one call on one stream, with no host round trip in
+ * between (the reference reads the logits back to the host, src/engine.ts:
+ * 1526-1531, and samples there): hs_gemv_device into d_logits ([M][ldl],
+ * N = vocab), then hs_sample_batch_device over its M rows. */
+int hs_lm_head_sample_device(hs_context *ctx, const float *d_x, int32_t M,
+                             int64_t ldx, int32_t K, const void *d_w,
+                             int32_t w_type, int32_t N, float *d_logits,
+                             int64_t ldl, const int32_t *d_hist_ids,
+                             const int64_t *d_hist_offsets,
+                             const hs_sample_config *configs,
+                             const double *d_uniforms, int32_t *d_tokens,
+                             void *stream);
+
 /* Diagnostics (no counterpart in the reference, which has no GPU sampler):
  * while enabled, every sampling call records HIP events on its stream around
  * each of its kernel launches.  hs_context_kernel_times() waits for the
  * recorded calls, writes the summed device milliseconds per kernel
  * (ms[0] presence/frequency pre-pass, ms[1] row kernel, ms[2] chunk kernel,
  * ms[3] finalize, ms[4] large-k kernel, ms[5] mid-k kernel, ms[6] greedy-route
- * argmax; a kernel a call did not launch adds 0)
+ * argmax, ms[7] lm_head GEMV; a kernel a call did not launch adds 0)
  * and the number of
  * timed calls, and resets the totals. */
 int hs_context_set_timing(hs_context *ctx, int enable);
