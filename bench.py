@@ -12,6 +12,12 @@ timed with HIP events on the launch stream) and a CPU
 baseline (the JavaScript restatement of sampler.ts under Node on this host).
 
   python bench.py [--steps K] [--warmup W] [--workload NAME] [--sets N]
+
+Other paths (one JSON line each, same fields):
+  --path greedy-route   the engine's greedy route: the WGSL-order argmax over
+                        the workload's logits (hs_argmax_device)
+  --path lmhead         the lm_head GEMV (hs_gemv_device) over a synthetic
+                        vocab x hidden weight in GGUF blocks (--wfmt, --hidden)
 """
 from __future__ import annotations
 
@@ -124,6 +130,9 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
+    ap.add_argument("--path", default="sample", choices=["sample", "greedy-route", "lmhead"])
+    ap.add_argument("--wfmt", default="q6_k", help="lm_head weight format (--path lmhead)")
+    ap.add_argument("--hidden", type=int, default=2048, help="lm_head K (--path lmhead)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="end with one device-to-device copy of one input set (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -137,6 +146,9 @@ def main() -> int:
 
     from hachiue_amd import Sampler, hip, workloads
     from hachiue_amd.sampler import make_configs
+
+    if args.path != "sample":
+        return other_path(args)
 
     t_gen = time.time()
     wl = workloads.make(args.workload, seed=0)
@@ -252,6 +264,104 @@ def main() -> int:
             "ms_per_step_instrumented": round(inst_ms / args.steps, 5),
         },
         "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(line), flush=True)
+    sampler.close()
+    return 0
+
+
+def other_path(args) -> int:
+    """The greedy-route argmax or the lm_head GEMV, timed like the sampler."""
+    from hachiue_amd import Sampler, hip, workloads
+
+    sampler = Sampler(0)
+    stream = hip.Stream()
+    sets = max(1, args.sets)
+    if args.path == "greedy-route":
+        wl = workloads.make(args.workload, seed=0)
+        rows, vocab = wl.rows, wl.vocab
+        d_in = [hip.DeviceArray.from_numpy(wl.logits) for _ in range(sets)]
+        d_tok = hip.DeviceArray(rows, np.int32)
+        kernel, unit = "argmax_kernel", "rows/s"
+        alg = rows * (4 * vocab + 4)
+        desc = f"greedy route (WGSL-order argmax) over {wl.name}: {rows} rows x {vocab} fp32 logits"
+
+        def step(i: int) -> None:
+            sampler.argmax_device(d_in[i % sets].addr, rows, vocab, vocab, d_tok.addr, stream=stream)
+
+        def check() -> dict:
+            from oracle import pyoracle
+            want = pyoracle.wgsl_argmax(wl.logits, vocab)
+            got = d_tok.download()
+            return {"rows": rows, "ids_equal": int((got == want).sum())}
+        count = rows
+    else:
+        lh = workloads.make_lmhead(args.wfmt, args.hidden)
+        rows, vocab, K = lh.x.shape[0], lh.vocab, lh.hidden
+        d_in = [hip.DeviceArray.from_numpy(lh.weights.reshape(-1)) for _ in range(sets)]
+        d_x = hip.DeviceArray.from_numpy(lh.x)
+        d_y = hip.DeviceArray((rows, vocab), np.float32)
+        kernel, unit = "gemv_kernel", "logit rows/s"
+        alg = lh.algorithmic_bytes()
+        desc = (f"lm_head GEMV: {vocab} x {K} {lh.fmt} weights ({lh.weights.nbytes} bytes, GGUF "
+                f"blocks), {rows} hidden state(s)")
+
+        def step(i: int) -> None:
+            sampler.gemv_device(d_x.addr, rows, K, K, d_in[i % sets].addr, lh.wtype, vocab,
+                                d_y.addr, vocab, stream=stream)
+
+        def check() -> dict:
+            from oracle import pyoracle
+            got = d_y.download().astype(np.float64)
+            exact, mag = pyoracle.gemv_exact(lh.wtype, lh.x, lh.weights, vocab)
+            rel = np.abs(got - exact) / np.maximum(mag, 1e-30)
+            return {"logits": int(got.size), "within_2^-16_of_sum_abs": int((rel <= 2 ** -16).sum()),
+                    "max_rel": float(rel.max())}
+        count = rows
+
+    step(0)
+    stream.synchronize()
+    parity = None if args.no_parity else check()
+    log(f"[bench] {args.path}: parity {parity}")
+    for i in range(args.warmup):
+        step(i)
+    stream.synchronize()
+
+    def region(instrumented: bool) -> float:
+        sampler.set_timing(instrumented)
+        sampler.kernel_times()
+        e0, e1 = hip.Event(), hip.Event()
+        hip.synchronize()
+        e0.record(stream)
+        for i in range(args.steps):
+            step(i)
+        e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_ms(e1)
+
+    total_ms = region(False)
+    region(True)
+    kms, calls = sampler.kernel_times()
+    sampler.set_timing(False)
+    kms_avg = kms[kernel] / max(calls, 1)
+    ms_per_step = total_ms / args.steps
+    achieved = alg / (kms_avg * 1e-3) / 1e9
+    line = {
+        "metric": f"{args.path}: {unit} and HBM GB/s (% roofline)",
+        "value": round(count / (ms_per_step * 1e-3), 1),
+        "unit": unit,
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic",
+        "config": {"workload": desc, "rows": rows, "vocab": vocab, "input_sets": sets,
+                   "algorithmic_bytes_per_step": alg},
+        "roofline": {"bound": "hbm", "kernel": kernel, "achieved": round(achieved, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel_ms": round(kms_avg, 5)},
+        "cpu_baseline": None,
         "parity": parity,
     }
     print(json.dumps(line), flush=True)

@@ -158,3 +158,51 @@ def make(name: str, seed: int = 0, rows: int | None = None, vocab: int | None = 
 
 
 NAMES = ("single", "batch64", "perrow256", "gumbel1024", "v262k512", "headline")
+
+
+# ---- lm_head GEMV workloads ---------------------------------------------------
+
+# GGML weight type ids (src/types.ts:4-15) and (weights, bytes) per block.
+W_TYPES = {"f32": (0, 1, 4), "q4_0": (2, 32, 18), "q4_1": (3, 32, 20), "q4_k": (12, 256, 144),
+           "q6_k": (14, 256, 210)}
+
+
+@dataclass
+class LmHead:
+    """A synthetic lm_head: output.weight [vocab rows x hidden] in GGUF blocks
+    of one format (random quants, binary16 scales near `scale`) and M hidden
+    states x [M x hidden]."""
+    wtype: int
+    fmt: str
+    vocab: int
+    hidden: int
+    weights: np.ndarray   # uint8 [vocab, row_bytes]
+    x: np.ndarray         # float32 [M, hidden]
+
+    def algorithmic_bytes(self) -> int:
+        """The weights once, x once, the logits once."""
+        return int(self.weights.nbytes + self.x.nbytes + 4 * self.x.shape[0] * self.vocab)
+
+
+def make_lmhead(fmt: str = "q6_k", hidden: int = 2048, vocab: int = V_QWEN, m: int = 1,
+                seed: int = 0, scale: float = 0.02) -> LmHead:
+    wtype, bw, bb = W_TYPES[fmt]
+    rng = np.random.default_rng([seed, hidden, wtype])
+    x = rng.standard_normal((m, hidden)).astype(np.float32)
+    if wtype == 0:
+        w = (rng.standard_normal((vocab, hidden)) * scale).astype(np.float32).view(np.uint8)
+        return LmHead(wtype, fmt, vocab, hidden, w, x)
+    nb = hidden // bw
+    raw = rng.integers(0, 256, (vocab, nb, bb), dtype=np.uint8)
+    d = (rng.random((vocab, nb)) * 2 * scale).astype(np.float16).view(np.uint8).reshape(vocab, nb, 2)
+    if wtype in (2, 3, 12):
+        raw[:, :, 0:2] = d
+    if wtype == 3:
+        raw[:, :, 2:4] = (rng.standard_normal((vocab, nb)) * scale).astype(np.float16).view(
+            np.uint8).reshape(vocab, nb, 2)
+    if wtype == 12:
+        raw[:, :, 2:4] = (rng.random((vocab, nb)) * scale).astype(np.float16).view(
+            np.uint8).reshape(vocab, nb, 2)
+    if wtype == 14:
+        raw[:, :, 208:210] = d
+    return LmHead(wtype, fmt, vocab, hidden, raw.reshape(vocab, nb * bb), x)
