@@ -298,13 +298,13 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
                   const hs_sample_config *configs, const double *d_uniforms, int32_t *d_tokens,
                   int32_t cand_stride, int32_t *d_cand_ids, float *d_cand_probs,
                   int32_t *d_cand_count, int32_t *d_cutoff, uint32_t *d_row_flags,
-                  hipStream_t stream) {
+                  hipStream_t stream, const int64_t *d_hist_len = nullptr, int64_t hist_cap = 0) {
   if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
   if (rows < 0) return fail(HS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %d)", rows);
   if (rows == 0) return HS_OK;
   if (!configs || !d_uniforms || !d_tokens)
     return fail(HS_ERR_INVALID_ARGUMENT, "configs, uniforms and tokens must not be null");
-  if ((d_hist_ids == nullptr) != (d_hist_offsets == nullptr))
+  if (hist_cap == 0 && (d_hist_ids == nullptr) != (d_hist_offsets == nullptr))
     return fail(HS_ERR_INVALID_ARGUMENT, "history ids and offsets must both be given or both null");
   if (cand_stride < 0) return fail(HS_ERR_INVALID_ARGUMENT, "cand_stride must be >= 0");
   if ((d_cand_ids || d_cand_probs) && cand_stride == 0)
@@ -382,6 +382,8 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   a.n_mid = n_mid;
   a.hist_ids = d_hist_ids;
   a.hist_off = d_hist_offsets;
+  a.hist_len = d_hist_len;
+  a.hist_cap = hist_cap;
   a.uniforms = d_uniforms;
   a.tokens = d_tokens;
   a.cand_stride = cand_stride;
@@ -675,6 +677,46 @@ int hs_lm_head_sample_device(hs_context *ctx, const float *d_x, int32_t M, int64
   if (rc) return rc;
   return sample_device(ctx, d_logits, M, ldl, N, d_hist_ids, d_hist_offsets, configs, d_uniforms,
                        d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr, st);
+}
+
+// src/engine.ts:1626-1644 (one step of the decode loop) with the token
+// history kept on the GPU.
+int hs_decode_step_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_stride,
+                          int32_t vocab, int32_t *d_ring, int64_t ring_cap, int64_t *d_len,
+                          int32_t *d_done, const int32_t *d_stop_ids, int32_t n_stop,
+                          const hs_sample_config *configs, const double *d_uniforms,
+                          int32_t *d_tokens, void *stream) {
+  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  if (rows < 0) return fail(HS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %d)", rows);
+  if (rows == 0) return HS_OK;
+  if (!d_ring || !d_len || !d_done)
+    return fail(HS_ERR_INVALID_ARGUMENT, "ring, len and done must not be null");
+  if (ring_cap < 128 || ring_cap > (int64_t(1) << 29))
+    return fail(HS_ERR_INVALID_ARGUMENT, "ring_cap must be in [128, 2^29] (got %lld)",
+                (long long)ring_cap);
+  if (n_stop < 0 || n_stop > hs::kMaxStopIds)
+    return fail(HS_ERR_INVALID_ARGUMENT, "n_stop must be in [0, %d] (got %d)", hs::kMaxStopIds,
+                n_stop);
+  if (n_stop > 0 && !d_stop_ids) return fail(HS_ERR_INVALID_ARGUMENT, "stop ids must not be null");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = sample_device(ctx, d_logits, rows, row_stride, vocab, d_ring, nullptr, configs,
+                         d_uniforms, d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr, st,
+                         d_len, ring_cap);
+  if (rc) return rc;
+  DeviceGuard guard(ctx->device);
+  hs::DecodeArgs d;
+  d.tokens = d_tokens;
+  d.ring = d_ring;
+  d.cap = ring_cap;
+  d.len = d_len;
+  d.done = d_done;
+  d.stop_ids = d_stop_ids;
+  d.n_stop = n_stop;
+  d.rows = rows;
+  const hipError_t e = hs::launch_decode_append(d, st);
+  if (e != hipSuccess)
+    return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  return HS_OK;
 }
 
 int hs_argmax(hs_context *ctx, const float *logits, int32_t rows, int64_t row_stride,

@@ -126,7 +126,9 @@ struct LaunchArgs {
   int32_t n_argmax;          // rows of the GPU greedy route (a call of its own)
   int32_t split;             // row / argmax kernel: workgroups per row (1: whole rows)
   const int32_t *hist_ids;
-  const int64_t *hist_off;
+  const int64_t *hist_off;   // packed lists: row r is hist_ids[off[r], off[r+1])
+  const int64_t *hist_len;   // rings (hist_cap > 0): row r is hist_ids[r * cap, +cap),
+  int64_t hist_cap;          //   len[r] ids appended so far, the last min(len, cap) kept
   const double *uniforms;
   int32_t *tokens;
   int32_t cand_stride;
@@ -183,6 +185,20 @@ constexpr int gemv_batch_chunks(int type) {
 }
 constexpr int gemv_lds_bytes(int type) { return (kGemvThreads / 64) * gemv_batch_chunks(type) * 1024; }
 hipError_t launch_gemv(const GemvArgs &g, hipStream_t stream, hipEvent_t *ev);
+
+// ---- decode step bookkeeping (after the sampler, same stream)
+struct DecodeArgs {
+  int32_t *tokens;           // [rows] the sampled tokens; -1 written for rows already done
+  int32_t *ring;             // [rows][cap] history rings
+  int64_t cap;
+  int64_t *len;              // [rows] ids appended so far
+  int32_t *done;             // [rows] 0 while generating, 1 once a stop token was drawn
+  const int32_t *stop_ids;   // [n_stop]
+  int32_t n_stop;
+  int32_t rows;
+};
+constexpr int kMaxStopIds = 1024;
+hipError_t launch_decode_append(const DecodeArgs &d, hipStream_t stream);
 hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,
                          hipEvent_t *ev);
 hipError_t prepare_kernels();   // per device, once: raise dynamic LDS limits

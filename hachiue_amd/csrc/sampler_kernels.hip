@@ -403,6 +403,40 @@ __device__ void sort_packed(unsigned long long *a, int n) {
   }
 }
 
+// ---------------------------------------------------------------- histories
+
+// A row's history: n ids, the j-th (0 <= j < n) at p[hist_pos(h, j)].  Two
+// layouts: the packed lists of hist_off (row r: hist_ids[off[r], off[r+1]),
+// cap 0), and the rings of a decode state (row r: hist_ids[r * cap, ...), of
+// which the last min(len[r], cap) appended ids count, the oldest at
+// (len - n) mod cap).
+struct HistRow {
+  const int32_t *p;
+  int64_t start, n, cap;
+};
+
+__device__ __forceinline__ HistRow hist_row(const LaunchArgs &a, int row) {
+  HistRow h{a.hist_ids, 0, 0, 0};
+  if (a.hist_cap > 0) {
+    int64_t len = a.hist_len[row];
+    if (len < 0) len = 0;
+    h.p = a.hist_ids + (int64_t)row * a.hist_cap;
+    h.n = len < a.hist_cap ? len : a.hist_cap;
+    h.start = (len - h.n) % a.hist_cap;
+    h.cap = a.hist_cap;
+  } else if (a.hist_off) {
+    const int64_t h0 = a.hist_off[row];
+    h.p = a.hist_ids + h0;
+    h.n = a.hist_off[row + 1] - h0;
+  }
+  return h;
+}
+
+__device__ __forceinline__ int64_t hist_pos(const HistRow &h, int64_t j) {
+  const int64_t i = h.start + j;
+  return (h.cap > 0 && i >= h.cap) ? i - h.cap : i;
+}
+
 // ---------------------------------------------------------------- penalties
 
 // src/sampler.ts:29-30 (v < 0 ? v * p : v / p, stored binary32) followed by
@@ -439,8 +473,8 @@ __global__ __launch_bounds__(kPenThreads) void pen_kernel(LaunchArgs a, Workspac
   const RowPlan P = ws.plans[row];
   float *rowp = a.logits + (int64_t)row * a.stride;
   const int V = a.vocab;
-  const int64_t h0 = a.hist_off ? a.hist_off[row] : 0;
-  const int64_t hl = a.hist_off ? a.hist_off[row + 1] - h0 : 0;
+  const HistRow h = hist_row(a, row);
+  const int64_t hl = h.n;
   const int64_t rep0 = (P.pen & kPenRep) ? hl - (hl < 128 ? hl : 128) : hl;   // history.slice(-128)
   const bool pf = (P.pen & kPenPF) != 0;
   for (int i = tid; i < kPenSlots; i += kPenThreads) { keys[i] = -1; cnts[i] = 0; }
@@ -449,7 +483,7 @@ __global__ __launch_bounds__(kPenThreads) void pen_kernel(LaunchArgs a, Workspac
   // the repetition-only entries (before rep0 without presence / frequency)
   // are not counted: their count is not used
   for (int64_t t = pf ? tid : rep0 + tid; t < hl; t += kPenThreads) {
-    const int id = a.hist_ids[h0 + t];
+    const int id = h.p[hist_pos(h, t)];
     if (id < 0 || id >= V) continue;
     uint32_t h = pen_hash(id);
     int probe = 0;
@@ -485,7 +519,7 @@ __global__ __launch_bounds__(kPenThreads) void pen_kernel(LaunchArgs a, Workspac
     for (int i = tid; i < kPenRange / 32; i += kPenThreads) repbits[i] = 0;
     __syncthreads();
     for (int64_t t = pf ? tid : rep0 + tid; t < hl; t += kPenThreads) {
-      const int id = a.hist_ids[h0 + t];
+      const int id = h.p[hist_pos(h, t)];
       if (id < lo || id >= hi) continue;
       atomicAdd(&counts[id - lo], 1u);
       if (t >= rep0) atomicOr(&repbits[(id - lo) >> 5], 1u << ((id - lo) & 31));
@@ -873,6 +907,31 @@ constexpr int kReadNT = 2;   // cache policy of a streamed read: nt
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void *p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)bytes, 0x00020000);
+}
+
+// The last <= 128 ids of a row's history (src/sampler.ts:26,
+// history.slice(-128)), the t-th to thread t, requested with one buffer load
+// (threads past them read outside the resource: 0, no memory touched).
+struct HistTail {
+  int id;
+  int n;
+};
+
+__device__ __forceinline__ HistTail hist_tail(const LaunchArgs &a, int row, int tid) {
+  const HistRow h = hist_row(a, row);
+  const int n = (int)(h.n < 128 ? h.n : 128);
+  const int64_t j0 = h.n - n;
+  const int32_t *p = h.p + j0;
+  uint32_t bytes = 4u * (uint32_t)n, off = 4u * (uint32_t)tid;
+  if (h.cap > 0) {   // a ring: the window may wrap
+    p = h.p;
+    bytes = 4u * (uint32_t)h.cap;
+    off = tid < n ? 4u * (uint32_t)hist_pos(h, j0 + tid) : bytes;
+  }
+  HistTail t;
+  t.id = (int)__builtin_amdgcn_raw_buffer_load_b32(make_rsrc(p, bytes), off, 0, 0);
+  t.n = n;
+  return t;
 }
 
 // The row as the rounds read it.  With VEC (16-byte aligned rows) x4 covers
@@ -1453,18 +1512,9 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   const int nr = row_rounds(V);
 
   // The last <= 128 history ids, one per thread of waves 0-1, are requested
-  // before the stream: a wave's reads complete in order.  Threads past them
-  // read outside the resource (0, no memory touched).
-  const int32_t *hist_p = a.hist_ids;
-  int hist_n = 0;
-  if (a.hist_off) {
-    const int64_t h0 = load_scalar(a.hist_off + row);
-    const int64_t hl = load_scalar(a.hist_off + row + 1) - h0;
-    hist_n = (int)(hl < 128 ? hl : 128);   // history.slice(-128)
-    hist_p = a.hist_ids + (h0 + hl - hist_n);
-  }
-  const int hraw = (int)__builtin_amdgcn_raw_buffer_load_b32(make_rsrc(hist_p, 4u * hist_n),
-                                                             tid * 4, 0, 0);
+  // before the stream: a wave's reads complete in order.
+  const HistTail ht = hist_tail(a, row, tid);
+  const int hraw = ht.id, hist_n = ht.n;
   RowSrc src;
   src.lim = VEC ? (V & ~3) : V;
   src.x4 = make_rsrc(rowp, 4u * (uint32_t)(V & ~3));
@@ -1993,16 +2043,8 @@ __global__ __launch_bounds__(kRowThreads) void mid_kernel(LaunchArgs a, Workspac
   const int nr = row_rounds(V);
 
   // history ids first, then rounds 0 and 1 (as in row_kernel)
-  const int32_t *hist_p = a.hist_ids;
-  int hist_n = 0;
-  if (a.hist_off) {
-    const int64_t h0 = load_scalar(a.hist_off + row);
-    const int64_t hl = load_scalar(a.hist_off + row + 1) - h0;
-    hist_n = (int)(hl < 128 ? hl : 128);   // history.slice(-128)
-    hist_p = a.hist_ids + (h0 + hl - hist_n);
-  }
-  const int hraw = (int)__builtin_amdgcn_raw_buffer_load_b32(make_rsrc(hist_p, 4u * hist_n),
-                                                             tid * 4, 0, 0);
+  const HistTail ht = hist_tail(a, row, tid);
+  const int hraw = ht.id, hist_n = ht.n;
   RowSrc src;
   src.lim = VEC ? (V & ~3) : V;
   src.x4 = make_rsrc(rowp, 4u * (uint32_t)(V & ~3));
@@ -2190,11 +2232,10 @@ __global__ __launch_bounds__(kThreads) void chunk_kernel(LaunchArgs a, Workspace
   if ((P.pen & kPenRep) && !(P.pen & kPenPF)) {
     for (int i = tid; i < kChunk / 32; i += kThreads) repbits[i] = 0;
     __syncthreads();
-    const int64_t h0 = a.hist_off ? a.hist_off[row] : 0;
-    const int64_t hl = a.hist_off ? a.hist_off[row + 1] - h0 : 0;
-    const int64_t last = hl < 128 ? hl : 128;
+    const HistRow h = hist_row(a, row);
+    const int64_t last = h.n < 128 ? h.n : 128;
     for (int64_t t = tid; t < last; t += kThreads) {
-      const int id = a.hist_ids[h0 + hl - last + t];
+      const int id = h.p[hist_pos(h, h.n - last + t)];
       if (id >= lo && id < hi) atomicOr(&repbits[(id - lo) >> 5], 1u << ((id - lo) & 31));
     }
     __syncthreads();
@@ -3314,6 +3355,38 @@ hipError_t launch_one(K kernel, dim3 grid, dim3 block, size_t smem, hipStream_t 
 }
 
 }  // namespace
+
+// One decode step's bookkeeping per row, after the sampler (src/engine.ts:
+// 1626-1644): a row already done reports -1 and keeps its state; a drawn
+// token of the stop set ends the row without joining the history (the stop
+// check comes first, :1628); any other token joins the history ring
+// (tokenHistory.push, :1638) for the next step's penalties.
+__global__ __launch_bounds__(256) void decode_append_kernel(DecodeArgs d) {
+  const int r = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (r >= d.rows) return;
+  if (d.done[r] != 0) {
+    d.tokens[r] = -1;
+    return;
+  }
+  const int t = d.tokens[r];
+  bool stop = false;
+  for (int i = 0; i < d.n_stop; ++i) stop |= d.stop_ids[i] == t;
+  if (stop) {
+    d.done[r] = 1;
+    return;
+  }
+  int64_t len = d.len[r];
+  if (len < 0) len = 0;
+  d.ring[(int64_t)r * d.cap + len % d.cap] = t;
+  d.len[r] = len + 1;
+}
+
+hipError_t launch_decode_append(const DecodeArgs &d, hipStream_t stream) {
+  if (d.rows <= 0) return hipSuccess;
+  hipLaunchKernelGGL(decode_append_kernel, dim3((unsigned)((d.rows + 255) / 256)), dim3(256), 0,
+                     stream, d);
+  return hipGetLastError();
+}
 
 hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,
                          hipEvent_t *ev) {

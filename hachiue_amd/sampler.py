@@ -35,8 +35,8 @@ ROW_GREEDY, ROW_REPLAYED, ROW_TIES, ROW_SINGLE = 0x1, 0x2, 0x4, 0x8
 EXPORTS = ("hs_abi_version", "hs_last_error", "hs_config_default", "hs_context_create",
            "hs_context_destroy", "hs_sample_logits", "hs_sample_logits_batch",
            "hs_sample_batch_device", "hs_sample_batch_device_ex", "hs_argmax_device",
-           "hs_argmax", "hs_gemv_device", "hs_lm_head_sample_device", "hs_context_set_timing",
-           "hs_context_kernel_times")
+           "hs_argmax", "hs_gemv_device", "hs_lm_head_sample_device", "hs_decode_step_device",
+           "hs_context_set_timing", "hs_context_kernel_times")
 
 
 class SamplerError(RuntimeError):
@@ -109,6 +109,8 @@ def _load() -> ctypes.CDLL:
     L.hs_gemv_device.argtypes = [vp, vp, i32, i64, i32, vp, i32, i32, vp, i64, vp]
     L.hs_lm_head_sample_device.argtypes = [vp, vp, i32, i64, i32, vp, i32, i32, vp, i64, vp, vp,
                                            P(SampleConfigC), vp, vp, vp]
+    L.hs_decode_step_device.argtypes = [vp, vp, i32, i64, i32, vp, i64, vp, vp, vp, i32,
+                                        P(SampleConfigC), vp, vp, vp]
     L.hs_context_set_timing.argtypes = [vp, ctypes.c_int]
     L.hs_context_kernel_times.argtypes = [vp, P(dbl), i32, P(i64)]
     return L
@@ -299,6 +301,20 @@ class Sampler:
         _check(lib().hs_lm_head_sample_device(
             self._ctx, vp(d_x), int(M), int(ldx), int(K), vp(d_w), int(w_type), int(N),
             vp(d_logits), int(ldl), vp(d_hist_ids or 0), vp(d_hist_off or 0), cfgs,
+            vp(d_uniforms), vp(d_tokens), st))
+
+    def decode_step_device(self, d_logits: int, rows: int, row_stride: int, vocab: int,
+                           d_ring: int, ring_cap: int, d_len: int, d_done: int,
+                           d_stop_ids: int | None, n_stop: int, configs, d_uniforms: int,
+                           d_tokens: int, stream=None) -> None:
+        """One decode step (src/engine.ts:1626-1644) with the histories in
+        device rings: draw, stop check, history append, no synchronisation."""
+        cfgs = configs if isinstance(configs, ctypes.Array) else _configs(configs, rows)
+        vp = ctypes.c_void_p
+        st = stream.handle if isinstance(stream, hip.Stream) else stream
+        _check(lib().hs_decode_step_device(
+            self._ctx, vp(d_logits), int(rows), int(row_stride), int(vocab), vp(d_ring),
+            int(ring_cap), vp(d_len), vp(d_done), vp(d_stop_ids or 0), int(n_stop), cfgs,
             vp(d_uniforms), vp(d_tokens), st))
 
     # ---- device-resident batch ----------------------------------------------

@@ -175,6 +175,36 @@ int hs_lm_head_sample_device(hs_context *ctx, const float *d_x, int32_t M,
                              const double *d_uniforms, int32_t *d_tokens,
                              void *stream);
 
+/* One step of the decode loop with the token history on the GPU
+ * (src/engine.ts:1626-1644, whose tokenHistory is a host array, and whose
+ * stopSet check, :1628, runs on the host after a readback of the token).
+ * Per row r, on `stream`, without a host synchronisation:
+ *   1. the token is drawn from d_logits as hs_sample_batch_device does, with
+ *      row r's history read from its ring: d_ring[r * ring_cap, +ring_cap)
+ *      holds the last min(d_len[r], ring_cap) ids appended, the id appended
+ *      as the j-th (0-based) at slot j mod ring_cap;
+ *   2. a row with d_done[r] != 0 (done before this step) gets
+ *      d_tokens[r] = -1 and keeps its state; a drawn id in
+ *      d_stop_ids[0, n_stop) sets d_done[r] = 1 (the id is reported in
+ *      d_tokens[r] and does not join the history); any other id is written
+ *      to slot d_len[r] mod ring_cap and d_len[r] is incremented.
+ * The repetition penalty reads the last 128 ids (ring_cap >= 128 keeps that
+ * window exact); presence / frequency count the last min(len, ring_cap) ids,
+ * the full history while ring_cap >= len.  The caller fills the rings with
+ * the prompt ids (d_len[r] = prompt length) before the first step, bounds
+ * the steps (maxNewTokens, the sequence length) and reads d_done / d_tokens
+ * when it wants to (src/engine.ts:1631, onToken).  Greedy rows
+ * (temperature <= 0) take src/sampler.ts:36-46's first maximum, not the
+ * WGSL argmax order of hs_argmax_device.  ring_cap in [128, 2^29], n_stop in
+ * [0, 1024]; d_uniforms[r] as in hs_sample_batch_device (one set per step). */
+int hs_decode_step_device(hs_context *ctx, float *d_logits, int32_t rows,
+                          int64_t row_stride, int32_t vocab, int32_t *d_ring,
+                          int64_t ring_cap, int64_t *d_len, int32_t *d_done,
+                          const int32_t *d_stop_ids, int32_t n_stop,
+                          const hs_sample_config *configs,
+                          const double *d_uniforms, int32_t *d_tokens,
+                          void *stream);
+
 /* Diagnostics (no counterpart in the reference, which has no GPU sampler):
  * while enabled, every sampling call records HIP events on its stream around
  * each of its kernel launches.  hs_context_kernel_times() waits for the

@@ -323,3 +323,51 @@ def gemv_ref(wtype: int, x: np.ndarray, w: np.ndarray, N: int) -> np.ndarray:
                           _ptr(y, ctypes.c_float)):
         raise ValueError("bad type or K")
     return y
+
+
+# ---- the decode loop (src/engine.ts:1626-1644) ------------------------------
+
+class DecodeResult:
+    def __init__(self, tokens, histories, done, steps):
+        self.tokens = tokens          # [steps][rows] int32, -1 once a row is done
+        self.histories = histories    # per row: prompt + appended ids
+        self.done = done              # per row: a stop id was drawn
+        self.steps = steps            # per step: the BatchResult of its draw
+
+
+def decode_loop(step_logits, vocab: int, prompts, stop_ids, cfgs, uniforms,
+                ring_cap: int | None = None) -> DecodeResult:
+    """src/engine.ts:1626-1644 for independent rows: at each step every row
+    draws from that step's logits ([rows, stride] float32, mutated like the
+    reference's) with its token history (src/sampler.ts through sample_batch);
+    a drawn stop id ends the row before it joins the history (:1628), any
+    other id is pushed to the history (:1638), and a row once done reports
+    -1.  With ring_cap, a draw sees only the last ring_cap history ids (what a
+    device ring of that capacity holds)."""
+    rows = len(prompts)
+    hist = [list(int(t) for t in p) for p in prompts]
+    done = [False] * rows
+    stop = set(int(t) for t in stop_ids)
+    tokens, results = [], []
+    for s, logits in enumerate(step_logits):
+        seen = [h[-ring_cap:] if ring_cap else h for h in hist]
+        off = np.zeros(rows + 1, np.int64)
+        for r, h in enumerate(seen):
+            off[r + 1] = off[r] + len(h)
+        ids = np.array([t for h in seen for t in h], np.int32)
+        res = sample_batch(logits, vocab, ids, off, cfgs, uniforms[s])
+        row_tok = []
+        for r in range(rows):
+            if done[r]:
+                row_tok.append(-1)
+                continue
+            t = int(res.token[r])
+            row_tok.append(t)
+            if t in stop:
+                done[r] = True
+            else:
+                hist[r].append(t)
+        tokens.append(row_tok)
+        results.append(res)
+    return DecodeResult(np.array(tokens, np.int32).reshape(len(tokens), rows), hist, done,
+                        results)

@@ -1,0 +1,120 @@
+"""GPU parity of the device-resident decode step (hs_decode_step_device,
+src/engine.ts:1626-1644) against the oracle's decode loop: every step's
+tokens, the stop check, rows that stay done, and the final history rings and
+lengths, with all steps enqueued before one synchronisation.  Histories wrap
+their rings (the repetition window read across the wrap), presence /
+frequency rows count the ring's ids, and every routing of the sampler (row
+kernel whole or split, chunk kernels, large-k pre-pass) reads the rings."""
+import numpy as np
+import pytest
+
+from hachiue_amd import hip
+from hachiue_amd.decode import DecodeState
+from oracle import pyoracle as o
+
+pytestmark = pytest.mark.gpu
+
+CFGS = [
+    dict(temperature=0.0),                                            # sampler.ts greedy
+    dict(temperature=0.0, repetitionPenalty=1.3),
+    dict(temperature=0.7, topK=40, topP=0.9, repetitionPenalty=1.1),
+    dict(temperature=1.0, topK=200, topP=0.95, presencePenalty=0.5, frequencyPenalty=0.3),
+    dict(temperature=0.8, topK=0, topP=0.97, minP=0.05, repetitionPenalty=1.2),
+    dict(temperature=0.9, topK=2000, topP=0.9, repetitionPenalty=1.05),   # large-k path
+]
+
+
+def run_decode(sampler, V, prompts, stop_ids, cfgs, n_steps, ring_cap, seed, plant=None):
+    rows = len(prompts)
+    rng = np.random.default_rng(seed)
+    base = [(rng.standard_normal((rows, V)) * 2.0).astype(np.float32) for _ in range(n_steps)]
+    if plant:   # (step, row, id): that row's maximum at that step
+        for s, r, t in plant:
+            base[s][r, t] = np.float32(50.0)
+    u = rng.random((n_steps, rows))
+    print(f"[gpu] decode V={V} rows={rows} steps={n_steps} cap={ring_cap} seed={seed}", flush=True)
+    ref_in = [b.copy() for b in base]
+    ref = o.decode_loop(ref_in, V, prompts, stop_ids, cfgs, u, ring_cap=ring_cap)
+    st = DecodeState(sampler, prompts, stop_ids, ring_cap=ring_cap)
+    d_l = hip.DeviceArray.from_numpy(np.stack(base))
+    d_u = hip.DeviceArray.from_numpy(u)
+    d_t = hip.DeviceArray((n_steps, rows), np.int32)
+    for s in range(n_steps):
+        st.step(d_l.addr + s * rows * V * 4, V, V, cfgs, d_u.addr + s * rows * 8,
+                d_t.addr + s * rows * 4)
+    hip.synchronize()
+    tokens = d_t.download()
+    got = d_l.download()
+    # A draw within 1e-6 of a cumulative boundary (or a top-p cut within 1e-6)
+    # may go either way; the row's later steps then see another history.
+    diverged = {}
+    for s in range(n_steps):
+        res = ref.steps[s]
+        for r in range(rows):
+            if r in diverged:
+                continue
+            ok_logits = np.array_equal(got[s, r].view(np.uint32), ref_in[s][r].view(np.uint32))
+            assert ok_logits, f"step {s} row {r}: penalised logits differ"
+            if tokens[s, r] != ref.tokens[s, r]:
+                near = res.draw_margin[r] < 1e-6 or res.topp_margin[r] < 1e-6
+                assert near, f"step {s} row {r}: token {tokens[s, r]} != {ref.tokens[s, r]}"
+                diverged[r] = s
+    assert len(diverged) <= max(1, rows // 20), diverged
+    done, lens = st.finished(), st.lengths()
+    for r in range(rows):
+        if r in diverged:
+            continue
+        assert bool(done[r]) == ref.done[r]
+        assert lens[r] == len(ref.histories[r])
+        assert st.history(r).tolist() == ref.histories[r][-ring_cap:]
+    print(f"[gpu] decode ok, boundary divergences {diverged}", flush=True)
+    st.free()
+    return ref
+
+
+@pytest.mark.parametrize("V", [151936, 32000])
+def test_decode_steps_match_oracle(any_sampler, V):
+    rng = np.random.default_rng(V)
+    prompts = [[], rng.integers(0, V, 5).tolist(), rng.integers(0, V, 200).tolist(),
+               rng.integers(0, V, 1000).tolist(), rng.integers(0, 64, 300).tolist(),
+               rng.integers(0, V, 130).tolist()]
+    stop = [7, 11]
+    plant = [(3, 0, 7), (5, 2, 11), (2, 4, 3)]   # rows 0 and 2 stop, row 4 draws id 3
+    run_decode(any_sampler, V, prompts, stop, CFGS, 8, 256, seed=V + 1, plant=plant)
+
+
+def test_decode_exact_window_ring(sampler):
+    """ring_cap 128: the ring is exactly the repetition window; a prompt of
+    1000 ids has wrapped it many times."""
+    V = 4096
+    rng = np.random.default_rng(5)
+    prompts = [rng.integers(0, 32, 1000).tolist() for _ in range(4)]
+    cfgs = [dict(temperature=0.0, repetitionPenalty=2.0),
+            dict(temperature=0.6, topK=20, repetitionPenalty=1.5),
+            dict(temperature=0.0, repetitionPenalty=0.5),
+            dict(temperature=1.0, topK=64, topP=0.8, repetitionPenalty=1.3)]
+    run_decode(sampler, V, prompts, [], cfgs, 12, 128, seed=6)
+
+
+def test_decode_many_rows(sampler):
+    """300 rows: the row kernel takes whole rows (no split)."""
+    V = 32000
+    rng = np.random.default_rng(8)
+    prompts = [rng.integers(0, V, int(n)).tolist() for n in rng.integers(0, 400, 300)]
+    cfgs = [CFGS[i % 5] for i in range(300)]
+    run_decode(sampler, V, prompts, [1, 2, 3], cfgs, 3, 256, seed=9)
+
+
+def test_decode_rejects_bad_arguments(sampler):
+    from hachiue_amd.sampler import SamplerError
+    st = DecodeState(sampler, [[1, 2]], [], ring_cap=128)
+    d_l = hip.DeviceArray.from_numpy(np.zeros((1, 16), np.float32))
+    d_u = hip.DeviceArray.from_numpy(np.zeros(1))
+    d_t = hip.DeviceArray(1, np.int32)
+    with pytest.raises(SamplerError):
+        sampler.decode_step_device(d_l.addr, 1, 16, 16, st.ring.addr, 64, st.len.addr,
+                                   st.done.addr, None, 0, [None], d_u.addr, d_t.addr)
+    with pytest.raises(SamplerError):
+        sampler.decode_step_device(d_l.addr, 1, 16, 16, st.ring.addr, 128, st.len.addr,
+                                   st.done.addr, None, 3, [None], d_u.addr, d_t.addr)
+    st.free()
