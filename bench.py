@@ -130,7 +130,7 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
-    ap.add_argument("--path", default="sample", choices=["sample", "greedy-route", "lmhead"])
+    ap.add_argument("--path", default="sample", choices=["sample", "greedy-route", "lmhead", "decode"])
     ap.add_argument("--wfmt", default="q6_k", help="lm_head weight format (--path lmhead)")
     ap.add_argument("--hidden", type=int, default=2048, help="lm_head K (--path lmhead)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -272,7 +272,8 @@ def main() -> int:
 
 
 def other_path(args) -> int:
-    """The greedy-route argmax or the lm_head GEMV, timed like the sampler."""
+    """The greedy-route argmax, the lm_head GEMV or the device-resident decode
+    step, timed like the sampler."""
     from hachiue_amd import Sampler, hip, workloads
 
     sampler = Sampler(0)
@@ -295,6 +296,34 @@ def other_path(args) -> int:
             want = pyoracle.wgsl_argmax(wl.logits, vocab)
             got = d_tok.download()
             return {"rows": rows, "ids_equal": int((got == want).sum())}
+        count = rows
+    elif args.path == "decode":
+        from hachiue_amd.decode import DecodeState
+        wl = workloads.make(args.workload, seed=0)
+        rows, vocab = wl.rows, wl.vocab
+        d_in = [hip.DeviceArray.from_numpy(wl.logits) for _ in range(sets)]
+        d_u = hip.DeviceArray.from_numpy(wl.uniforms)
+        d_tok = hip.DeviceArray(rows, np.int32)
+        prompts = [wl.history(r) for r in range(rows)]
+        state = DecodeState(sampler, prompts, stop_ids=(), ring_cap=4096)
+        from hachiue_amd.sampler import make_configs
+        cfgs = make_configs(wl.configs, rows)
+        kernel, unit = "row_kernel", "rows/s"
+        alg = wl.algorithmic_bytes()
+        desc = (f"decode step (draw, stop check, history append) over {wl.name}: {rows} rows x "
+                f"{vocab} fp32 logits, histories in 4096-id device rings")
+
+        def step(i: int) -> None:
+            state.step(d_in[i % sets].addr, vocab, vocab, cfgs, d_u.addr, d_tok.addr, stream=stream)
+
+        def check() -> dict:
+            from oracle import pyoracle
+            ref = pyoracle.decode_loop([wl.logits.copy()], vocab, prompts, [], wl.configs,
+                                       [wl.uniforms])
+            got = d_tok.download()
+            lens = state.lengths()
+            return {"rows": rows, "tokens_equal": int((got == ref.tokens[0]).sum()),
+                    "appended": int((lens == np.array([len(h) for h in ref.histories])).sum())}
         count = rows
     else:
         lh = workloads.make_lmhead(args.wfmt, args.hidden)

@@ -15,7 +15,7 @@
 //   every row, with the sums the formats' offsets need (sum x over a group).
 //   A row takes `seg` lanes (the row's units rounded up to a power of two;
 //   64 / seg rows per wave step), or all 64 lanes with two units each.
-//   The lanes of a row add their partial sums by a butterfly and the first
+//   The lanes of a row add their partial sums by DPP moves and the last
 //   writes y.  Weights are read once, through a buffer resource: Q4_K and F32
 //   in aligned 16-byte loads; Q4_0 and Q6_K blocks are 2-byte aligned, so
 //   their bytes come from aligned dwords and a funnel shift.
@@ -113,6 +113,23 @@ __device__ __forceinline__ float dot4u8(uint32_t w, const float *x, float acc) {
   acc = fmaf(x[2], (float)((w >> 16) & 0xFFu), acc);
   acc = fmaf(x[3], (float)(w >> 24), acc);
   return acc;
+}
+
+// Sum over aligned groups of `seg` lanes (a power of two, at most 64) by DPP
+// moves, without LDS: quad swaps, row mirrors, then row broadcasts for 32 and
+// 64.  The group's last lane holds its total.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
+__device__ __forceinline__ float seg_sum(float x, int seg) {
+  if (seg >= 2) x += dpp_mov<0xB1, 0xF>(x);    // quad_perm [1, 0, 3, 2]
+  if (seg >= 4) x += dpp_mov<0x4E, 0xF>(x);    // quad_perm [2, 3, 0, 1]
+  if (seg >= 8) x += dpp_mov<0x141, 0xF>(x);   // row_half_mirror
+  if (seg >= 16) x += dpp_mov<0x140, 0xF>(x);  // row_mirror
+  if (seg >= 32) x += dpp_mov<0x142, 0xA>(x);  // row_bcast:15 into rows 1 and 3
+  if (seg >= 64) x += dpp_mov<0x143, 0x8>(x);  // row_bcast:31 into row 3
+  return x;
 }
 
 // ---- per-format unit geometry, reads and dot products ------------------------
@@ -363,9 +380,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_kernel(GemvArgs g) {
 #pragma unroll
       for (int u = 0; u < NRU; ++u)
         if (live[u]) acc += U::dot(raw[k][u], unit[u], xr[u], xs[u]);
-      for (int o = seg >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+      acc = seg_sum(acc, seg);
       const int n = k ? n1 : n0;
-      if (lane % seg == 0 && n < g.N) g.y[(int64_t)m * g.ldy + n] = acc;
+      if (lane % seg == seg - 1 && n < g.N) g.y[(int64_t)m * g.ldy + n] = acc;
     }
   }
 }
@@ -441,19 +458,25 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_lds_kernel(GemvArgs g) {
     const int nb = b + nwaves;
     if (nb < batches) fetch(nb);
     const LSrc src{reinterpret_cast<const uint32_t *>(buf), a0};
+    // every step's unit bytes first, then the dot products: the LDS reads
+    // of a batch are in flight together
+    typename U::Raw rw[SB][NRU];
+#pragma unroll
+    for (int k = 0; k < SB; ++k) {
+      const int n = (b * SB + k) * rows_per_step + slot;
+#pragma unroll
+      for (int u = 0; u < NRU; ++u) U::load(src, (uint32_t)n * g.row_bytes, unit[u], rw[k][u]);
+    }
+#pragma unroll
     for (int k = 0; k < SB; ++k) {
       const int n = (b * SB + k) * rows_per_step + slot;
       float acc = 0.f;
 #pragma unroll
       for (int u = 0; u < NRU; ++u) {
-        if (live[u]) {
-          typename U::Raw raw;
-          U::load(src, (uint32_t)n * g.row_bytes, unit[u], raw);
-          acc += U::dot(raw, unit[u], xr[u], xs[u]);
-        }
+        if (live[u]) acc += U::dot(rw[k][u], unit[u], xr[u], xs[u]);
       }
-      for (int o = seg >> 1; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
-      if (lane % seg == 0 && n < g.N) g.y[(int64_t)m * g.ldy + n] = acc;
+      acc = seg_sum(acc, seg);
+      if (lane % seg == seg - 1 && n < g.N) g.y[(int64_t)m * g.ldy + n] = acc;
     }
     b = nb;
   }

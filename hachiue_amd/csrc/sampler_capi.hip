@@ -298,7 +298,8 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
                   const hs_sample_config *configs, const double *d_uniforms, int32_t *d_tokens,
                   int32_t cand_stride, int32_t *d_cand_ids, float *d_cand_probs,
                   int32_t *d_cand_count, int32_t *d_cutoff, uint32_t *d_row_flags,
-                  hipStream_t stream, const int64_t *d_hist_len = nullptr, int64_t hist_cap = 0) {
+                  hipStream_t stream, const int64_t *d_hist_len = nullptr, int64_t hist_cap = 0,
+                  const hs::DecodeArgs *dec = nullptr) {
   if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
   if (rows < 0) return fail(HS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %d)", rows);
   if (rows == 0) return HS_OK;
@@ -316,6 +317,11 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
     if (d_cand_count) HS_HIP(hipMemsetAsync(d_cand_count, 0, sizeof(int32_t) * rows, stream));
     if (d_cutoff) HS_HIP(hipMemsetAsync(d_cutoff, 0, sizeof(int32_t) * rows, stream));
     if (d_row_flags) HS_HIP(hipMemsetAsync(d_row_flags, 0, sizeof(uint32_t) * rows, stream));
+    if (dec) {   // the drawn 0s go through the decode bookkeeping
+      const hipError_t e = hs::launch_decode_append(*dec, stream);
+      if (e != hipSuccess)
+        return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+    }
     return HS_OK;
   }
   if (!d_logits) return fail(HS_ERR_INVALID_ARGUMENT, "logits must not be null");
@@ -384,6 +390,13 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   a.hist_off = d_hist_offsets;
   a.hist_len = d_hist_len;
   a.hist_cap = hist_cap;
+  if (dec) {
+    a.dec_ring = dec->ring;
+    a.dec_len = dec->len;
+    a.dec_done = dec->done;
+    a.dec_stop = dec->stop_ids;
+    a.dec_nstop = dec->n_stop;
+  }
   a.uniforms = d_uniforms;
   a.tokens = d_tokens;
   a.cand_stride = cand_stride;
@@ -698,12 +711,6 @@ int hs_decode_step_device(hs_context *ctx, float *d_logits, int32_t rows, int64_
     return fail(HS_ERR_INVALID_ARGUMENT, "n_stop must be in [0, %d] (got %d)", hs::kMaxStopIds,
                 n_stop);
   if (n_stop > 0 && !d_stop_ids) return fail(HS_ERR_INVALID_ARGUMENT, "stop ids must not be null");
-  const hipStream_t st = static_cast<hipStream_t>(stream);
-  int rc = sample_device(ctx, d_logits, rows, row_stride, vocab, d_ring, nullptr, configs,
-                         d_uniforms, d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr, st,
-                         d_len, ring_cap);
-  if (rc) return rc;
-  DeviceGuard guard(ctx->device);
   hs::DecodeArgs d;
   d.tokens = d_tokens;
   d.ring = d_ring;
@@ -713,10 +720,10 @@ int hs_decode_step_device(hs_context *ctx, float *d_logits, int32_t rows, int64_
   d.stop_ids = d_stop_ids;
   d.n_stop = n_stop;
   d.rows = rows;
-  const hipError_t e = hs::launch_decode_append(d, st);
-  if (e != hipSuccess)
-    return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
-  return HS_OK;
+  // the bookkeeping runs where each row's token is written
+  return sample_device(ctx, d_logits, rows, row_stride, vocab, d_ring, nullptr, configs, d_uniforms,
+                       d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr,
+                       static_cast<hipStream_t>(stream), d_len, ring_cap, &d);
 }
 
 int hs_argmax(hs_context *ctx, const float *logits, int32_t rows, int64_t row_stride,

@@ -129,6 +129,13 @@ struct LaunchArgs {
   const int64_t *hist_off;   // packed lists: row r is hist_ids[off[r], off[r+1])
   const int64_t *hist_len;   // rings (hist_cap > 0): row r is hist_ids[r * cap, +cap),
   int64_t hist_cap;          //   len[r] ids appended so far, the last min(len, cap) kept
+  // a decode step: where a row's token is written, its stop check and the
+  // append to its ring (the writable hist_ids) happen too; null otherwise
+  int32_t *dec_ring;
+  int64_t *dec_len;
+  int32_t *dec_done;
+  const int32_t *dec_stop;
+  int32_t dec_nstop;
   const double *uniforms;
   int32_t *tokens;
   int32_t cand_stride;

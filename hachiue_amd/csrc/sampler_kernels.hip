@@ -437,6 +437,37 @@ __device__ __forceinline__ int64_t hist_pos(const HistRow &h, int64_t j) {
   return (h.cap > 0 && i >= h.cap) ? i - h.cap : i;
 }
 
+// Writes a row's token.  In a decode step (src/engine.ts:1626-1644) the
+// token's bookkeeping follows in the same lane: a row already done reports
+// -1 and keeps its state; a stop id ends the row without joining the history
+// (the stop check comes first, :1628); any other id joins the ring
+// (tokenHistory.push, :1638).  A row the sampler leaves unresolved (-1)
+// keeps its state.  The reads are issued together, before any write; the
+// ring slot written is the oldest one, which no later read of this call
+// needs (every read of the row's history precedes its token).
+__device__ __forceinline__ void put_token(const LaunchArgs &a, int row, int token) {
+  if (!a.dec_ring) {
+    a.tokens[row] = token;
+    return;
+  }
+  const int done = a.dec_done[row];
+  int64_t len = a.dec_len[row];
+  bool stop = false;
+  for (int i = 0; i < a.dec_nstop; ++i) stop |= a.dec_stop[i] == token;
+  if (done != 0 || token < 0) {
+    a.tokens[row] = -1;
+    return;
+  }
+  a.tokens[row] = token;
+  if (stop) {
+    a.dec_done[row] = 1;
+    return;
+  }
+  if (len < 0) len = 0;
+  a.dec_ring[(int64_t)row * a.hist_cap + len % a.hist_cap] = token;
+  a.dec_len[row] = len + 1;
+}
+
 // ---------------------------------------------------------------- penalties
 
 // src/sampler.ts:29-30 (v < 0 ? v * p : v / p, stored binary32) followed by
@@ -544,28 +575,61 @@ size_t pen_smem_bytes() {
 // Exact replace-min scan of src/sampler.ts:50-69 over the whole (penalised)
 // row by one wave: slot j holds (sv[j], sid[j]); a logit enters iff it is
 // strictly greater than the current minimum, into the first slot holding that
-// minimum.  Logits are consumed in index order.
+// minimum.  Logits are consumed in index order, 64 * BLK per step; the next
+// step's loads are in flight while a step is scanned (one wave alone is
+// bound by the latency of its reads).  BLK is what the caller's registers
+// allow.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x);
+
+template <int BLK>
 __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, float *sv, int32_t *sid) {
   const int lane = lane_id();
-  for (int j = lane; j < k; j += 64) { sv[j] = -INFINITY; sid[j] = -1; }
+  // k <= 64: slot j lives in lane j's registers; the minimum is found by DPP
+  // moves (no LDS round trip per entering logit)
+  const bool in_regs = k <= 64;
+  float rv = lane < k ? -INFINITY : INFINITY;
+  int32_t rid = -1;
+  if (!in_regs)
+    for (int j = lane; j < k; j += 64) { sv[j] = -INFINITY; sid[j] = -1; }
   float mv = -INFINITY;
   int mi = 0;
-  constexpr int kBlk = 16;   // 1024 logits per step, loads issued together
-  for (int base = 0; base < vocab; base += 64 * kBlk) {
-    float x[kBlk];
+  float nx[BLK];
 #pragma unroll
-    for (int q = 0; q < kBlk; ++q) {
-      const int e = base + q * 64 + lane;
-      x[q] = e < vocab ? rowp[e] : __builtin_nanf("");
+  for (int q = 0; q < BLK; ++q) {
+    const int e = q * 64 + lane;
+    nx[q] = e < vocab ? rowp[e] : __builtin_nanf("");
+  }
+  for (int base = 0; base < vocab; base += 64 * BLK) {
+    float x[BLK];
+#pragma unroll
+    for (int q = 0; q < BLK; ++q) x[q] = nx[q];
+    if (base + 64 * BLK < vocab) {
+#pragma unroll
+      for (int q = 0; q < BLK; ++q) {
+        const int e = base + 64 * BLK + q * 64 + lane;
+        nx[q] = e < vocab ? rowp[e] : __builtin_nanf("");
+      }
     }
 #pragma unroll
-    for (int q = 0; q < kBlk; ++q) {
+    for (int q = 0; q < BLK; ++q) {
       int done = -1;
       for (;;) {
         const unsigned long long b = __ballot(x[q] > mv && lane > done);
         if (!b) break;
         const int L = __ffsll((long long)b) - 1;
-        const float vL = __shfl(x[q], L);
+        const float vL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[q]), L));
+        if (in_regs) {
+          if (lane == mi) { rv = vL; rid = base + q * 64 + L; }
+          // the smallest slot holding the minimum (binary32 order: -0 == +0;
+          // f2key maps -Infinity to 0)
+          const uint32_t mk = lane < k ? ~f2key(rv) : 0u;
+          const uint32_t m = wave_max_u32(mk);
+          const float mvf = m == 0xFFFFFFFFu ? -INFINITY : key2f(~m);
+          mi = (int)__ffsll((long long)__ballot(lane < k && rv == mvf)) - 1;
+          mv = mvf;
+          done = L;
+          continue;
+        }
         // a wave's LDS accesses complete in program order, so every lane's
         // rescan below observes this store
         if (lane == 0) { sv[mi] = vL; sid[mi] = base + q * 64 + L; }
@@ -588,6 +652,10 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
         done = L;
       }
     }
+  }
+  if (in_regs && lane < k) {
+    sv[lane] = rv;
+    sid[lane] = rid;
   }
 }
 
@@ -753,7 +821,7 @@ __device__ __forceinline__ void finish_row(const LaunchArgs &a, const RowPlan &P
   const double u = a.uniforms[row];
   for (int attempt = 0; attempt < 2; ++attempt) {
     if (need_replay) {
-      if (tid < 64) replay_row(rowp, a.vocab, k, s.rsv, s.rsid);
+      if (tid < 64) replay_row<NT == kRowThreads ? 8 : 32>(rowp, a.vocab, k, s.rsv, s.rsid);
       __syncthreads();
       if (tid == 0) f.n_sel = 0;
       __syncthreads();
@@ -800,7 +868,7 @@ __device__ __forceinline__ void finish_row(const LaunchArgs &a, const RowPlan &P
   const int cs = a.cand_stride;
   if (tid == 0) {
     const int pick = f.pick;
-    a.tokens[row] = pick >= 0 ? s.sids[pick] : 0;
+    put_token(a, row, pick >= 0 ? s.sids[pick] : 0);
     if (a.cand_count_out) a.cand_count_out[row] = n;
     if (a.cutoff_out) a.cutoff_out[row] = f.cutoff;
     if (a.row_flags) {
@@ -826,7 +894,7 @@ __device__ __forceinline__ void write_greedy(const LaunchArgs &a, int row, float
                              unsigned long long best) {
   int token = best ? (int)cand_idx(best) : 0;
   if (isnan(x0)) token = 0;   // bestVal = logits[0] = NaN: nothing is '>' it
-  a.tokens[row] = token;
+  put_token(a, row, token);
   if (a.cand_count_out) a.cand_count_out[row] = 0;
   if (a.cutoff_out) a.cutoff_out[row] = 0;
   if (a.row_flags) a.row_flags[row] = HS_ROW_GREEDY;
@@ -1367,7 +1435,7 @@ __device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &
     }
     if (need) {
       if (acquire_replay) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      replay_row(rowp, a.vocab, k, rsv, rsid);
+      replay_row<32>(rowp, a.vocab, k, rsv, rsid);
       const bool filled = lane < k && rsid[lane] >= 0;
       unsigned long long x = filled ? pack_cand(f2key(rsv[lane]), (uint32_t)lane) : 0ull;
       x = wave_sort_desc64(x);   // value descending, slot ascending (stable sort)
@@ -1380,7 +1448,7 @@ __device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &
   }
   const int token = pick >= 0 ? __shfl(id, pick) : 0;
   if (lane == 0) {
-    a.tokens[row] = token;
+    put_token(a, row, token);
     if (a.cand_count_out) a.cand_count_out[row] = n;
     if (a.cutoff_out) a.cutoff_out[row] = cut;
     if (a.row_flags) {
@@ -2995,7 +3063,7 @@ __global__ __launch_bounds__(kLT) void large_kernel(LaunchArgs a, Workspace ws) 
 
   if (n <= 1) {   // src/sampler.ts:76-77: no draw
     if (tid == 0) {
-      a.tokens[row] = n == 1 ? (int)cand_idx(best) : 0;
+      put_token(a, row, n == 1 ? (int)cand_idx(best) : 0);
       if (a.cand_count_out) a.cand_count_out[row] = n;
       if (a.cutoff_out) a.cutoff_out[row] = n;
       if (a.row_flags) a.row_flags[row] = HS_ROW_SINGLE | HS_ROW_LARGE;
@@ -3131,7 +3199,7 @@ __global__ __launch_bounds__(kLT) void large_kernel(LaunchArgs a, Workspace ws) 
   uint32_t flags = HS_ROW_LARGE;
   if (ambiguous) flags |= HS_ROW_UNSUPPORTED | HS_ROW_TIES;
   if (tid == 0) {
-    a.tokens[row] = ambiguous ? -1 : lpick.id;
+    put_token(a, row, ambiguous ? -1 : lpick.id);
     if (a.cand_count_out) a.cand_count_out[row] = n;
     if (a.cutoff_out) a.cutoff_out[row] = cut;
   }
@@ -3356,26 +3424,26 @@ hipError_t launch_one(K kernel, dim3 grid, dim3 block, size_t smem, hipStream_t 
 
 }  // namespace
 
-// One decode step's bookkeeping per row, after the sampler (src/engine.ts:
-// 1626-1644): a row already done reports -1 and keeps its state; a drawn
-// token of the stop set ends the row without joining the history (the stop
-// check comes first, :1628); any other token joins the history ring
-// (tokenHistory.push, :1638) for the next step's penalties.
+// A decode step's bookkeeping as a kernel of its own (put_token's, one
+// thread per row), for the calls whose tokens no sampler kernel writes (an
+// empty vocabulary: every token 0).
 __global__ __launch_bounds__(256) void decode_append_kernel(DecodeArgs d) {
   const int r = (int)(blockIdx.x * blockDim.x + threadIdx.x);
   if (r >= d.rows) return;
-  if (d.done[r] != 0) {
+  // every read first (one round trip), then the decision and the writes
+  const int done = d.done[r];
+  const int t = d.tokens[r];
+  int64_t len = d.len[r];
+  bool stop = false;
+  for (int i = 0; i < d.n_stop; ++i) stop |= d.stop_ids[i] == t;
+  if (done != 0) {
     d.tokens[r] = -1;
     return;
   }
-  const int t = d.tokens[r];
-  bool stop = false;
-  for (int i = 0; i < d.n_stop; ++i) stop |= d.stop_ids[i] == t;
   if (stop) {
     d.done[r] = 1;
     return;
   }
-  int64_t len = d.len[r];
   if (len < 0) len = 0;
   d.ring[(int64_t)r * d.cap + len % d.cap] = t;
   d.len[r] = len + 1;

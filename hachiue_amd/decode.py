@@ -12,6 +12,8 @@ them.
 """
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 
 from . import hip
@@ -47,8 +49,9 @@ class DecodeState:
     def step(self, d_logits: int, row_stride: int, vocab: int, configs, d_uniforms: int,
              d_tokens: int, stream=None) -> None:
         """Enqueue one step: d_tokens[r] = the drawn id (-1 for rows done
-        before it)."""
-        cfgs = _configs(configs, self.rows)
+        before it).  `configs`: SampleConfig dicts, or an array built once by
+        sampler.make_configs."""
+        cfgs = configs if isinstance(configs, ctypes.Array) else _configs(configs, self.rows)
         self.sampler.decode_step_device(d_logits, self.rows, row_stride, vocab, self.ring.addr,
                                         self.ring_cap, self.len.addr, self.done.addr,
                                         self.stop.addr if self.n_stop else None, self.n_stop, cfgs,

@@ -183,14 +183,16 @@ int hs_lm_head_sample_device(hs_context *ctx, const float *d_x, int32_t M,
  *      row r's history read from its ring: d_ring[r * ring_cap, +ring_cap)
  *      holds the last min(d_len[r], ring_cap) ids appended, the id appended
  *      as the j-th (0-based) at slot j mod ring_cap;
- *   2. a row with d_done[r] != 0 (done before this step) gets
- *      d_tokens[r] = -1 and keeps its state; a drawn id in
+ *   2. a row with d_done[r] != 0 (done before this step), or whose draw
+ *      is left unresolved (HS_ROW_UNSUPPORTED), gets d_tokens[r] = -1 and
+ *      keeps its state; a drawn id in
  *      d_stop_ids[0, n_stop) sets d_done[r] = 1 (the id is reported in
  *      d_tokens[r] and does not join the history); any other id is written
  *      to slot d_len[r] mod ring_cap and d_len[r] is incremented.
  * The repetition penalty reads the last 128 ids (ring_cap >= 128 keeps that
  * window exact); presence / frequency count the last min(len, ring_cap) ids,
- * the full history while ring_cap >= len.  The caller fills the rings with
+ * the full history while ring_cap >= len.  The stop check and the append run
+ * in the lane that writes the row's token, inside the sampler's kernels.  The caller fills the rings with
  * the prompt ids (d_len[r] = prompt length) before the first step, bounds
  * the steps (maxNewTokens, the sequence length) and reads d_done / d_tokens
  * when it wants to (src/engine.ts:1631, onToken).  Greedy rows

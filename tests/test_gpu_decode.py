@@ -105,6 +105,29 @@ def test_decode_many_rows(sampler):
     run_decode(sampler, V, prompts, [1, 2, 3], cfgs, 3, 256, seed=9)
 
 
+def test_decode_empty_vocabulary(sampler):
+    """vocab 0: every draw is 0 (src/sampler.ts reads no logit); the stop
+    check and the append still run."""
+    st = DecodeState(sampler, [[5], [], [1, 2, 3]], [0], ring_cap=128)
+    st2 = DecodeState(sampler, [[5], [], [1, 2, 3]], [], ring_cap=128)
+    d_u = hip.DeviceArray.from_numpy(np.zeros(3))
+    d_t = hip.DeviceArray(3, np.int32)
+    print("[gpu] decode vocab 0", flush=True)
+    st.step(0, 0, 0, [None] * 3, d_u.addr, d_t.addr)
+    st.step(0, 0, 0, [None] * 3, d_u.addr, d_t.addr)
+    hip.synchronize()
+    assert d_t.download().tolist() == [-1, -1, -1]
+    assert st.finished().tolist() == [True, True, True]
+    assert st.lengths().tolist() == [1, 0, 3]
+    st2.step(0, 0, 0, [None] * 3, d_u.addr, d_t.addr)
+    hip.synchronize()
+    assert d_t.download().tolist() == [0, 0, 0]
+    assert st2.lengths().tolist() == [2, 1, 4]
+    assert st2.history(2).tolist() == [1, 2, 3, 0]
+    st.free()
+    st2.free()
+
+
 def test_decode_rejects_bad_arguments(sampler):
     from hachiue_amd.sampler import SamplerError
     st = DecodeState(sampler, [[1, 2]], [], ring_cap=128)
