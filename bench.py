@@ -374,6 +374,10 @@ def other_path(args) -> int:
     kms, calls = sampler.kernel_times()
     sampler.set_timing(False)
     kms_avg = kms[kernel] / max(calls, 1)
+    if args.copy_probe and sets > 1:   # a copy of known size for the counters' scale
+        d_in[1].copy_from(d_in[0])
+        hip.synchronize()
+        log(f"[bench] copy probe: {d_in[0].nbytes} bytes device to device")
     ms_per_step = total_ms / args.steps
     achieved = alg / (kms_avg * 1e-3) / 1e9
     line = {

@@ -73,6 +73,7 @@ struct hs_context {
   // workspace
   DevBuf plans, cand, cand_count, info;
   DevBuf split_list, split_meta, split_cnt;   // split rows (split_cnt: zero between calls)
+  DevBuf gemv_part, gemv_cnt;   // Q6_K GEMV tiles cut between waves (gemv_cnt: zero between calls)
   int64_t cand_count_rows = 0;     // rows whose counter is known to be zero
   // plan upload cache
   std::vector<hs::RowPlan> last_plans;
@@ -487,7 +488,8 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32
   if ((reinterpret_cast<uintptr_t>(d_w) & 15u) || (reinterpret_cast<uintptr_t>(d_x) & 3u))
     return fail(HS_ERR_INVALID_ARGUMENT, "w must be 16-byte and x 4-byte aligned");
   const int64_t row_bytes = (int64_t)(K / bw) * bb;
-  if ((int64_t)N * row_bytes > 0xFFFFFF00LL)
+  // (Q6_K's slabs read up to 3 KiB past a row's start)
+  if ((int64_t)N * row_bytes > (w_type == hs::kW_Q6_K ? 0xFFFF0000LL : 0xFFFFFF00LL))
     return fail(HS_ERR_UNSUPPORTED, "weights of %lld bytes above 4 GiB", (long long)(N * row_bytes));
   hs::GemvArgs g;
   memset(&g, 0, sizeof g);
@@ -513,6 +515,19 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32
   g.blocks = (int32_t)std::min<int64_t>((steps + wpb - 1) / wpb, 1 << 20);
   if (M > 65535) return fail(HS_ERR_UNSUPPORTED, "M %d above 65535", M);
   DeviceGuard guard(ctx->device);
+  if (w_type == hs::kW_Q6_K) {   // the hand-over slots of tiles cut between waves
+    int cus = 0;
+    HS_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device));
+    g.part_cap = cus * hs::kGemvWavesPerCU;
+    const size_t slots = (size_t)g.part_cap * (size_t)M;
+    HS_HIP(ctx->gemv_part.ensure(slots * 16 * sizeof(float)));
+    if (ctx->gemv_cnt.bytes < slots * sizeof(uint32_t)) {
+      HS_HIP(ctx->gemv_cnt.ensure(slots * sizeof(uint32_t)));
+      HS_HIP(hipMemset(ctx->gemv_cnt.p, 0, ctx->gemv_cnt.bytes));
+    }
+    g.part = static_cast<float *>(ctx->gemv_part.p);
+    g.tile_cnt = static_cast<uint32_t *>(ctx->gemv_cnt.p);
+  }
   hipEvent_t *ev = nullptr;
   if (ctx->timing) {
     hs_context::TimedCall tc{};
@@ -634,6 +649,8 @@ int hs_context_destroy(hs_context *ctx) {
     ctx->split_list.release();
     ctx->split_meta.release();
     ctx->split_cnt.release();
+    ctx->gemv_part.release();
+    ctx->gemv_cnt.release();
     ctx->h_logits.release();
     ctx->h_hist.release();
     ctx->h_off.release();

@@ -179,7 +179,13 @@ struct GemvArgs {
   int32_t seg;               // lanes per row (power of two, <= 64) when nru == 1
   int32_t nru;               // units per lane: 1, or 2 (a row takes all 64 lanes)
   int32_t blocks;            // workgroups per activation row
+  // Q6_K: per activation row, part_cap slots of 16 partial sums and tile
+  // counters (zero between calls) for the tiles cut between waves
+  float *part;
+  uint32_t *tile_cnt;
+  int32_t part_cap;          // at least the waves of one activation row
 };
+constexpr int kGemvWavesPerCU = 16;   // Q6_K: the part_cap a CU needs
 // Block formats go through LDS in batches of row steps (a step: the rows of
 // one wave pass, 64 units): steps per batch and 16-byte reads per lane that
 // hold a batch (its bytes plus the alignment of its start).
