@@ -4,21 +4,20 @@
 // final normalised hidden state (src/engine.ts:1493-1515), dispatched to one
 // of its WGSL GEMV pipelines by weight type (src/engine.ts:1156-1183,
 // src/kernels.ts:244-290, :717-1090).  The weight tensor is the GGUF tensor's
-// raw blocks, rows back to back (src/engine.ts:772-800); this kernel reads it
+// raw blocks, rows back to back (src/engine.ts:772-800); these kernels read it
 // in place: F32, Q4_0 (18 B / 32 weights), Q4_1 (20 B / 32), Q4_K (144 B /
 // 256), Q6_K (210 B / 256).
 //
-// Layout of the work (one wave per group of rows):
+// Q6_K runs on the matrix cores (gemv_q6k_mfma_kernel, described there).  The
+// other formats use the vector units, one wave per group of rows:
 //   every lane owns a fixed "unit" of each row: 32 weights (F32, Q4_0, Q4_1,
-//   Q4_K: half of a 32-byte quant pair) or 64 (Q6_K: 16 positions of one half
-//   of a super-block, four quarters).  Its slice of x stays in registers for
-//   every row, with the sums the formats' offsets need (sum x over a group).
-//   A row takes `seg` lanes (the row's units rounded up to a power of two;
-//   64 / seg rows per wave step), or all 64 lanes with two units each.
+//   Q4_K: half of a 32-byte quant pair).  Its slice of x stays in registers
+//   for every row, with the sums the formats' offsets need (sum x over a
+//   group).  A row takes `seg` lanes (the row's units rounded up to a power of
+//   two; 64 / seg rows per wave step), or all 64 lanes with two units each.
 //   The lanes of a row add their partial sums by DPP moves and the last
-//   writes y.  Weights are read once, through a buffer resource: Q4_K and F32
-//   in aligned 16-byte loads; Q4_0 and Q6_K blocks are 2-byte aligned, so
-//   their bytes come from aligned dwords and a funnel shift.
+//   writes y.  Weights are read once, through a buffer resource: F32 in
+//   aligned 16-byte loads, the block formats through LDS (gemv_lds_kernel).
 // Quant nibbles become floats a byte at a time (v_cvt_f32_ubyte*), four per
 // dword, and enter binary32 fused multiply-adds; the result differs from the
 // reference's binary32 sums by rounding only (its own order is not a
@@ -272,68 +271,6 @@ template <> struct Unit<kW_Q4_K> {
   }
 };
 
-// Q6_K: super-block s = j / 4 (ql 128 B, qh 64 B, 16 int8 scales, d), part
-// t = j % 4: half n = t / 2, positions l = 16 h + i (h = t % 2, i < 16) of
-// the four quarters: weight 128 n + 32 qq + l has low bits from ql byte
-// 64 n + 32 (qq & 1) + l (low nibble for qq < 2, high otherwise), high bits
-// 2 qq .. 2 qq + 1 of qh byte 32 n + l, scale 8 n + h + 2 qq;
-// w = d sc (q - 32) (src/gguf.ts:206-232).
-template <> struct Unit<kW_Q6_K> {
-  static constexpr int W = 64;
-  struct Raw { Span<4> qa, qb, qh; Span<2> sc; uint32_t dd, dsh; };
-  static __device__ __forceinline__ int xidx(int j, int i) {
-    const int s = j >> 2, t = j & 3, n = t >> 1, h = t & 1, qq = i >> 4;
-    return 256 * s + 128 * n + 32 * qq + 16 * h + (i & 15);
-  }
-  static __device__ __forceinline__ void sums(const float *x, float *s) {
-#pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      float a = 0.f;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) a += x[16 * qq + i];
-      s[qq] = a;
-    }
-  }
-  template <typename S>
-  static __device__ __forceinline__ void load(const S &r, uint32_t rb, int j, Raw &a) {
-    const int sb = j >> 2, t = j & 3, n = t >> 1, h = t & 1;
-    const uint32_t o = rb + 210u * sb;
-    const uint32_t oa = o + 64u * n + 16u * h, ob = oa + 32u, oh = o + 128u + 32u * n + 16u * h;
-    const uint32_t os = o + 192u + 8u * n, od = o + 208u;
-    a.qa.load(r, oa, oa + 15u);   // ql, quarters 0 and 2
-    a.qb.load(r, ob, ob + 15u);   // ql, quarters 1 and 3
-    a.qh.load(r, oh, oh + 15u);
-    a.sc.load(r, os, os + 7u);    // this half's 8 scales
-    a.dd = r.dw(od & ~3u);
-    a.dsh = 8u * (od & 3u);
-  }
-  static __device__ __forceinline__ float dot(const Raw &a, int j, const float *x, const float *s) {
-    const int h = j & 1;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const uint32_t qa = a.qa.at(v), qb = a.qb.at(v), hv = a.qh.at(v);
-      const uint32_t q0 = (qa & 0x0F0F0F0Fu) | ((hv << 4) & 0x30303030u);
-      const uint32_t q1 = (qb & 0x0F0F0F0Fu) | ((hv << 2) & 0x30303030u);
-      const uint32_t q2 = ((qa >> 4) & 0x0F0F0F0Fu) | (hv & 0x30303030u);
-      const uint32_t q3 = ((qb >> 4) & 0x0F0F0F0Fu) | ((hv >> 2) & 0x30303030u);
-      acc[0] = dot4u8(q0, x + 4 * v, acc[0]);
-      acc[1] = dot4u8(q1, x + 16 + 4 * v, acc[1]);
-      acc[2] = dot4u8(q2, x + 32 + 4 * v, acc[2]);
-      acc[3] = dot4u8(q3, x + 48 + 4 * v, acc[3]);
-    }
-    // scales: byte h + 2 qq of the half's 8 (dword qq / 2)
-    float tot = 0.f;
-#pragma unroll
-    for (int qq = 0; qq < 4; ++qq) {
-      const uint32_t sh = 8u * (uint32_t)(h + 2 * (qq & 1));
-      const float sc = (float)(int8_t)((a.sc.at(qq >> 1) >> sh) & 0xFFu);
-      tot = fmaf(sc, fmaf(-32.f, s[qq], acc[qq]), tot);
-    }
-    return h2f(a.dd >> a.dsh) * tot;
-  }
-};
-
 }  // namespace
 
 // One wave per group of rows; see the top of the file.  NRU: units per lane
@@ -508,7 +445,9 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_lds_kernel(GemvArgs g) {
 // bytes in flight per CU are what keep HBM busy).
 // q bytes of a lane: half n = G / 2, positions 16 h .. 16 h + 15 (h = G % 2)
 // of quarter qq, from ql (low nibbles for quarters 0 and 1, high for 2 and
-// 3) and qh (bits 2 qq) -- the layout of Unit<kW_Q6_K>.
+// 3) and qh (bits 2 qq): weight 128 n + 32 qq + l of a super-block has its
+// low bits in ql byte 64 n + 32 (qq & 1) + l and its high bits in qh byte
+// 32 n + l; scale 8 n + h + 2 qq (src/gguf.ts:206-232).
 namespace q6m {
 constexpr int kSB = 1;                               // super-blocks per slab
 constexpr int kNB = 2;                               // ring depth (slabs per wave)

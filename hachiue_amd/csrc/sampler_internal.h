@@ -189,9 +189,9 @@ constexpr int kGemvWavesPerCU = 16;   // Q6_K: the part_cap a CU needs
 // Block formats go through LDS in batches of row steps (a step: the rows of
 // one wave pass, 64 units): steps per batch and 16-byte reads per lane that
 // hold a batch (its bytes plus the alignment of its start).
-constexpr int gemv_batch_steps(int type) { return type == kW_Q6_K ? 2 : 4; }
+constexpr int gemv_batch_steps(int) { return 4; }
 constexpr int gemv_unit_bytes2(int type) {   // twice a unit's bytes
-  return type == kW_Q6_K ? 105 : type == kW_Q4_1 ? 40 : 36;
+  return type == kW_Q4_1 ? 40 : 36;
 }
 constexpr int gemv_batch_chunks(int type) {
   return (gemv_batch_steps(type) * 32 * gemv_unit_bytes2(type) + 32 + 1023) / 1024;

@@ -117,3 +117,19 @@ def test_lm_head_then_sample(sampler):
     res = o.sample_batch(ref, N, ids, off, cfgs, u)
     assert tokens.tolist() == res.token.tolist()
     assert np.array_equal(pen.view(np.uint32), ref.view(np.uint32))
+
+
+def test_q6k_heavy_tailed_activations(sampler):
+    """The Q6_K kernel holds x as four int8 limbs per 16-position scale group,
+    exact to 2^-28 of the group's largest |x|.  Hidden states with outlier
+    channels (a few positions 100-1000x the rest) and exact zeros stay within
+    the bound."""
+    wtype, K, N = o.W_Q6_K, 2048, 4099
+    rng = np.random.default_rng(77)
+    w = random_blocks(wtype, N, K, rng)
+    x = rng.standard_normal((3, K)).astype(np.float32)
+    x[0, rng.integers(0, K, 12)] *= 1000.0
+    x[1, ::5] = 0.0
+    x[2] = (rng.standard_normal(K) * np.exp2(rng.integers(-30, 30, K))).astype(np.float32)
+    y = run_gemv(sampler, wtype, x, w, N)
+    check(wtype, x, w, N, y)
