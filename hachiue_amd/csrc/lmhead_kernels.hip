@@ -539,11 +539,16 @@ __global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_mfma_kernel(GemvArg
       const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)reinterpret_cast<uintptr_t>(
           (__attribute__((address_space(3))) uint8_t *)(dst + c * 1024)));
       // the last load's lanes past the slab are masked off: they write no LDS
-      if (c + 1 < kLoads || lane < kLastLanes)
-        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                     :
-                     : "s"(m0), "v"(off), "s"(rs)
-                     : "memory", "m0");
+      // (M0 is the compiler's: it is saved and restored around the load)
+      if (c + 1 < kLoads || lane < kLastLanes) {
+        uint32_t keep;
+        asm volatile(
+            "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %1\n\t"
+            "buffer_load_dwordx4 %2, %3, 0 offen lds\n\ts_mov_b32 m0, %0"
+            : "=&s"(keep)
+            : "s"(m0), "v"(off), "s"(rs)
+            : "memory");
+      }
     }
   };
 
