@@ -743,14 +743,6 @@ hipError_t launch_fmt(GemvArgs g, hipStream_t stream, hipEvent_t *ev) {
 
 hipError_t launch_q6k_mfma(GemvArgs g, hipStream_t stream, hipEvent_t *ev) {
   const size_t lds = gemv_q6k_mfma_lds_bytes(g.K);
-  static bool attr = false;
-  if (!attr) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_q6k_mfma_kernel),
-                                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                                             (int)gemv_q6k_mfma_lds_bytes(kGemvMaxK));
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
   const int ntiles = (g.N + 15) / 16;
   const int res = resident_blocks(reinterpret_cast<const void *>(gemv_q6k_mfma_kernel), (uint32_t)lds,
                                   q6m::kThreads);
@@ -768,6 +760,14 @@ hipError_t launch_q6k_mfma(GemvArgs g, hipStream_t stream, hipEvent_t *ev) {
 }
 
 }  // namespace
+
+// Per device, once (with the sampler's kernels): the Q6_K kernel's dynamic
+// LDS limit.
+hipError_t prepare_gemv() {
+  return hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_q6k_mfma_kernel),
+                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)gemv_q6k_mfma_lds_bytes(kGemvMaxK));
+}
 
 hipError_t launch_gemv(const GemvArgs &g, hipStream_t stream, hipEvent_t *ev) {
   const bool two = g.nru == 2;

@@ -198,6 +198,7 @@ constexpr int gemv_batch_chunks(int type) {
 }
 constexpr int gemv_lds_bytes(int type) { return (kGemvThreads / 64) * gemv_batch_chunks(type) * 1024; }
 hipError_t launch_gemv(const GemvArgs &g, hipStream_t stream, hipEvent_t *ev);
+hipError_t prepare_gemv();      // per device, once (called by prepare_kernels)
 
 // ---- decode step bookkeeping (after the sampler, same stream)
 struct DecodeArgs {

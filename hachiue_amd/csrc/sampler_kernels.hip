@@ -3378,6 +3378,8 @@ __global__ __launch_bounds__(kRowThreads) void argmax_kernel(LaunchArgs a, Works
 // ---------------------------------------------------------------- launch
 
 hipError_t prepare_kernels() {
+  hipError_t e0 = prepare_gemv();
+  if (e0 != hipSuccess) return e0;
   const int pen_smem = (int)pen_smem_bytes();
   const int row_smem = (int)row_smem_bytes(kRowMaxVocab);
   hipError_t e;
