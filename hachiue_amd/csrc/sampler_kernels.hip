@@ -582,13 +582,75 @@ size_t pen_smem_bytes() {
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t x);
 
 template <int BLK>
-__device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, float *sv, int32_t *sid) {
+__device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, float *sv, int32_t *sid,
+                                           const uint32_t *bkey = nullptr) {
   const int lane = lane_id();
   // k <= 64: slot j lives in lane j's registers; the minimum is found by DPP
   // moves (no LDS round trip per entering logit)
   const bool in_regs = k <= 64;
   float rv = lane < k ? -INFINITY : INFINITY;
   int32_t rid = -1;
+  // the smallest slot holding the minimum (binary32 order: -0 == +0;
+  // f2key maps -Infinity to 0)
+  auto slot_min = [&](float &mv, int &mi) {
+    const uint32_t mk = lane < k ? ~f2key(rv) : 0u;
+    const uint32_t m = wave_max_u32(mk);
+    const float mvf = m == 0xFFFFFFFFu ? -INFINITY : key2f(~m);
+    mi = (int)__ffsll((long long)__ballot(lane < k && rv == mvf)) - 1;
+    mv = mvf;
+  };
+  if (bkey && in_regs) {
+    // bkey[b]: key of the largest logit of block b (64 logits).  A block
+    // whose largest logit is not above the current minimum holds no logit
+    // that enters, so it is not read.  Windows of 64 blocks; of a window's
+    // blocks that can hold one (against the minimum at the window's start),
+    // BLK at a time are read together, then scanned in order.
+    float mv = -INFINITY;
+    int mi = 0;
+    const int nb = (vocab + 63) >> 6;
+    for (int b = 0; b < nb; b += 64) {
+      const uint32_t kb = b + lane < nb ? bkey[b + lane] : 0u;
+      unsigned long long m = __ballot(kb > f2key(mv));
+      while (m) {
+        unsigned long long mm = m;
+        float x[BLK];
+#pragma unroll
+        for (int q = 0; q < BLK; ++q) {
+          const int t = mm ? (int)__ffsll((long long)mm) - 1 : -1;
+          if (mm) mm &= mm - 1;
+          const int e = (b + t) * 64 + lane;
+          const bool in = t >= 0 && e < vocab;
+          const float v = rowp[in ? e : 0];   // always a read inside the row
+          x[q] = in ? v : __builtin_nanf("");
+        }
+        unsigned long long m2 = m;
+#pragma unroll
+        for (int q = 0; q < BLK; ++q) {
+          if (m2) {
+            const int t = (int)__ffsll((long long)m2) - 1;
+            m2 &= m2 - 1;
+            const int base = (b + t) * 64;
+            int done = -1;
+            for (;;) {
+              const unsigned long long bl = __ballot(x[q] > mv && lane > done);
+              if (!bl) break;
+              const int L = __ffsll((long long)bl) - 1;
+              const float vL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[q]), L));
+              if (lane == mi) { rv = vL; rid = base + L; }
+              slot_min(mv, mi);
+              done = L;
+            }
+          }
+        }
+        m = mm;
+      }
+    }
+    if (lane < k) {
+      sv[lane] = rv;
+      sid[lane] = rid;
+    }
+    return;
+  }
   if (!in_regs)
     for (int j = lane; j < k; j += 64) { sv[j] = -INFINITY; sid[j] = -1; }
   float mv = -INFINITY;
@@ -620,13 +682,7 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
         const float vL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[q]), L));
         if (in_regs) {
           if (lane == mi) { rv = vL; rid = base + q * 64 + L; }
-          // the smallest slot holding the minimum (binary32 order: -0 == +0;
-          // f2key maps -Infinity to 0)
-          const uint32_t mk = lane < k ? ~f2key(rv) : 0u;
-          const uint32_t m = wave_max_u32(mk);
-          const float mvf = m == 0xFFFFFFFFu ? -INFINITY : key2f(~m);
-          mi = (int)__ffsll((long long)__ballot(lane < k && rv == mvf)) - 1;
-          mv = mvf;
+          slot_min(mv, mi);
           done = L;
           continue;
         }
@@ -1404,66 +1460,95 @@ __device__ __forceinline__ int wave_tail(uint32_t key, int n, const RowPlan &P, 
 // always when force_replay (the candidate list overflowed).
 // acquire_replay: other workgroups wrote parts of the row (split rows), so a
 // replay first acquires their stores at agent scope.
-__device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &P, int row, const float *rowp,
-                            unsigned long long F, bool extra_ties, bool force_replay, double u,
-                            float *rsv, int32_t *rsid, double *sp, bool acquire_replay = false) {
+// The tail's state between its decision and its outputs.
+struct TailState {
+  uint32_t key, T;
+  int32_t id;
+  int n, cut, pick;
+  float prob;
+  bool boundary_tie, internal_tie, need;
+};
+
+// The draw from F, and whether the slot replay is needed (need).
+__device__ __forceinline__ TailState tail_decide(const LaunchArgs &a, const RowPlan &P,
+                                                 unsigned long long F, bool extra_ties,
+                                                 bool force_replay, double u, double *sp) {
   const int lane = lane_id();
   const int k = P.k;
+  TailState st;
   const uint32_t fkey = cand_key(F);
   const unsigned long long Fk = __shfl(F, k - 1);
-  const uint32_t T = cand_key(Fk);           // 0: fewer than k candidates
-  const int n_sel = __popcll(__ballot(F != 0ull && fkey >= T));
-  int n = n_sel < k ? n_sel : k;
-  const bool boundary_tie = n_sel > k || (T != 0 && extra_ties);
+  st.T = cand_key(Fk);           // 0: fewer than k candidates
+  const int n_sel = __popcll(__ballot(F != 0ull && fkey >= st.T));
+  st.n = n_sel < k ? n_sel : k;
+  st.boundary_tie = n_sel > k || (st.T != 0 && extra_ties);
   const uint32_t next_key = __shfl_down(fkey, 1);
-  const bool internal_tie = __ballot(lane + 1 < n && next_key == fkey) != 0;
-
-  uint32_t key = fkey;
-  int32_t id = (int32_t)cand_idx(F);
-  int cut = 0;
-  float prob = 0.f;
-  int pick = force_replay ? -1 : wave_tail(key, n, P, u, &cut, &prob, sp);
-  bool replayed = false;
-  if (boundary_tie || internal_tie || force_replay) {
+  st.internal_tie = __ballot(lane + 1 < st.n && next_key == fkey) != 0;
+  st.key = fkey;
+  st.id = (int32_t)cand_idx(F);
+  st.cut = 0;
+  st.prob = 0.f;
+  st.pick = force_replay ? -1 : wave_tail(st.key, st.n, P, u, &st.cut, &st.prob, sp);
+  st.need = false;
+  if (st.boundary_tie || st.internal_tie || force_replay) {
     // the order inside a group of equal values follows the slot history
-    bool need = a.want_cands != 0 || force_replay;
-    if (!need && pick >= 0) {
-      const uint32_t kp = readlane_u32(key, pick);
-      const uint32_t km = pick > 0 ? readlane_u32(key, pick - 1) : 0u;
-      const uint32_t kn = pick + 1 < n ? readlane_u32(key, pick + 1) : 0u;
-      need = (pick > 0 && km == kp) || (pick + 1 < n && kn == kp) || (boundary_tie && kp == T);
-    }
-    if (need) {
-      if (acquire_replay) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      replay_row<32>(rowp, a.vocab, k, rsv, rsid);
-      const bool filled = lane < k && rsid[lane] >= 0;
-      unsigned long long x = filled ? pack_cand(f2key(rsv[lane]), (uint32_t)lane) : 0ull;
-      x = wave_sort_desc64(x);   // value descending, slot ascending (stable sort)
-      n = __popcll(__ballot(filled));
-      key = cand_key(x);
-      id = lane < n ? rsid[cand_idx(x)] : -1;
-      pick = wave_tail(key, n, P, u, &cut, &prob, sp);
-      replayed = true;
+    st.need = a.want_cands != 0 || force_replay;
+    if (!st.need && st.pick >= 0) {
+      const uint32_t kp = readlane_u32(st.key, st.pick);
+      const uint32_t km = st.pick > 0 ? readlane_u32(st.key, st.pick - 1) : 0u;
+      const uint32_t kn = st.pick + 1 < st.n ? readlane_u32(st.key, st.pick + 1) : 0u;
+      st.need = (st.pick > 0 && km == kp) || (st.pick + 1 < st.n && kn == kp) ||
+                (st.boundary_tie && kp == st.T);
     }
   }
-  const int token = pick >= 0 ? __shfl(id, pick) : 0;
+  return st;
+}
+
+// The replay when needed, then the token and the optional outputs.
+__device__ __forceinline__ void tail_finish(const LaunchArgs &a, const RowPlan &P, int row,
+                                            const float *rowp, TailState st, double u,
+                                            float *rsv, int32_t *rsid, double *sp,
+                                            bool acquire_replay, const uint32_t *bkey) {
+  const int lane = lane_id();
+  const int k = P.k;
+  bool replayed = false;
+  if (st.need) {
+    if (acquire_replay) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    replay_row<32>(rowp, a.vocab, k, rsv, rsid, bkey);
+    const bool filled = lane < k && rsid[lane] >= 0;
+    unsigned long long x = filled ? pack_cand(f2key(rsv[lane]), (uint32_t)lane) : 0ull;
+    x = wave_sort_desc64(x);   // value descending, slot ascending (stable sort)
+    st.n = __popcll(__ballot(filled));
+    st.key = cand_key(x);
+    st.id = lane < st.n ? rsid[cand_idx(x)] : -1;
+    st.pick = wave_tail(st.key, st.n, P, u, &st.cut, &st.prob, sp);
+    replayed = true;
+  }
+  const int token = st.pick >= 0 ? __shfl(st.id, st.pick) : 0;
   if (lane == 0) {
     put_token(a, row, token);
-    if (a.cand_count_out) a.cand_count_out[row] = n;
-    if (a.cutoff_out) a.cutoff_out[row] = cut;
+    if (a.cand_count_out) a.cand_count_out[row] = st.n;
+    if (a.cutoff_out) a.cutoff_out[row] = st.cut;
     if (a.row_flags) {
       uint32_t fl = 0;
       if (replayed) fl |= HS_ROW_REPLAYED;
-      if (boundary_tie || internal_tie) fl |= HS_ROW_TIES;
-      if (n < 2) fl |= HS_ROW_SINGLE;
+      if (st.boundary_tie || st.internal_tie) fl |= HS_ROW_TIES;
+      if (st.n < 2) fl |= HS_ROW_SINGLE;
       a.row_flags[row] = fl;
     }
   }
   const int cs = a.cand_stride;
-  if (lane < n && lane < cs) {
-    if (a.cand_ids) a.cand_ids[(int64_t)row * cs + lane] = id;
-    if (a.cand_probs) a.cand_probs[(int64_t)row * cs + lane] = prob;
+  if (lane < st.n && lane < cs) {
+    if (a.cand_ids) a.cand_ids[(int64_t)row * cs + lane] = st.id;
+    if (a.cand_probs) a.cand_probs[(int64_t)row * cs + lane] = st.prob;
   }
+}
+
+__device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &P, int row, const float *rowp,
+                            unsigned long long F, bool extra_ties, bool force_replay, double u,
+                            float *rsv, int32_t *rsid, double *sp, bool acquire_replay = false) {
+  const TailState st = tail_decide(a, P, F, extra_ties, force_replay, u, sp);
+  tail_finish(a, P, row, rowp, st, u, rsv, rsid, sp, acquire_replay, nullptr);
 }
 
 size_t row_smem_bytes(int vocab) {
@@ -1538,6 +1623,43 @@ __device__ __forceinline__ unsigned long long merge_top64(unsigned long long a, 
   return c;
 }
 
+// Every thread of the block: bkey[b] = key of the largest logit of logits
+// [64 b, 64 b + 64) of the row (0 when none is above -Infinity), for the slot
+// replay to skip blocks.  A 16-lane DPP row takes one block, a float4 per
+// lane; eight float4 reads per thread are in flight at a time.
+template <int NT>
+__device__ void block_keys(const float *rowp, int V, uint32_t *bkey) {
+  const int tid = threadIdx.x;
+  const int nf = ((V + 63) >> 6) * 16;   // float4 slots, 16 per block
+  for (int f0 = 0; f0 < nf; f0 += 8 * NT) {
+    uint32_t key[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int f = f0 + u * NT + tid;
+      uint32_t kk = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = 4 * f + q;
+        const float v = rowp[e < V ? e : 0];   // always a read inside the row
+        const uint32_t kv = e < V ? f2key(v) : 0u;
+        kk = kk > kv ? kk : kv;
+      }
+      key[u] = kk;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      uint32_t x = key[u], y;
+      // max over the 16 lanes of the DPP row (row_shr:1, 2, 4, 8): lane 15 holds it
+      y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x111, 0xF, 0xF, false); x = x > y ? x : y;
+      y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x112, 0xF, 0xF, false); x = x > y ? x : y;
+      y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x114, 0xF, 0xF, false); x = x > y ? x : y;
+      y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x118, 0xF, 0xF, false); x = x > y ? x : y;
+      const int f = f0 + u * NT + tid;
+      if ((tid & 15) == 15 && f < nf) bkey[f >> 4] = x;
+    }
+  }
+}
+
 struct RowSmem {
   SelectSmem sel;
   TailSmem tail;
@@ -1546,6 +1668,7 @@ struct RowSmem {
   uint32_t theta2;             // refined bound, published by wave 0 mid-row
   int32_t wcnt[kRowWaves];     // candidates each wave has appended (published)
   int32_t n_l, n_f, ovf, done, last;
+  int32_t tie;                 // wave 0's draw needs the slot replay
 };
 
 // SPLIT: a.split workgroups share a row, each streaming one part of it (a
@@ -1918,10 +2041,11 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   }
   if (!overflow && n_all <= kRowThreads) {
     rank_top64(srt, n_all, top, &rs.key64);
-    if (wave != 0) return;
-    F = top[lane];
-    const uint32_t Tk = cand_key(__shfl(F, k - 1));
-    extra = rs.key64 != 0u && rs.key64 == Tk;
+    if (wave == 0) {
+      F = top[lane];
+      const uint32_t Tk = cand_key(__shfl(F, k - 1));
+      extra = rs.key64 != 0u && rs.key64 == Tk;
+    }
   } else if (!overflow) {
     // rare: many candidates reach the bound (ties); select block-wide first,
     // from srt into cbuf (the segments are no longer needed)
@@ -1929,21 +2053,35 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
         n_all, [srt](int p) { return srt[p]; }, 1u, k, cbuf, rs.sel, rs.tail);
     const int n_sel = sel.n_sel;
     if (n_sel < 0) overflow = true;
-    if (wave != 0) return;
-    if (!overflow) {
+    if (wave == 0 && !overflow) {
       F = lane < n_sel ? cbuf[lane] : 0ull;
       extra = n_sel > 64;
     }
-  } else if (wave != 0) {
-    return;
   }
+  // Wave 0 draws; when an equal-value group makes the reference's slot
+  // replay necessary, the whole block first records the largest logit of
+  // every 64-logit block of the row (into cbuf, read into F already), so that
+  // the replay, by wave 0 alone, reads only the blocks that can hold an
+  // entering logit.  The other waves wait for the decision.
   RowPlan P;
   P.temperature = temperature;
   P.top_p = top_p;
   P.min_p = min_p;
   P.k = k;
-  finish_wave(a, P, row, rowp, F, extra, overflow, u, rsv, rsid,
-              reinterpret_cast<double *>(top));   // top[] is read into F already
+  TailState st;
+  if (wave == 0) {
+    st = tail_decide(a, P, F, extra, overflow, u, reinterpret_cast<double *>(top));
+    if (lane == 0) rs.tie = st.need ? 1 : 0;
+  }
+  __syncthreads();
+  const uint32_t *bkey = nullptr;
+  if (rs.tie) {
+    block_keys<kRowThreads>(rowp, V, reinterpret_cast<uint32_t *>(cbuf));
+    __syncthreads();
+    bkey = reinterpret_cast<const uint32_t *>(cbuf);
+  }
+  if (wave != 0) return;
+  tail_finish(a, P, row, rowp, st, u, rsv, rsid, reinterpret_cast<double *>(top), false, bkey);
 }
 
 // ---------------------------------------------------------------- mid kernel
