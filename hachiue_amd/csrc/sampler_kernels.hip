@@ -585,19 +585,27 @@ template <int BLK>
 __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, float *sv, int32_t *sid,
                                            const uint32_t *bkey = nullptr) {
   const int lane = lane_id();
-  // k <= 64: slot j lives in lane j's registers; the minimum is found by DPP
-  // moves (no LDS round trip per entering logit)
+  // k <= 64: slot j lives in lane j's registers with its rank rk among the
+  // slots by (value, slot index), binary32 order (-0 == +0); the slot of
+  // rank 0 is the reference's minimum (the smallest index among equal
+  // minima).  An entering logit takes that slot; its new rank is the number
+  // of other slots below it, and the slots it passes move down by one.
   const bool in_regs = k <= 64;
   float rv = lane < k ? -INFINITY : INFINITY;
   int32_t rid = -1;
-  // the smallest slot holding the minimum (binary32 order: -0 == +0;
-  // f2key maps -Infinity to 0)
-  auto slot_min = [&](float &mv, int &mi) {
-    const uint32_t mk = lane < k ? ~f2key(rv) : 0u;
-    const uint32_t m = wave_max_u32(mk);
-    const float mvf = m == 0xFFFFFFFFu ? -INFINITY : key2f(~m);
-    mi = (int)__ffsll((long long)__ballot(lane < k && rv == mvf)) - 1;
-    mv = mvf;
+  int rk = lane < k ? lane : 64;
+  auto take_min = [&](float vL, int idx, float &mv, int &mi) {
+    const bool less = lane < k && lane != mi && (rv < vL || (rv == vL && lane < mi));
+    const int r = __popcll(__ballot(less));
+    if (lane == mi) {
+      rv = vL;
+      rid = idx;
+      rk = r;
+    } else if (rk >= 1 && rk <= r) {
+      rk -= 1;
+    }
+    mi = (int)__ffsll((long long)__ballot(lane < k && rk == 0)) - 1;
+    mv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rv), mi));
   };
   if (bkey && in_regs) {
     // bkey[b]: key of the largest logit of block b (64 logits).  A block
@@ -614,14 +622,16 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
       while (m) {
         unsigned long long mm = m;
         float x[BLK];
+        uint32_t ok = 0;   // bit q: x[q] is a logit of the row
+        // (the reads are only issued here; nothing uses them before the scan)
 #pragma unroll
         for (int q = 0; q < BLK; ++q) {
           const int t = mm ? (int)__ffsll((long long)mm) - 1 : -1;
           if (mm) mm &= mm - 1;
           const int e = (b + t) * 64 + lane;
           const bool in = t >= 0 && e < vocab;
-          const float v = rowp[in ? e : 0];   // always a read inside the row
-          x[q] = in ? v : __builtin_nanf("");
+          x[q] = rowp[in ? e : 0];   // always a read inside the row
+          ok |= (in ? 1u : 0u) << q;
         }
         unsigned long long m2 = m;
 #pragma unroll
@@ -632,12 +642,11 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
             const int base = (b + t) * 64;
             int done = -1;
             for (;;) {
-              const unsigned long long bl = __ballot(x[q] > mv && lane > done);
+              const unsigned long long bl = __ballot(((ok >> q) & 1u) && x[q] > mv && lane > done);
               if (!bl) break;
               const int L = __ffsll((long long)bl) - 1;
               const float vL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[q]), L));
-              if (lane == mi) { rv = vL; rid = base + L; }
-              slot_min(mv, mi);
+              take_min(vL, base + L, mv, mi);
               done = L;
             }
           }
@@ -655,34 +664,40 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
     for (int j = lane; j < k; j += 64) { sv[j] = -INFINITY; sid[j] = -1; }
   float mv = -INFINITY;
   int mi = 0;
+  // the reads of a step are only issued when the step before is scanned
+  // (nothing uses them earlier); `ok` marks the lanes inside the row
   float nx[BLK];
+  uint32_t nok = 0;
 #pragma unroll
   for (int q = 0; q < BLK; ++q) {
     const int e = q * 64 + lane;
-    nx[q] = e < vocab ? rowp[e] : __builtin_nanf("");
+    nx[q] = rowp[e < vocab ? e : 0];   // always a read inside the row
+    nok |= (e < vocab ? 1u : 0u) << q;
   }
   for (int base = 0; base < vocab; base += 64 * BLK) {
     float x[BLK];
 #pragma unroll
     for (int q = 0; q < BLK; ++q) x[q] = nx[q];
+    const uint32_t ok = nok;
     if (base + 64 * BLK < vocab) {
+      nok = 0;
 #pragma unroll
       for (int q = 0; q < BLK; ++q) {
         const int e = base + 64 * BLK + q * 64 + lane;
-        nx[q] = e < vocab ? rowp[e] : __builtin_nanf("");
+        nx[q] = rowp[e < vocab ? e : 0];
+        nok |= (e < vocab ? 1u : 0u) << q;
       }
     }
 #pragma unroll
     for (int q = 0; q < BLK; ++q) {
       int done = -1;
       for (;;) {
-        const unsigned long long b = __ballot(x[q] > mv && lane > done);
+        const unsigned long long b = __ballot(((ok >> q) & 1u) && x[q] > mv && lane > done);
         if (!b) break;
         const int L = __ffsll((long long)b) - 1;
         const float vL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[q]), L));
         if (in_regs) {
-          if (lane == mi) { rv = vL; rid = base + q * 64 + L; }
-          slot_min(mv, mi);
+          take_min(vL, base + q * 64 + L, mv, mi);
           done = L;
           continue;
         }
@@ -1514,7 +1529,7 @@ __device__ __forceinline__ void tail_finish(const LaunchArgs &a, const RowPlan &
   bool replayed = false;
   if (st.need) {
     if (acquire_replay) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    replay_row<32>(rowp, a.vocab, k, rsv, rsid, bkey);
+    replay_row<16>(rowp, a.vocab, k, rsv, rsid, bkey);
     const bool filled = lane < k && rsid[lane] >= 0;
     unsigned long long x = filled ? pack_cand(f2key(rsv[lane]), (uint32_t)lane) : 0ull;
     x = wave_sort_desc64(x);   // value descending, slot ascending (stable sort)
@@ -1626,28 +1641,36 @@ __device__ __forceinline__ unsigned long long merge_top64(unsigned long long a, 
 // Every thread of the block: bkey[b] = key of the largest logit of logits
 // [64 b, 64 b + 64) of the row (0 when none is above -Infinity), for the slot
 // replay to skip blocks.  A 16-lane DPP row takes one block, a float4 per
-// lane; eight float4 reads per thread are in flight at a time.
+// lane; UN float4 reads per thread are in flight at a time.
 template <int NT>
 __device__ void block_keys(const float *rowp, int V, uint32_t *bkey) {
+  constexpr int UN = 4;
   const int tid = threadIdx.x;
   const int nf = ((V + 63) >> 6) * 16;   // float4 slots, 16 per block
-  for (int f0 = 0; f0 < nf; f0 += 8 * NT) {
-    uint32_t key[8];
+  for (int f0 = 0; f0 < nf; f0 += UN * NT) {
+    // every read issued before any is used
+    float v[UN][4];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < UN; ++u)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int e = 4 * (f0 + u * NT + tid) + q;
+        v[u][q] = rowp[e < V ? e : 0];   // always a read inside the row
+      }
+    uint32_t key[UN];
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
       const int f = f0 + u * NT + tid;
       uint32_t kk = 0;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int e = 4 * f + q;
-        const float v = rowp[e < V ? e : 0];   // always a read inside the row
-        const uint32_t kv = e < V ? f2key(v) : 0u;
+        const uint32_t kv = 4 * f + q < V ? f2key(v[u][q]) : 0u;
         kk = kk > kv ? kk : kv;
       }
       key[u] = kk;
     }
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < UN; ++u) {
       uint32_t x = key[u], y;
       // max over the 16 lanes of the DPP row (row_shr:1, 2, 4, 8): lane 15 holds it
       y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x111, 0xF, 0xF, false); x = x > y ? x : y;
