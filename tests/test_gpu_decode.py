@@ -141,3 +141,34 @@ def test_decode_rejects_bad_arguments(sampler):
         sampler.decode_step_device(d_l.addr, 1, 16, 16, st.ring.addr, 128, st.len.addr,
                                    st.done.addr, None, 3, [None], d_u.addr, d_t.addr)
     st.free()
+
+
+def test_decode_unresolved_row_keeps_state(sampler):
+    """A large-k row whose draw lands in a group of equal logits is left
+    unresolved by the sampler (HS_ROW_UNSUPPORTED, token -1); in a decode step
+    that row reports -1 and keeps its history, length and done flag, while the
+    other rows advance."""
+    V = 20000
+    logits = np.zeros((2, V), np.float32)
+    logits[1] = np.random.default_rng(3).standard_normal(V).astype(np.float32)
+    cfgs = [dict(temperature=1.0, topK=5000.0, topP=0.95), dict(temperature=0.0)]
+    st = DecodeState(sampler, [[1, 2], [3]], [], ring_cap=128)
+    d_l = hip.DeviceArray.from_numpy(logits)
+    d_u = hip.DeviceArray.from_numpy(np.array([0.999, 0.5]))
+    d_t = hip.DeviceArray(2, np.int32)
+    print("[gpu] decode unresolved row", flush=True)
+    st.step(d_l.addr, V, V, cfgs, d_u.addr, d_t.addr)
+    hip.synchronize()
+    tok = d_t.download().tolist()
+    want = o.sample_batch(logits.copy(), V, None, None, cfgs, np.array([0.999, 0.5])).token
+    assert tok[1] == want[1]
+    if tok[0] == -1:   # unresolved: the row's state stays as it was
+        assert st.lengths().tolist() == [2, 2]
+        assert st.history(0).tolist() == [1, 2]
+    else:
+        assert tok[0] == want[0]
+        assert st.lengths().tolist() == [3, 2]
+        assert st.history(0).tolist() == [1, 2, tok[0]]
+    assert st.finished().tolist() == [False, False]
+    assert st.history(1).tolist() == [3, tok[1]]
+    st.free()
