@@ -718,7 +718,7 @@ int resident_blocks(const void *kernel, uint32_t lds, int threads = kGemvThreads
 }
 
 template <int FMT, int NRU>
-hipError_t launch_fmt(GemvArgs g, hipStream_t stream, hipEvent_t *ev) {
+hipError_t launch_fmt(GemvArgs g, hipStream_t stream, hipEvent_t *ev, hipEvent_t done) {
   // one pass of resident workgroups over the rows (g.blocks: the most useful)
   const int res = FMT == kW_F32
                       ? resident_blocks(reinterpret_cast<const void *>(gemv_kernel<FMT, NRU>), 0u)
@@ -729,19 +729,23 @@ hipError_t launch_fmt(GemvArgs g, hipStream_t stream, hipEvent_t *ev) {
   if constexpr (FMT == kW_F32) {
     if (ev)
       hipExtLaunchKernelGGL((gemv_kernel<FMT, NRU>), grid, block, 0, stream, ev[0], ev[1], 0u, g);
+    else if (done)
+      hipExtLaunchKernelGGL((gemv_kernel<FMT, NRU>), grid, block, 0, stream, nullptr, done, 0u, g);
     else
       hipLaunchKernelGGL((gemv_kernel<FMT, NRU>), grid, block, 0, stream, g);
   } else {
     const uint32_t lds = (uint32_t)gemv_lds_bytes(FMT);
     if (ev)
       hipExtLaunchKernelGGL((gemv_lds_kernel<FMT, NRU>), grid, block, lds, stream, ev[0], ev[1], 0u, g);
+    else if (done)
+      hipExtLaunchKernelGGL((gemv_lds_kernel<FMT, NRU>), grid, block, lds, stream, nullptr, done, 0u, g);
     else
       hipLaunchKernelGGL((gemv_lds_kernel<FMT, NRU>), grid, block, lds, stream, g);
   }
   return hipGetLastError();
 }
 
-hipError_t launch_q6k_mfma(GemvArgs g, hipStream_t stream, hipEvent_t *ev) {
+hipError_t launch_q6k_mfma(GemvArgs g, hipStream_t stream, hipEvent_t *ev, hipEvent_t done) {
   const size_t lds = gemv_q6k_mfma_lds_bytes(g.K);
   const int ntiles = (g.N + 15) / 16;
   const int res = resident_blocks(reinterpret_cast<const void *>(gemv_q6k_mfma_kernel), (uint32_t)lds,
@@ -754,6 +758,8 @@ hipError_t launch_q6k_mfma(GemvArgs g, hipStream_t stream, hipEvent_t *ev) {
   const dim3 grid((unsigned)blocks, (unsigned)g.M), block(q6m::kThreads);
   if (ev)
     hipExtLaunchKernelGGL(gemv_q6k_mfma_kernel, grid, block, lds, stream, ev[0], ev[1], 0u, g);
+  else if (done)
+    hipExtLaunchKernelGGL(gemv_q6k_mfma_kernel, grid, block, lds, stream, nullptr, done, 0u, g);
   else
     hipLaunchKernelGGL(gemv_q6k_mfma_kernel, grid, block, lds, stream, g);
   return hipGetLastError();
@@ -769,14 +775,14 @@ hipError_t prepare_gemv() {
                              (int)gemv_q6k_mfma_lds_bytes(kGemvMaxK));
 }
 
-hipError_t launch_gemv(const GemvArgs &g, hipStream_t stream, hipEvent_t *ev) {
+hipError_t launch_gemv(const GemvArgs &g, hipStream_t stream, hipEvent_t *ev, hipEvent_t done) {
   const bool two = g.nru == 2;
   switch (g.type) {
-    case kW_F32: return two ? launch_fmt<kW_F32, 2>(g, stream, ev) : launch_fmt<kW_F32, 1>(g, stream, ev);
-    case kW_Q4_0: return two ? launch_fmt<kW_Q4_0, 2>(g, stream, ev) : launch_fmt<kW_Q4_0, 1>(g, stream, ev);
-    case kW_Q4_1: return two ? launch_fmt<kW_Q4_1, 2>(g, stream, ev) : launch_fmt<kW_Q4_1, 1>(g, stream, ev);
-    case kW_Q4_K: return two ? launch_fmt<kW_Q4_K, 2>(g, stream, ev) : launch_fmt<kW_Q4_K, 1>(g, stream, ev);
-    case kW_Q6_K: return launch_q6k_mfma(g, stream, ev);
+    case kW_F32: return two ? launch_fmt<kW_F32, 2>(g, stream, ev, done) : launch_fmt<kW_F32, 1>(g, stream, ev, done);
+    case kW_Q4_0: return two ? launch_fmt<kW_Q4_0, 2>(g, stream, ev, done) : launch_fmt<kW_Q4_0, 1>(g, stream, ev, done);
+    case kW_Q4_1: return two ? launch_fmt<kW_Q4_1, 2>(g, stream, ev, done) : launch_fmt<kW_Q4_1, 1>(g, stream, ev, done);
+    case kW_Q4_K: return two ? launch_fmt<kW_Q4_K, 2>(g, stream, ev, done) : launch_fmt<kW_Q4_K, 1>(g, stream, ev, done);
+    case kW_Q6_K: return launch_q6k_mfma(g, stream, ev, done);
     default: return hipErrorInvalidValue;
   }
 }

@@ -70,6 +70,14 @@ std::vector<int> g_prepared;
 
 struct hs_context {
   int device = 0;
+  // every entry point holds it for the whole call: calls on one context are
+  // serialised (the workspace, staging and host buffers are shared)
+  std::mutex mu;
+  // recorded at the end of each call's last kernel on done_stream; a call on
+  // another stream waits for it before it touches the workspace
+  hipEvent_t done_ev = nullptr;
+  hipStream_t done_stream = nullptr;
+  bool has_done = false;
   // workspace
   DevBuf plans, cand, cand_count, info;
   DevBuf split_list, split_meta, split_cnt;   // split rows (split_cnt: zero between calls)
@@ -114,6 +122,22 @@ struct DeviceGuard {
     if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
   }
 };
+
+// The workspace is shared by every call on a context: a call on another
+// stream than the previous call's waits for that call's last kernel.
+int enter_stream(hs_context *ctx, hipStream_t s) {
+  if (ctx->has_done && s != ctx->done_stream) HS_HIP(hipStreamWaitEvent(s, ctx->done_ev, 0));
+  return HS_OK;
+}
+
+// After a call's launches on `s`: `recorded` says whether done_ev was
+// attached to its last kernel; otherwise it is recorded here.
+int leave_stream(hs_context *ctx, hipStream_t s, bool recorded) {
+  if (!recorded) HS_HIP(hipEventRecord(ctx->done_ev, s));
+  ctx->done_stream = s;
+  ctx->has_done = true;
+  return HS_OK;
+}
 
 // src/sampler.ts:49 k = Math.max(1, Math.min(topK > 0 ? topK : 64, vocab)),
 // truncated as `new Int32Array(k)` truncates a fractional length.
@@ -312,6 +336,8 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   if ((d_cand_ids || d_cand_probs) && cand_stride == 0)
     return fail(HS_ERR_INVALID_ARGUMENT, "candidate outputs need cand_stride > 0");
   DeviceGuard guard(ctx->device);
+  int rc0 = enter_stream(ctx, stream);
+  if (rc0) return rc0;
   if (vocab <= 0) {
     // src/sampler.ts: no logit is read; every path returns 0.
     HS_HIP(hipMemsetAsync(d_tokens, 0, sizeof(int32_t) * (size_t)rows, stream));
@@ -323,7 +349,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
       if (e != hipSuccess)
         return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
     }
-    return HS_OK;
+    return leave_stream(ctx, stream, false);
   }
   if (!d_logits) return fail(HS_ERR_INVALID_ARGUMENT, "logits must not be null");
   if (row_stride < vocab)
@@ -409,12 +435,13 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   hipEvent_t *ev = nullptr;
   rc = begin_timed(ctx, a, &ev);
   if (rc) return rc;
-  hipError_t e = hs::launch_sample(a, ws, stream, ev);
+  hipError_t e = hs::launch_sample(a, ws, stream, ev, ctx->done_ev);
   if (e != hipSuccess) {
     reset_counters(ctx, stream);
+    (void)leave_stream(ctx, stream, false);
     return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
   }
-  return HS_OK;
+  return leave_stream(ctx, stream, ev == nullptr);
 }
 
 // src/kernels.ts:1613-1654 (the argmax pipeline of the engine's greedy route).
@@ -425,9 +452,11 @@ int argmax_device(hs_context *ctx, const float *d_logits, int32_t rows, int64_t 
   if (rows == 0) return HS_OK;
   if (!d_tokens) return fail(HS_ERR_INVALID_ARGUMENT, "tokens must not be null");
   DeviceGuard guard(ctx->device);
+  int rc0 = enter_stream(ctx, stream);
+  if (rc0) return rc0;
   if (vocab <= 0) {   // no invocation scans an id: every slot keeps id 0
     HS_HIP(hipMemsetAsync(d_tokens, 0, sizeof(int32_t) * (size_t)rows, stream));
-    return HS_OK;
+    return leave_stream(ctx, stream, false);
   }
   if (!d_logits) return fail(HS_ERR_INVALID_ARGUMENT, "logits must not be null");
   if (row_stride < vocab)
@@ -454,12 +483,13 @@ int argmax_device(hs_context *ctx, const float *d_logits, int32_t rows, int64_t 
   hipEvent_t *ev = nullptr;
   rc = begin_timed(ctx, a, &ev);
   if (rc) return rc;
-  hipError_t e = hs::launch_sample(a, ws, stream, ev);
+  hipError_t e = hs::launch_sample(a, ws, stream, ev, ctx->done_ev);
   if (e != hipSuccess) {
     reset_counters(ctx, stream);
+    (void)leave_stream(ctx, stream, false);
     return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
   }
-  return HS_OK;
+  return leave_stream(ctx, stream, ev == nullptr);
 }
 
 // src/engine.ts:1493-1515 (the lm_head GEMV; see lmhead_kernels.hip).
@@ -515,6 +545,8 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32
   g.blocks = (int32_t)std::min<int64_t>((steps + wpb - 1) / wpb, 1 << 20);
   if (M > 65535) return fail(HS_ERR_UNSUPPORTED, "M %d above 65535", M);
   DeviceGuard guard(ctx->device);
+  int rc0 = enter_stream(ctx, stream);
+  if (rc0) return rc0;
   if (w_type == hs::kW_Q6_K) {   // the hand-over slots of tiles cut between waves
     int cus = 0;
     HS_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device));
@@ -544,12 +576,20 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32
     ctx->timed.push_back(tc);
     ev = ctx->timed.back().ev + 2 * hs::kGemvTimedSlot;
   }
-  const hipError_t e = hs::launch_gemv(g, stream, ev);
-  if (e != hipSuccess) return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
-  return HS_OK;
+  const hipError_t e = hs::launch_gemv(g, stream, ev, ctx->done_ev);
+  if (e != hipSuccess) {
+    (void)leave_stream(ctx, stream, false);
+    return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  }
+  return leave_stream(ctx, stream, ev == nullptr);
 }
 
 }  // namespace
+
+// Every entry point that uses a context holds its mutex for the whole call.
+#define HS_LOCK(ctx)                                                   \
+  if (!(ctx)) return fail(HS_ERR_INVALID_ARGUMENT, "null context");    \
+  std::lock_guard<std::mutex> hs_lock_((ctx)->mu)
 
 extern "C" {
 
@@ -593,6 +633,7 @@ int hs_context_create(int device, hs_context **out) {
   if (const char *env = getenv("HS_ROW_KERNEL_MIN_ROWS")) ctx->row_min_rows = atoi(env);
   if (const char *env = getenv("HS_ROW_SPLIT")) ctx->row_split = atoi(env);
   e = hipEventCreateWithFlags(&ctx->plan_done, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->done_ev, hipEventDisableTiming);
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     hs_context_destroy(ctx);
@@ -603,13 +644,13 @@ int hs_context_create(int device, hs_context **out) {
 }
 
 int hs_context_set_timing(hs_context *ctx, int enable) {
-  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  HS_LOCK(ctx);
   ctx->timing = enable != 0;
   return HS_OK;
 }
 
 int hs_context_kernel_times(hs_context *ctx, double *ms, int32_t count, int64_t *calls) {
-  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  HS_LOCK(ctx);
   if (count < 0 || (count > 0 && !ms)) return fail(HS_ERR_INVALID_ARGUMENT, "bad output array");
   DeviceGuard guard(ctx->device);
   for (const hs_context::TimedCall &tc : ctx->timed) {
@@ -658,6 +699,7 @@ int hs_context_destroy(hs_context *ctx) {
     ctx->h_tok.release();
     if (ctx->plan_staging) (void)hipHostFree(ctx->plan_staging);
     if (ctx->plan_done) (void)hipEventDestroy(ctx->plan_done);
+    if (ctx->done_ev) (void)hipEventDestroy(ctx->done_ev);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   }
   delete ctx;
@@ -670,6 +712,7 @@ int hs_sample_batch_device_ex(hs_context *ctx, float *d_logits, int32_t rows, in
                               const double *d_uniforms, int32_t *d_tokens, int32_t cand_stride,
                               int32_t *d_cand_ids, float *d_cand_probs, int32_t *d_cand_count,
                               int32_t *d_cutoff, uint32_t *d_row_flags, void *stream) {
+  HS_LOCK(ctx);
   return sample_device(ctx, d_logits, rows, row_stride, vocab, d_hist_ids, d_hist_offsets, configs,
                        d_uniforms, d_tokens, cand_stride, d_cand_ids, d_cand_probs, d_cand_count,
                        d_cutoff, d_row_flags, static_cast<hipStream_t>(stream));
@@ -679,6 +722,7 @@ int hs_sample_batch_device(hs_context *ctx, float *d_logits, int32_t rows, int64
                            int32_t vocab, const int32_t *d_hist_ids,
                            const int64_t *d_hist_offsets, const hs_sample_config *configs,
                            const double *d_uniforms, int32_t *d_tokens, void *stream) {
+  HS_LOCK(ctx);
   return sample_device(ctx, d_logits, rows, row_stride, vocab, d_hist_ids, d_hist_offsets, configs,
                        d_uniforms, d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr,
                        static_cast<hipStream_t>(stream));
@@ -686,6 +730,7 @@ int hs_sample_batch_device(hs_context *ctx, float *d_logits, int32_t rows, int64
 
 int hs_argmax_device(hs_context *ctx, const float *d_logits, int32_t rows, int64_t row_stride,
                      int32_t vocab, int32_t *d_tokens, void *stream) {
+  HS_LOCK(ctx);
   return argmax_device(ctx, d_logits, rows, row_stride, vocab, d_tokens,
                        static_cast<hipStream_t>(stream));
 }
@@ -693,6 +738,7 @@ int hs_argmax_device(hs_context *ctx, const float *d_logits, int32_t rows, int64
 int hs_gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32_t K,
                    const void *d_w, int32_t w_type, int32_t N, float *d_y, int64_t ldy,
                    void *stream) {
+  HS_LOCK(ctx);
   return gemv_device(ctx, d_x, M, ldx, K, d_w, w_type, N, d_y, ldy,
                      static_cast<hipStream_t>(stream));
 }
@@ -702,6 +748,7 @@ int hs_lm_head_sample_device(hs_context *ctx, const float *d_x, int32_t M, int64
                              int64_t ldl, const int32_t *d_hist_ids, const int64_t *d_hist_offsets,
                              const hs_sample_config *configs, const double *d_uniforms,
                              int32_t *d_tokens, void *stream) {
+  HS_LOCK(ctx);
   const hipStream_t st = static_cast<hipStream_t>(stream);
   int rc = gemv_device(ctx, d_x, M, ldx, K, d_w, w_type, N, d_logits, ldl, st);
   if (rc) return rc;
@@ -716,7 +763,7 @@ int hs_decode_step_device(hs_context *ctx, float *d_logits, int32_t rows, int64_
                           int32_t *d_done, const int32_t *d_stop_ids, int32_t n_stop,
                           const hs_sample_config *configs, const double *d_uniforms,
                           int32_t *d_tokens, void *stream) {
-  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  HS_LOCK(ctx);
   if (rows < 0) return fail(HS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %d)", rows);
   if (rows == 0) return HS_OK;
   if (!d_ring || !d_len || !d_done)
@@ -745,7 +792,7 @@ int hs_decode_step_device(hs_context *ctx, float *d_logits, int32_t rows, int64_
 
 int hs_argmax(hs_context *ctx, const float *logits, int32_t rows, int64_t row_stride,
               int32_t vocab, int32_t *tokens_out) {
-  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  HS_LOCK(ctx);
   if (rows < 0) return fail(HS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %d)", rows);
   if (rows == 0) return HS_OK;
   if (!tokens_out) return fail(HS_ERR_INVALID_ARGUMENT, "tokens_out must not be null");
@@ -779,7 +826,7 @@ int hs_sample_logits_batch(hs_context *ctx, float *logits, int32_t rows, int64_t
                            int32_t vocab, const int32_t *hist_ids, const int64_t *hist_offsets,
                            const hs_sample_config *configs, const double *uniforms,
                            int32_t *tokens_out) {
-  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  HS_LOCK(ctx);
   if (rows < 0) return fail(HS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %d)", rows);
   if (rows == 0) return HS_OK;
   if (!configs || !uniforms || !tokens_out)

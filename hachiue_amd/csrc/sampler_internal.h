@@ -197,7 +197,7 @@ constexpr int gemv_batch_chunks(int type) {
   return (gemv_batch_steps(type) * 32 * gemv_unit_bytes2(type) + 32 + 1023) / 1024;
 }
 constexpr int gemv_lds_bytes(int type) { return (kGemvThreads / 64) * gemv_batch_chunks(type) * 1024; }
-hipError_t launch_gemv(const GemvArgs &g, hipStream_t stream, hipEvent_t *ev);
+hipError_t launch_gemv(const GemvArgs &g, hipStream_t stream, hipEvent_t *ev, hipEvent_t done);
 hipError_t prepare_gemv();      // per device, once (called by prepare_kernels)
 
 // ---- decode step bookkeeping (after the sampler, same stream)
@@ -213,8 +213,10 @@ struct DecodeArgs {
 };
 constexpr int kMaxStopIds = 1024;
 hipError_t launch_decode_append(const DecodeArgs &d, hipStream_t stream);
+// `done`, when not null and `ev` is null, is recorded at the end of the
+// call's last kernel (hipExtLaunchKernelGGL's stop event: no marker packet).
 hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,
-                         hipEvent_t *ev);
+                         hipEvent_t *ev, hipEvent_t done);
 hipError_t prepare_kernels();   // per device, once: raise dynamic LDS limits
 size_t row_smem_bytes(int vocab);
 size_t mid_smem_bytes(int vocab);

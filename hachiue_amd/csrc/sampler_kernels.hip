@@ -3574,12 +3574,18 @@ namespace {
 
 // One launch; with events, hipExtLaunchKernelGGL stamps the start and end of
 // the kernel's own dispatch (no marker packets are added to the stream).
+// Without them, `done` (when not null) is recorded at the kernel's end the
+// same way.
 template <typename K>
 hipError_t launch_one(K kernel, dim3 grid, dim3 block, size_t smem, hipStream_t stream,
-                      hipEvent_t *ev, int slot, const LaunchArgs &a, const Workspace &ws) {
+                      hipEvent_t *ev, int slot, hipEvent_t done, const LaunchArgs &a,
+                      const Workspace &ws) {
   if (ev)
     hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t)smem, stream, ev[2 * slot],
                           ev[2 * slot + 1], 0u, a, ws);
+  else if (done)
+    hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t)smem, stream, nullptr, done, 0u, a,
+                          ws);
   else
     hipLaunchKernelGGL(kernel, grid, block, smem, stream, a, ws);
   return hipGetLastError();
@@ -3620,52 +3626,56 @@ hipError_t launch_decode_append(const DecodeArgs &d, hipStream_t stream) {
 }
 
 hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,
-                         hipEvent_t *ev) {
+                         hipEvent_t *ev, hipEvent_t done) {
   hipError_t e;
+  // the last kernel of the call records `done`
+  const int last = a.n_argmax > 0 ? 6 : a.n_large > 0 ? 4 : a.n_chunk > 0 ? 3 : a.n_mid > 0 ? 5
+                 : a.n_row > 0 ? 1 : 0;
+  auto dn = [&](int slot) { return slot == last ? done : nullptr; };
   if (a.n_pf > 0) {
     e = launch_one(pen_kernel, dim3((unsigned)a.n_pf), dim3(kPenThreads), pen_smem_bytes(),
-                   stream, ev, 0, a, ws);
+                   stream, ev, 0, dn(0), a, ws);
     if (e != hipSuccess) return e;
   }
   if (a.n_row > 0) {
     const size_t smem = row_smem_bytes(a.vocab);
     if (a.split > 1) {
       const dim3 grid((unsigned)(a.n_row * a.split));
-      e = a.vec ? launch_one(row_kernel<true, true>, grid, dim3(kRowThreads), smem, stream, ev, 1, a, ws)
-                : launch_one(row_kernel<false, true>, grid, dim3(kRowThreads), smem, stream, ev, 1, a, ws);
+      e = a.vec ? launch_one(row_kernel<true, true>, grid, dim3(kRowThreads), smem, stream, ev, 1, dn(1), a, ws)
+                : launch_one(row_kernel<false, true>, grid, dim3(kRowThreads), smem, stream, ev, 1, dn(1), a, ws);
     } else {
       const dim3 grid((unsigned)a.n_row);
-      e = a.vec ? launch_one(row_kernel<true, false>, grid, dim3(kRowThreads), smem, stream, ev, 1, a, ws)
-                : launch_one(row_kernel<false, false>, grid, dim3(kRowThreads), smem, stream, ev, 1, a, ws);
+      e = a.vec ? launch_one(row_kernel<true, false>, grid, dim3(kRowThreads), smem, stream, ev, 1, dn(1), a, ws)
+                : launch_one(row_kernel<false, false>, grid, dim3(kRowThreads), smem, stream, ev, 1, dn(1), a, ws);
     }
     if (e != hipSuccess) return e;
   }
   if (a.n_mid > 0) {
     const size_t smem = mid_smem_bytes(a.vocab);
     e = a.vec ? launch_one(mid_kernel<true>, dim3((unsigned)a.n_mid), dim3(kRowThreads), smem,
-                           stream, ev, 5, a, ws)
+                           stream, ev, 5, dn(5), a, ws)
               : launch_one(mid_kernel<false>, dim3((unsigned)a.n_mid), dim3(kRowThreads), smem,
-                           stream, ev, 5, a, ws);
+                           stream, ev, 5, dn(5), a, ws);
     if (e != hipSuccess) return e;
   }
   if (a.n_chunk > 0) {
     const dim3 grid((unsigned)(a.n_chunk * a.chunks));
-    e = a.vec ? launch_one(chunk_kernel<true>, grid, dim3(kThreads), 0, stream, ev, 2, a, ws)
-              : launch_one(chunk_kernel<false>, grid, dim3(kThreads), 0, stream, ev, 2, a, ws);
+    e = a.vec ? launch_one(chunk_kernel<true>, grid, dim3(kThreads), 0, stream, ev, 2, dn(2), a, ws)
+              : launch_one(chunk_kernel<false>, grid, dim3(kThreads), 0, stream, ev, 2, dn(2), a, ws);
     if (e != hipSuccess) return e;
     e = launch_one(finalize_kernel, dim3((unsigned)a.n_chunk), dim3(kThreads),
-                   finalize_smem_bytes(), stream, ev, 3, a, ws);
+                   finalize_smem_bytes(), stream, ev, 3, dn(3), a, ws);
     if (e != hipSuccess) return e;
   }
   if (a.n_large > 0) {
     e = launch_one(large_kernel, dim3((unsigned)a.n_large), dim3(kLT), large_smem_bytes(), stream,
-                   ev, 4, a, ws);
+                   ev, 4, dn(4), a, ws);
     if (e != hipSuccess) return e;
   }
   if (a.n_argmax > 0) {
     const dim3 grid((unsigned)(a.n_argmax * a.split));
-    e = a.vec ? launch_one(argmax_kernel<true>, grid, dim3(kRowThreads), 0, stream, ev, 6, a, ws)
-              : launch_one(argmax_kernel<false>, grid, dim3(kRowThreads), 0, stream, ev, 6, a, ws);
+    e = a.vec ? launch_one(argmax_kernel<true>, grid, dim3(kRowThreads), 0, stream, ev, 6, dn(6), a, ws)
+              : launch_one(argmax_kernel<false>, grid, dim3(kRowThreads), 0, stream, ev, 6, dn(6), a, ws);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

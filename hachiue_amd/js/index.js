@@ -58,12 +58,62 @@ function packConfig(config, vocab, out, offset) {
   }
 }
 
-// Math.random() is reached only with a positive temperature and more than
-// one slot (src/sampler.ts:36, :49, :77).
-function mayDraw(cfg, offset, vocab) {
-  if (!(cfg[offset] > 0)) return false;
+// Whether sampleLogits would call Math.random() for a row (src/sampler.ts:
+// 36, :49-50, :76-77, :112): once iff !(temperature <= 0) (a NaN temperature
+// draws) and order.length >= 2, where order.length = min(k, the number of
+// penalised logits > -Infinity).  Penalties touch only history ids, so two
+// logits > -Infinity at ids outside the history settle it before the call.
+// Returns 1 (draws), 0 (does not) or -1 (only the penalised row can tell).
+const DRAW = 1;
+const NO_DRAW = 0;
+const DRAW_UNKNOWN = -1;
+function drawRule(cfg, offset, vocab, logits, base, n, ids, h0, h1) {
+  if (cfg[offset] <= 0) return NO_DRAW;
   const t = cfg[offset + 1] > 0 ? cfg[offset + 1] : 64;
-  return Math.max(1, Math.min(t, vocab)) >= 2;
+  if (Math.trunc(Math.max(1, Math.min(t, vocab))) < 2) return NO_DRAW;
+  const rep = cfg[offset + 4] !== 1;
+  const pf = cfg[offset + 5] !== 0 || cfg[offset + 6] !== 0;
+  // ids a penalty may change: the last 128 entries for the repetition
+  // penalty alone, the whole history with presence / frequency
+  const lo = pf ? h0 : Math.max(h0, h1 - 128);
+  const touched = (rep || pf) && h1 > lo;
+  let set = null;
+  let checks = 0;
+  let found = 0;
+  for (let i = 0; i < n; i++) {
+    if (!(logits[base + i] > -Infinity)) continue;
+    if (touched) {
+      let hit;
+      if (set !== null) hit = set.has(i);
+      else if (++checks <= 8) hit = ids.subarray(lo, h1).indexOf(i) >= 0;
+      else {
+        set = new Set(ids.subarray(lo, h1));
+        hit = set.has(i);
+      }
+      if (hit) continue;
+    }
+    if (++found === 2) return DRAW;
+  }
+  return touched ? DRAW_UNKNOWN : NO_DRAW;
+}
+
+// order.length >= 2 on a penalised row (k >= 2 known)
+function twoCandidates(logits, base, n) {
+  let found = 0;
+  for (let i = 0; i < n; i++) if (logits[base + i] > -Infinity && ++found === 2) return true;
+  return false;
+}
+
+// The same configs with the penalties switched off, for a second pass over
+// logits that already hold the penalised values.
+function withoutPenalties(cfg) {
+  const out = Float64Array.from(cfg);
+  for (let o = 0; o < out.length; o += FIELDS.length) {
+    out[o + 4] = 1;
+    out[o + 5] = 0;
+    out[o + 6] = 0;
+  }
+  return out;
 }
 
 // Ids that index nothing in the reference (non-integers, out of int32) -> -1.
@@ -95,17 +145,28 @@ function sampleLogits(logits, vocab, history, config) {
   if (!(vocab > 0)) return 0;   // no logit is read; every path returns 0
   const cfg = new Float64Array(FIELDS.length);
   packConfig(config, vocab, cfg, 0);
-  let u = config ? option(config.uniform, null) : null;
-  if (u === null) u = mayDraw(cfg, 0, vocab) ? Math.random() : 0;
   const n = scanLength(vocab);
   const ids = historyIds(history);
-  if (n <= logits.length) return native().sampleRow(context(), logits, n, ids, cfg, u);
   // indices past the array read `undefined` in the reference, which no
   // comparison selects: pad with NaN and copy the penalised values back
-  const padded = new Float32Array(n).fill(NaN);
-  padded.set(logits);
-  const token = native().sampleRow(context(), padded, n, ids, cfg, u);
-  logits.set(padded.subarray(0, logits.length));
+  const row = n <= logits.length ? logits : new Float32Array(n).fill(NaN);
+  if (row !== logits) row.set(logits);
+  const given = config ? option(config.uniform, null) : null;
+  let token;
+  const rule = given !== null ? DRAW : drawRule(cfg, 0, vocab, row, 0, n, ids, 0, ids.length);
+  if (rule !== DRAW_UNKNOWN) {
+    const u = given !== null ? given : (rule === DRAW ? Math.random() : 0);
+    token = native().sampleRow(context(), row, n, ids, cfg, u);
+  } else {
+    // a penalty decides whether two candidates remain: penalise and sample
+    // without a draw, then draw on the penalised row only if it has them
+    token = native().sampleRow(context(), row, n, ids, cfg, 0);
+    if (twoCandidates(row, 0, n)) {
+      token = native().sampleRow(context(), row, n, new Int32Array(0), withoutPenalties(cfg),
+        Math.random());
+    }
+  }
+  if (row !== logits) logits.set(row.subarray(0, logits.length));
   return token;
 }
 
@@ -163,12 +224,6 @@ function batchArgs(logits, vocab, histories, configs, uniforms, shape) {
     const c = Array.isArray(configs) ? configs[r] : configs;
     packConfig(c, vocab, cfg, FIELDS.length * r);
   }
-  const u = new Float64Array(rows);
-  for (let r = 0; r < rows; r++) {
-    const given = uniforms ? uniforms[r] : undefined;
-    u[r] = given !== undefined && given !== null ? given
-      : (mayDraw(cfg, FIELDS.length * r, vocab) ? Math.random() : 0);
-  }
   let ids = null;
   let off = null;
   if (histories) {
@@ -182,24 +237,61 @@ function batchArgs(logits, vocab, histories, configs, uniforms, shape) {
     ids = new Int32Array(off[rows] || 1);
     for (let r = 0; r < rows; r++) ids.set(parts[r], off[r]);
   }
-  return [context(), logits, rows, stride, vocab, ids, off, cfg, u];
+  // one Math.random() per row that draws, in row order; a row whose draw
+  // only its penalised values decide leaves the rest to a second pass
+  const u = new Float64Array(rows);
+  const rules = new Int8Array(rows);
+  let unknown = false;
+  for (let r = 0; r < rows; r++) {
+    const given = uniforms ? uniforms[r] : undefined;
+    if (given !== undefined && given !== null) {
+      u[r] = given;
+      rules[r] = DRAW;
+      continue;
+    }
+    rules[r] = vocab > 0 ? drawRule(cfg, FIELDS.length * r, vocab, logits, r * stride, vocab,
+      ids, off ? off[r] : 0, off ? off[r + 1] : 0) : NO_DRAW;
+    if (rules[r] === DRAW_UNKNOWN) unknown = true;
+  }
+  if (!unknown) {
+    for (let r = 0; r < rows; r++) if (rules[r] === DRAW && !(uniforms && uniforms[r] != null)) u[r] = Math.random();
+  }
+  const args = [context(), logits, rows, stride, vocab, ids, off, cfg, u];
+  if (!unknown) return { args: args, second: null };
+  // pass 1 penalises with no draw; the draws then follow the penalised rows
+  const second = function () {
+    const u2 = new Float64Array(rows);
+    for (let r = 0; r < rows; r++) {
+      const given = uniforms ? uniforms[r] : undefined;
+      if (given !== undefined && given !== null) u2[r] = given;
+      else if (rules[r] === DRAW || (rules[r] === DRAW_UNKNOWN && twoCandidates(logits, r * stride, vocab))) {
+        u2[r] = Math.random();
+      }
+    }
+    return [context(), logits, rows, stride, vocab, null, null, withoutPenalties(cfg), u2];
+  };
+  return { args: args, second: second };
 }
 
 /**
  * Many rows in one call: logits holds `rows` rows of `stride` floats
  * (default stride = vocab); histories[r], configs[r] (or one shared config)
- * and uniforms[r] (or Math.random() when the reference would draw).
+ * and uniforms[r] (or Math.random(), called once for each row that draws,
+ * in row order, under sampleLogits' rule).
  * @returns {Int32Array} tokens
  */
 function sampleLogitsBatch(logits, vocab, histories, configs, uniforms, shape) {
   const a = batchArgs(logits, vocab, histories, configs, uniforms, shape);
-  return native().sampleBatch.apply(null, a);
+  const tokens = native().sampleBatch.apply(null, a.args);
+  return a.second === null ? tokens : native().sampleBatch.apply(null, a.second());
 }
 
 /** Promise-returning variant of sampleLogitsBatch (runs off the main thread). */
 function sampleLogitsBatchAsync(logits, vocab, histories, configs, uniforms, shape) {
   const a = batchArgs(logits, vocab, histories, configs, uniforms, shape);
-  return native().sampleBatchAsync.apply(null, a);
+  const p = native().sampleBatchAsync.apply(null, a.args);
+  return a.second === null ? p
+    : p.then(function () { return native().sampleBatchAsync.apply(null, a.second()); });
 }
 
 module.exports = {
@@ -210,6 +302,7 @@ module.exports = {
   argmaxLogits: argmaxLogits,
   argmaxLogitsBatch: argmaxLogitsBatch,
   nextToken: nextToken,
+  drawRule: drawRule,
   DEFAULTS: Object.freeze({
     temperature: 0.6, topK: 20, topP: 0.95, minP: 0.0, repetitionPenalty: 1.0,
   }),

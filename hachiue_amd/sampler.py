@@ -214,8 +214,8 @@ class Sampler:
         """sampleLogits(logits, vocab, history, config) on the GPU.  `logits`
         (float32, contiguous, length >= vocab) receives the penalised values
         in place.  Without `uniform`, ``random.random()`` stands in for
-        Math.random() and is drawn only when the reference would draw: a
-        positive temperature and more than one slot."""
+        Math.random() and is drawn only when the reference would draw
+        (draw_rule)."""
         if not (isinstance(logits, np.ndarray) and logits.dtype == np.float32
                 and logits.flags.c_contiguous):
             raise TypeError("logits must be a contiguous float32 numpy array")
@@ -223,13 +223,25 @@ class Sampler:
         cfg = resolve_config(config)
         if vocab > logits.size:
             raise ValueError("vocab exceeds the logits length")
-        if uniform is None:
-            uniform = random.random() if _may_draw(cfg, vocab) else 0.0
         ids = _history_ids(list(history) if not isinstance(history, np.ndarray) else history)
+        rule = DRAW if uniform is not None else draw_rule(cfg, vocab, logits, ids)
+        if rule != DRAW_UNKNOWN:
+            if uniform is None:
+                uniform = random.random() if rule == DRAW else 0.0
+            return self._sample_row(logits, vocab, ids, cfg, float(uniform))
+        # a penalty decides whether two candidates remain: penalise and sample
+        # without a draw, then draw on the penalised row only if it has them
+        tok = self._sample_row(logits, vocab, ids, cfg, 0.0)
+        if _two_candidates(logits, vocab):
+            tok = self._sample_row(logits, vocab, np.zeros(0, np.int32), _without_penalties(cfg),
+                                   random.random())
+        return tok
+
+    def _sample_row(self, logits, vocab, ids, cfg, uniform: float) -> int:
         tok = ctypes.c_int32()
         _check(lib().hs_sample_logits(self._ctx, _f32p(logits), vocab,
                                       ids.ctypes.data_as(ctypes.POINTER(ctypes.c_int32)),
-                                      int(ids.size), ctypes.byref(cfg), float(uniform),
+                                      int(ids.size), ctypes.byref(cfg), uniform,
                                       ctypes.byref(tok)))
         return int(tok.value)
 
@@ -243,10 +255,31 @@ class Sampler:
             raise TypeError("logits must be a contiguous 2-D float32 numpy array")
         rows, stride = logits.shape
         cfgs = _configs(configs, rows)
-        if uniforms is None:
-            uniforms = np.array([random.random() for _ in range(rows)])
-        u = np.ascontiguousarray(uniforms, dtype=np.float64)
         ids, off = _histories(histories, rows)
+        second = False
+        if uniforms is None:
+            # random.random() once for each row that draws, in row order
+            rules = [draw_rule(cfgs[r], int(vocab), logits[r],
+                               ids[off[r]:off[r + 1]] if ids is not None else None)
+                     for r in range(rows)] if vocab > 0 else [NO_DRAW] * rows
+            second = DRAW_UNKNOWN in rules
+            u = np.zeros(rows) if second else np.array(
+                [random.random() if x == DRAW else 0.0 for x in rules])
+        else:
+            u = np.ascontiguousarray(uniforms, dtype=np.float64)
+        tok = self._batch(logits, vocab, ids, off, cfgs, u)
+        if not second:
+            return tok
+        # pass 1 applied the penalties without drawing; the draws follow the
+        # penalised rows
+        u = np.array([random.random() if rules[r] == DRAW or (
+            rules[r] == DRAW_UNKNOWN and _two_candidates(logits[r], int(vocab))) else 0.0
+            for r in range(rows)])
+        plain = (SampleConfigC * rows)(*[_without_penalties(c) for c in cfgs])
+        return self._batch(logits, vocab, None, None, plain, u)
+
+    def _batch(self, logits, vocab, ids, off, cfgs, u) -> np.ndarray:
+        rows, stride = logits.shape
         tok = np.zeros(rows, np.int32)
         P = ctypes.POINTER
         _check(lib().hs_sample_logits_batch(
@@ -360,14 +393,45 @@ def make_configs(configs, rows: int):
     return _configs(configs, rows)
 
 
-def _may_draw(cfg: SampleConfigC, vocab: int) -> bool:
-    """Math.random() is reached only for temperature > 0 with k > 1
-    (src/sampler.ts:36, :49, :77)."""
-    if not (cfg.temperature > 0):
-        return False
+DRAW, NO_DRAW, DRAW_UNKNOWN = 1, 0, -1
+
+
+def draw_rule(cfg: SampleConfigC, vocab: int, row: np.ndarray, hist: np.ndarray | None) -> int:
+    """Whether sampleLogits calls Math.random() for this row
+    (src/sampler.ts:36, :49-50, :76-77, :112): once iff !(temperature <= 0)
+    (a NaN temperature draws) and order.length >= 2, where order.length is
+    min(k, the number of penalised logits > -Infinity).  Penalties touch only
+    history ids, so two logits > -Infinity at ids outside the history settle
+    it before the call.  Returns DRAW, NO_DRAW, or DRAW_UNKNOWN when only the
+    penalised row can tell."""
+    if cfg.temperature <= 0:
+        return NO_DRAW
     t = cfg.top_k if cfg.top_k > 0 else 64.0
-    k = math.floor(max(1.0, min(t, float(vocab))))
-    return k > 1
+    if math.floor(max(1.0, min(t, float(vocab)))) < 2:
+        return NO_DRAW
+    rep = cfg.repetition_penalty != 1.0
+    pf = cfg.presence_penalty != 0.0 or cfg.frequency_penalty != 0.0
+    h = np.zeros(0, np.int32) if hist is None else np.asarray(hist)
+    window = h if pf else h[-128:]
+    touched = (rep or pf) and window.size > 0
+    cand = row[:vocab] > -np.inf
+    if touched:
+        ids = window[(window >= 0) & (window < vocab)]
+        cand[ids] = False
+    if int(np.count_nonzero(cand)) >= 2:
+        return DRAW
+    return DRAW_UNKNOWN if touched else NO_DRAW
+
+
+def _two_candidates(row: np.ndarray, vocab: int) -> bool:
+    return int(np.count_nonzero(row[:vocab] > -np.inf)) >= 2
+
+
+def _without_penalties(cfg: SampleConfigC) -> SampleConfigC:
+    c = SampleConfigC()
+    ctypes.memmove(ctypes.byref(c), ctypes.byref(cfg), ctypes.sizeof(c))
+    c.repetition_penalty, c.presence_penalty, c.frequency_penalty = 1.0, 0.0, 0.0
+    return c
 
 
 @dataclass

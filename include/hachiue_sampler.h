@@ -13,8 +13,12 @@
  *    a message for the calling thread.  No C++ exception crosses the ABI.
  *  - Logits are mutated in place by the penalties, exactly as the reference
  *    mutates its Float32Array (src/sampler.ts:30).
- *  - A context owns one device, a workspace and the staging buffers; it is not
- *    thread-safe.  Calls on one context are serialised by the caller.
+ *  - A context owns one device, a workspace and the staging buffers.  Every
+ *    entry point holds the context's lock for the whole call, so calls from
+ *    several threads on one context run one after the other.  Device entry
+ *    points enqueue work and return; a call on another stream than the
+ *    previous call's first makes its stream wait for that call's last kernel
+ *    (the workspace is shared), so streams may change between calls.
  *  - "device pointer" arguments must be device memory on the context's device
  *    (hipMalloc); "stream" is a hipStream_t or NULL for the null stream.
  */

@@ -6,6 +6,9 @@
 //   node dropin_check.js argmax <workload dir>   argmaxLogits / argmaxLogitsBatch / nextToken
 //   node dropin_check.js route                   isGreedyRoute on option objects
 //   node dropin_check.js nogpu                   error behaviour without a GPU
+//   node dropin_check.js rule <cases.json>       drawRule's decision per case (no GPU)
+//   node dropin_check.js draws <cases.json>      Math.random() calls and tokens of
+//                                                sampleLogits / sampleLogitsBatch
 const fs = require('fs');
 const path = require('path');
 const hs = require(path.join(__dirname, '..', '..', 'hachiue_amd', 'js', 'index.js'));
@@ -89,6 +92,46 @@ if (mode === 'kat') {
     { temperature: 0, repetitionPenalty: 1.0 }, { temperature: 0, repetitionPenalty: 1.1 },
     { temperature: 0, repetitionPenalty: null }, { temperature: 0.5 }, { temperature: NaN }];
   console.log(JSON.stringify(cases.map(hs.isGreedyRoute)));
+} else if (mode === 'rule' || mode === 'draws') {
+  const data = JSON.parse(fs.readFileSync(process.argv[3], 'utf8'));
+  const FIELDS = ['temperature', 'topK', 'topP', 'minP', 'repetitionPenalty',
+    'presencePenalty', 'frequencyPenalty'];
+  const DEF = [0.6, 20, 0.95, 0, 1, 0, 0];
+  const real = Math.random;
+  let calls = 0;
+  Math.random = function () { calls++; return 0.5; };
+  const rows = data.cases.map(function (c) {
+    const cfg = {};
+    Object.keys(c.config).forEach(function (k) { cfg[k] = special(c.config[k]); });
+    const logits = new Float32Array(c.logits.map(special));
+    if (mode === 'rule') {
+      const packed = new Float64Array(FIELDS.map(function (f, i) {
+        return cfg[f] === undefined ? DEF[i] : cfg[f];
+      }));
+      const ids = new Int32Array(c.history);
+      return { name: c.name, rule: hs.drawRule(packed, 0, c.vocab, logits, 0, c.vocab, ids, 0, ids.length) };
+    }
+    calls = 0;
+    const token = hs.sampleLogits(logits, c.vocab, c.history.slice(), cfg);
+    return { name: c.name, token: token, calls: calls };
+  });
+  if (mode === 'draws') {
+    // the same cases as one batch (rows padded with -Infinity to one stride)
+    const V = Math.max.apply(null, data.cases.map(function (c) { return c.vocab; }));
+    const all = new Float32Array(V * data.cases.length).fill(-Infinity);
+    data.cases.forEach(function (c, r) { all.set(new Float32Array(c.logits.map(special)), r * V); });
+    const cfgs = data.cases.map(function (c) {
+      const o = {};
+      Object.keys(c.config).forEach(function (k) { o[k] = special(c.config[k]); });
+      return o;
+    });
+    calls = 0;
+    const tok = hs.sampleLogitsBatch(all, V, data.cases.map(function (c) { return c.history; }), cfgs,
+      null, { rows: data.cases.length, stride: V });
+    rows.push({ name: '(batch)', tokens: Array.from(tok), calls: calls });
+  }
+  Math.random = real;
+  rows.forEach(function (r) { console.log(JSON.stringify(r)); });
 } else if (mode === 'nogpu') {
   const out = {};
   out.vocab0 = hs.sampleLogits(new Float32Array([1, 2]), 0, [], {});

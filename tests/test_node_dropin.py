@@ -115,3 +115,23 @@ def test_dropin_argmax_matches_oracle():
     assert out["rows"] == want
     assert out["next"] == want          # nextToken on the greedy route
     assert out["unchanged"]             # the argmax reads the logits only
+
+
+DRAW_CASES = os.path.join(ROOT, "tests", "golden", "draw_cases.json")
+
+
+@needs_node
+@pytest.mark.gpu
+def test_dropin_math_random_calls_follow_the_reference():
+    """Math.random() is called exactly when sampleLogits calls it (the
+    hand-derived counts of tests/golden/draw_cases.json), row by row and in
+    the batch API, and the tokens are the hand-derived ones."""
+    with open(DRAW_CASES) as f:
+        cases = json.load(f)["cases"]
+    out = {r["name"]: r for r in _node("draws", DRAW_CASES)}
+    for c in cases:
+        assert out[c["name"]]["calls"] == c["calls"], c["name"]
+        assert out[c["name"]]["token"] == c["token"], c["name"]
+    batch = out["(batch)"]
+    assert batch["calls"] == sum(c["calls"] for c in cases)
+    assert batch["tokens"] == [c["token"] for c in cases]
