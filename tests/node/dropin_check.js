@@ -6,6 +6,8 @@
 //   node dropin_check.js argmax <workload dir>   argmaxLogits / argmaxLogitsBatch / nextToken
 //   node dropin_check.js route                   isGreedyRoute on option objects
 //   node dropin_check.js nogpu                   error behaviour without a GPU
+//   node dropin_check.js concurrent <dir>        two async batches in flight together with
+//                                                sync calls on the shared default context
 //   node dropin_check.js rule <cases.json>       drawRule's decision per case (no GPU)
 //   node dropin_check.js draws <cases.json>      Math.random() calls and tokens of
 //                                                sampleLogits / sampleLogitsBatch
@@ -72,6 +74,26 @@ if (mode === 'kat') {
     console.log(JSON.stringify({ tokens: Array.from(tok), tokens_async: Array.from(tok2),
       logits_same: bits(logits).join() === bits(logits2).join(),
       penalised: bits(logits) }));
+  }, function (e) { console.error(e); process.exit(1); });
+} else if (mode === 'concurrent') {
+  const w = load(process.argv[3]);
+  const hists = w.ids ? w.configs.map(function (_, r) { return w.history(r); }) : null;
+  const shape = { rows: w.meta.rows, stride: w.meta.stride };
+  const a = w.logits.slice();
+  const b = w.logits.slice();
+  const pa = hs.sampleLogitsBatchAsync(a, w.meta.vocab, hists, w.configs, w.uniforms, shape);
+  const pb = hs.sampleLogitsBatchAsync(b, w.meta.vocab, hists, w.configs, w.uniforms, shape);
+  // sync calls while both batches are in flight on the same context
+  const s = w.meta.stride;
+  const rows = [];
+  for (let r = 0; r < w.meta.rows; r++) {
+    const row = w.logits.slice(r * s, r * s + s);
+    rows.push(hs.sampleLogits(row, w.meta.vocab, w.history(r),
+      Object.assign({ uniform: w.uniforms[r] }, w.configs[r])));
+  }
+  Promise.all([pa, pb]).then(function (t) {
+    console.log(JSON.stringify({ a: Array.from(t[0]), b: Array.from(t[1]), rows: rows,
+      a_bits: bits(a), b_same: bits(a).join() === bits(b).join() }));
   }, function (e) { console.error(e); process.exit(1); });
 } else if (mode === 'argmax') {
   const w = load(process.argv[3]);

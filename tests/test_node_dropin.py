@@ -135,3 +135,20 @@ def test_dropin_math_random_calls_follow_the_reference():
     batch = out["(batch)"]
     assert batch["calls"] == sum(c["calls"] for c in cases)
     assert batch["tokens"] == [c["token"] for c in cases]
+
+
+@needs_node
+@pytest.mark.gpu
+def test_dropin_concurrent_calls_on_one_context():
+    """Two sampleLogitsBatchAsync calls in flight at once (libuv worker
+    threads) and sync sampleLogits calls on the main thread, all on the
+    default context: every result equals the oracle's."""
+    wl = workloads.make("batch64", 9, rows=12)
+    with tempfile.TemporaryDirectory() as d:
+        _workload_dir(wl, d)
+        out = _node("concurrent", d)[0]
+    res, ref = _oracle(wl)
+    ok = lambda t: ((np.array(t) == res.token) | (res.draw_margin < 1e-6)).all()
+    assert ok(out["a"]) and ok(out["b"]) and ok(out["rows"])
+    assert out["b_same"]
+    assert np.array_equal(np.array(out["a_bits"], np.uint32), ref.reshape(-1).view(np.uint32))
