@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <new>
 #include <string>
@@ -15,6 +16,34 @@
 
 #include "hachiue_sampler.h"
 #include "sampler_internal.h"
+
+// ---- workspace of hs_sample_batch_device_noalloc: one array per GPU, in
+// device memory for the life of the process.  Layout (offsets 256-aligned):
+// plans [kNoAllocMaxRows] | routing lists [4][kNoAllocMaxRows] | split-row
+// hand-over lists [kSplitCUs][kPartCap] | their meta data [kSplitCUs] | the
+// split rows' arrival counters [kSplitCUs] (zero between calls).
+namespace na {
+constexpr int kMaxRows = 2048;
+constexpr size_t kPlansOff = 0;
+constexpr size_t kPlansBytes = sizeof(hs::RowPlan) * kMaxRows;
+constexpr size_t kListsOff = kPlansOff + kPlansBytes;
+constexpr size_t kListsBytes = sizeof(int32_t) * 4 * kMaxRows;
+constexpr size_t kSplitListOff = kListsOff + kListsBytes;
+constexpr size_t kSplitListBytes = sizeof(unsigned long long) * hs::kSplitCUs * hs::kPartCap;
+constexpr size_t kSplitMetaOff = kSplitListOff + kSplitListBytes;
+constexpr size_t kSplitMetaBytes = sizeof(hs::SplitMeta) * hs::kSplitCUs;
+constexpr size_t kSplitCntOff = kSplitMetaOff + kSplitMetaBytes;
+constexpr size_t kSplitCntBytes = sizeof(uint32_t) * hs::kSplitCUs;
+constexpr size_t kBytes = kSplitCntOff + kSplitCntBytes;
+static_assert(kListsOff % 256 == 0 && kSplitListOff % 256 == 0 && kSplitMetaOff % 256 == 0 &&
+                  kSplitCntOff % 256 == 0,
+              "scratch layout alignment");
+constexpr int kMaxDevices = 64;
+}  // namespace na
+
+// In host code `scratch` names a host-side stand-in: kernels and copies take
+// the per-device address from hipGetSymbolAddress (g_scratch below).
+static __device__ __align__(256) unsigned char scratch[na::kBytes];
 
 namespace {
 
@@ -65,6 +94,10 @@ struct DevBuf {
 
 std::mutex g_prep_mu;
 std::vector<int> g_prepared;
+// per device: the address of `scratch` on that device (set once, at the
+// first context created on it) and a count of the plan uploads into it
+void *g_scratch[na::kMaxDevices];
+std::atomic<uint64_t> g_scratch_gen[na::kMaxDevices];
 
 }  // namespace
 
@@ -107,6 +140,16 @@ struct hs_context {
   // workgroups per row of the row kernel: 0 chooses by batch size
   int row_split = 0;
   int64_t timed_calls = 0;
+  // hs_sample_batch_device_noalloc: pinned staging of plans and lists, the
+  // configs of this context's last upload into the device's scratch, and the
+  // device's upload count after it (all set up at creation)
+  void *na_staging = nullptr;
+  hipEvent_t na_upload_ev = nullptr;
+  bool na_pending = false;
+  hs_sample_config *na_last = nullptr;
+  int na_rows = -1, na_vocab = -1;
+  int na_count[4] = {0, 0, 0, 0};   // pf, row, large, mid
+  uint64_t na_gen = 0;
 };
 
 namespace {
@@ -153,6 +196,38 @@ struct Routing {
   std::vector<int32_t> pf, row, chunk, large, mid;
 };
 
+// One row's plan: the `??`-resolved config of src/sampler.ts:18-22 with k
+// resolved (:49) and the kernel mode.
+hs::RowPlan plan_row(const hs_sample_config &c, int vocab) {
+  hs::RowPlan p;
+  memset(&p, 0, sizeof p);
+  p.temperature = c.temperature;
+  p.top_p = c.top_p;
+  p.min_p = c.min_p;
+  p.rep = c.repetition_penalty;
+  p.pres = c.presence_penalty;
+  p.freq = c.frequency_penalty;
+  p.pen = (c.repetition_penalty != 1.0 ? hs::kPenRep : 0) |
+          ((c.presence_penalty != 0.0 || c.frequency_penalty != 0.0) ? hs::kPenPF : 0);
+  if (c.temperature <= 0) {   // src/sampler.ts:36 (NaN is not <= 0)
+    p.mode = hs::kModeGreedy;
+    p.k = 1;
+  } else {
+    const int64_t k = resolve_k(c.top_k, vocab);
+    p.k = (int32_t)k;
+    if (k <= hs::kSmallK) p.mode = hs::kModeSmall;
+    else if (k <= hs::kMaxK) p.mode = hs::kModeGeneric;
+    else p.mode = hs::kModeLarge;
+  }
+  return p;
+}
+
+// The large-k kernel takes penalised logits: its rows' penalties run in the
+// pre-pass, like the presence / frequency rows of the other kernels.
+bool in_prepass(const hs::RowPlan &p) {
+  return (p.pen & hs::kPenPF) || (p.pen && p.mode == hs::kModeLarge);
+}
+
 int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_rows,
                 std::vector<hs::RowPlan> &out, Routing &rt) {
   out.resize((size_t)rows);
@@ -162,31 +237,9 @@ int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_r
   rt.large.clear();
   rt.mid.clear();
   for (int r = 0; r < rows; ++r) {
-    const hs_sample_config &c = cfgs[r];
-    hs::RowPlan p;
-    memset(&p, 0, sizeof p);
-    p.temperature = c.temperature;
-    p.top_p = c.top_p;
-    p.min_p = c.min_p;
-    p.rep = c.repetition_penalty;
-    p.pres = c.presence_penalty;
-    p.freq = c.frequency_penalty;
-    p.pen = (c.repetition_penalty != 1.0 ? hs::kPenRep : 0) |
-            ((c.presence_penalty != 0.0 || c.frequency_penalty != 0.0) ? hs::kPenPF : 0);
-    if (c.temperature <= 0) {   // src/sampler.ts:36 (NaN is not <= 0)
-      p.mode = hs::kModeGreedy;
-      p.k = 1;
-    } else {
-      const int64_t k = resolve_k(c.top_k, vocab);
-      p.k = (int32_t)k;
-      if (k <= hs::kSmallK) p.mode = hs::kModeSmall;
-      else if (k <= hs::kMaxK) p.mode = hs::kModeGeneric;
-      else p.mode = hs::kModeLarge;
-    }
+    const hs::RowPlan p = plan_row(cfgs[r], vocab);
     out[(size_t)r] = p;
-    // the large-k kernel takes penalised logits: its rows' penalties run in
-    // the pre-pass, like the presence / frequency rows of the other kernels
-    if ((p.pen & hs::kPenPF) || (p.pen && p.mode == hs::kModeLarge)) rt.pf.push_back(r);
+    if (in_prepass(p)) rt.pf.push_back(r);
     if (p.mode == hs::kModeLarge) {
       rt.large.push_back(r);
       continue;
@@ -584,6 +637,149 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32
   return leave_stream(ctx, stream, ev == nullptr);
 }
 
+// Plans and routing lists written into fixed arrays (no allocation): the
+// lists pf | row | large | mid back to back, in row order, their lengths in
+// n[0..3].  Routing as build_plans with every row on the one-pass kernels
+// (vocab <= kRowMaxVocab): rows with k <= 64 join the mid kernel's launch
+// when it has rows.
+void build_plans_fixed(const hs_sample_config *cfgs, int rows, int vocab, hs::RowPlan *plans,
+                       int32_t *lists, int n[4]) {
+  int n_pf = 0, n_row = 0, n_large = 0, n_mid = 0, n_small = 0;
+  for (int r = 0; r < rows; ++r) {
+    const hs::RowPlan p = plan_row(cfgs[r], vocab);
+    plans[r] = p;
+    n_pf += in_prepass(p);
+    n_large += p.mode == hs::kModeLarge;
+    n_mid += p.mode == hs::kModeGeneric;
+    n_row += p.mode == hs::kModeGreedy || p.mode == hs::kModeSmall;
+    n_small += p.mode == hs::kModeSmall;
+  }
+  const bool merge = n_mid > 0 && n_row > 0;
+  if (merge) {
+    n_row -= n_small;
+    n_mid += n_small;
+  }
+  int32_t *pf = lists, *row = pf + n_pf, *large = row + n_row, *mid = large + n_large;
+  for (int r = 0; r < rows; ++r) {
+    const hs::RowPlan &p = plans[r];
+    if (in_prepass(p)) *pf++ = r;
+    if (p.mode == hs::kModeLarge) *large++ = r;
+    else if (p.mode == hs::kModeGeneric || (merge && p.mode == hs::kModeSmall)) *mid++ = r;
+    else *row++ = r;
+  }
+  n[0] = n_pf;
+  n[1] = n_row;
+  n[2] = n_large;
+  n[3] = n_mid;
+}
+
+// hs_sample_batch_device with the device's `scratch` array as its workspace:
+// no allocation of any kind.  The plans go through the context's pinned
+// staging (set up at creation) and are not uploaded again while this
+// context's last upload is the latest one into the device's scratch and the
+// configs, rows and vocab are unchanged.
+int sample_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_stride,
+                          int32_t vocab, const int32_t *d_hist_ids, const int64_t *d_hist_offsets,
+                          const hs_sample_config *configs, const double *d_uniforms,
+                          int32_t *d_tokens, hipStream_t stream) {
+  if (rows < 0) return fail(HS_ERR_INVALID_ARGUMENT, "rows must be >= 0 (got %d)", rows);
+  if (rows == 0) return HS_OK;
+  if (!configs || !d_uniforms || !d_tokens)
+    return fail(HS_ERR_INVALID_ARGUMENT, "configs, uniforms and tokens must not be null");
+  if ((d_hist_ids == nullptr) != (d_hist_offsets == nullptr))
+    return fail(HS_ERR_INVALID_ARGUMENT, "history ids and offsets must both be given or both null");
+  if (rows > na::kMaxRows)
+    return fail(HS_ERR_UNSUPPORTED, "rows %d above the no-allocation limit %d", rows, na::kMaxRows);
+  if (vocab > hs::kRowMaxVocab)
+    return fail(HS_ERR_UNSUPPORTED, "vocab %d above the no-allocation limit %d", vocab,
+                hs::kRowMaxVocab);
+  if (ctx->device < 0 || ctx->device >= na::kMaxDevices || !g_scratch[ctx->device] ||
+      !ctx->na_staging || !ctx->na_last)
+    return fail(HS_ERR_UNSUPPORTED, "no scratch workspace on device %d", ctx->device);
+  DeviceGuard guard(ctx->device);
+  int rc = enter_stream(ctx, stream);
+  if (rc) return rc;
+  if (vocab <= 0) {   // src/sampler.ts: no logit is read; every path returns 0
+    const hipError_t e = hs::launch_fill_u32(reinterpret_cast<uint32_t *>(d_tokens), rows, 0u, stream);
+    if (e != hipSuccess) return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+    return leave_stream(ctx, stream, false);
+  }
+  if (!d_logits) return fail(HS_ERR_INVALID_ARGUMENT, "logits must not be null");
+  if (row_stride < vocab)
+    return fail(HS_ERR_INVALID_ARGUMENT, "row_stride %lld < vocab %d", (long long)row_stride, vocab);
+  char *base = static_cast<char *>(g_scratch[ctx->device]);
+  std::atomic<uint64_t> &gen = g_scratch_gen[ctx->device];
+  const size_t cbytes = sizeof(hs_sample_config) * (size_t)rows;
+  const bool same = ctx->na_gen == gen.load() && ctx->na_rows == rows && ctx->na_vocab == vocab &&
+                    memcmp(ctx->na_last, configs, cbytes) == 0;
+  if (!same) {
+    if (ctx->na_pending) {   // the staging may still be read by the last upload
+      HS_HIP(hipEventSynchronize(ctx->na_upload_ev));
+      ctx->na_pending = false;
+    }
+    char *st = static_cast<char *>(ctx->na_staging);
+    hs::RowPlan *plans = reinterpret_cast<hs::RowPlan *>(st);
+    int32_t *lists = reinterpret_cast<int32_t *>(st + na::kPlansBytes);
+    build_plans_fixed(configs, rows, vocab, plans, lists, ctx->na_count);
+    const int nl = ctx->na_count[0] + ctx->na_count[1] + ctx->na_count[2] + ctx->na_count[3];
+    HS_HIP(hipMemcpyAsync(base + na::kPlansOff, plans, sizeof(hs::RowPlan) * (size_t)rows,
+                          hipMemcpyHostToDevice, stream));
+    HS_HIP(hipMemcpyAsync(base + na::kListsOff, lists, sizeof(int32_t) * (size_t)nl,
+                          hipMemcpyHostToDevice, stream));
+    HS_HIP(hipEventRecord(ctx->na_upload_ev, stream));
+    ctx->na_pending = true;
+    memcpy(ctx->na_last, configs, cbytes);
+    ctx->na_rows = rows;
+    ctx->na_vocab = vocab;
+    ctx->na_gen = ++gen;
+  }
+  const int n_pf = ctx->na_count[0], n_row = ctx->na_count[1], n_large = ctx->na_count[2],
+            n_mid = ctx->na_count[3];
+  // small batches split each row of the row kernel (at most kSplitCUs parts)
+  int split = choose_split(ctx, n_row, vocab);
+  while (split > 1 && (int64_t)n_row * split > hs::kSplitCUs) --split;
+
+  hs::Workspace ws;
+  memset(&ws, 0, sizeof ws);
+  ws.plans = reinterpret_cast<hs::RowPlan *>(base + na::kPlansOff);
+  const int32_t *lists = reinterpret_cast<const int32_t *>(base + na::kListsOff);
+  ws.pf_list = lists;
+  ws.row_list = lists + n_pf;
+  ws.chunk_list = lists + n_pf + n_row;
+  ws.large_list = lists + n_pf + n_row;
+  ws.mid_list = lists + n_pf + n_row + n_large;
+  ws.split_list = reinterpret_cast<unsigned long long *>(base + na::kSplitListOff);
+  ws.split_meta = reinterpret_cast<hs::SplitMeta *>(base + na::kSplitMetaOff);
+  ws.split_cnt = reinterpret_cast<uint32_t *>(base + na::kSplitCntOff);
+
+  hs::LaunchArgs a;
+  memset(&a, 0, sizeof a);
+  a.logits = d_logits;
+  a.stride = row_stride;
+  a.rows = rows;
+  a.vocab = vocab;
+  a.chunks = (int32_t)((vocab + hs::kChunk - 1) / hs::kChunk);
+  a.vec = ((reinterpret_cast<uintptr_t>(d_logits) & 15u) == 0 && (row_stride & 3) == 0) ? 1 : 0;
+  a.n_pf = n_pf;
+  a.n_row = n_row;
+  a.split = split;
+  a.rows_direct = n_row == rows ? 1 : 0;
+  a.n_large = n_large;
+  a.n_mid = n_mid;
+  a.hist_ids = d_hist_ids;
+  a.hist_off = d_hist_offsets;
+  a.uniforms = d_uniforms;
+  a.tokens = d_tokens;
+  const hipError_t e = hs::launch_sample(a, ws, stream, nullptr, ctx->done_ev);
+  if (e != hipSuccess) {
+    // a kernel that did not run may leave a split counter raised
+    (void)hs::launch_fill_u32(ws.split_cnt, hs::kSplitCUs, 0u, stream);
+    (void)leave_stream(ctx, stream, false);
+    return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+  }
+  return leave_stream(ctx, stream, true);
+}
+
 }  // namespace
 
 // Every entry point that uses a context holds its mutex for the whole call.
@@ -624,6 +820,15 @@ int hs_context_create(int device, hs_context **out) {
     for (int d : g_prepared) done |= d == device;
     if (!done) {
       HS_HIP(hs::prepare_kernels());
+      if (device < na::kMaxDevices) {
+        // the no-allocation entry point's workspace on this device: its
+        // address here, once; its arrival counters start at zero
+        void *p = nullptr;
+        HS_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        HS_HIP(hipMemset(static_cast<char *>(p) + na::kSplitCntOff, 0, na::kSplitCntBytes));
+        HS_HIP(hipDeviceSynchronize());
+        g_scratch[device] = p;
+      }
       g_prepared.push_back(device);
     }
   }
@@ -634,6 +839,12 @@ int hs_context_create(int device, hs_context **out) {
   if (const char *env = getenv("HS_ROW_SPLIT")) ctx->row_split = atoi(env);
   e = hipEventCreateWithFlags(&ctx->plan_done, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->done_ev, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->na_upload_ev, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipHostMalloc(&ctx->na_staging, na::kPlansBytes + na::kListsBytes);
+  if (e == hipSuccess) {
+    ctx->na_last = new (std::nothrow) hs_sample_config[na::kMaxRows];
+    if (!ctx->na_last) e = hipErrorOutOfMemory;
+  }
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
   if (e != hipSuccess) {
     hs_context_destroy(ctx);
@@ -700,6 +911,9 @@ int hs_context_destroy(hs_context *ctx) {
     if (ctx->plan_staging) (void)hipHostFree(ctx->plan_staging);
     if (ctx->plan_done) (void)hipEventDestroy(ctx->plan_done);
     if (ctx->done_ev) (void)hipEventDestroy(ctx->done_ev);
+    if (ctx->na_upload_ev) (void)hipEventDestroy(ctx->na_upload_ev);
+    if (ctx->na_staging) (void)hipHostFree(ctx->na_staging);
+    delete[] ctx->na_last;
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   }
   delete ctx;
@@ -726,6 +940,15 @@ int hs_sample_batch_device(hs_context *ctx, float *d_logits, int32_t rows, int64
   return sample_device(ctx, d_logits, rows, row_stride, vocab, d_hist_ids, d_hist_offsets, configs,
                        d_uniforms, d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr,
                        static_cast<hipStream_t>(stream));
+}
+
+int hs_sample_batch_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows,
+                                   int64_t row_stride, int32_t vocab, const int32_t *d_hist_ids,
+                                   const int64_t *d_hist_offsets, const hs_sample_config *configs,
+                                   const double *d_uniforms, int32_t *d_tokens, void *stream) {
+  HS_LOCK(ctx);
+  return sample_device_noalloc(ctx, d_logits, rows, row_stride, vocab, d_hist_ids, d_hist_offsets,
+                               configs, d_uniforms, d_tokens, static_cast<hipStream_t>(stream));
 }
 
 int hs_argmax_device(hs_context *ctx, const float *d_logits, int32_t rows, int64_t row_stride,

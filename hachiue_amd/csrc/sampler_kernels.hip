@@ -3618,6 +3618,20 @@ __global__ __launch_bounds__(256) void decode_append_kernel(DecodeArgs d) {
   d.len[r] = len + 1;
 }
 
+// Sets n words to v: a kernel, not hipMemsetAsync, so that a caller may
+// capture it in a graph.
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t *p, int64_t n, uint32_t v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+hipError_t launch_fill_u32(uint32_t *p, int64_t n, uint32_t v, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p,
+                     n, v);
+  return hipGetLastError();
+}
+
 hipError_t launch_decode_append(const DecodeArgs &d, hipStream_t stream) {
   if (d.rows <= 0) return hipSuccess;
   hipLaunchKernelGGL(decode_append_kernel, dim3((unsigned)((d.rows + 255) / 256)), dim3(256), 0,

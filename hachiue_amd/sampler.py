@@ -34,7 +34,8 @@ ROW_GREEDY, ROW_REPLAYED, ROW_TIES, ROW_SINGLE = 0x1, 0x2, 0x4, 0x8
 # Every symbol include/hachiue_sampler.h declares.
 EXPORTS = ("hs_abi_version", "hs_last_error", "hs_config_default", "hs_context_create",
            "hs_context_destroy", "hs_sample_logits", "hs_sample_logits_batch",
-           "hs_sample_batch_device", "hs_sample_batch_device_ex", "hs_argmax_device",
+           "hs_sample_batch_device", "hs_sample_batch_device_ex",
+           "hs_sample_batch_device_noalloc", "hs_argmax_device",
            "hs_argmax", "hs_gemv_device", "hs_lm_head_sample_device", "hs_decode_step_device",
            "hs_context_set_timing", "hs_context_kernel_times")
 
@@ -104,6 +105,8 @@ def _load() -> ctypes.CDLL:
                                          vp, vp]
     L.hs_sample_batch_device_ex.argtypes = [vp, vp, i32, i64, i32, vp, vp, P(SampleConfigC),
                                             vp, vp, i32, vp, vp, vp, vp, vp, vp]
+    L.hs_sample_batch_device_noalloc.argtypes = [vp, vp, i32, i64, i32, vp, vp,
+                                                 P(SampleConfigC), vp, vp, vp]
     L.hs_argmax_device.argtypes = [vp, vp, i32, i64, i32, vp, vp]
     L.hs_argmax.argtypes = [vp, P(ctypes.c_float), i32, i64, i32, P(i32)]
     L.hs_gemv_device.argtypes = [vp, vp, i32, i64, i32, vp, i32, i32, vp, i64, vp]
@@ -366,6 +369,19 @@ class Sampler:
             vp(d_hist_off or 0), cfgs, vp(d_uniforms), vp(d_tokens), int(cand_stride),
             vp(d_cand_ids or 0), vp(d_cand_probs or 0), vp(d_cand_count or 0), vp(d_cutoff or 0),
             vp(d_row_flags or 0), st))
+
+
+    def sample_device_noalloc(self, d_logits: int, rows: int, row_stride: int, vocab: int,
+                              d_hist_ids: int | None, d_hist_off: int | None, configs,
+                              d_uniforms: int, d_tokens: int, stream=None) -> None:
+        """sample_device through hs_sample_batch_device_noalloc: the same
+        step with the GPU's static scratch array as the workspace."""
+        cfgs = configs if isinstance(configs, ctypes.Array) else _configs(configs, rows)
+        vp = ctypes.c_void_p
+        st = stream.handle if isinstance(stream, hip.Stream) else stream
+        _check(lib().hs_sample_batch_device_noalloc(
+            self._ctx, vp(d_logits), int(rows), int(row_stride), int(vocab), vp(d_hist_ids or 0),
+            vp(d_hist_off or 0), cfgs, vp(d_uniforms), vp(d_tokens), st))
 
 
 def _configs(configs, rows: int):

@@ -131,6 +131,27 @@ int hs_sample_batch_device_ex(hs_context *ctx, float *d_logits, int32_t rows,
                               int32_t *d_cutoff, uint32_t *d_row_flags,
                               void *stream);
 
+/* hs_sample_batch_device without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate during the call (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, semantics and outputs as
+ * hs_sample_batch_device; the workspace is one static device array per GPU
+ * (about 310 KB, held until the process ends, its address taken once per
+ * device when the first context on it is created), and the plans are staged
+ * through pinned memory the context set up at creation.  The call makes no
+ * hipMalloc, hipFree, host allocation or hipMemset.  Limits: rows <= 2048 and
+ * vocab <= 524288 (HS_ERR_UNSUPPORTED beyond).  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU through different contexts
+ * race (calls on one context are serialised as usual).  Kernel timing
+ * (hs_context_set_timing) does not cover this entry point. */
+int hs_sample_batch_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows,
+                                   int64_t row_stride, int32_t vocab,
+                                   const int32_t *d_hist_ids,
+                                   const int64_t *d_hist_offsets,
+                                   const hs_sample_config *configs,
+                                   const double *d_uniforms, int32_t *d_tokens,
+                                   void *stream);
+
 /* The engine's GPU greedy route.  hachiue's engine decodes greedily without
  * sampleLogits when temperature <= 0 and no repetition penalty is set
  * (src/engine.ts:1600-1601): the forward pass ends in the WGSL argmax
