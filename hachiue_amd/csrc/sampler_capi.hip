@@ -19,23 +19,27 @@
 
 // ---- workspace of hs_sample_batch_device_noalloc: one array per GPU, in
 // device memory for the life of the process.  Layout (offsets 256-aligned):
-// plans [kNoAllocMaxRows] | routing lists [4][kNoAllocMaxRows] | split-row
-// hand-over lists [kSplitCUs][kPartCap] | their meta data [kSplitCUs] | the
-// split rows' arrival counters [kSplitCUs] (zero between calls).
+// plans [kMaxRows] | routing lists [5][kMaxRows] | the two-pass large-k
+// rows handed back [kMaxRows] | split-row hand-over lists
+// [kSplitCUs][kPartCap] | their meta data [kSplitCUs] | the split rows'
+// arrival counters [kSplitCUs] (zero between calls).
 namespace na {
 constexpr int kMaxRows = 2048;
 constexpr size_t kPlansOff = 0;
 constexpr size_t kPlansBytes = sizeof(hs::RowPlan) * kMaxRows;
 constexpr size_t kListsOff = kPlansOff + kPlansBytes;
-constexpr size_t kListsBytes = sizeof(int32_t) * 4 * kMaxRows;
-constexpr size_t kSplitListOff = kListsOff + kListsBytes;
+constexpr size_t kListsBytes = sizeof(int32_t) * 5 * kMaxRows;
+constexpr size_t kRetryOff = kListsOff + kListsBytes;
+constexpr size_t kRetryBytes = sizeof(int32_t) * kMaxRows;
+constexpr size_t kSplitListOff = kRetryOff + kRetryBytes;
 constexpr size_t kSplitListBytes = sizeof(unsigned long long) * hs::kSplitCUs * hs::kPartCap;
 constexpr size_t kSplitMetaOff = kSplitListOff + kSplitListBytes;
 constexpr size_t kSplitMetaBytes = sizeof(hs::SplitMeta) * hs::kSplitCUs;
 constexpr size_t kSplitCntOff = kSplitMetaOff + kSplitMetaBytes;
 constexpr size_t kSplitCntBytes = sizeof(uint32_t) * hs::kSplitCUs;
 constexpr size_t kBytes = kSplitCntOff + kSplitCntBytes;
-static_assert(kListsOff % 256 == 0 && kSplitListOff % 256 == 0 && kSplitMetaOff % 256 == 0 &&
+static_assert(kListsOff % 256 == 0 && kRetryOff % 256 == 0 && kSplitListOff % 256 == 0 &&
+                  kSplitMetaOff % 256 == 0 &&
                   kSplitCntOff % 256 == 0,
               "scratch layout alignment");
 constexpr int kMaxDevices = 64;
@@ -115,6 +119,7 @@ struct hs_context {
   DevBuf plans, cand, cand_count, info;
   DevBuf split_list, split_meta, split_cnt;   // split rows (split_cnt: zero between calls)
   DevBuf gemv_part, gemv_cnt;   // Q6_K GEMV tiles cut between waves (gemv_cnt: zero between calls)
+  DevBuf large_retry;           // two-pass large-k rows handed back
   int64_t cand_count_rows = 0;     // rows whose counter is known to be zero
   // plan upload cache
   std::vector<hs::RowPlan> last_plans;
@@ -148,7 +153,7 @@ struct hs_context {
   bool na_pending = false;
   hs_sample_config *na_last = nullptr;
   int na_rows = -1, na_vocab = -1;
-  int na_count[4] = {0, 0, 0, 0};   // pf, row, large, mid
+  int na_count[5] = {0, 0, 0, 0, 0};   // pf, row, large, mid, two-pass large
   uint64_t na_gen = 0;
 };
 
@@ -193,8 +198,14 @@ int64_t resolve_k(double top_k, int64_t vocab) {
 
 // Routing of rows to kernels, uploaded next to the plans.
 struct Routing {
-  std::vector<int32_t> pf, row, chunk, large, mid;
+  std::vector<int32_t> pf, row, chunk, large, mid, lfast;
 };
+
+// k = vocab (no slot is ever evicted) and no min-p: the two-pass large-k
+// kernel's rows.
+bool two_pass_large(const hs::RowPlan &p, int vocab) {
+  return p.mode == hs::kModeLarge && p.k >= vocab && !(p.min_p > 0.0);
+}
 
 // One row's plan: the `??`-resolved config of src/sampler.ts:18-22 with k
 // resolved (:49) and the kernel mode.
@@ -236,12 +247,13 @@ int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_r
   rt.chunk.clear();
   rt.large.clear();
   rt.mid.clear();
+  rt.lfast.clear();
   for (int r = 0; r < rows; ++r) {
     const hs::RowPlan p = plan_row(cfgs[r], vocab);
     out[(size_t)r] = p;
     if (in_prepass(p)) rt.pf.push_back(r);
     if (p.mode == hs::kModeLarge) {
-      rt.large.push_back(r);
+      (two_pass_large(p, vocab) ? rt.lfast : rt.large).push_back(r);
       continue;
     }
     const bool one_pass = vocab <= hs::kRowMaxVocab && rows >= row_min_rows;
@@ -266,8 +278,8 @@ int upload_plans(hs_context *ctx, const std::vector<hs::RowPlan> &plans, const R
   const size_t rows = plans.size();
   const size_t pbytes = rows * sizeof(hs::RowPlan);
   const size_t lbytes =
-      sizeof(int32_t) *
-      (rt.pf.size() + rt.row.size() + rt.chunk.size() + rt.large.size() + rt.mid.size());
+      sizeof(int32_t) * (rt.pf.size() + rt.row.size() + rt.chunk.size() + rt.large.size() +
+                         rt.mid.size() + rt.lfast.size());
   const size_t bytes = pbytes + lbytes;
   if (ctx->last_plans.size() == rows && ctx->last_vocab == vocab && ctx->plans.bytes >= bytes &&
       memcmp(ctx->last_plans.data(), plans.data(), pbytes) == 0)
@@ -294,6 +306,8 @@ int upload_plans(hs_context *ctx, const std::vector<hs::RowPlan> &plans, const R
          sizeof(int32_t) * rt.large.size());
   memcpy(lists + rt.pf.size() + rt.row.size() + rt.chunk.size() + rt.large.size(), rt.mid.data(),
          sizeof(int32_t) * rt.mid.size());
+  memcpy(lists + rt.pf.size() + rt.row.size() + rt.chunk.size() + rt.large.size() + rt.mid.size(),
+         rt.lfast.data(), sizeof(int32_t) * rt.lfast.size());
   HS_HIP(hipMemcpyAsync(ctx->plans.p, st, bytes, hipMemcpyHostToDevice, stream));
   HS_HIP(hipEventRecord(ctx->plan_done, stream));
   ctx->plan_pending = true;
@@ -421,6 +435,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   }
   const int n_pf = (int)rt.pf.size(), n_row = (int)rt.row.size(), n_chunk = (int)rt.chunk.size();
   const int n_large = (int)rt.large.size(), n_mid = (int)rt.mid.size();
+  const int n_lfast = (int)rt.lfast.size();
 
   // workspace (the chunk path only)
   if (n_chunk > 0) {
@@ -431,6 +446,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
       HS_HIP(hipMemset(ctx->cand_count.p, 0, ctx->cand_count.bytes));
     }
   }
+  if (n_lfast > 0) HS_HIP(ctx->large_retry.ensure(sizeof(int32_t) * (size_t)n_lfast));
   // small batches split each row of the row kernel over several workgroups
   const int split = choose_split(ctx, n_row, vocab);
   int rc = ensure_split(ctx, n_row, split);
@@ -446,6 +462,8 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   ws.chunk_list = lists + n_pf + n_row;
   ws.large_list = lists + n_pf + n_row + n_chunk;
   ws.mid_list = lists + n_pf + n_row + n_chunk + n_large;
+  ws.lfast_list = lists + n_pf + n_row + n_chunk + n_large + n_mid;
+  ws.large_retry = static_cast<int32_t *>(ctx->large_retry.p);
   ws.cand = static_cast<uint2 *>(ctx->cand.p);
   ws.cand_count = static_cast<int32_t *>(ctx->cand_count.p);
   ws.info = static_cast<hs::ChunkInfo *>(ctx->info.p);
@@ -466,6 +484,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   a.n_chunk = n_chunk;
   a.n_large = n_large;
   a.n_mid = n_mid;
+  a.n_lfast = n_lfast;
   a.hist_ids = d_hist_ids;
   a.hist_off = d_hist_offsets;
   a.hist_len = d_hist_len;
@@ -638,18 +657,19 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32
 }
 
 // Plans and routing lists written into fixed arrays (no allocation): the
-// lists pf | row | large | mid back to back, in row order, their lengths in
-// n[0..3].  Routing as build_plans with every row on the one-pass kernels
+// lists pf | row | large | mid | two-pass large back to back, in row order,
+// their lengths in n[0..4].  Routing as build_plans with every row on the one-pass kernels
 // (vocab <= kRowMaxVocab): rows with k <= 64 join the mid kernel's launch
 // when it has rows.
 void build_plans_fixed(const hs_sample_config *cfgs, int rows, int vocab, hs::RowPlan *plans,
-                       int32_t *lists, int n[4]) {
-  int n_pf = 0, n_row = 0, n_large = 0, n_mid = 0, n_small = 0;
+                       int32_t *lists, int n[5]) {
+  int n_pf = 0, n_row = 0, n_large = 0, n_mid = 0, n_small = 0, n_lfast = 0;
   for (int r = 0; r < rows; ++r) {
     const hs::RowPlan p = plan_row(cfgs[r], vocab);
     plans[r] = p;
     n_pf += in_prepass(p);
-    n_large += p.mode == hs::kModeLarge;
+    n_lfast += two_pass_large(p, vocab);
+    n_large += p.mode == hs::kModeLarge && !two_pass_large(p, vocab);
     n_mid += p.mode == hs::kModeGeneric;
     n_row += p.mode == hs::kModeGreedy || p.mode == hs::kModeSmall;
     n_small += p.mode == hs::kModeSmall;
@@ -660,10 +680,12 @@ void build_plans_fixed(const hs_sample_config *cfgs, int rows, int vocab, hs::Ro
     n_mid += n_small;
   }
   int32_t *pf = lists, *row = pf + n_pf, *large = row + n_row, *mid = large + n_large;
+  int32_t *lfast = mid + n_mid;
   for (int r = 0; r < rows; ++r) {
     const hs::RowPlan &p = plans[r];
     if (in_prepass(p)) *pf++ = r;
-    if (p.mode == hs::kModeLarge) *large++ = r;
+    if (two_pass_large(p, vocab)) *lfast++ = r;
+    else if (p.mode == hs::kModeLarge) *large++ = r;
     else if (p.mode == hs::kModeGeneric || (merge && p.mode == hs::kModeSmall)) *mid++ = r;
     else *row++ = r;
   }
@@ -671,6 +693,7 @@ void build_plans_fixed(const hs_sample_config *cfgs, int rows, int vocab, hs::Ro
   n[1] = n_row;
   n[2] = n_large;
   n[3] = n_mid;
+  n[4] = n_lfast;
 }
 
 // hs_sample_batch_device with the device's `scratch` array as its workspace:
@@ -721,7 +744,8 @@ int sample_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows, int64_
     hs::RowPlan *plans = reinterpret_cast<hs::RowPlan *>(st);
     int32_t *lists = reinterpret_cast<int32_t *>(st + na::kPlansBytes);
     build_plans_fixed(configs, rows, vocab, plans, lists, ctx->na_count);
-    const int nl = ctx->na_count[0] + ctx->na_count[1] + ctx->na_count[2] + ctx->na_count[3];
+    const int nl = ctx->na_count[0] + ctx->na_count[1] + ctx->na_count[2] + ctx->na_count[3] +
+                   ctx->na_count[4];
     HS_HIP(hipMemcpyAsync(base + na::kPlansOff, plans, sizeof(hs::RowPlan) * (size_t)rows,
                           hipMemcpyHostToDevice, stream));
     HS_HIP(hipMemcpyAsync(base + na::kListsOff, lists, sizeof(int32_t) * (size_t)nl,
@@ -734,7 +758,7 @@ int sample_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows, int64_
     ctx->na_gen = ++gen;
   }
   const int n_pf = ctx->na_count[0], n_row = ctx->na_count[1], n_large = ctx->na_count[2],
-            n_mid = ctx->na_count[3];
+            n_mid = ctx->na_count[3], n_lfast = ctx->na_count[4];
   // small batches split each row of the row kernel (at most kSplitCUs parts)
   int split = choose_split(ctx, n_row, vocab);
   while (split > 1 && (int64_t)n_row * split > hs::kSplitCUs) --split;
@@ -748,6 +772,8 @@ int sample_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows, int64_
   ws.chunk_list = lists + n_pf + n_row;
   ws.large_list = lists + n_pf + n_row;
   ws.mid_list = lists + n_pf + n_row + n_large;
+  ws.lfast_list = lists + n_pf + n_row + n_large + n_mid;
+  ws.large_retry = reinterpret_cast<int32_t *>(base + na::kRetryOff);
   ws.split_list = reinterpret_cast<unsigned long long *>(base + na::kSplitListOff);
   ws.split_meta = reinterpret_cast<hs::SplitMeta *>(base + na::kSplitMetaOff);
   ws.split_cnt = reinterpret_cast<uint32_t *>(base + na::kSplitCntOff);
@@ -766,6 +792,7 @@ int sample_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows, int64_
   a.rows_direct = n_row == rows ? 1 : 0;
   a.n_large = n_large;
   a.n_mid = n_mid;
+  a.n_lfast = n_lfast;
   a.hist_ids = d_hist_ids;
   a.hist_off = d_hist_offsets;
   a.uniforms = d_uniforms;
@@ -903,6 +930,7 @@ int hs_context_destroy(hs_context *ctx) {
     ctx->split_cnt.release();
     ctx->gemv_part.release();
     ctx->gemv_cnt.release();
+    ctx->large_retry.release();
     ctx->h_logits.release();
     ctx->h_hist.release();
     ctx->h_off.release();

@@ -105,6 +105,8 @@ struct Workspace {
   const int32_t *chunk_list; // rows of the chunk + finalize kernels
   const int32_t *large_list; // rows of the large-k kernel
   const int32_t *mid_list;   // rows of the mid kernel
+  const int32_t *lfast_list; // rows of the two-pass large-k kernel (k = vocab, no min-p)
+  int32_t *large_retry;      // [n_lfast] 1: the two-pass kernel handed the row back
   uint2 *cand;               // [n_chunk][S][kChunkCap] (key, index)
   int32_t *cand_count;       // [n_chunk]
   ChunkInfo *info;           // [n_chunk][S]
@@ -123,6 +125,7 @@ struct LaunchArgs {
   int32_t want_cands;        // exact candidate order must be produced
   int32_t rows_direct;       // the row kernel takes every row: row = block index
   int32_t n_pf, n_row, n_chunk, n_large, n_mid;
+  int32_t n_lfast;           // rows of the two-pass large-k kernel
   int32_t n_argmax;          // rows of the GPU greedy route (a call of its own)
   int32_t split;             // row / argmax kernel: workgroups per row (1: whole rows)
   const int32_t *hist_ids;
@@ -149,13 +152,15 @@ struct LaunchArgs {
 // Launches the kernels of one call on `stream`.  When `ev` is not null,
 // ev[2i] and ev[2i + 1] receive the start and end of kernel i's dispatch
 // (0 penalty pre-pass, 1 row kernel, 2 chunk kernel, 3 finalize, 4 large-k
-// kernel, 5 mid kernel, 6 GPU greedy-route argmax; 7 is the lm_head GEMV,
-// launched apart), for the kernels that launch only: launched_kernels() says
-// which.
-constexpr int kTimedKernels = 8;
+// kernel, 5 mid kernel, 6 GPU greedy-route argmax, 8 two-pass large-k kernel;
+// 7 is the lm_head GEMV, launched apart), for the kernels that launch only:
+// launched_kernels() says which.  The large-k kernel launches whenever a row
+// has k > 1024: it also takes the rows the two-pass kernel hands back.
+constexpr int kTimedKernels = 9;
 inline unsigned launched_kernels(const LaunchArgs &a) {
   return (a.n_pf > 0 ? 1u : 0u) | (a.n_row > 0 ? 2u : 0u) | (a.n_chunk > 0 ? 12u : 0u) |
-         (a.n_large > 0 ? 16u : 0u) | (a.n_mid > 0 ? 32u : 0u) | (a.n_argmax > 0 ? 64u : 0u);
+         (a.n_large + a.n_lfast > 0 ? 16u : 0u) | (a.n_mid > 0 ? 32u : 0u) |
+         (a.n_argmax > 0 ? 64u : 0u) | (a.n_lfast > 0 ? 256u : 0u);
 }
 // Largest vocabulary of the GPU greedy route (byte offsets of a row stay
 // below 2^31).

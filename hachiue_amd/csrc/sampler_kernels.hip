@@ -43,6 +43,7 @@
 #include <hip/hip_ext.h>
 
 #include <float.h>
+#include <type_traits>
 #include <math.h>
 
 #include "hachiue_sampler.h"
@@ -3190,12 +3191,10 @@ __device__ __forceinline__ LargeLoc large_locate(const LargeRow &L, int mode, do
   return r;
 }
 
-__global__ __launch_bounds__(kLT) void large_kernel(LaunchArgs a, Workspace ws) {
-  extern __shared__ unsigned long long ldyn[];
-  LargeSmem &sm = *reinterpret_cast<LargeSmem *>(ldyn);
+// The general large-k path for one row: any k > 1024, min-p, candidate
+// outputs, and the rows the two-pass path below hands back.
+__device__ __forceinline__ void large_row(const LaunchArgs &a, const RowPlan &P, int row, LargeSmem &sm) {
   const int tid = threadIdx.x;
-  const int row = ws.large_list[blockIdx.x];
-  const RowPlan P = ws.plans[row];
   LargeRow L;
   L.rowp = a.logits + (int64_t)row * a.stride;
   L.V = a.vocab;
@@ -3415,6 +3414,609 @@ __global__ __launch_bounds__(kLT) void large_kernel(LaunchArgs a, Workspace ws) 
   if (tid == 0 && a.row_flags) a.row_flags[row] = flags;
 }
 
+// ---------------------------------------------------------------- large-k, two passes
+
+// Rows with k = vocab (topK = Infinity or >= vocab: no slot is ever evicted,
+// so the order is value descending, index ascending), no min-p and no
+// candidate outputs: the common form of "top-p only" sampling.  Two passes
+// over the row instead of the general path's four to six:
+//
+//  1. (HBM) m0 = the maximum of the first 32768 logits.  Every candidate
+//     v <= m0 adds w = 2^(q * -log2(e) / 256) to bucket floor(q) of an LDS
+//     histogram (binary64 sums), q = (m0 - v) * 256 / T in binary32 (one
+//     fma, shared by the bucket and the weight); the few v > m0 go to a list
+//     of their own.  m = max(m0, list), S = e^((m0 - m)/T) * sum + the
+//     list's exp((v - m)/T).
+//  2. From the buckets' cumulative probabilities the kernel picks the bucket
+//     range that holds the top-p crossing and the one that holds the draw
+//     (each widened where a bucket edge lies within kFEps of its target),
+//     streams the row once more gathering only the logits of those buckets,
+//     sorts them and walks them with exact probabilities
+//     f32(f32(exp((v - m)/T)) / S) from the bucket sums before them.
+//
+// q's binary32 roundings and the hardware exp2 leave each weight within a few
+// 1e-7 of exp((v - m0)/T), and the cumulative sums within about 1e-7 of the
+// reference's sequential ones: a position can differ from the reference's
+// only when its target lies that close to a cumulative boundary.  Rows the
+// histogram does not suit (a non-finite maximum or temperature, fewer than
+// two candidates, more than kFTop logits above m0, a crossing in the last
+// bucket or none, more than kFCap gathered logits) are handed back to
+// large_row.
+constexpr int kFT = 1024;             // threads per workgroup
+constexpr int kFB = 8192;             // buckets of 1/256 in (m0 - v) / T
+constexpr float kFBScale = 256.0f;
+constexpr int kFTop = 1024;           // logits above m0
+constexpr int kFSpan = 2048;          // buckets of one gathered range
+constexpr int kFCap = 2048;           // logits gathered for the walks
+constexpr double kFEps = 1e-6;        // margin around a bucket edge (probability)
+
+struct FastSmem {
+  double mass[kFB];
+  unsigned long long top[kFTop];
+  unsigned long long buf[kFCap];
+  double pb[kFCap];
+  double dred[kFT / 64];
+  unsigned long long ured[kFT / 64];
+  int ntop, nbuf, hit, flag;
+};
+
+size_t large_fast_smem_bytes() { return sizeof(FastSmem); }
+static_assert(kFT * 8 == kFB, "each thread owns eight buckets");
+
+// Bucket of a candidate v <= m0 from q = (m0 - v) * 256 / T, computed once
+// per logit with one rounding (fma): q never increases with v, so neither
+// does the bucket; clamped to the last bucket.
+__device__ __forceinline__ float fast_q(float v, float cz, float m0cz) { return fmaf(v, -cz, m0cz); }
+__device__ __forceinline__ int fast_bucket_q(float q) {
+  return (int)fminf(fmaxf(q, 0.0f), (float)(kFB - 1));
+}
+__device__ __forceinline__ int fast_bucket(float v, float cz, float m0cz) {
+  return fast_bucket_q(fast_q(v, cz, m0cz));
+}
+
+template <typename T>
+__device__ __forceinline__ T fast_block_sum(T x, T *red) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) x += __shfl_xor(x, m);
+  if (lane_id() == 0) red[threadIdx.x >> 6] = x;
+  __syncthreads();
+  T r = 0;
+  for (int w = 0; w < kFT / 64; ++w) r += red[w];
+  __syncthreads();
+  return r;
+}
+
+__device__ __forceinline__ float fast_block_max(float x, double *red) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const float y = __shfl_xor(x, m);
+    x = y > x ? y : x;
+  }
+  if (lane_id() == 0) red[threadIdx.x >> 6] = (double)x;
+  __syncthreads();
+  float r = -INFINITY;
+  for (int w = 0; w < kFT / 64; ++w) r = (float)red[w] > r ? (float)red[w] : r;
+  __syncthreads();
+  return r;
+}
+
+// In place, mass[b] becomes the sum of buckets 0..b.  Wave w owns buckets
+// [512 w, 512 w + 512), read 64 consecutive at a time (no bank conflicts).
+__device__ __forceinline__ void fast_prefix(FastSmem &sm) {
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  constexpr int per = kFB / (kFT / 64);
+  double carry = 0;
+#pragma unroll
+  for (int i = 0; i < per / 64; ++i) {
+    const int b = per * wave + 64 * i + lane;
+    const double c = wave_scan_incl_f64(sm.mass[b]) + carry;
+    sm.mass[b] = c;
+    carry = readlane_f64(c, 63);
+  }
+  if (lane == 0) sm.dred[wave] = carry;
+  __syncthreads();
+  double base = 0;
+  for (int w = 0; w < wave; ++w) base += sm.dred[w];
+#pragma unroll
+  for (int i = 0; i < per / 64; ++i) sm.mass[per * wave + 64 * i + lane] += base;
+  __syncthreads();
+}
+
+// The first bucket b (-1: the list above m0) whose cumulative probability
+// top_total + scale * mass[b] reaches x, kFB when none does.  Each wave
+// searches alone, 64 probes per round (8192 -> 128 -> 2 -> 1): no barrier.
+__device__ __forceinline__ int fast_first_reaching(double x, double top_total, double scale,
+                                                   const FastSmem &sm) {
+  if (top_total >= x) return -1;
+  const int lane = lane_id();
+  int base = 0, width = kFB;
+  while (width > 1) {
+    const int step = width >= 64 ? width / 64 : 1;
+    const int idx = base + (lane + 1) * step - 1;
+    const bool ok = lane * step < width && top_total + scale * sm.mass[idx] >= x;
+    const unsigned long long m = __ballot(ok);
+    if (!m) return width == kFB ? kFB : base + width;   // (the level above guarantees a hit)
+    base += __builtin_ctzll(m) * step;
+    width = step;
+  }
+  return base;
+}
+
+// The cumulative probability before bucket b (b = -1: 0).
+__device__ __forceinline__ double fast_start(int b, double top_total, double scale,
+                                             const FastSmem &sm) {
+  if (b < 0) return 0.0;
+  return top_total + (b > 0 ? scale * sm.mass[b - 1] : 0.0);
+}
+
+// Scratch of the walks, in the bucket array once the ranges are chosen.
+struct FastWalk {
+  double bsum[kFSpan];                 // exact probability per bucket of a range
+  uint32_t bcnt[kFSpan];               // logits per bucket of a range
+  unsigned long long one[kFCap];       // the logits of the located bucket
+  double pone[kFCap];                  // their probabilities, then cumulative sums
+  double ssum[16];                     // the located bucket in 16 parts: probability,
+  uint32_t scnt[16];                   //   logits
+  unsigned long long few[64];          // the logits of the located part
+  int res_id, res_pos;
+  double res_cum;
+};
+static_assert(sizeof(FastWalk) <= sizeof(double) * kFB, "the walks fit the bucket array");
+
+// Located position in a gathered range.
+struct FastLoc {
+  int id;          // logit index (-1: not found)
+  int pos;         // position within the range (logits of earlier buckets first)
+  double cum;      // cumulative probability through it
+};
+
+// Within the range of buckets [glo, ghi] (-1: the list above m0), whose
+// logits are among the nl gathered entries buf / pb (probabilities) and
+// whose cumulative probability before its first logit is c_start: the first
+// logit, in the reference's order (value descending, index ascending), whose
+// cumulative probability reaches `target`.  The probabilities are summed
+// exactly per bucket (binary64 sums of binary32 values), only the located
+// bucket's logits are sorted, and the walk through them is a block prefix sum.
+__device__ __forceinline__ FastLoc fast_locate(int glo, int ghi, double c_start, double target,
+                                               int nl, float cz, float m0cz, float m0, double md,
+                                               double it, double S, FastSmem &sm) {
+  FastWalk &w = *reinterpret_cast<FastWalk *>(sm.mass);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int span = ghi - glo + 1;
+  FastLoc r{-1, 0, 0.0};
+  for (int i = tid; i < span; i += kFT) { w.bsum[i] = 0.0; w.bcnt[i] = 0u; }
+  __syncthreads();
+  for (int i = tid; i < nl; i += kFT) {
+    const float v = key2f(cand_key(sm.buf[i]));
+    const int b = v > m0 ? -1 : fast_bucket(v, cz, m0cz);
+    if (b >= glo && b <= ghi) {
+      atomicAdd(&w.bsum[b - glo], sm.pb[i]);
+      atomicAdd(&w.bcnt[b - glo], 1u);
+    }
+  }
+  __syncthreads();
+  // exclusive prefix over the range's buckets: thread t owns buckets 2t, 2t+1
+  static_assert(2 * kFT == kFSpan, "two buckets per thread");
+  const double m0s = 2 * tid < span ? w.bsum[2 * tid] : 0.0;
+  const double m1s = 2 * tid + 1 < span ? w.bsum[2 * tid + 1] : 0.0;
+  const uint32_t n0 = 2 * tid < span ? w.bcnt[2 * tid] : 0u;
+  const uint32_t n1 = 2 * tid + 1 < span ? w.bcnt[2 * tid + 1] : 0u;
+  double cm = wave_scan_incl_f64(m0s + m1s);
+  uint32_t cn = n0 + n1;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t t = __shfl_up(cn, d);
+    if (lane >= d) cn += t;
+  }
+  if (lane == 63) { sm.dred[wave] = cm; sm.ured[wave] = cn; }
+  if (tid == 0) sm.hit = 0x7FFFFFFF;
+  __syncthreads();
+  double bm = c_start;
+  uint32_t bn = 0;
+  for (int q = 0; q < wave; ++q) { bm += sm.dred[q]; bn += (uint32_t)sm.ured[q]; }
+  const double e0 = bm + cm - (m0s + m1s);   // cumulative before bucket 2t
+  const uint32_t k0 = bn + cn - (n0 + n1);
+  if (2 * tid < span && n0 && e0 + m0s >= target) atomicMin(&sm.hit, 2 * tid);
+  else if (2 * tid + 1 < span && n1 && e0 + m0s + m1s >= target) atomicMin(&sm.hit, 2 * tid + 1);
+  __syncthreads();
+  const int lb = sm.hit;
+  if (lb >= span) { __syncthreads(); return r; }
+  // the located bucket's cumulative start and position, from its owner
+  if (tid == (lb >> 1)) {
+    sm.dred[0] = (lb & 1) ? e0 + m0s : e0;
+    sm.ured[0] = (lb & 1) ? k0 + n0 : k0;
+    sm.flag = (int)((lb & 1) ? n1 : n0);
+    sm.nbuf = 0;
+  }
+  __syncthreads();
+  const double cb = sm.dred[0];
+  const int kb = (int)sm.ured[0];
+  const int nb = sm.flag;
+  // its logits
+  const int bq = glo + lb;   // the bucket (-1: the list above m0)
+  for (int i = tid; i < nl; i += kFT) {
+    const float v = key2f(cand_key(sm.buf[i]));
+    const int b = v > m0 ? -1 : fast_bucket(v, cz, m0cz);
+    if (b == bq) w.one[atomicAdd(&sm.nbuf, 1)] = sm.buf[i];
+  }
+  if (tid < 16) { w.ssum[tid] = 0.0; w.scnt[tid] = 0u; }
+  if (tid == 0) w.res_id = -2;
+  __syncthreads();
+  auto prob = [&](unsigned long long c) {
+    return (double)(float)((double)(float)exp(((double)key2f(cand_key(c)) - md) * it) / S);
+  };
+  // A bucket of more than 64 logits is cut in 16 parts by (q - bq) * 16,
+  // clamped to [0, 15] (q - bq is exact, and the part never decreases as the
+  // value falls); when the part holding the target has at most 64 logits,
+  // one wave sorts and walks it.
+  double cs = cb;
+  int ks = kb, ns = nb;
+  const unsigned long long *few = w.one;
+  if (nb > 64 && bq >= 0) {
+    for (int i = tid; i < nb; i += kFT) {
+      const float q = fast_q(key2f(cand_key(w.one[i])), cz, m0cz);
+      const int part = (int)fminf(fmaxf((q - (float)bq) * 16.0f, 0.0f), 15.0f);
+      atomicAdd(&w.ssum[part], prob(w.one[i]));
+      atomicAdd(&w.scnt[part], 1u);
+    }
+    __syncthreads();
+    if (tid < 64) {
+      const double pm = lane < 16 ? w.ssum[lane] : 0.0;
+      const uint32_t pc = lane < 16 ? w.scnt[lane] : 0u;
+      const double incl = wave_scan_incl_f64(pm) + cb;
+      uint32_t ci = pc;
+#pragma unroll
+      for (int d = 1; d < 16; d <<= 1) {
+        const uint32_t t = __shfl_up(ci, d);
+        if (lane >= d) ci += t;
+      }
+      const unsigned long long hit = __ballot(lane < 16 && pc > 0 && incl >= target);
+      if (hit) {
+        const int L = __builtin_ctzll(hit);
+        if (lane == L) {
+          sm.dred[0] = incl - pm;
+          sm.ured[0] = kb + ci - pc;
+          sm.flag = (int)pc;
+          sm.hit = L;
+        }
+      } else if (lane == 0) {
+        sm.flag = -1;
+      }
+    }
+    __syncthreads();
+    if (sm.flag >= 0 && sm.flag <= 64) {
+      cs = sm.dred[0];
+      ks = (int)sm.ured[0];
+      ns = sm.flag;
+      const int L = sm.hit;
+      if (tid == 0) sm.nbuf = 0;
+      __syncthreads();
+      for (int i = tid; i < nb; i += kFT) {
+        const float q = fast_q(key2f(cand_key(w.one[i])), cz, m0cz);
+        if ((int)fminf(fmaxf((q - (float)bq) * 16.0f, 0.0f), 15.0f) == L)
+          w.few[atomicAdd(&sm.nbuf, 1)] = w.one[i];
+      }
+      few = w.few;
+    }
+    __syncthreads();
+  }
+  if (ns <= 64) {
+    // one wave: sort, probabilities, prefix sum from cs, first reaching target
+    if (tid < 64) {
+      unsigned long long x = lane < ns ? few[lane] : 0ull;
+      x = wave_sort_desc64(x);
+      const double c = wave_scan_incl_f64(lane < ns ? prob(x) : 0.0) + cs;
+      const unsigned long long hit = __ballot(lane < ns && c >= target);
+      if (hit) {
+        const int L = __builtin_ctzll(hit);
+        if (lane == L) {
+          w.res_id = (int)cand_idx(x);
+          w.res_pos = ks + L;
+          w.res_cum = c;
+        }
+      } else if (lane == 0) {
+        w.res_id = -1;
+      }
+    }
+    __syncthreads();
+    if (w.res_id >= 0) {
+      r.id = w.res_id;
+      r.pos = w.res_pos;
+      r.cum = w.res_cum;
+    }
+    __syncthreads();
+    return r;
+  }
+  int P2 = 1;
+  while (P2 < nb) P2 <<= 1;
+  for (int i = nb + tid; i < P2; i += kFT) w.one[i] = 0ull;
+  __syncthreads();
+  if (P2 <= 64) {
+    if (tid < 64) {
+      unsigned long long x = lane < P2 ? w.one[lane] : 0ull;
+      x = wave_sort_desc64(x);
+      if (lane < P2) w.one[lane] = x;
+    }
+    __syncthreads();
+  } else {
+    bitonic_reg<kFT, kFCap / kFT>(w.one, P2);
+  }
+  // their probabilities in sorted order (a function of the value alone)
+  for (int i = tid; i < nb; i += kFT) {
+    const float v = key2f(cand_key(w.one[i]));
+    w.pone[i] = (double)(float)((double)(float)exp(((double)v - md) * it) / S);
+  }
+  if (tid == 0) sm.hit = 0x7FFFFFFF;
+  __syncthreads();
+  double carry = cb;
+  for (int base = 0; base < nb; base += kFT) {
+    const int i = base + tid;
+    double c = wave_scan_incl_f64(i < nb ? w.pone[i] : 0.0);
+    if (lane == 63) sm.dred[wave] = c;
+    __syncthreads();
+    double add = carry, tot = carry;
+    for (int q = 0; q < kFT / 64; ++q) {
+      if (q < wave) add += sm.dred[q];
+      tot += sm.dred[q];
+    }
+    __syncthreads();
+    c += add;
+    if (i < nb && c >= target) atomicMin(&sm.hit, i);
+    if (i < nb) w.pone[i] = c;
+    carry = tot;
+  }
+  __syncthreads();
+  const int h = sm.hit;
+  if (h < nb) {
+    r.id = (int)cand_idx(w.one[h]);
+    r.pos = kb + h;
+    r.cum = w.pone[h];
+  }
+  __syncthreads();
+  return r;
+}
+
+// One row of the two-pass path; false (block-uniform) hands it back.
+__device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P, int row,
+                                           FastSmem &sm) {
+  constexpr int U = 8;   // float4 per thread per buffer; two buffers in flight
+  const int tid = threadIdx.x;
+  const float *rowp = a.logits + (int64_t)row * a.stride;
+  const int V = a.vocab;
+  const int nfull = V >> 2;
+  const rsrc_t r4 = make_rsrc(rowp, 16u * (uint32_t)nfull);
+  const int iters = (nfull + U * kFT - 1) / (U * kFT);
+  const double it = 1.0 / P.temperature;
+
+  for (int i = tid; i < kFB; i += kFT) sm.mass[i] = 0.0;
+  if (tid == 0) { sm.ntop = 0; sm.nbuf = 0; }
+
+  f32x4 A[U], B[U];
+  // pass 1 reads cached (pass 2 reads the row again), pass 2 non-temporal
+  auto load = [&](f32x4 (&t)[U], int c, auto policy) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(r4, (c * U * kFT + u * kFT + tid) * 16, 0,
+                                                           decltype(policy)::value);
+      t[u] = f32x4{__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]),
+                   __uint_as_float(x[3])};
+    }
+  };
+  using cached = std::integral_constant<int, 0>;
+  using nontemporal = std::integral_constant<int, kReadNT>;
+  // every read is unconditional (past the row a buffer read returns 0 and
+  // touches no memory), so the compiler keeps both buffers in flight
+  load(A, 0, cached{});
+  load(B, 1, cached{});
+  // m0: the largest of the first 4 U kFT logits (NaN is never > anything)
+  float mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (u * kFT + tid < nfull) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) mx = A[u][c] > mx ? A[u][c] : mx;
+    }
+  }
+  const float m0 = fast_block_max(mx, sm.dred);   // (its barriers order the clears above)
+  const float cz = (float)(it * (double)kFBScale);
+  const float m0cz = m0 * cz;
+  if (!(m0 > -INFINITY && m0 < INFINITY && cz > 0.0f && cz < INFINITY && m0cz > -INFINITY &&
+        m0cz < INFINITY))
+    return false;   // (uniform: every thread read the same values)
+  const float kq = -1.4426950408889634f / kFBScale;   // w = 2^(q kq) = e^((v - m0) / T)
+
+  // Per logit, without a branch: every one adds to some bucket (0 for those
+  // that do not belong: NaN, -Infinity, and the rare v > m0, which go to
+  // the list instead under one wave-uniform branch per float4).
+  uint32_t nf = 0;
+  auto add4 = [&](const f32x4 &t, int e) {
+    const bool up0 = t[0] > m0, up1 = t[1] > m0, up2 = t[2] > m0, up3 = t[3] > m0;
+    if (__builtin_expect(__any(up0 || up1 || up2 || up3), 0)) {
+      const bool up[4] = {up0, up1, up2, up3};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (up[c]) {
+          const int slot = atomicAdd(&sm.ntop, 1);
+          if (slot < kFTop) sm.top[slot] = pack_cand(f2key(t[c]), (uint32_t)(e + c));
+        }
+      }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float v = t[c];
+      const bool cand = v > -INFINITY;
+      nf += cand ? 1u : 0u;
+      const float q = fast_q(v, cz, m0cz);
+      const float w = __builtin_amdgcn_exp2f(q * kq);
+      atomicAdd(&sm.mass[fast_bucket_q(q)], (double)(cand && !(v > m0) ? w : 0.0f));
+    }
+  };
+  auto process = [&](const f32x4 (&t)[U], int c) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = c * U * kFT + u * kFT + tid;
+      if (i < nfull) add4(t[u], 4 * i);
+    }
+  };
+  for (int c = 0; c < iters; c += 2) {
+    process(A, c);
+    load(A, c + 2, cached{});
+    process(B, c + 1);   // (past the row: every element skipped)
+    load(B, c + 3, cached{});
+  }
+  if (tid < (V & 3)) {   // the logits past the last whole float4
+    const int e = 4 * nfull + tid;
+    const float v = rowp[e];
+    if (v > -INFINITY) {
+      ++nf;
+      if (v > m0) {
+        const int slot = atomicAdd(&sm.ntop, 1);
+        if (slot < kFTop) sm.top[slot] = pack_cand(f2key(v), (uint32_t)e);
+      } else {
+        const float q = fast_q(v, cz, m0cz);
+        atomicAdd(&sm.mass[fast_bucket_q(q)], (double)__builtin_amdgcn_exp2f(q * kq));
+      }
+    }
+  }
+  const uint32_t n_f = fast_block_sum(nf, reinterpret_cast<uint32_t *>(sm.ured));
+  const int ntop = sm.ntop;
+  if (n_f <= 1 || ntop > kFTop) return false;
+
+  // the maximum, S, and the exact probabilities of the list above m0
+  float tmx = m0;
+  for (int i = tid; i < ntop; i += kFT) {
+    const float v = key2f(cand_key(sm.top[i]));
+    tmx = v > tmx ? v : tmx;
+  }
+  const float m = fast_block_max(tmx, sm.dred);
+  const double md = (double)m;
+  const double R = exp(((double)m0 - md) * it);
+  fast_prefix(sm);
+  double st = 0;
+  for (int i = tid; i < ntop; i += kFT) st += exp(((double)key2f(cand_key(sm.top[i])) - md) * it);
+  const double S = R * sm.mass[kFB - 1] + fast_block_sum(st, sm.dred);
+  if (!(S > 0.0 && S < INFINITY)) return false;
+  // the list's probabilities as the reference rounds them
+  double tt = 0;
+  for (int i = tid; i < ntop; i += kFT)
+    tt += (double)(float)((double)(float)exp(((double)key2f(cand_key(sm.top[i])) - md) * it) / S);
+  const double top_total = fast_block_sum(tt, sm.dred);
+  const double scale = R / S;   // bucket sum -> probability
+
+  // 3. the bucket ranges of the top-p crossing and of the draw
+  const double tp = P.top_p;
+  const int b1lo = fast_first_reaching(tp - kFEps, top_total, scale, sm);
+  const int b1hi = fast_first_reaching(tp + kFEps, top_total, scale, sm);
+  if (!(tp == tp) || b1hi >= kFB - 1) return false;   // no crossing, or in the clamped tail
+  const double u = a.uniforms[row];
+  const double k_hi = fast_start(b1hi + 1, top_total, scale, sm) + kFEps;
+  const double r_lo = u * (tp > 0.0 ? tp : 0.0) - 2 * kFEps;
+  const double r_hi = u * k_hi + kFEps;
+  if (!(r_lo == r_lo) || !(r_hi == r_hi)) return false;
+  int b2lo = fast_first_reaching(r_lo, top_total, scale, sm);
+  int b2hi = fast_first_reaching(r_hi, top_total, scale, sm);
+  b2lo = b2lo < b1hi ? b2lo : b1hi;
+  b2hi = b2hi < b1hi ? b2hi : b1hi;
+  // range 0 holds the crossing, range 1 (above it, when apart) the draw;
+  // ranges that touch become one, whose walks then share one cumulative sum
+  int g0lo = b1lo, g0hi = b1hi, g1lo = b2lo, g1hi = b2hi;
+  const bool two = b2hi < b1lo - 1;
+  if (!two) { g0lo = b2lo < b1lo ? b2lo : b1lo; g1lo = 0; g1hi = -2; }
+
+  // 4. gather the ranges' logits (the list above m0 joins them all).  This
+  // is the row's last read: non-temporal.
+  uint32_t below0 = 0;   // candidates v <= m0 in buckets before g0lo
+  auto gather = [&](float v, int e) {
+    if (!(v > -INFINITY) || v > m0) return;
+    const int b = fast_bucket(v, cz, m0cz);
+    below0 += b < g0lo;
+    if ((b >= g0lo && b <= g0hi) || (b >= g1lo && b <= g1hi)) {
+      const int slot = atomicAdd(&sm.nbuf, 1);
+      if (slot < kFCap) sm.buf[slot] = pack_cand(f2key(v), (uint32_t)e);
+    }
+  };
+  auto scan = [&](const f32x4 (&t)[U], int c) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = c * U * kFT + u * kFT + tid;
+      if (i < nfull) {
+        gather(t[u][0], 4 * i); gather(t[u][1], 4 * i + 1); gather(t[u][2], 4 * i + 2);
+        gather(t[u][3], 4 * i + 3);
+      }
+    }
+  };
+  load(A, 0, nontemporal{});
+  load(B, 1, nontemporal{});
+  for (int c = 0; c < iters; c += 2) {
+    scan(A, c);
+    load(A, c + 2, nontemporal{});
+    scan(B, c + 1);
+    load(B, c + 3, nontemporal{});
+  }
+  if (tid < (V & 3)) gather(rowp[4 * nfull + tid], 4 * nfull + tid);
+  const uint32_t below = fast_block_sum(below0, reinterpret_cast<uint32_t *>(sm.ured));
+  const int ng = sm.nbuf;
+  const int nl = ng + ntop;
+  if (nl > kFCap || g0hi - g0lo + 1 > kFSpan || g1hi - g1lo + 1 > kFSpan) return false;
+  for (int i = tid; i < ntop; i += kFT) sm.buf[ng + i] = sm.top[i];
+  __syncthreads();
+  // the gathered logits' probabilities as the reference rounds them
+  for (int i = tid; i < nl; i += kFT) {
+    const float v = key2f(cand_key(sm.buf[i]));
+    sm.pb[i] = (double)(float)((double)(float)exp(((double)v - md) * it) / S);
+  }
+  // the ranges' cumulative starts, read before the walks reuse the buckets
+  const double c0 = fast_start(g0lo, top_total, scale, sm);
+  const double c1 = two ? fast_start(g1lo, top_total, scale, sm) : 0.0;
+  __syncthreads();
+
+  // 5. src/sampler.ts:93-117 on the gathered ranges: the top-p crossing
+  // (keptSum = cumProb through it), then the draw r = u keptSum
+  const FastLoc l1 = fast_locate(g0lo, g0hi, c0, tp, nl, cz, m0cz, m0, md, it, S, sm);
+  if (l1.id < 0) return false;
+  const double r = u * l1.cum;
+  if (!(r == r)) return false;
+  const FastLoc l2 = two ? fast_locate(g1lo, g1hi, c1, r, nl, cz, m0cz, m0, md, it, S, sm)
+                         : fast_locate(g0lo, g0hi, c0, r, nl, cz, m0cz, m0, md, it, S, sm);
+  if (l2.id < 0) return false;
+  const int pos1 = (g0lo < 0 ? 0 : ntop + (int)below) + l1.pos;
+  if (tid == 0) {
+    put_token(a, row, l2.id);
+    if (a.cand_count_out) a.cand_count_out[row] = (int)n_f;
+    if (a.cutoff_out) a.cutoff_out[row] = pos1 + 1;
+    if (a.row_flags) a.row_flags[row] = HS_ROW_LARGE | HS_ROW_TWO_PASS;
+  }
+  return true;
+}
+
+// Rows of lfast_list; a row it cannot finish is marked in large_retry for
+// large_kernel.  Unaligned rows and calls that want candidate outputs are
+// all handed back.  Four waves per SIMD: two workgroups per CU.
+__global__ __launch_bounds__(kFT, 4) void large_fast_kernel(LaunchArgs a, Workspace ws) {
+  extern __shared__ unsigned long long ldyn[];
+  const int row = ws.lfast_list[blockIdx.x];
+  const RowPlan P = ws.plans[row];
+  const bool ok = a.vec && !a.want_cands && a.vocab < (1 << 26) &&
+                  large_fast(a, P, row, *reinterpret_cast<FastSmem *>(ldyn));
+  if (threadIdx.x == 0) ws.large_retry[blockIdx.x] = ok ? 0 : 1;
+}
+
+// Rows of large_list (blocks [0, n_large)), then the rows large_fast_kernel
+// handed back (block n_large + i takes lfast_list[i] when large_retry[i]).
+__global__ __launch_bounds__(kLT) void large_kernel(LaunchArgs a, Workspace ws) {
+  extern __shared__ unsigned long long ldyn[];
+  int row;
+  if ((int)blockIdx.x < a.n_large) {
+    row = ws.large_list[blockIdx.x];
+  } else {
+    const int i = (int)blockIdx.x - a.n_large;
+    if (!ws.large_retry[i]) return;
+    row = ws.lfast_list[i];
+  }
+  const RowPlan P = ws.plans[row];
+  large_row(a, P, row, *reinterpret_cast<LargeSmem *>(ldyn));
+}
+
 // ---------------------------------------------------------------- GPU greedy route
 
 // The engine sends greedy decoding without a repetition penalty
@@ -3566,6 +4168,10 @@ hipError_t prepare_kernels() {
                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)finalize_smem_bytes())) != hipSuccess)
     return e;
+  if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&large_fast_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)large_fast_smem_bytes())) != hipSuccess)
+    return e;
   return hipFuncSetAttribute(reinterpret_cast<const void *>(&large_kernel),
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)large_smem_bytes());
 }
@@ -3643,8 +4249,8 @@ hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t s
                          hipEvent_t *ev, hipEvent_t done) {
   hipError_t e;
   // the last kernel of the call records `done`
-  const int last = a.n_argmax > 0 ? 6 : a.n_large > 0 ? 4 : a.n_chunk > 0 ? 3 : a.n_mid > 0 ? 5
-                 : a.n_row > 0 ? 1 : 0;
+  const int last = a.n_argmax > 0 ? 6 : a.n_large + a.n_lfast > 0 ? 4 : a.n_chunk > 0 ? 3
+                 : a.n_mid > 0 ? 5 : a.n_row > 0 ? 1 : 0;
   auto dn = [&](int slot) { return slot == last ? done : nullptr; };
   if (a.n_pf > 0) {
     e = launch_one(pen_kernel, dim3((unsigned)a.n_pf), dim3(kPenThreads), pen_smem_bytes(),
@@ -3681,9 +4287,14 @@ hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t s
                    finalize_smem_bytes(), stream, ev, 3, dn(3), a, ws);
     if (e != hipSuccess) return e;
   }
-  if (a.n_large > 0) {
-    e = launch_one(large_kernel, dim3((unsigned)a.n_large), dim3(kLT), large_smem_bytes(), stream,
-                   ev, 4, dn(4), a, ws);
+  if (a.n_lfast > 0) {
+    e = launch_one(large_fast_kernel, dim3((unsigned)a.n_lfast), dim3(kFT), large_fast_smem_bytes(),
+                   stream, ev, 8, dn(8), a, ws);
+    if (e != hipSuccess) return e;
+  }
+  if (a.n_large + a.n_lfast > 0) {
+    e = launch_one(large_kernel, dim3((unsigned)(a.n_large + a.n_lfast)), dim3(kLT),
+                   large_smem_bytes(), stream, ev, 4, dn(4), a, ws);
     if (e != hipSuccess) return e;
   }
   if (a.n_argmax > 0) {

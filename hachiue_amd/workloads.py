@@ -26,6 +26,9 @@ its distributions.
 """
 from __future__ import annotations
 
+import os
+from concurrent.futures import ThreadPoolExecutor
+
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -135,7 +138,13 @@ def make(name: str, seed: int = 0, rows: int | None = None, vocab: int | None = 
         R = rows or 1024
         V = vocab or V_QWEN
         u = rng.random((R, V))
-        logits = (-np.log(-np.log(u))).astype(np.float32)
+        logits = np.empty((R, V), np.float32)
+
+        def gumbel(a: int) -> None:   # row blocks in threads (numpy's log releases the GIL)
+            logits[a:a + 64] = -np.log(-np.log(u[a:a + 64]))
+        with ThreadPoolExecutor(max_workers=min(16, os.cpu_count() or 1)) as ex:
+            list(ex.map(gumbel, range(0, R, 64)))
+        del u
         hists = None
         configs = [dict(temperature=1.0, topK=float("inf"), topP=0.98) for _ in range(R)]
     elif name == "v262k512":

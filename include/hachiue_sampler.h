@@ -67,6 +67,9 @@ typedef struct hs_sample_config {
                                     replay at that size; token is -1 */
 #define HS_ROW_LARGE       0x20u /* top-k > 1024 path: binary64 sums in another order
                                     than the reference's (probabilities within 1e-5) */
+#define HS_ROW_TWO_PASS    0x40u /* with HS_ROW_LARGE: a top-k = vocab row finished by
+                                    the two-pass kernel (bucketed probability mass,
+                                    exact walk of the buckets at the cutoff and draw) */
 
 typedef struct hs_context hs_context;
 
@@ -238,7 +241,8 @@ int hs_decode_step_device(hs_context *ctx, float *d_logits, int32_t rows,
  * recorded calls, writes the summed device milliseconds per kernel
  * (ms[0] presence/frequency pre-pass, ms[1] row kernel, ms[2] chunk kernel,
  * ms[3] finalize, ms[4] large-k kernel, ms[5] mid-k kernel, ms[6] greedy-route
- * argmax, ms[7] lm_head GEMV; a kernel a call did not launch adds 0)
+ * argmax, ms[7] lm_head GEMV, ms[8] two-pass large-k kernel; a kernel a call
+ * did not launch adds 0)
  * and the number of
  * timed calls, and resets the totals. */
 int hs_context_set_timing(hs_context *ctx, int enable);

@@ -221,12 +221,18 @@ class BatchResult:
 
 def sample_batch(logits: np.ndarray, vocab: int, hist_ids: np.ndarray | None,
                  hist_off: np.ndarray | None, cfgs: list[dict] | dict,
-                 u: np.ndarray, method: int = HEAP, cap: int = 0) -> BatchResult:
-    """Row-by-row oracle over a [rows, stride] float32 batch (mutated in place)."""
+                 u: np.ndarray, method: int = HEAP, cap: int = 0,
+                 threads: int | None = None) -> BatchResult:
+    """Row-by-row oracle over a [rows, stride] float32 batch (mutated in place).
+    Large batches run in blocks of rows on `threads` threads (the C call
+    releases the GIL); the rows are independent, so the result is the same."""
     assert logits.dtype == np.float32 and logits.ndim == 2 and logits.flags.c_contiguous
     rows, stride = logits.shape
     if isinstance(cfgs, dict) or cfgs is None:
         cfgs = [cfgs] * rows
+    threads = min(16, os.cpu_count() or 1) if threads is None else threads
+    if threads > 1 and rows >= 32:
+        return _sample_blocks(logits, vocab, hist_ids, hist_off, cfgs, u, method, cap, threads)
     carr = (OrcConfig * rows)(*[make_config(c) for c in cfgs])
     u = np.ascontiguousarray(u, dtype=np.float64)
     res = (OrcResult * rows)()
@@ -248,6 +254,31 @@ def sample_batch(logits: np.ndarray, vocab: int, hist_ids: np.ndarray | None,
     return BatchResult(g("token").astype(np.int32), g("path"), g("n"), g("cutoff"),
                        g("draw_index"), g("draw_margin"), g("topp_margin"),
                        ids, vals, probs)
+
+
+def _sample_blocks(logits, vocab, hist_ids, hist_off, cfgs, u, method, cap, threads):
+    from concurrent.futures import ThreadPoolExecutor
+    rows = logits.shape[0]
+    u = np.ascontiguousarray(u, dtype=np.float64)
+    step = max(8, -(-rows // (4 * threads)))
+    blocks = [(a, min(rows, a + step)) for a in range(0, rows, step)]
+
+    def one(ab):
+        a, b = ab
+        ids = off = None
+        if hist_ids is not None:
+            o = np.asarray(hist_off, np.int64)
+            ids = np.ascontiguousarray(hist_ids[o[a]:o[b]], dtype=np.int32)
+            off = o[a:b + 1] - o[a]
+        return sample_batch(logits[a:b], vocab, ids, off, cfgs[a:b], u[a:b], method, cap,
+                            threads=1)
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        parts = list(ex.map(one, blocks))
+    cat = lambda f: np.concatenate([getattr(p, f) for p in parts])  # noqa: E731
+    return BatchResult(cat("token"), cat("path"), cat("n"), cat("cutoff"), cat("draw_index"),
+                       cat("draw_margin"), cat("topp_margin"),
+                       cat("cand_ids") if cap else None, cat("cand_vals") if cap else None,
+                       cat("cand_probs") if cap else None)
 
 
 def topk_slots(logits: np.ndarray, vocab: int, k: int, method: int = LITERAL):

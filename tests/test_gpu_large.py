@@ -14,11 +14,19 @@ pytestmark = pytest.mark.gpu
 
 HS_ROW_UNSUPPORTED = 0x10
 HS_ROW_LARGE = 0x20
+HS_ROW_TWO_PASS = 0x40
 
 
-def _check(sampler, logits, vocab, hist_ids, hist_off, configs, uniforms, cap, label):
-    got = run_gpu(sampler, logits, vocab, hist_ids, hist_off, configs, uniforms, cap)
+def _check(sampler, logits, vocab, hist_ids, hist_off, configs, uniforms, cap, label,
+           want_cands=True):
+    """want_cands=False asks for tokens, counts and cutoffs only: rows with
+    k = vocab and no min-p then take the two-pass kernel."""
+    got = run_gpu(sampler, logits, vocab, hist_ids, hist_off, configs, uniforms, cap,
+                  want_cands=want_cands)
     want, want_logits = run_oracle(logits, vocab, hist_ids, hist_off, configs, uniforms, cap)
+    if not want_cands:
+        compare(got, want, want_logits, configs, vocab, cap, label + " (tokens only)")
+        return got, want
     unsupported = (got.flags & HS_ROW_UNSUPPORTED) != 0
     for r in np.flatnonzero(unsupported):
         m = min(int(want.n[r]), cap)
@@ -44,6 +52,54 @@ def test_gumbel_k_vocab(sampler):
     assert not (got.flags & HS_ROW_UNSUPPORTED).any()
 
 
+def test_gumbel_full_batch_two_pass(sampler):
+    """The 1024-row Gumbel workload at full size (k = vocab, top-p 0.98):
+    every row through the two-pass kernel, tokens against the oracle."""
+    wl = workloads.make("gumbel1024", 0)
+    got, want = _check(sampler, wl.logits, wl.vocab, None, None, wl.configs, wl.uniforms, 64,
+                       "gumbel 1024 x V", want_cands=False)
+    two = (got.flags & HS_ROW_TWO_PASS) != 0
+    print(f"[large] two-pass rows {int(two.sum())}/{two.size}; tokens equal "
+          f"{int((got.tokens == want.token).sum())}, oracle draw margins < 1e-6: "
+          f"{int((want.draw_margin < 1e-6).sum())}")
+    assert two.mean() > 0.99
+
+
+@pytest.mark.parametrize("name", ["gumbel", "normal", "low_t", "high_t", "penalised"])
+def test_two_pass_distributions(sampler, name):
+    """The two-pass kernel over other logit shapes and temperatures, with
+    rows it must hand back (sorted ascending, so nearly every logit lies
+    above the first chunk's maximum) mixed in."""
+    rng = np.random.default_rng(len(name))
+    rows, vocab = 40, 151936
+    hist_ids = hist_off = None
+    if name == "gumbel":
+        logits = rng.gumbel(size=(rows, vocab)).astype(np.float32)
+        cfg = dict(temperature=1.0, topK=float("inf"), topP=0.9)
+    elif name == "normal":
+        logits = (rng.standard_normal((rows, vocab)) * 2.5).astype(np.float32)
+        cfg = dict(temperature=0.8, topK=float("inf"), topP=0.95)
+    elif name == "low_t":
+        logits = (rng.standard_normal((rows, vocab)) * 3).astype(np.float32)
+        cfg = dict(temperature=0.3, topK=vocab, topP=0.9)
+    elif name == "high_t":
+        logits = rng.gumbel(size=(rows, vocab)).astype(np.float32)
+        cfg = dict(temperature=1.5, topK=float("inf"), topP=0.99)
+    else:
+        wl = workloads.make("v262k512", 4, rows=rows, vocab=vocab)
+        logits, hist_ids, hist_off = wl.logits, wl.hist_ids, wl.hist_off
+        cfg = dict(temperature=0.9, topK=float("inf"), topP=0.9, repetitionPenalty=1.15,
+                   presencePenalty=0.4, frequencyPenalty=0.2)
+    logits[3] = np.sort(logits[3])                 # handed back: rises past the first chunk
+    logits[5, :1000] = -np.inf                     # a masked prefix
+    u = rng.random(rows)
+    u[7] = 0.0
+    got, _ = _check(sampler, logits, vocab, hist_ids, hist_off, [cfg] * rows, u, 64,
+                    f"two-pass {name}", want_cands=False)
+    assert (got.flags[[r for r in range(rows) if r != 3]] & HS_ROW_TWO_PASS).all()
+    assert not got.flags[3] & HS_ROW_TWO_PASS
+
+
 def test_partial_large_k(sampler):
     rng = np.random.default_rng(11)
     rows, vocab = 24, 151936
@@ -67,6 +123,7 @@ def test_large_equal_logits(sampler):
                dict(temperature=1.0, topK=5000.0, topP=0.95)]
     u = np.array([0.25, 0.5, 0.75, 0.999])
     _check(sampler, logits, vocab, None, None, configs, u, 64, "equal logits")
+    _check(sampler, logits, vocab, None, None, configs, u, 64, "equal logits", want_cands=False)
 
 
 def test_large_non_finite(sampler):
@@ -81,6 +138,7 @@ def test_large_non_finite(sampler):
     configs = [dict(temperature=1.0, topK=float("inf"), topP=0.9) for _ in range(rows)]
     u = np.array([0.3, 0.6, 0.9, 0.1])
     _check(sampler, logits, vocab, None, None, configs, u, 64, "non-finite")
+    _check(sampler, logits, vocab, None, None, configs, u, 64, "non-finite", want_cands=False)
 
 
 def test_large_with_penalties(sampler):
@@ -89,6 +147,8 @@ def test_large_with_penalties(sampler):
     configs[0] = dict(temperature=0.9, topK=2048, topP=0.9, repetitionPenalty=1.15)
     _check(sampler, wl.logits, wl.vocab, wl.hist_ids, wl.hist_off, configs, wl.uniforms, 64,
            "large k + penalties")
+    _check(sampler, wl.logits, wl.vocab, wl.hist_ids, wl.hist_off, configs, wl.uniforms, 64,
+           "large k + penalties", want_cands=False)
 
 
 def test_min_p_and_top_p_edges_large(sampler):
@@ -103,3 +163,5 @@ def test_min_p_and_top_p_edges_large(sampler):
                dict(temperature=50.0, topK=float("inf"), topP=0.3)]
     u = np.array([0.5, 0.0, 0.7, 0.999999, 0.4, 0.2])
     _check(sampler, logits, vocab, None, None, configs, u, 64, "min-p / top-p edges")
+    _check(sampler, logits, vocab, None, None, configs, u, 64, "min-p / top-p edges",
+           want_cands=False)
