@@ -3457,6 +3457,7 @@ struct FastSmem {
   double pb[kFCap];
   double dred[kFT / 64];
   unsigned long long ured[kFT / 64];
+  double top_m, top_s;                 // the list's maximum and exp sum
   int ntop, nbuf, hit, flag;
 };
 
@@ -3779,7 +3780,7 @@ __device__ __forceinline__ FastLoc fast_locate(int glo, int ghi, double c_start,
 // One row of the two-pass path; false (block-uniform) hands it back.
 __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P, int row,
                                            FastSmem &sm) {
-  constexpr int U = 8;   // float4 per thread per buffer; two buffers in flight
+  constexpr int U = 4;   // float4 per thread per buffer; two buffers in flight
   const int tid = threadIdx.x;
   const float *rowp = a.logits + (int64_t)row * a.stride;
   const int V = a.vocab;
@@ -3788,6 +3789,10 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
   const int iters = (nfull + U * kFT - 1) / (U * kFT);
   const double it = 1.0 / P.temperature;
 
+  // the only plain loads (before the buffer reads: a wait for a later load
+  // would wait for every read before it)
+  const double u = a.uniforms[row];
+  const float vtail = tid < (V & 3) ? rowp[4 * nfull + tid] : -INFINITY;
   for (int i = tid; i < kFB; i += kFT) sm.mass[i] = 0.0;
   if (tid == 0) { sm.ntop = 0; sm.nbuf = 0; }
 
@@ -3864,9 +3869,12 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
     process(B, c + 1);   // (past the row: every element skipped)
     load(B, c + 3, cached{});
   }
+  // pass 2's first reads go out now, under the analysis below
+  load(A, 0, nontemporal{});
+  load(B, 1, nontemporal{});
   if (tid < (V & 3)) {   // the logits past the last whole float4
     const int e = 4 * nfull + tid;
-    const float v = rowp[e];
+    const float v = vtail;
     if (v > -INFINITY) {
       ++nf;
       if (v > m0) {
@@ -3882,25 +3890,34 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
   const int ntop = sm.ntop;
   if (n_f <= 1 || ntop > kFTop) return false;
 
-  // the maximum, S, and the exact probabilities of the list above m0
-  float tmx = m0;
-  for (int i = tid; i < ntop; i += kFT) {
-    const float v = key2f(cand_key(sm.top[i]));
-    tmx = v > tmx ? v : tmx;
+  // the maximum and S.  The list above m0 is short: one wave scans it.
+  if (tid < 64) {
+    float tmx = m0;
+    for (int i = tid; i < ntop; i += 64) {
+      const float v = key2f(cand_key(sm.top[i]));
+      tmx = v > tmx ? v : tmx;
+    }
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) {
+      const float y = __shfl_xor(tmx, d);
+      tmx = y > tmx ? y : tmx;
+    }
+    const double mdw = (double)tmx;
+    double st = 0;
+    for (int i = tid; i < ntop; i += 64) st += exp(((double)key2f(cand_key(sm.top[i])) - mdw) * it);
+#pragma unroll
+    for (int d = 32; d > 0; d >>= 1) st += __shfl_xor(st, d);
+    if (tid == 0) { sm.top_m = mdw; sm.top_s = st; }
   }
-  const float m = fast_block_max(tmx, sm.dred);
+  fast_prefix(sm);   // (its barriers publish top_m, top_s)
+  const float m = (float)sm.top_m;
   const double md = (double)m;
   const double R = exp(((double)m0 - md) * it);
-  fast_prefix(sm);
-  double st = 0;
-  for (int i = tid; i < ntop; i += kFT) st += exp(((double)key2f(cand_key(sm.top[i])) - md) * it);
-  const double S = R * sm.mass[kFB - 1] + fast_block_sum(st, sm.dred);
+  const double S = R * sm.mass[kFB - 1] + sm.top_s;
+  // the list's probability mass (its own probabilities differ from these
+  // binary64 quotients by their binary32 roundings only)
+  const double top_total = sm.top_s / S;
   if (!(S > 0.0 && S < INFINITY)) return false;
-  // the list's probabilities as the reference rounds them
-  double tt = 0;
-  for (int i = tid; i < ntop; i += kFT)
-    tt += (double)(float)((double)(float)exp(((double)key2f(cand_key(sm.top[i])) - md) * it) / S);
-  const double top_total = fast_block_sum(tt, sm.dred);
   const double scale = R / S;   // bucket sum -> probability
 
   // 3. the bucket ranges of the top-p crossing and of the draw
@@ -3908,7 +3925,6 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
   const int b1lo = fast_first_reaching(tp - kFEps, top_total, scale, sm);
   const int b1hi = fast_first_reaching(tp + kFEps, top_total, scale, sm);
   if (!(tp == tp) || b1hi >= kFB - 1) return false;   // no crossing, or in the clamped tail
-  const double u = a.uniforms[row];
   const double k_hi = fast_start(b1hi + 1, top_total, scale, sm) + kFEps;
   const double r_lo = u * (tp > 0.0 ? tp : 0.0) - 2 * kFEps;
   const double r_hi = u * k_hi + kFEps;
@@ -3945,15 +3961,13 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
       }
     }
   };
-  load(A, 0, nontemporal{});
-  load(B, 1, nontemporal{});
   for (int c = 0; c < iters; c += 2) {
     scan(A, c);
     load(A, c + 2, nontemporal{});
     scan(B, c + 1);
     load(B, c + 3, nontemporal{});
   }
-  if (tid < (V & 3)) gather(rowp[4 * nfull + tid], 4 * nfull + tid);
+  if (tid < (V & 3)) gather(vtail, 4 * nfull + tid);
   const uint32_t below = fast_block_sum(below0, reinterpret_cast<uint32_t *>(sm.ured));
   const int ng = sm.nbuf;
   const int nl = ng + ntop;
