@@ -130,6 +130,9 @@ struct hs_context {
   bool plan_pending = false;
   // host entry points
   DevBuf h_logits, h_hist, h_off, h_u, h_tok;
+  DevBuf h_gidx, h_gval;          // the penalised entries copied back
+  std::vector<int64_t> gidx;      // their offsets in the logits block
+  std::vector<float> gval;
   hipStream_t stream = nullptr;
   // per-kernel timing diagnostics
   bool timing = false;
@@ -936,6 +939,8 @@ int hs_context_destroy(hs_context *ctx) {
     ctx->h_off.release();
     ctx->h_u.release();
     ctx->h_tok.release();
+    ctx->h_gidx.release();
+    ctx->h_gval.release();
     if (ctx->plan_staging) (void)hipHostFree(ctx->plan_staging);
     if (ctx->plan_done) (void)hipEventDestroy(ctx->plan_done);
     if (ctx->done_ev) (void)hipEventDestroy(ctx->done_ev);
@@ -1127,14 +1132,48 @@ int hs_sample_logits_batch(hs_context *ctx, float *logits, int32_t rows, int64_t
     (void)hipStreamSynchronize(st);
     return rc;
   }
-  bool penalised = false;
-  for (int r = 0; r < rows && !penalised; ++r)
-    penalised = configs[r].repetition_penalty != 1.0 || configs[r].presence_penalty != 0.0 ||
-                configs[r].frequency_penalty != 0.0;
+  // The reference writes the penalised values back (src/sampler.ts:30).
+  // Only history ids change: the last 128 of a row for the repetition
+  // penalty, all of them with presence / frequency.  Those entries are
+  // gathered on the device and copied back, not the whole block.
+  try {
+    ctx->gidx.clear();
+    for (int r = 0; r < rows && hist_offsets; ++r) {
+      const hs_sample_config &c = configs[r];
+      const bool rep = c.repetition_penalty != 1.0;
+      const bool pf = c.presence_penalty != 0.0 || c.frequency_penalty != 0.0;
+      if (!(rep || pf)) continue;
+      const int64_t h1 = hist_offsets[r + 1];
+      const int64_t h0 = pf ? hist_offsets[r] : std::max(hist_offsets[r], h1 - 128);
+      for (int64_t j = h0; j < h1; ++j) {
+        const int32_t id = hist_ids[j];
+        if (id >= 0 && id < vocab) ctx->gidx.push_back((int64_t)r * row_stride + id);
+      }
+    }
+    ctx->gval.resize(ctx->gidx.size());
+  } catch (const std::bad_alloc &) {
+    (void)hipStreamSynchronize(st);
+    return fail(HS_ERR_OUT_OF_MEMORY, "host allocation failed");
+  }
+  const int64_t ng = (int64_t)ctx->gidx.size();
   HS_HIP(hipMemcpyAsync(tokens_out, ctx->h_tok.p, sizeof(int32_t) * rows, hipMemcpyDeviceToHost, st));
-  if (penalised)   // the reference writes penalised values back (src/sampler.ts:30)
-    HS_HIP(hipMemcpyAsync(logits, ctx->h_logits.p, lbytes, hipMemcpyDeviceToHost, st));
+  if (ng > 0) {
+    HS_HIP(ctx->h_gidx.ensure(sizeof(int64_t) * (size_t)ng));
+    HS_HIP(ctx->h_gval.ensure(sizeof(float) * (size_t)ng));
+    HS_HIP(hipMemcpyAsync(ctx->h_gidx.p, ctx->gidx.data(), sizeof(int64_t) * (size_t)ng,
+                          hipMemcpyHostToDevice, st));
+    const hipError_t e = hs::launch_gather_f32(static_cast<const float *>(ctx->h_logits.p),
+                                               static_cast<const int64_t *>(ctx->h_gidx.p),
+                                               static_cast<float *>(ctx->h_gval.p), ng, st);
+    if (e != hipSuccess) {
+      (void)hipStreamSynchronize(st);
+      return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+    }
+    HS_HIP(hipMemcpyAsync(ctx->gval.data(), ctx->h_gval.p, sizeof(float) * (size_t)ng,
+                          hipMemcpyDeviceToHost, st));
+  }
   HS_HIP(hipStreamSynchronize(st));
+  for (int64_t i = 0; i < ng; ++i) logits[ctx->gidx[i]] = ctx->gval[i];
   for (int r = 0; r < rows; ++r)
     if (tokens_out[r] < 0)
       return fail(HS_ERR_UNSUPPORTED,

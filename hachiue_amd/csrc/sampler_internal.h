@@ -219,6 +219,8 @@ struct DecodeArgs {
 constexpr int kMaxStopIds = 1024;
 hipError_t launch_decode_append(const DecodeArgs &d, hipStream_t stream);
 hipError_t launch_fill_u32(uint32_t *p, int64_t n, uint32_t v, hipStream_t stream);
+hipError_t launch_gather_f32(const float *src, const int64_t *idx, float *dst, int64_t n,
+                             hipStream_t stream);
 // `done`, when not null and `ev` is null, is recorded at the end of the
 // call's last kernel (hipExtLaunchKernelGGL's stop event: no marker packet).
 hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t stream,

@@ -4238,6 +4238,22 @@ __global__ __launch_bounds__(256) void decode_append_kernel(DecodeArgs d) {
   d.len[r] = len + 1;
 }
 
+// dst[i] = src[idx[i]] for i < n: the penalised logits a host call copies
+// back, instead of whole rows.
+__global__ __launch_bounds__(256) void gather_f32_kernel(const float *src, const int64_t *idx,
+                                                         float *dst, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src[idx[i]];
+}
+
+hipError_t launch_gather_f32(const float *src, const int64_t *idx, float *dst, int64_t n,
+                             hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                     src, idx, dst, n);
+  return hipGetLastError();
+}
+
 // Sets n words to v: a kernel, not hipMemsetAsync, so that a caller may
 // capture it in a graph.
 __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t *p, int64_t n, uint32_t v) {
