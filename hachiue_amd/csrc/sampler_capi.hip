@@ -20,7 +20,8 @@
 // ---- workspace of hs_sample_batch_device_noalloc: one array per GPU, in
 // device memory for the life of the process.  Layout (offsets 256-aligned):
 // plans [kMaxRows] | routing lists [5][kMaxRows] | the two-pass large-k
-// rows handed back [kMaxRows] | split-row hand-over lists
+// rows handed back [kMaxRows] | slot-replay requests [kMaxRows] | split-row
+// hand-over lists
 // [kSplitCUs][kPartCap] | their meta data [kSplitCUs] | the split rows'
 // arrival counters [kSplitCUs] (zero between calls).
 namespace na {
@@ -31,14 +32,17 @@ constexpr size_t kListsOff = kPlansOff + kPlansBytes;
 constexpr size_t kListsBytes = sizeof(int32_t) * 5 * kMaxRows;
 constexpr size_t kRetryOff = kListsOff + kListsBytes;
 constexpr size_t kRetryBytes = sizeof(int32_t) * kMaxRows;
-constexpr size_t kSplitListOff = kRetryOff + kRetryBytes;
+constexpr size_t kReplayOff = kRetryOff + kRetryBytes;
+constexpr size_t kReplayBytes = sizeof(hs::ReplayReq) * kMaxRows;
+constexpr size_t kSplitListOff = kReplayOff + kReplayBytes;
 constexpr size_t kSplitListBytes = sizeof(unsigned long long) * hs::kSplitCUs * hs::kPartCap;
 constexpr size_t kSplitMetaOff = kSplitListOff + kSplitListBytes;
 constexpr size_t kSplitMetaBytes = sizeof(hs::SplitMeta) * hs::kSplitCUs;
 constexpr size_t kSplitCntOff = kSplitMetaOff + kSplitMetaBytes;
 constexpr size_t kSplitCntBytes = sizeof(uint32_t) * hs::kSplitCUs;
 constexpr size_t kBytes = kSplitCntOff + kSplitCntBytes;
-static_assert(kListsOff % 256 == 0 && kRetryOff % 256 == 0 && kSplitListOff % 256 == 0 &&
+static_assert(kListsOff % 256 == 0 && kRetryOff % 256 == 0 && kReplayOff % 256 == 0 &&
+                  kSplitListOff % 256 == 0 &&
                   kSplitMetaOff % 256 == 0 &&
                   kSplitCntOff % 256 == 0,
               "scratch layout alignment");
@@ -120,6 +124,7 @@ struct hs_context {
   DevBuf split_list, split_meta, split_cnt;   // split rows (split_cnt: zero between calls)
   DevBuf gemv_part, gemv_cnt;   // Q6_K GEMV tiles cut between waves (gemv_cnt: zero between calls)
   DevBuf large_retry;           // two-pass large-k rows handed back
+  DevBuf large_replay;          // slot-history replays asked for by the large-k kernel
   int64_t cand_count_rows = 0;     // rows whose counter is known to be zero
   // plan upload cache
   std::vector<hs::RowPlan> last_plans;
@@ -450,6 +455,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
     }
   }
   if (n_lfast > 0) HS_HIP(ctx->large_retry.ensure(sizeof(int32_t) * (size_t)n_lfast));
+  if (n_large > 0) HS_HIP(ctx->large_replay.ensure(sizeof(hs::ReplayReq) * (size_t)n_large));
   // small batches split each row of the row kernel over several workgroups
   const int split = choose_split(ctx, n_row, vocab);
   int rc = ensure_split(ctx, n_row, split);
@@ -467,6 +473,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   ws.mid_list = lists + n_pf + n_row + n_chunk + n_large;
   ws.lfast_list = lists + n_pf + n_row + n_chunk + n_large + n_mid;
   ws.large_retry = static_cast<int32_t *>(ctx->large_retry.p);
+  ws.large_replay = static_cast<hs::ReplayReq *>(ctx->large_replay.p);
   ws.cand = static_cast<uint2 *>(ctx->cand.p);
   ws.cand_count = static_cast<int32_t *>(ctx->cand_count.p);
   ws.info = static_cast<hs::ChunkInfo *>(ctx->info.p);
@@ -777,6 +784,7 @@ int sample_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows, int64_
   ws.mid_list = lists + n_pf + n_row + n_large;
   ws.lfast_list = lists + n_pf + n_row + n_large + n_mid;
   ws.large_retry = reinterpret_cast<int32_t *>(base + na::kRetryOff);
+  ws.large_replay = reinterpret_cast<hs::ReplayReq *>(base + na::kReplayOff);
   ws.split_list = reinterpret_cast<unsigned long long *>(base + na::kSplitListOff);
   ws.split_meta = reinterpret_cast<hs::SplitMeta *>(base + na::kSplitMetaOff);
   ws.split_cnt = reinterpret_cast<uint32_t *>(base + na::kSplitCntOff);
@@ -934,6 +942,7 @@ int hs_context_destroy(hs_context *ctx) {
     ctx->gemv_part.release();
     ctx->gemv_cnt.release();
     ctx->large_retry.release();
+    ctx->large_replay.release();
     ctx->h_logits.release();
     ctx->h_hist.release();
     ctx->h_off.release();
@@ -1177,9 +1186,9 @@ int hs_sample_logits_batch(hs_context *ctx, float *logits, int32_t rows, int64_t
   for (int r = 0; r < rows; ++r)
     if (tokens_out[r] < 0)
       return fail(HS_ERR_UNSUPPORTED,
-                  "row %d: top-k above 1024 with equal logits at the drawn position; the "
-                  "reference orders them by its slot history, which this build does not replay "
-                  "at that size", r);
+                  "row %d: top-k above %d with equal logits at the drawn position; the "
+                  "reference orders them by its slot history, which this build replays up to "
+                  "that top-k only", r, hs::kReplayMaxK);
   return HS_OK;
 }
 

@@ -98,6 +98,18 @@ struct SplitMeta {
 };
 static_assert(sizeof(SplitMeta) == 24, "SplitMeta layout");
 
+// What a large-k row leaves for large_replay_kernel when equal values make
+// its order depend on the reference's slot history (k < the finite count).
+struct ReplayReq {
+  int32_t need;              // bit 0: the token; bit 1: the candidate ids
+  uint32_t xkey;             // the drawn value's key
+  int32_t pos;               // the drawn position (value descending)
+  int32_t mo;                // candidate positions to write
+};
+static_assert(sizeof(ReplayReq) == 16, "ReplayReq layout");
+constexpr int kReplayMaxK = 16384;     // slots the replay holds in LDS
+constexpr int kReplayCands = 1024;     // candidate positions it can order
+
 struct Workspace {
   RowPlan *plans;            // [rows]
   const int32_t *pf_list;    // rows penalised by the pre-pass
@@ -107,6 +119,7 @@ struct Workspace {
   const int32_t *mid_list;   // rows of the mid kernel
   const int32_t *lfast_list; // rows of the two-pass large-k kernel (k = vocab, no min-p)
   int32_t *large_retry;      // [n_lfast] 1: the two-pass kernel handed the row back
+  ReplayReq *large_replay;   // [n_large] slot-history replays asked for by large_row
   uint2 *cand;               // [n_chunk][S][kChunkCap] (key, index)
   int32_t *cand_count;       // [n_chunk]
   ChunkInfo *info;           // [n_chunk][S]
@@ -152,15 +165,16 @@ struct LaunchArgs {
 // Launches the kernels of one call on `stream`.  When `ev` is not null,
 // ev[2i] and ev[2i + 1] receive the start and end of kernel i's dispatch
 // (0 penalty pre-pass, 1 row kernel, 2 chunk kernel, 3 finalize, 4 large-k
-// kernel, 5 mid kernel, 6 GPU greedy-route argmax, 8 two-pass large-k kernel;
+// kernel, 5 mid kernel, 6 GPU greedy-route argmax, 8 two-pass large-k kernel,
+// 9 the large-k slot replay;
 // 7 is the lm_head GEMV, launched apart), for the kernels that launch only:
 // launched_kernels() says which.  The large-k kernel launches whenever a row
 // has k > 1024: it also takes the rows the two-pass kernel hands back.
-constexpr int kTimedKernels = 9;
+constexpr int kTimedKernels = 10;
 inline unsigned launched_kernels(const LaunchArgs &a) {
   return (a.n_pf > 0 ? 1u : 0u) | (a.n_row > 0 ? 2u : 0u) | (a.n_chunk > 0 ? 12u : 0u) |
          (a.n_large + a.n_lfast > 0 ? 16u : 0u) | (a.n_mid > 0 ? 32u : 0u) |
-         (a.n_argmax > 0 ? 64u : 0u) | (a.n_lfast > 0 ? 256u : 0u);
+         (a.n_argmax > 0 ? 64u : 0u) | (a.n_lfast > 0 ? 256u : 0u) | (a.n_large > 0 ? 512u : 0u);
 }
 // Largest vocabulary of the GPU greedy route (byte offsets of a row stay
 // below 2^31).

@@ -3193,8 +3193,13 @@ __device__ __forceinline__ LargeLoc large_locate(const LargeRow &L, int mode, do
 
 // The general large-k path for one row: any k > 1024, min-p, candidate
 // outputs, and the rows the two-pass path below hands back.
-__device__ __forceinline__ void large_row(const LaunchArgs &a, const RowPlan &P, int row, LargeSmem &sm) {
+// With k below the finite count, an equal-value group whose order decides
+// the token or the candidate list is left to large_replay_kernel through
+// *req (k <= kReplayMaxK); beyond that the row reports HS_ROW_UNSUPPORTED.
+__device__ __forceinline__ void large_row(const LaunchArgs &a, const RowPlan &P, int row,
+                                          LargeSmem &sm, ReplayReq *req) {
   const int tid = threadIdx.x;
+  if (tid == 0) req->need = 0;
   LargeRow L;
   L.rowp = a.logits + (int64_t)row * a.stride;
   L.V = a.vocab;
@@ -3356,10 +3361,12 @@ __device__ __forceinline__ void large_row(const LaunchArgs &a, const RowPlan &P,
     lpick = large_locate(L, kByPos, 0.0, 0u, sm);
   }
   const bool ambiguous = L.T != 0u && lpick.tie;   // slot history orders equal values
+  const bool replay = ambiguous && k <= kReplayMaxK;
   uint32_t flags = HS_ROW_LARGE;
-  if (ambiguous) flags |= HS_ROW_UNSUPPORTED | HS_ROW_TIES;
+  if (ambiguous) flags |= HS_ROW_TIES | (replay ? HS_ROW_REPLAYED : HS_ROW_UNSUPPORTED);
+  int need = replay ? 1 : 0, need_mo = 0;
   if (tid == 0) {
-    put_token(a, row, ambiguous ? -1 : lpick.id);
+    if (!replay) put_token(a, row, ambiguous ? -1 : lpick.id);
     if (a.cand_count_out) a.cand_count_out[row] = n;
     if (a.cutoff_out) a.cutoff_out[row] = cut;
   }
@@ -3409,9 +3416,237 @@ __device__ __forceinline__ void large_row(const LaunchArgs &a, const RowPlan &P,
       }
     }
     if (rest > 1 || (kend == L.T && L.teq > L.tin)) tie = 1;
-    if (__syncthreads_or(tie) && L.T) flags |= HS_ROW_UNSUPPORTED | HS_ROW_TIES;
+    if (__syncthreads_or(tie) && L.T) {
+      if (k <= kReplayMaxK && mo <= kReplayCands && !too_long) {
+        need |= 2;
+        need_mo = mo;
+        flags |= HS_ROW_TIES | HS_ROW_REPLAYED;
+      } else {
+        flags |= HS_ROW_UNSUPPORTED | HS_ROW_TIES;
+      }
+    }
   }
-  if (tid == 0 && a.row_flags) a.row_flags[row] = flags;
+  if (tid == 0) {
+    if (a.row_flags) a.row_flags[row] = flags;
+    req->xkey = lpick.key;
+    req->pos = lpick.pos;
+    req->mo = need_mo;
+    req->need = need;
+  }
+}
+
+// ---------------------------------------------------------------- large-k slot replay
+
+// src/sampler.ts:50-69 replayed for a row whose equal values large_row could
+// not order (k <= kReplayMaxK, below the finite count).  The k slots live in
+// LDS under a 64-ary min tree: lvl1[b] is the smallest (key, slot) of slots
+// 64b .. 64b+63, lvl2[c] of lvl1 entries 64c .. 64c+63, and the root of
+// lvl2 is the slot the reference's rescan finds (the first slot holding the
+// minimum: packed (key << 32 | slot), an empty slot's key 0).
+//  - The first k finite logits fill slots 0..k-1 in index order (the rescan
+//    always finds the first empty slot), placed in parallel.
+//  - Then the row is read in chunks of kLT logits; those above the chunk's
+//    starting minimum queue up in index order, and one wave takes them one
+//    by one: a logit above the current minimum replaces that slot, and the
+//    three tree levels on its path are recomputed (a 64-lane minimum each).
+//  - The final slots then order each equal-value group by slot index (the
+//    stable sort of src/sampler.ts:72-75): the token is the member of the
+//    drawn value at the drawn rank, and the candidate ids follow
+//    (value descending, slot ascending).
+struct ReplaySmem {
+  uint32_t keys[kReplayMaxK];
+  int32_t ids[kReplayMaxK];
+  unsigned long long lvl1[kReplayMaxK / 64];
+  unsigned long long lvl2[kReplayMaxK / 4096];
+  unsigned long long queue[kLT];
+  uint32_t wsum[kLT / 64];
+  int32_t nq, fill_end, res;
+  unsigned long long root;
+};
+size_t replay_smem_bytes() { return sizeof(ReplaySmem); }
+
+__device__ __forceinline__ unsigned long long wave_min64(unsigned long long x) {
+#pragma unroll
+  for (int m = 32; m > 0; m >>= 1) {
+    const unsigned long long y = __shfl_xor(x, m);
+    x = x < y ? x : y;
+  }
+  return x;
+}
+
+__device__ __forceinline__ unsigned long long slot_pack(uint32_t key, uint32_t slot) {
+  return ((unsigned long long)key << 32) | slot;
+}
+
+__global__ __launch_bounds__(kLT) void large_replay_kernel(LaunchArgs a, Workspace ws) {
+  extern __shared__ unsigned long long rdyn[];
+  ReplaySmem &sm = *reinterpret_cast<ReplaySmem *>(rdyn);
+  const ReplayReq req = ws.large_replay[blockIdx.x];
+  if (!req.need) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row = ws.large_list[blockIdx.x];
+  const int k = ws.plans[row].k;
+  const float *rowp = a.logits + (int64_t)row * a.stride;
+  const int V = a.vocab;
+  constexpr unsigned long long kNone = ~0ull;
+  // inclusive block prefix of x, and the block's total
+  auto scan = [&](uint32_t x, uint32_t &total) {
+    const uint32_t incl = block_scan_incl<kLT>(x, sm.wsum);
+    uint32_t t = 0;
+    for (int w = 0; w < kLT / 64; ++w) t += sm.wsum[w];
+    total = t;
+    __syncthreads();   // before wsum is used again
+    return incl;
+  };
+
+  // 1. the first k finite logits fill slots 0..k-1 in index order
+  if (tid == 0) sm.fill_end = V;
+  int filled = 0;
+  for (int base = 0; base < V && filled < k; base += kLT) {
+    const int e = base + tid;
+    const uint32_t key = e < V ? f2key(rowp[e]) : 0u;
+    uint32_t total;
+    const uint32_t incl = scan(key ? 1u : 0u, total);
+    const int slot = filled + (int)incl - 1;
+    if (key && slot < k) {
+      sm.keys[slot] = key;
+      sm.ids[slot] = e;
+      if (slot == k - 1) sm.fill_end = e + 1;
+    }
+    filled += (int)total;
+  }
+  for (int s = filled + tid; s < k; s += kLT) { sm.keys[s] = 0u; sm.ids[s] = -1; }
+  __syncthreads();
+  const int nl1 = (k + 63) >> 6, nl2 = (nl1 + 63) >> 6;
+  for (int b = wave; b < nl1; b += kLT / 64) {
+    const int sl = 64 * b + lane;
+    const unsigned long long m = wave_min64(sl < k ? slot_pack(sm.keys[sl], (uint32_t)sl) : kNone);
+    if (lane == 0) sm.lvl1[b] = m;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    unsigned long long top = kNone;
+    for (int c = 0; c < nl2; ++c) {
+      const int i = 64 * c + lane;
+      const unsigned long long m = wave_min64(i < nl1 ? sm.lvl1[i] : kNone);
+      if (lane == 0) sm.lvl2[c] = m;
+      top = m < top ? m : top;
+    }
+    if (lane == 0) sm.root = top;
+  }
+  __syncthreads();
+
+  // 2. the rest of the row, in index order
+  const int start = sm.fill_end;
+  for (int base = start; base < V; base += kLT) {
+    const uint32_t lo = (uint32_t)(sm.root >> 32);   // the minimum at the chunk's start
+    const int e = base + tid;
+    const uint32_t key = e < V ? f2key(rowp[e]) : 0u;
+    const bool enter = key > lo;
+    uint32_t total;
+    const uint32_t incl = scan(enter ? 1u : 0u, total);
+    if (enter) sm.queue[incl - 1] = slot_pack(key, (uint32_t)e);
+    const int nq = (int)total;
+    __syncthreads();
+    if (wave == 0) {
+      unsigned long long top = sm.root;
+      for (int q = 0; q < nq; ++q) {
+        const unsigned long long item = sm.queue[q];
+        const uint32_t kv = (uint32_t)(item >> 32);
+        if (kv <= (uint32_t)(top >> 32)) continue;   // not above the current minimum
+        const int s = (int)(uint32_t)top;
+        if (lane == 0) {
+          sm.keys[s] = kv;
+          sm.ids[s] = (int)(uint32_t)item;
+        }
+        const int b1 = s >> 6, sl = 64 * b1 + lane;
+        const unsigned long long m1 = wave_min64(
+            sl < k ? slot_pack(sl == s ? kv : sm.keys[sl], (uint32_t)sl) : kNone);
+        const int b2 = b1 >> 6, i1 = 64 * b2 + lane;
+        const unsigned long long m2 = wave_min64(i1 < nl1 ? (i1 == b1 ? m1 : sm.lvl1[i1]) : kNone);
+        const unsigned long long m3 = wave_min64(lane < nl2 ? (lane == b2 ? m2 : sm.lvl2[lane]) : kNone);
+        if (lane == 0) {
+          sm.lvl1[b1] = m1;
+          sm.lvl2[b2] = m2;
+        }
+        top = m3;
+      }
+      if (lane == 0) sm.root = top;
+    }
+    __syncthreads();
+  }
+
+  // 3. the token: the member of the drawn value at its rank in slot order
+  const int span = (k + kLT - 1) / kLT;
+  const int s0 = tid * span, s1 = min(k, s0 + span);
+  if (req.need & 1) {
+    uint32_t above = 0, eq = 0;
+    for (int s = s0; s < s1; ++s) {
+      above += sm.keys[s] > req.xkey;
+      eq += sm.keys[s] == req.xkey;
+    }
+    uint32_t n_above, n_eq;
+    (void)scan(above, n_above);
+    const uint32_t incl = scan(eq, n_eq);
+    const int j = req.pos - (int)n_above;     // rank in the group
+    if (tid == 0) sm.res = -1;
+    __syncthreads();
+    uint32_t seen = incl - eq;
+    if (j >= 0 && (uint32_t)j >= seen && (uint32_t)j < incl) {
+      for (int s = s0; s < s1; ++s) {
+        if (sm.keys[s] == req.xkey) {
+          if (seen == (uint32_t)j) { sm.res = sm.ids[s]; break; }
+          ++seen;
+        }
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      put_token(a, row, sm.res);
+      if (sm.res < 0 && a.row_flags) a.row_flags[row] |= HS_ROW_UNSUPPORTED;
+    }
+    __syncthreads();
+  }
+
+  // 4. the candidate ids of positions 0..mo-1 (value descending, slot
+  // ascending): the mo largest (key << 32 | ~slot), by a search for the key
+  // at position mo - 1 and a sort of at most mo entries
+  if ((req.need & 2) && a.cand_ids) {
+    const int mo = req.mo;
+    uint32_t lo = 1, hi = 0xFFFFFFFFu;   // largest key t with count(key >= t) >= mo
+    while (lo < hi) {
+      const uint32_t mid = lo + (hi - lo + 1) / 2;
+      uint32_t c = 0, tot;
+      for (int s = s0; s < s1; ++s) c += sm.keys[s] >= mid;
+      (void)scan(c, tot);
+      if (tot >= (uint32_t)mo) lo = mid; else hi = mid - 1;
+    }
+    const uint32_t X = lo;
+    uint32_t gt = 0, eq = 0;
+    for (int s = s0; s < s1; ++s) {
+      gt += sm.keys[s] > X;
+      eq += sm.keys[s] == X;
+    }
+    uint32_t n_gt, n_eq;
+    const uint32_t ig = scan(gt, n_gt);
+    const uint32_t ie = scan(eq, n_eq);
+    uint32_t pg = ig - gt, pe = ie - eq;
+    for (int s = s0; s < s1; ++s) {
+      const uint32_t key = sm.keys[s];
+      if (key > X) sm.queue[pg++] = pack_cand(key, (uint32_t)s);
+      else if (key == X && n_gt + pe < (uint32_t)mo) sm.queue[n_gt + pe++] = pack_cand(key, (uint32_t)s);
+      else if (key == X) ++pe;
+    }
+    __syncthreads();
+    int P2 = 1;
+    while (P2 < mo) P2 <<= 1;
+    for (int i = mo + tid; i < P2; i += kLT) sm.queue[i] = 0ull;
+    __syncthreads();
+    block_sort_desc<kLT>(sm.queue, P2);
+    const int cs = a.cand_stride;
+    for (int i = tid; i < mo; i += kLT)
+      a.cand_ids[(int64_t)row * cs + i] = sm.ids[cand_idx(sm.queue[i])];
+  }
 }
 
 // ---------------------------------------------------------------- large-k, two passes
@@ -4019,16 +4254,19 @@ __global__ __launch_bounds__(kFT, 4) void large_fast_kernel(LaunchArgs a, Worksp
 // handed back (block n_large + i takes lfast_list[i] when large_retry[i]).
 __global__ __launch_bounds__(kLT) void large_kernel(LaunchArgs a, Workspace ws) {
   extern __shared__ unsigned long long ldyn[];
+  __shared__ ReplayReq unused_req;   // the handed-back rows have k = vocab: never a replay
   int row;
+  ReplayReq *req = &unused_req;
   if ((int)blockIdx.x < a.n_large) {
     row = ws.large_list[blockIdx.x];
+    req = ws.large_replay + blockIdx.x;
   } else {
     const int i = (int)blockIdx.x - a.n_large;
     if (!ws.large_retry[i]) return;
     row = ws.lfast_list[i];
   }
   const RowPlan P = ws.plans[row];
-  large_row(a, P, row, *reinterpret_cast<LargeSmem *>(ldyn));
+  large_row(a, P, row, *reinterpret_cast<LargeSmem *>(ldyn), req);
 }
 
 // ---------------------------------------------------------------- GPU greedy route
@@ -4186,6 +4424,10 @@ hipError_t prepare_kernels() {
                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)large_fast_smem_bytes())) != hipSuccess)
     return e;
+  if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&large_replay_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)replay_smem_bytes())) != hipSuccess)
+    return e;
   return hipFuncSetAttribute(reinterpret_cast<const void *>(&large_kernel),
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)large_smem_bytes());
 }
@@ -4279,8 +4521,8 @@ hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t s
                          hipEvent_t *ev, hipEvent_t done) {
   hipError_t e;
   // the last kernel of the call records `done`
-  const int last = a.n_argmax > 0 ? 6 : a.n_large + a.n_lfast > 0 ? 4 : a.n_chunk > 0 ? 3
-                 : a.n_mid > 0 ? 5 : a.n_row > 0 ? 1 : 0;
+  const int last = a.n_argmax > 0 ? 6 : a.n_large > 0 ? 9 : a.n_lfast > 0 ? 4
+                 : a.n_chunk > 0 ? 3 : a.n_mid > 0 ? 5 : a.n_row > 0 ? 1 : 0;
   auto dn = [&](int slot) { return slot == last ? done : nullptr; };
   if (a.n_pf > 0) {
     e = launch_one(pen_kernel, dim3((unsigned)a.n_pf), dim3(kPenThreads), pen_smem_bytes(),
@@ -4325,6 +4567,11 @@ hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t s
   if (a.n_large + a.n_lfast > 0) {
     e = launch_one(large_kernel, dim3((unsigned)(a.n_large + a.n_lfast)), dim3(kLT),
                    large_smem_bytes(), stream, ev, 4, dn(4), a, ws);
+    if (e != hipSuccess) return e;
+  }
+  if (a.n_large > 0) {   // rows of large_list that asked for the slot replay
+    e = launch_one(large_replay_kernel, dim3((unsigned)a.n_large), dim3(kLT), replay_smem_bytes(),
+                   stream, ev, 9, dn(9), a, ws);
     if (e != hipSuccess) return e;
   }
   if (a.n_argmax > 0) {

@@ -202,7 +202,8 @@ class Sampler:
         _check(lib().hs_context_set_timing(self._ctx, 1 if enable else 0))
 
     KERNELS = ("pen_kernel", "row_kernel", "chunk_kernel", "finalize_kernel", "large_kernel",
-               "mid_kernel", "argmax_kernel", "gemv_kernel", "large_fast_kernel")
+               "mid_kernel", "argmax_kernel", "gemv_kernel", "large_fast_kernel",
+               "large_replay_kernel")
 
     def kernel_times(self):
         """({kernel: total device ms}, calls) since the last query."""

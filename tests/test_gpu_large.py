@@ -165,3 +165,29 @@ def test_min_p_and_top_p_edges_large(sampler):
     _check(sampler, logits, vocab, None, None, configs, u, 64, "min-p / top-p edges")
     _check(sampler, logits, vocab, None, None, configs, u, 64, "min-p / top-p edges",
            want_cands=False)
+
+
+HS_ROW_REPLAYED = 0x2
+
+
+@pytest.mark.parametrize("k", [2048, 5000, 16384])
+def test_large_k_ties_replayed(sampler, k):
+    """Rows of many equal values with 1024 < k < the finite count: the order
+    inside an equal-value group follows the reference's slot history
+    (src/sampler.ts:55-74), which the slot replay reproduces; tokens and
+    candidate ids equal the oracle's, and no row is left unsupported."""
+    rng = np.random.default_rng(k)
+    rows, vocab = 12, 60000
+    logits = np.round(rng.standard_normal((rows, vocab)) * 3).astype(np.float32)   # ~30 values
+    logits[1] = np.round(logits[1] / 4)             # very coarse: a few huge groups
+    logits[2, ::3] = np.nan
+    configs = [dict(temperature=float(rng.uniform(0.5, 2.0)), topK=k, topP=float(rng.uniform(0.6, 1.0)))
+               for _ in range(rows)]
+    configs[3]["minP"] = 0.02
+    u = rng.random(rows)
+    u[4] = 0.0
+    for want in (True, False):
+        got, want_res = _check(sampler, logits, vocab, None, None, configs, u, 64,
+                               f"ties k={k}", want_cands=want)
+        assert not (got.flags & HS_ROW_UNSUPPORTED).any()
+        assert (got.flags & HS_ROW_REPLAYED).any()
