@@ -204,10 +204,10 @@ def test_ragged_vocab_and_stride(any_sampler, vocab, pad):
 
 
 def test_mid_k_tail_without_candidate_outputs(any_sampler):
-    """Rows with 64 < k <= 1024 and no candidate outputs: the sort-free tail
-    (positions by probability-weighted selects) and its fallbacks (ties at or
-    inside the top k, probabilities below 2^-29, u = 0, min-p and top-p
-    edges, an infinite logit)."""
+    """Rows with 64 < k <= 1024 and no candidate outputs: the block-parallel
+    tail (exact prefix sums over the sorted list) and its sequential
+    fallbacks (ties at or inside the top k, probabilities below 2^-29, u = 0,
+    min-p and top-p edges, an infinite logit)."""
     V = 30000
     r = _rng(12)
     base = (r.standard_normal(V) * 2.5).astype(np.float32)
@@ -230,3 +230,22 @@ def test_mid_k_tail_without_candidate_outputs(any_sampler):
              (base, list(r.integers(0, V, 100)), dict(temperature=0.9, topK=80, topP=0.9,
                                                      repetitionPenalty=1.2), 0.25)]
     _run(any_sampler, cases, V, cap=1024, label="mid-k tokens only", want_cands=False)
+
+
+@pytest.mark.parametrize("k", [40, 500])
+def test_every_logit_enters_the_candidate_lists(any_sampler, k):
+    """Full-size rows on which every logit of the stream passes the bound:
+    all equal, and increasing with the index (each round lies above every
+    bound taken before it).  The per-wave candidate segments overflow, the
+    row goes to the slot replay, and the repetition write-back touches the
+    first and the last id of the row."""
+    V = 151936
+    eq = np.ones(V, np.float32)
+    inc = (np.arange(V, dtype=np.float32) * np.float32(1e-3)).astype(np.float32)
+    edge = [0, V - 1, 1, V - 2, V - 1]
+    cfg = dict(temperature=0.7, topK=k, topP=0.9)
+    rep = dict(repetitionPenalty=1.3, **cfg)
+    cases = [(eq, [], cfg, 0.5), (eq, edge, rep, 0.25), (inc, [], cfg, 0.6),
+             (inc, edge, rep, 0.9), (inc, edge, dict(temperature=0.0, repetitionPenalty=1.3), 0.5),
+             (eq, edge, dict(temperature=1.0, topK=k, topP=1.0, repetitionPenalty=0.5), 0.999)]
+    _run(any_sampler, cases, V, cap=64, label=f"every logit enters, k={k}")
