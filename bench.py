@@ -99,27 +99,36 @@ def cpu_baseline(wl, seconds: float, threads: int, rows: int) -> dict | None:
 def host_api(wl, rows: int, calls: int) -> dict | None:
     """End-to-end time of the synchronous drop-in as the engine calls it
     (src/engine.ts:1642): Node sampleLogits on one host row per call (H2D of
-    the row, the kernels, D2H of the token and penalised logits)."""
+    the row, the kernels, D2H of the token and penalised logits).  Beside it,
+    the same calls on the drop-in's CPU backend (createSampler({backend:
+    'cpu'}), the JavaScript sampler a host without the GPU would use)."""
     node = "node"
     addon = os.path.join(ROOT, "hachiue_amd", "node", "hachiue_sampler.node")
     if not os.path.exists(addon):
         return None
+    res = {}
     with tempfile.TemporaryDirectory(prefix="hs_api_") as d:
         write_workload_dir(wl, rows, d)
-        cmd = [node, os.path.join(ROOT, "hachiue_amd", "js", "dropin_timing.js"), d, str(calls)]
-        log(f"[bench] host api: {' '.join(cmd[1:2])} ... {calls} calls")
-        try:
-            out = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
-        except (OSError, subprocess.TimeoutExpired):
-            return None
-    if out.returncode != 0:
-        log(f"[bench] host api timing failed: {out.stderr[-2000:]}")
-        return None
-    r = json.loads(out.stdout.strip().splitlines()[-1])
+        for backend in ("hip", "cpu"):
+            cmd = [node, os.path.join(ROOT, "hachiue_amd", "js", "dropin_timing.js"), d,
+                   str(calls), backend]
+            log(f"[bench] host api ({backend}): {calls} calls")
+            try:
+                out = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
+            except (OSError, subprocess.TimeoutExpired):
+                return None
+            if out.returncode != 0:
+                log(f"[bench] host api timing failed: {out.stderr[-2000:]}")
+                return None
+            res[backend] = json.loads(out.stdout.strip().splitlines()[-1])
+    r, c = res["hip"], res["cpu"]
     return dict(value=round(r["us_median"], 2), unit="us per row (median)",
                 mean_us=round(r["us_mean"], 2), calls=r["calls"],
                 path=(f"Node {r['node']} sampleLogits -> N-API -> hs_sample_logits: one host row "
-                      f"per call (PCIe both ways), rows 0..{rows - 1} of the workload"))
+                      f"per call (PCIe both ways), rows 0..{rows - 1} of the workload"),
+                cpu_backend=dict(value=round(c["us_median"], 2), unit="us per row (median)",
+                                 path="the same calls through createSampler({backend: 'cpu'}) "
+                                      "(hachiue_amd/js/cpu.js, one thread)"))
 
 
 def oracle_parity(wl, tokens: np.ndarray) -> dict:

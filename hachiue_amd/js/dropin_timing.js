@@ -5,16 +5,18 @@
  * per call, so each call copies the row to the GPU, samples it and copies the
  * token (and the penalised logits) back.
  *
- *   node dropin_timing.js <workload dir> <calls>
+ *   node dropin_timing.js <workload dir> <calls> [hip|cpu]
  *
  * The directory holds meta.json, logits.f32, uniforms.f64 and, with
  * histories, hist_ids.i32 / hist_off.f64 (as bench.py writes them).  Each
  * call gets a fresh copy of a row (the copy is not timed).  Prints one JSON
- * line: the median and mean microseconds per call.
+ * line: the median and mean microseconds per call.  With a backend name the
+ * calls go through createSampler({ backend }) (cpu: the JavaScript sampler).
  */
 const fs = require('fs');
 const path = require('path');
-const hs = require(path.join(__dirname, 'index.js'));
+const index = require(path.join(__dirname, 'index.js'));
+const hs = process.argv[4] ? index.createSampler({ backend: process.argv[4] }) : index;
 
 function typed(file, Ctor) {
   const buf = fs.readFileSync(file);
@@ -51,4 +53,4 @@ for (let i = 0; i < calls + 10; i++) {
 times.sort(function (a, b) { return a - b; });
 const mean = times.reduce(function (a, b) { return a + b; }, 0) / times.length;
 console.log(JSON.stringify({ calls: calls, us_median: times[times.length >> 1], us_mean: mean,
-  node: process.version }));
+  node: process.version, backend: hs.info ? hs.info.backend : 'hip' }));

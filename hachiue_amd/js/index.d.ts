@@ -83,3 +83,31 @@ export function nextToken(
 
 export const DEFAULTS: Readonly<Required<Pick<SampleConfig,
   'temperature' | 'topK' | 'topP' | 'minP' | 'repetitionPenalty'>>>
+
+/** src/engine.ts:532-539 (BackendInfo): which backend a sampler runs on. */
+export interface SamplerInfo {
+  backend: 'hip' | 'cpu'
+  label: string
+  /** present when 'auto' fell back to the CPU: why the HIP backend did not start */
+  fallbackReason?: string
+}
+
+export interface Sampler {
+  readonly info: SamplerInfo
+  sampleLogits: typeof sampleLogits
+  sampleLogitsBatch: typeof sampleLogitsBatch
+  sampleLogitsBatchAsync: typeof sampleLogitsBatchAsync
+  isGreedyRoute: typeof isGreedyRoute
+  /** on the CPU backend: the Wasm backend's greedy loop (src/wasm-backend.ts:1204-1215),
+   * the first id of the largest logit above -1e30 */
+  argmaxLogits: typeof argmaxLogits
+  argmaxLogitsBatch: typeof argmaxLogitsBatch
+  nextToken: typeof nextToken
+}
+
+/**
+ * A sampler on the requested backend (src/engine.ts:521, :626-639): 'hip'
+ * (default) throws when the HIP backend cannot start, 'cpu' is the
+ * JavaScript sampler, 'auto' falls back to it with `info.fallbackReason`.
+ */
+export function createSampler(options?: { backend?: 'hip' | 'cpu' | 'auto' }): Sampler

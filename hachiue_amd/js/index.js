@@ -6,8 +6,14 @@
  * names, `??` defaults, in-place penalties and return values of
  * src/sampler.ts:12-118 (exported at src/index.ts:15); the work runs in the
  * HIP kernels behind the C ABI (include/hachiue_sampler.h) through the
- * Node-API addon.  There is no CPU fallback: without the addon or a GPU the
- * first call throws.
+ * Node-API addon.  These module-level functions never fall back to the CPU:
+ * without the addon or a GPU the first call throws (code 'HS_ERR_HIP').
+ *
+ * createSampler({ backend }) picks a backend the way the engine does
+ * (src/engine.ts:521, :556-557, :626-639): 'hip' (the default here) throws
+ * when the HIP backend cannot start; 'cpu' takes the JavaScript sampler of
+ * cpu.js; 'auto' takes HIP when it starts and the CPU otherwise, with the
+ * reason in info.fallbackReason.
  *
  * Extensions (absent by default, so existing callers see no change):
  *   config.presencePenalty / config.frequencyPenalty  (x - freq*n) - pres
@@ -294,7 +300,39 @@ function sampleLogitsBatchAsync(logits, vocab, histories, configs, uniforms, sha
     : p.then(function () { return native().sampleBatchAsync.apply(null, a.second()); });
 }
 
+const API = ['sampleLogits', 'sampleLogitsBatch', 'sampleLogitsBatchAsync', 'isGreedyRoute',
+  'argmaxLogits', 'argmaxLogitsBatch', 'nextToken'];
+
+function backendObject(impl, info) {
+  const b = { info: Object.freeze(info) };
+  API.forEach(function (name) { b[name] = impl[name]; });
+  return Object.freeze(b);
+}
+
+/**
+ * A sampler on the requested backend: 'hip' (default), 'cpu' or 'auto'.
+ * The result has the module's functions and `info` = { backend, label,
+ * fallbackReason? } (BackendInfo, src/engine.ts:532-539).
+ */
+function createSampler(options) {
+  const requested = option(options && options.backend, 'hip');
+  if (requested === 'cpu') return backendObject(require('./cpu.js'), { backend: 'cpu', label: 'CPU (JavaScript)' });
+  if (requested !== 'hip' && requested !== 'auto') {
+    throw new TypeError("backend must be 'hip', 'cpu' or 'auto'");
+  }
+  try {
+    context();
+  } catch (err) {
+    if (requested === 'hip') throw err;
+    const reason = err instanceof Error ? err.message : String(err);
+    return backendObject(require('./cpu.js'),
+      { backend: 'cpu', label: 'CPU (JavaScript)', fallbackReason: reason });
+  }
+  return backendObject(module.exports, { backend: 'hip', label: 'HIP (gfx950)' });
+}
+
 module.exports = {
+  createSampler: createSampler,
   sampleLogits: sampleLogits,
   sampleLogitsBatch: sampleLogitsBatch,
   sampleLogitsBatchAsync: sampleLogitsBatchAsync,

@@ -134,6 +134,9 @@ def lib() -> ctypes.CDLL:
         L.orc_wgsl_argmax.restype = None
         L.orc_wgsl_argmax.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int64,
                                       ctypes.c_int64, P(ctypes.c_int32)]
+        L.orc_wasm_greedy.restype = None
+        L.orc_wasm_greedy.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int64,
+                                      ctypes.c_int64, P(ctypes.c_int32)]
         L.orc_topk_slots.restype = ctypes.c_int
         L.orc_topk_slots.argtypes = [P(ctypes.c_float), ctypes.c_int64,
                                      ctypes.c_int64, ctypes.c_int,
@@ -303,6 +306,21 @@ def wgsl_argmax(logits: np.ndarray, vocab: int, rows: int | None = None,
     stride = x.shape[1] if stride is None else stride
     out = np.zeros(rows, np.int32)
     lib().orc_wgsl_argmax(_ptr(x, ctypes.c_float), rows, stride, vocab,
+                          _ptr(out, ctypes.c_int32))
+    return out
+
+
+def wasm_greedy(logits: np.ndarray, vocab: int, rows: int | None = None,
+                stride: int | None = None) -> np.ndarray:
+    """The Wasm backend's greedy route (src/wasm-backend.ts:1204-1215), one
+    id per row: the first id of the largest logit above -1e30."""
+    x = np.ascontiguousarray(logits, np.float32)
+    if x.ndim == 1:
+        x = x.reshape(1, -1)
+    rows = x.shape[0] if rows is None else rows
+    stride = x.shape[1] if stride is None else stride
+    out = np.zeros(rows, np.int32)
+    lib().orc_wasm_greedy(_ptr(x, ctypes.c_float), rows, stride, vocab,
                           _ptr(out, ctypes.c_int32))
     return out
 

@@ -350,3 +350,23 @@ void orc_wgsl_argmax(const float *logits, int64_t rows, int64_t stride, int64_t 
     tokens[r] = (int32_t)sidx[0];   /* src/kernels.ts:1650-1652 */
   }
 }
+
+/* src/wasm-backend.ts:1204-1215: the Wasm backend's greedy route.  bestVal
+ * starts at the binary64 -1e30 and each logit (read exactly from its
+ * Float32Array) replaces it only when strictly larger. */
+void orc_wasm_greedy(const float *logits, int64_t rows, int64_t stride, int64_t vocab,
+                     int32_t *tokens) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float *row = logits + r * stride;
+    double best_val = -1e30;
+    int32_t best_idx = 0;
+    for (int64_t i = 0; i < vocab; ++i) {
+      const double v = (double)row[i];
+      if (v > best_val) {
+        best_val = v;
+        best_idx = (int32_t)i;
+      }
+    }
+    tokens[r] = best_idx;
+  }
+}

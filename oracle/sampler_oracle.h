@@ -92,6 +92,11 @@ int orc_topk_slots(const float *logits, int64_t vocab, int64_t k, int method,
 void orc_wgsl_argmax(const float *logits, int64_t rows, int64_t stride, int64_t vocab,
                      int32_t *tokens);
 
+/* src/wasm-backend.ts:1204-1215: the first id of the largest logit above the
+ * binary64 -1e30 (strict '>'), 0 when none is; one id per row. */
+void orc_wasm_greedy(const float *logits, int64_t rows, int64_t stride, int64_t vocab,
+                     int32_t *tokens);
+
 #ifdef __cplusplus
 }
 #endif

@@ -11,9 +11,14 @@
 //   node dropin_check.js rule <cases.json>       drawRule's decision per case (no GPU)
 //   node dropin_check.js draws <cases.json>      Math.random() calls and tokens of
 //                                                sampleLogits / sampleLogitsBatch
+//   node dropin_check.js greedy <cases.json>     argmaxLogits / nextToken on hand cases
+//   node dropin_check.js backend <name>          createSampler's choice and its info
+//   node dropin_check.js cpu-candidates <dir>    cpu.js sampleLogitsCandidates row by row
 const fs = require('fs');
 const path = require('path');
-const hs = require(path.join(__dirname, '..', '..', 'hachiue_amd', 'js', 'index.js'));
+const mod = require(path.join(__dirname, '..', '..', 'hachiue_amd', 'js', 'index.js'));
+// HS_BACKEND=cpu|auto|hip runs the modes through createSampler on that backend
+const hs = process.env.HS_BACKEND ? mod.createSampler({ backend: process.env.HS_BACKEND }) : mod;
 
 function special(x) {
   return x === 'NaN' ? NaN : x === 'Infinity' ? Infinity : x === '-Infinity' ? -Infinity
@@ -131,7 +136,7 @@ if (mode === 'kat') {
         return cfg[f] === undefined ? DEF[i] : cfg[f];
       }));
       const ids = new Int32Array(c.history);
-      return { name: c.name, rule: hs.drawRule(packed, 0, c.vocab, logits, 0, c.vocab, ids, 0, ids.length) };
+      return { name: c.name, rule: mod.drawRule(packed, 0, c.vocab, logits, 0, c.vocab, ids, 0, ids.length) };
     }
     calls = 0;
     const token = hs.sampleLogits(logits, c.vocab, c.history.slice(), cfg);
@@ -154,6 +159,39 @@ if (mode === 'kat') {
   }
   Math.random = real;
   rows.forEach(function (r) { console.log(JSON.stringify(r)); });
+} else if (mode === 'greedy') {
+  const data = JSON.parse(fs.readFileSync(process.argv[3], 'utf8'));
+  data.cases.forEach(function (c) {
+    const logits = new Float32Array(c.logits.map(special));
+    const before = bits(logits).join();
+    const id = hs.argmaxLogits(logits, c.vocab);
+    const next = hs.nextToken(logits, c.vocab, [], { temperature: 0 });
+    const batch = hs.argmaxLogitsBatch(logits, c.vocab, { rows: 1, stride: c.vocab })[0];
+    console.log(JSON.stringify({ name: c.name, id: id, next: next, batch: batch,
+      unchanged: bits(logits).join() === before }));
+  });
+} else if (mode === 'cpu-candidates') {
+  // the CPU backend's candidate lists, row by row
+  const cpu = require(path.join(__dirname, '..', '..', 'hachiue_amd', 'js', 'cpu.js'));
+  const w = load(process.argv[3]);
+  const s = w.meta.stride;
+  for (let r = 0; r < w.meta.rows; r++) {
+    const row = w.logits.slice(r * s, r * s + s);
+    const cfg = Object.assign({ uniform: w.uniforms[r] }, w.configs[r]);
+    const o = cpu.sampleLogitsCandidates(row, w.meta.vocab, w.history(r), cfg);
+    console.log(JSON.stringify({ row: r, token: o.token, ids: Array.from(o.ids),
+      probs: bits(o.probs), cutoff: o.cutoff }));
+  }
+} else if (mode === 'backend') {
+  const out = {};
+  try {
+    const b = mod.createSampler({ backend: process.argv[3] });
+    out.info = b.info;
+    out.token = b.sampleLogits(new Float32Array([1, 3, 2]), 3, [], { temperature: 0 });
+  } catch (e) {
+    out.error = e.code || e.name;
+  }
+  console.log(JSON.stringify(out));
 } else if (mode === 'nogpu') {
   const out = {};
   out.vocab0 = hs.sampleLogits(new Float32Array([1, 2]), 0, [], {});
