@@ -13,6 +13,7 @@ int orc_block_weights(int type) {
     case ORC_W_F32: return 1;
     case ORC_W_Q4_0: case ORC_W_Q4_1: return 32;
     case ORC_W_Q4_K: case ORC_W_Q6_K: return 256;
+    case ORC_W_Q1_0: case ORC_W_PQ2_0: case ORC_W_PTQ1_0: return 128;
     default: return 0;
   }
 }
@@ -24,6 +25,9 @@ int orc_block_bytes(int type) {
     case ORC_W_Q4_1: return 20;
     case ORC_W_Q4_K: return 144;
     case ORC_W_Q6_K: return 210;
+    case ORC_W_Q1_0: return 18;    /* 2 B binary16 scale + 16 B sign bits */
+    case ORC_W_PQ2_0: return 34;   /* 2 B scale + 32 B 2-bit codes */
+    case ORC_W_PTQ1_0: return 28;  /* 24 B qs + 2 B qh (base-3 trits) + 2 B scale */
     default: return 0;
   }
 }
@@ -62,7 +66,32 @@ static void q6k_weight(const uint8_t *blk, int i, int *q, int *sidx) {
   *sidx = n * 8 + (l >> 4) + 2 * qq;
 }
 
-/* src/gguf.ts:149-230 */
+/* Code c (0, 1 or 2) of weight j of a PTQ1_0 block, and the PTQ1_0 trit of
+ * byte b (src/gguf.ts:111-144): bytes 0..15 hold weights m + 16 n, bytes
+ * 16..23 weights 80 + m + 8 n (n = 0..4), bytes 24..25 weights 120 + h + 2 n
+ * (n = 0..3); trit n of byte b is ((b * 3^n mod 256) * 3) >> 8. */
+static int ptq1_trit(uint8_t b, int n) {
+  static const int pow3[5] = {1, 3, 9, 27, 81};
+  return (((b * pow3[n]) & 0xff) * 3) >> 8;
+}
+static int ptq1_code(const uint8_t *blk, int j) {
+  if (j < 80) return ptq1_trit(blk[j % 16], j / 16);
+  if (j < 120) return ptq1_trit(blk[16 + (j - 80) % 8], (j - 80) / 8);
+  return ptq1_trit(blk[24 + (j - 120) % 2], (j - 120) / 2);
+}
+
+/* Signed multiple of the block scale of weight j of a Q1_0 / PQ2_0 / PTQ1_0
+ * block (src/gguf.ts:95-144): Q1_0 bit ? 1 : -1, PQ2_0 q - 1, PTQ1_0 c - 1. */
+static int tern_code(int type, const uint8_t *blk, int j) {
+  if (type == ORC_W_Q1_0) return ((blk[2 + (j >> 3)] >> (j & 7)) & 1) ? 1 : -1;
+  if (type == ORC_W_PQ2_0) return ((blk[2 + (j >> 2)] >> ((j & 3) * 2)) & 3) - 1;
+  return ptq1_code(blk, j) - 1;
+}
+static uint16_t tern_scale(int type, const uint8_t *blk) {
+  return type == ORC_W_PTQ1_0 ? rd16(blk + 26) : rd16(blk);
+}
+
+/* src/gguf.ts:149-230 and :93-147 */
 int orc_dequant_row(int type, const uint8_t *row, int64_t K, float *out) {
   const int B = orc_block_weights(type), BB = orc_block_bytes(type);
   if (!B || K % B) return -1;
@@ -103,6 +132,9 @@ int orc_dequant_row(int type, const uint8_t *row, int64_t K, float *out) {
         q6k_weight(blk, i, &q, &si);
         o[i] = d * (float)(int8_t)blk[192 + si] * (float)q;
       }
+    } else if (type == ORC_W_Q1_0 || type == ORC_W_PQ2_0 || type == ORC_W_PTQ1_0) {
+      const double d = orc_fp16(tern_scale(type, blk));
+      for (int j = 0; j < 128; ++j) o[j] = (float)(tern_code(type, blk, j) * d);
     } else {
       return -1;
     }
@@ -129,6 +161,8 @@ static double exact_weight(int type, const uint8_t *row, int64_t i) {
     const int q = j < 16 ? (blk[4 + j] & 0x0f) : (blk[4 + j - 16] >> 4);
     return (double)orc_fp16(rd16(blk)) * q + (double)orc_fp16(rd16(blk + 2));
   }
+  if (type == ORC_W_Q1_0 || type == ORC_W_PQ2_0 || type == ORC_W_PTQ1_0)
+    return (double)orc_fp16(tern_scale(type, blk)) * tern_code(type, blk, j);
   if (type == ORC_W_Q4_K) {
     const int sub = j / 32, l = j % 32, p = sub / 2;
     int sc, mn;
@@ -250,6 +284,7 @@ int orc_gemv_ref(int type, const float *x, int64_t M, int64_t K, const uint8_t *
                  float *y) {
   const int B = orc_block_weights(type), BB = orc_block_bytes(type);
   if (!B || K % B || (type == ORC_W_F32 && K % 4)) return -1;
+  if (type == ORC_W_Q1_0 || type == ORC_W_PQ2_0 || type == ORC_W_PTQ1_0) return -1;
   const int64_t row_bytes = K / B * BB;
   float sdata[64];
   for (int64_t m = 0; m < M; ++m) {
@@ -258,6 +293,29 @@ int orc_gemv_ref(int type, const float *x, int64_t M, int64_t K, const uint8_t *
       for (int s = 32; s > 0; s >>= 1)   /* src/kernels.ts:783-787 */
         for (int t = 0; t < s; ++t) sdata[t] = sdata[t] + sdata[t + s];
       y[m * N + n] = sdata[0];
+    }
+  }
+  return 0;
+}
+
+/* src/kernels.ts:177-227 (hadamard_512, mode 0): pre-signs, nine butterfly
+ * stages h = 1 .. 256 over pairs (j, j + h), binary32 norm. */
+int orc_hadamard512(float *x, int64_t rows, int64_t width, const float *signs) {
+  if (width <= 0 || width % 512) return -1;
+  const float norm = (float)0.04419417382415922;
+  for (int64_t r = 0; r < rows; ++r) {
+    for (int64_t c0 = 0; c0 < width; c0 += 512) {
+      float *v = x + r * width + c0;
+      if (signs)
+        for (int i = 0; i < 512; ++i) v[i] = v[i] * signs[c0 + i];
+      for (int h = 1; h < 512; h <<= 1)
+        for (int i = 0; i < 512; i += 2 * h)
+          for (int j = i; j < i + h; ++j) {
+            const float a = v[j], b = v[j + h];
+            v[j] = a + b;
+            v[j + h] = a - b;
+          }
+      for (int i = 0; i < 512; ++i) v[i] = v[i] * norm;
     }
   }
   return 0;

@@ -131,6 +131,9 @@ def lib() -> ctypes.CDLL:
         L.orc_gemv_ref.argtypes = [ctypes.c_int, P(ctypes.c_float), ctypes.c_int64,
                                    ctypes.c_int64, P(ctypes.c_uint8), ctypes.c_int64,
                                    P(ctypes.c_float)]
+        L.orc_hadamard512.restype = ctypes.c_int
+        L.orc_hadamard512.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int64,
+                                      P(ctypes.c_float)]
         L.orc_wgsl_argmax.restype = None
         L.orc_wgsl_argmax.argtypes = [P(ctypes.c_float), ctypes.c_int64, ctypes.c_int64,
                                       ctypes.c_int64, P(ctypes.c_int32)]
@@ -327,6 +330,7 @@ def wasm_greedy(logits: np.ndarray, vocab: int, rows: int | None = None,
 
 # ---- lm_head GEMV (oracle/lmhead_oracle.h) ----------------------------------
 W_F32, W_Q4_0, W_Q4_1, W_Q4_K, W_Q6_K = 0, 2, 3, 12, 14
+W_Q1_0, W_PQ2_0, W_PTQ1_0 = 41, 142, 143
 
 
 def block_spec(wtype: int) -> tuple[int, int]:
@@ -359,6 +363,18 @@ def gemv_exact(wtype: int, x: np.ndarray, w: np.ndarray, N: int):
                             _ptr(y, ctypes.c_double), _ptr(mag, ctypes.c_double)):
         raise ValueError("bad type or K")
     return y, mag
+
+
+def hadamard512(x: np.ndarray, signs: np.ndarray | None = None) -> np.ndarray:
+    """The 512-wide rotation of a hadamard-folded weight's input
+    (src/kernels.ts:177-227, mode 0): a rotated copy of x [M x K]."""
+    y = np.array(x, np.float32, copy=True, order="C")
+    y2 = y.reshape(-1, y.shape[-1])
+    s = None if signs is None else np.ascontiguousarray(signs, np.float32)
+    if lib().orc_hadamard512(_ptr(y2, ctypes.c_float), y2.shape[0], y2.shape[1],
+                             _ptr(s, ctypes.c_float)):
+        raise ValueError("width must be a multiple of 512")
+    return y
 
 
 def gemv_ref(wtype: int, x: np.ndarray, w: np.ndarray, N: int) -> np.ndarray:

@@ -1,21 +1,29 @@
 """The lm_head GEMV oracle (oracle/lmhead_oracle.c) pinned without the C
 code's own formulas:
 
-- the reference's golden Q4_0 / Q4_1 blocks (test/gguf.test.ts:117-143);
+- the reference's golden Q4_0 / Q4_1 blocks (test/gguf.test.ts:117-143) and
+  its Q1_0 / PQ2_0 / PTQ1_0 blocks (test/gguf.test.ts:32-115);
+- the 512-wide Hadamard rotation against the dense Sylvester matrix, its
+  own inverse, and exact answers on integer inputs (test/gguf.test.ts:146-181);
 - binary16 conversion against numpy's float16 on every bit pattern;
-- dequantisation against an independent vectorised numpy decoder;
+- dequantisation against an independent vectorised numpy decoder (PTQ1_0
+  trits as base-3 digits of floor(243 b / 256));
 - K-quant bit layouts by round trips through packers written from the block
   layouts (scale index = weight / 16 for Q6_K, the 6-bit scale/min packing
   of Q4_K), so that a wrong shift or index in the decoder fails;
 - the exact GEMV against numpy's float64 product of the decoded weights;
 - the reference-order binary32 GEMV within the rounding bound of its sum.
 """
+import json
+import os
+
 import numpy as np
 import pytest
 
 from oracle import pyoracle as o
 
 TYPES = [o.W_F32, o.W_Q4_0, o.W_Q4_1, o.W_Q4_K, o.W_Q6_K]
+TERNARY = [o.W_Q1_0, o.W_PQ2_0, o.W_PTQ1_0]
 
 
 def f16_bytes(vals):
@@ -40,6 +48,10 @@ def random_blocks(wtype, n_rows, K, rng, scale=0.02):
         raw[:, :, 2:4] = dmin.view(np.uint8).reshape(n_rows, nb, 2)
     if wtype == o.W_Q6_K:
         raw[:, :, 208:210] = d.view(np.uint8).reshape(n_rows, nb, 2)
+    if wtype in (o.W_Q1_0, o.W_PQ2_0):
+        raw[:, :, 0:2] = d.view(np.uint8).reshape(n_rows, nb, 2)
+    if wtype == o.W_PTQ1_0:
+        raw[:, :, 26:28] = d.view(np.uint8).reshape(n_rows, nb, 2)
     return raw.reshape(n_rows, nb * BB)
 
 
@@ -60,6 +72,25 @@ def np_weights(wtype, w, K):
         else:
             out = q * h(b, 0)[..., None] + h(b, 2)[..., None]
         return out.reshape(n, K)
+    if wtype == o.W_Q1_0:   # bit j of the 16 sign bytes, least significant first
+        bits = np.unpackbits(b[:, :, 2:18], axis=2, bitorder="little").astype(np.float64)
+        return ((2 * bits - 1) * h(b, 0)[..., None]).reshape(n, K)
+    if wtype == o.W_PQ2_0:   # four 2-bit codes per byte, lowest first
+        q = np.stack([(b[:, :, 2:34] >> (2 * i)) & 3 for i in range(4)], axis=3)
+        return ((q.reshape(n, -1, 128).astype(np.float64) - 1) * h(b, 0)[..., None]).reshape(n, K)
+    if wtype == o.W_PTQ1_0:
+        # trit n of a byte = base-3 digit n (most significant first) of
+        # floor(243 b / 256), the inverse of the encoder's ceil(256 q / 243)
+        val = (b[:, :, 0:26].astype(np.int64) * 243) // 256
+        dig = np.stack([(val // 3 ** (4 - i)) % 3 for i in range(5)], axis=3)   # (n, nb, 26, 5)
+        t = np.zeros(b.shape[:2] + (128,), np.int64)
+        for m in range(16):
+            t[:, :, m + 16 * np.arange(5)] = dig[:, :, m, :]
+        for m in range(8):
+            t[:, :, 80 + m + 8 * np.arange(5)] = dig[:, :, 16 + m, :]
+        for hh in range(2):
+            t[:, :, 120 + hh + 2 * np.arange(4)] = dig[:, :, 24 + hh, :4]
+        return ((t.astype(np.float64) - 1) * h(b, 26)[..., None]).reshape(n, K)
     if wtype == o.W_Q4_K:
         s = b[:, :, 4:16].astype(np.int64)
         sc = np.zeros(b.shape[:2] + (8,), np.int64)
@@ -131,6 +162,64 @@ def test_reference_golden_blocks():
     assert o.dequant_row(o.W_Q4_1, q41, 32).tolist() == [2.0] * 16 + [3.0] * 16
 
 
+GOLDEN_BLOCKS = os.path.join(os.path.dirname(__file__), "golden", "ternary_blocks.json")
+
+
+def _golden_blocks():
+    with open(GOLDEN_BLOCKS) as f:
+        return json.load(f)["cases"]
+
+
+@pytest.mark.parametrize("case", _golden_blocks(), ids=lambda c: c["name"])
+def test_reference_golden_128_blocks(case):
+    """test/gguf.test.ts:32-124: Q1_0, PQ2_0 and PTQ1_0 (encoded by the
+    test's own base-3 packer) decode to the test's weights."""
+    B, _ = o.block_spec(case["type"])
+    blk = np.array(case["block"], np.uint8)
+    want = np.array(case["weights"], np.float32)
+    assert np.array_equal(o.dequant_row(case["type"], blk, B), want)
+    assert np.array_equal(np_weights(case["type"], blk.reshape(1, -1), B)[0], want)
+
+
+def _dense_hadamard(n=512):
+    # the reference test's dense Sylvester matrix: sign = parity of popcount(r & c)
+    r = np.arange(n)[:, None] & np.arange(n)[None, :]
+    par = np.zeros_like(r)
+    for b in range(10):
+        par ^= (r >> b) & 1
+    return np.where(par == 1, -1.0, 1.0) / np.sqrt(n)
+
+
+def test_hadamard_matches_dense_and_is_involutory():
+    """test/gguf.test.ts:146-181: the fast rotation equals the dense
+    Sylvester matrix product and applying it twice restores the input."""
+    orig = (np.sin(np.arange(512) * 0.13) - 0.5).astype(np.float32)[None, :]
+    H = _dense_hadamard()
+    fast = o.hadamard512(orig)
+    assert np.max(np.abs(fast[0] - H @ orig[0].astype(np.float64))) < 1e-5
+    assert np.max(np.abs(o.hadamard512(fast) - orig)) < 1e-5
+
+
+def test_hadamard_known_answers_and_signs():
+    norm = np.float32(1 / np.sqrt(512))
+    e0 = np.zeros((1, 1024), np.float32)
+    e0[0, 0] = 1
+    e0[0, 512 + 3] = 2                       # the second block is rotated on its own
+    y = o.hadamard512(e0)
+    assert np.all(y[0, :512] == norm)
+    col = _dense_hadamard()[:, 3] * np.sqrt(512)   # +-1 column 3 of the unnormalised matrix
+    assert np.array_equal(y[0, 512:], (2 * col).astype(np.float32) * norm)
+    # integer inputs: every butterfly sum is exact, so only the norm rounds
+    rng = np.random.default_rng(2)
+    x = rng.integers(-1000, 1000, (3, 512)).astype(np.float32)
+    want = (x.astype(np.float64) @ (_dense_hadamard() * np.sqrt(512)).T).astype(np.float32) * norm
+    assert np.array_equal(o.hadamard512(x), want)
+    # signs multiply the input first
+    signs = np.where(rng.random(1024) < 0.5, -1.0, 1.0).astype(np.float32)
+    x2 = rng.standard_normal((2, 1024)).astype(np.float32)
+    assert np.array_equal(o.hadamard512(x2, signs), o.hadamard512(x2 * signs))
+
+
 def test_fp16_every_pattern():
     h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
     want = h.view(np.float16).astype(np.float32)
@@ -140,7 +229,7 @@ def test_fp16_every_pattern():
     assert np.array_equal(got[ok].view(np.uint32), want[ok].view(np.uint32))
 
 
-@pytest.mark.parametrize("wtype", TYPES)
+@pytest.mark.parametrize("wtype", TYPES + TERNARY)
 def test_dequant_matches_numpy_decoder(wtype):
     rng = np.random.default_rng(wtype)
     K = 512
@@ -176,7 +265,7 @@ def test_q6k_layout_round_trip():
         assert np_weights(o.W_Q6_K, blk.reshape(1, -1), 256)[0].tolist() == want.tolist()
 
 
-@pytest.mark.parametrize("wtype", TYPES)
+@pytest.mark.parametrize("wtype", TYPES + TERNARY)
 def test_exact_gemv_matches_numpy(wtype):
     rng = np.random.default_rng(10 + wtype)
     K, N = 1024, 9
