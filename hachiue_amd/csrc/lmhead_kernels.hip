@@ -691,6 +691,275 @@ __global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_mfma_kernel(GemvArg
   }
 }
 
+// ---- Q1_0 / PQ2_0 / PTQ1_0 on the matrix cores
+//
+// The 128-weight formats of src/gguf.ts:56-63, in the planar form the
+// reference uploads (src/engine.ts:80-175): per row, nb = K / 128 blocks of
+// quant bytes back to back (16 B Q1_0 sign bits, 32 B PQ2_0 2-bit codes,
+// 26 B PTQ1_0 base-3 trits), and a tensor of binary16 block scales.  Weight
+// = d * (c1 * code - 1) with code = the bit (Q1_0, c1 = 2), the 2-bit code
+// (PQ2_0) or the trit (PTQ1_0) (src/gguf.ts:93-147, src/kernels.ts:376-700).
+//
+// As for Q6_K, x is held as four int8 limbs, here per 128-weight block: with
+// 2^E above the block's largest |x|, a_t = rint(r_{t-1} 2^(6 + 7t - E)), so
+// x - sum_t a_t 2^(E - 6 - 7t) is below 2^(E - 28).  A block is eight
+// v_mfma_i32_16x16x64_i8 into one accumulator: B (64 x 16) holds the codes
+// of 16 rows, A (16 x 64) in row 4G + t limb t of lane group G's positions,
+// zero elsewhere.  The four lane groups G of a wave take four consecutive
+// blocks of the same 16 rows, so the result's lane (j, G) holds the four
+// exact limb sums D_t of (row j, block 4r + G), and the block's dot product
+// is sum_t 2^(E - 6 - 7t) (c1 D_t - A_t), A_t the block's limb totals.
+//
+// The codes enter B in the order their bytes decode most cheaply; the
+// position of code k = 4 w + m (byte m of B dword w) of MFMA s is tern_pos,
+// and the A tables are built in that order:
+//   Q1_0   dword s/2 of the block, bits 4 (s & 1) + w of each byte (a shift
+//          and a mask per B dword);
+//   PQ2_0  dword s of the block, codes w of each byte;
+//   PTQ1_0 a 256-entry LDS table gives each byte's trits 0..3 (one dword)
+//          and trit 4: MFMAs 0..5 take the four trits of four bytes, MFMAs
+//          6 and 7 trit 4 of bytes 0..15 and 16..23 and the trits of the two
+//          tail bytes.
+namespace tm {
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kLutBytes = 256 * 8;
+typedef int v4i __attribute__((ext_vector_type(4)));
+}  // namespace tm
+
+// Position in the block (0..127) of code k = 4 w + m of MFMA s.
+template <int FMT>
+__device__ __forceinline__ int tern_pos(int s, int w, int m) {
+  if constexpr (FMT == kW_Q1_0) {
+    return 32 * (s >> 1) + 8 * m + 4 * (s & 1) + w;
+  } else if constexpr (FMT == kW_PQ2_0) {
+    return 16 * s + 4 * m + w;
+  } else {
+    if (s < 4) return 4 * s + w + 16 * m;        // bytes 0..15, trits 0..3
+    if (s < 6) return 80 + 4 * (s - 4) + w + 8 * m;   // bytes 16..23, trits 0..3
+    if (s == 6) return 64 + 4 * w + m;           // trit 4 of bytes 0..15
+    if (w < 2) return 112 + 4 * w + m;           // trit 4 of bytes 16..23
+    return 120 + (w - 2) + 2 * m;                // bytes 24, 25
+  }
+}
+
+size_t gemv_tern_lds_bytes(int K) {
+  const int nb = K / 128;
+  // LUT | A operands [nb][8 MFMAs][4 limbs] | limb totals | limb scales |
+  // exponents | non-finite flag
+  return (size_t)tm::kLutBytes + (size_t)nb * 512 + (size_t)nb * 32 + (size_t)nb * 4 + 16;
+}
+
+__device__ __forceinline__ uint32_t tern_bfi4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  return (a & 0xFFu) | (b & 0xFF00u) | (c & 0xFF0000u) | (d & 0xFF000000u);
+}
+
+template <int FMT>
+__global__ __launch_bounds__(tm::kThreads) void gemv_tern_kernel(GemvArgs g) {
+  using tm::v4i;
+  extern __shared__ uint4 tlds[];
+  constexpr int QB = tern_quant_bytes(FMT);
+  constexpr int C1 = FMT == kW_Q1_0 ? 2 : 1;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m = (int)blockIdx.y;
+  const int K = g.K, nb = K / 128;
+  uint8_t *base = reinterpret_cast<uint8_t *>(tlds);
+  const uint2 *lut = reinterpret_cast<const uint2 *>(base);
+  uint32_t *aop = reinterpret_cast<uint32_t *>(base + tm::kLutBytes);   // [nb][8][4] x 4 dwords
+  v4i *atot = reinterpret_cast<v4i *>(base + tm::kLutBytes + (size_t)nb * 512);
+  float4 *asc = reinterpret_cast<float4 *>(atot + nb);
+  int *aexp = reinterpret_cast<int *>(asc + nb);
+  int *bad = aexp + nb;
+
+  if constexpr (FMT == kW_PTQ1_0) {   // trits of every byte value (src/gguf.ts:111-144)
+    uint2 *lw = reinterpret_cast<uint2 *>(base);
+    for (int v = tid; v < 256; v += tm::kThreads) {
+      uint32_t t[5];
+      uint32_t q = (uint32_t)v;
+#pragma unroll
+      for (int n = 0; n < 5; ++n) {   // trit n = ((v * 3^n mod 256) * 3) >> 8
+        t[n] = (q * 3u) >> 8;
+        q = (q * 3u) & 0xFFu;
+      }
+      lw[v] = make_uint2(t[0] | (t[1] << 8) | (t[2] << 16) | (t[3] << 24), t[4] * 0x01010101u);
+    }
+  }
+  // ---- the limbs of activation row m, once per workgroup
+  const float *xm = g.x + (int64_t)m * g.ldx;
+  if (tid == 0) *bad = 0;
+  for (int b = wave; b < nb; b += tm::kWaves) {   // block exponents
+    const float v0 = xm[128 * b + lane], v1 = xm[128 * b + 64 + lane];
+    float mx = fmaxf(fabsf(v0), fabsf(v1));
+    const bool fin = __builtin_isfinite(v0) && __builtin_isfinite(v1);
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) {
+      int E = 0;
+      (void)frexpf(mx, &E);   // mx < 2^E
+      aexp[b] = E;
+      atot[b] = v4i{0, 0, 0, 0};
+      asc[b] = make_float4(ldexpf(1.f, E - 6), ldexpf(1.f, E - 13), ldexpf(1.f, E - 20),
+                           ldexpf(1.f, E - 27));
+    }
+    if (__ballot(!fin) && lane == 0) *bad = 1;
+  }
+  __syncthreads();
+  for (int it = tid; it < nb * 32; it += tm::kThreads) {   // item (b, s, w): 4 codes
+    const int b = it >> 5, s = (it >> 2) & 7, w = it & 3;
+    const int E = aexp[b];
+    uint32_t limb[4] = {0u, 0u, 0u, 0u};
+    int At[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+      float r = xm[128 * b + tern_pos<FMT>(s, w, mm)];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float a = rintf(ldexpf(r, 6 + 7 * t - E));
+        r -= ldexpf(a, E - 6 - 7 * t);   // exact: within half a step of r
+        const int ai = (int)a;
+        At[t] += ai;
+        limb[t] |= ((uint32_t)ai & 0xFFu) << (8 * mm);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      aop[((b * 8 + s) * 4 + t) * 4 + w] = limb[t];
+      atomicAdd(reinterpret_cast<int *>(&atot[b]) + t, At[t]);
+    }
+  }
+  __syncthreads();
+  const bool nonfinite = *bad != 0;
+
+  // ---- tiles of 16 rows, one wave each
+  // both resources cover their tensor rounded up to whole dwords: a dword
+  // read that straddles the limit would return 0 for its valid bytes too
+  // (the last PTQ1_0 block ends 2 bytes into a dword)
+  const rsrc_t rq = wrsrc(g.w, (g.w_bytes + 3u) & ~3u), rs = wrsrc(g.scales, (g.s_bytes + 3u) & ~3u);
+  const int j = lane & 15, G = lane >> 4, tl = lane & 3;
+  const bool a_live = ((lane & 15) >> 2) == G;
+  const int ntiles = (g.N + 15) >> 4, nr = (nb + 3) >> 2;
+  const int nw = (int)gridDim.x * tm::kWaves;
+  for (int tile = (int)blockIdx.x * tm::kWaves + wave; tile < ntiles; tile += nw) {
+    const int row = tile * 16 + j;
+    float acc = 0.f;
+    for (int r = 0; r < nr; ++r) {
+      const int b = 4 * r + G;
+      const bool live = b < nb && row < g.N;
+      const uint32_t blk = (uint32_t)row * (uint32_t)nb + (uint32_t)b;
+      const uint32_t qo = live ? blk * (uint32_t)QB : 0xFFFFFFF0u;   // past the resource: zeros
+      const uint32_t so = live ? blk * 2u : 0xFFFFFFF0u;
+      const uint32_t dw = __builtin_amdgcn_raw_buffer_load_b32(rs, so & ~3u, 0, 0);
+      const float d = h2f(dw >> (8u * (so & 2u)));
+      v4i D = v4i{0, 0, 0, 0};
+      const v4i *ab = reinterpret_cast<const v4i *>(aop) + (size_t)(b < nb ? b : 0) * 32 + tl;
+      auto mfma = [&](int s, v4i B) {
+        const v4i al = ab[s * 4];
+        const v4i A = a_live && b < nb ? al : v4i{0, 0, 0, 0};
+        D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, D, 0, 0, 0);
+      };
+      if constexpr (FMT == kW_Q1_0) {
+        const auto q = __builtin_amdgcn_raw_buffer_load_b128(rq, qo, 0, 0);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const uint32_t wd = (uint32_t)q[s >> 1];
+          v4i B;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) B[w] = (int)((wd >> (4 * (s & 1) + w)) & 0x01010101u);
+          mfma(s, B);
+        }
+      } else if constexpr (FMT == kW_PQ2_0) {
+        const auto q0 = __builtin_amdgcn_raw_buffer_load_b128(rq, qo, 0, 0);
+        const auto q1 = __builtin_amdgcn_raw_buffer_load_b128(rq, live ? qo + 16u : qo, 0, 0);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const uint32_t wd = (uint32_t)(s < 4 ? q0[s & 3] : q1[s & 3]);
+          v4i B;
+#pragma unroll
+          for (int w = 0; w < 4; ++w) B[w] = (int)((wd >> (2 * w)) & 0x03030303u);
+          mfma(s, B);
+        }
+      } else {
+        // 26 bytes from an even offset: seven aligned dwords, realigned
+        const uint32_t a0 = qo & ~3u, sh = qo & 3u;
+        uint32_t dd[7];
+#pragma unroll
+        for (int i = 0; i < 7; ++i)
+          dd[i] = __builtin_amdgcn_raw_buffer_load_b32(rq, live ? a0 + 4u * i : 0xFFFFFFF0u, 0, 0);
+        uint32_t q[7];
+#pragma unroll
+        for (int i = 0; i < 6; ++i) q[i] = __builtin_amdgcn_alignbyte(dd[i + 1], dd[i], sh);
+        q[6] = __builtin_amdgcn_alignbyte(0u, dd[6], sh);
+        uint2 e[26];
+#pragma unroll
+        for (int i = 0; i < 26; ++i) e[i] = lut[(q[i >> 2] >> (8 * (i & 3))) & 0xFFu];
+#pragma unroll
+        for (int s = 0; s < 6; ++s) {
+          const int b0 = s < 4 ? 4 * s : 16 + 4 * (s - 4);
+          mfma(s, v4i{(int)e[b0].x, (int)e[b0 + 1].x, (int)e[b0 + 2].x, (int)e[b0 + 3].x});
+        }
+        v4i B6;
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          B6[w] = (int)tern_bfi4(e[4 * w].y, e[4 * w + 1].y, e[4 * w + 2].y, e[4 * w + 3].y);
+        mfma(6, B6);
+        mfma(7, v4i{(int)tern_bfi4(e[16].y, e[17].y, e[18].y, e[19].y),
+                    (int)tern_bfi4(e[20].y, e[21].y, e[22].y, e[23].y), (int)e[24].x,
+                    (int)e[25].x});
+      }
+      if (b < nb) {
+        const v4i at = atot[b];
+        const float4 sc = asc[b];
+        float val = (float)(C1 * D[0] - at[0]) * sc.x;
+        val = fmaf((float)(C1 * D[1] - at[1]), sc.y, val);
+        val = fmaf((float)(C1 * D[2] - at[2]), sc.z, val);
+        val = fmaf((float)(C1 * D[3] - at[3]), sc.w, val);
+        acc = fmaf(d, val, acc);
+      }
+    }
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    if (lane < 16 && row < g.N)
+      g.y[(int64_t)m * g.ldy + row] = nonfinite ? __builtin_nanf("") : acc;
+  }
+}
+
+// ---- the 512-wide Hadamard rotation (src/kernels.ts:177-227, mode 0)
+//
+// One 256-thread workgroup per (row, 512-block), two values per thread: the
+// signs first, then the nine butterfly stages over pairs (i, i + h) in LDS
+// (a + b, a - b in binary32: the same network as the reference's, so the
+// same values), then binary32(1 / sqrt(512)).
+__global__ __launch_bounds__(256) void hadamard_kernel(const float *x, int64_t ldx,
+                                                       const float *signs, float *out, int K) {
+  __shared__ float sh[512];
+  const int tid = threadIdx.x;
+  const int bpr = K >> 9;
+  const int row = (int)blockIdx.x / bpr, c0 = ((int)blockIdx.x % bpr) * 512;
+  const float *src = x + (int64_t)row * ldx + c0;
+  float v0 = src[tid], v1 = src[tid + 256];
+  if (signs) {
+    v0 = v0 * signs[c0 + tid];
+    v1 = v1 * signs[c0 + tid + 256];
+  }
+  sh[tid] = v0;
+  sh[tid + 256] = v1;
+  __syncthreads();
+#pragma unroll
+  for (int st = 0; st < 9; ++st) {
+    const int h = 1 << st;
+    const int i0 = ((tid >> st) << (st + 1)) | (tid & (h - 1));
+    const float a = sh[i0], b = sh[i0 + h];
+    __syncthreads();
+    sh[i0] = a + b;
+    sh[i0 + h] = a - b;
+    __syncthreads();
+  }
+  const float norm = 0.04419417382415922f;
+  float *dst = out + (int64_t)row * K + c0;
+  dst[tid] = sh[tid] * norm;
+  dst[tid + 256] = sh[tid + 256] * norm;
+}
+
 namespace {
 
 // Workgroups that are resident at once on the current GPU, cached per
@@ -765,14 +1034,47 @@ hipError_t launch_q6k_mfma(GemvArgs g, hipStream_t stream, hipEvent_t *ev, hipEv
   return hipGetLastError();
 }
 
+template <int FMT>
+hipError_t launch_tern(GemvArgs g, hipStream_t stream, hipEvent_t *ev, hipEvent_t done) {
+  const size_t lds = gemv_tern_lds_bytes(g.K);
+  const int ntiles = (g.N + 15) / 16;
+  const int res = resident_blocks(reinterpret_cast<const void *>(gemv_tern_kernel<FMT>),
+                                  (uint32_t)lds, tm::kThreads);
+  int blocks = (ntiles + tm::kWaves - 1) / tm::kWaves;
+  blocks = blocks < res ? blocks : res;
+  const dim3 grid((unsigned)blocks, (unsigned)g.M), block(tm::kThreads);
+  if (ev)
+    hipExtLaunchKernelGGL(gemv_tern_kernel<FMT>, grid, block, lds, stream, ev[0], ev[1], 0u, g);
+  else if (done)
+    hipExtLaunchKernelGGL(gemv_tern_kernel<FMT>, grid, block, lds, stream, nullptr, done, 0u, g);
+  else
+    hipLaunchKernelGGL(gemv_tern_kernel<FMT>, grid, block, lds, stream, g);
+  return hipGetLastError();
+}
+
 }  // namespace
 
-// Per device, once (with the sampler's kernels): the Q6_K kernel's dynamic
-// LDS limit.
+// Per device, once (with the sampler's kernels): the matrix-core kernels'
+// dynamic LDS limits.
 hipError_t prepare_gemv() {
-  return hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_q6k_mfma_kernel),
-                             hipFuncAttributeMaxDynamicSharedMemorySize,
-                             (int)gemv_q6k_mfma_lds_bytes(kGemvMaxK));
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_q6k_mfma_kernel),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)gemv_q6k_mfma_lds_bytes(kGemvMaxK));
+  const void *tk[3] = {reinterpret_cast<const void *>(gemv_tern_kernel<kW_Q1_0>),
+                       reinterpret_cast<const void *>(gemv_tern_kernel<kW_PQ2_0>),
+                       reinterpret_cast<const void *>(gemv_tern_kernel<kW_PTQ1_0>)};
+  for (const void *f : tk)
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)gemv_tern_lds_bytes(kGemvMaxK));
+  return e;
+}
+
+hipError_t launch_hadamard(const float *x, int64_t ldx, const float *signs, float *out, int M,
+                           int K, hipStream_t stream) {
+  const unsigned blocks = (unsigned)M * (unsigned)(K / 512);
+  hipLaunchKernelGGL(hadamard_kernel, dim3(blocks), dim3(256), 0, stream, x, ldx, signs, out, K);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemv(const GemvArgs &g, hipStream_t stream, hipEvent_t *ev, hipEvent_t done) {
@@ -783,6 +1085,9 @@ hipError_t launch_gemv(const GemvArgs &g, hipStream_t stream, hipEvent_t *ev, hi
     case kW_Q4_1: return two ? launch_fmt<kW_Q4_1, 2>(g, stream, ev, done) : launch_fmt<kW_Q4_1, 1>(g, stream, ev, done);
     case kW_Q4_K: return two ? launch_fmt<kW_Q4_K, 2>(g, stream, ev, done) : launch_fmt<kW_Q4_K, 1>(g, stream, ev, done);
     case kW_Q6_K: return launch_q6k_mfma(g, stream, ev, done);
+    case kW_Q1_0: return launch_tern<kW_Q1_0>(g, stream, ev, done);
+    case kW_PQ2_0: return launch_tern<kW_PQ2_0>(g, stream, ev, done);
+    case kW_PTQ1_0: return launch_tern<kW_PTQ1_0>(g, stream, ev, done);
     default: return hipErrorInvalidValue;
   }
 }

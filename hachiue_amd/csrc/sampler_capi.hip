@@ -123,6 +123,7 @@ struct hs_context {
   DevBuf plans, cand, cand_count, info;
   DevBuf split_list, split_meta, split_cnt;   // split rows (split_cnt: zero between calls)
   DevBuf gemv_part, gemv_cnt;   // Q6_K GEMV tiles cut between waves (gemv_cnt: zero between calls)
+  DevBuf gemv_rot;              // the Hadamard-rotated input of a folded weight
   DevBuf large_retry;           // two-pass large-k rows handed back
   DevBuf large_replay;          // slot-history replays asked for by the large-k kernel
   int64_t cand_count_rows = 0;     // rows whose counter is known to be zero
@@ -575,10 +576,12 @@ int argmax_device(hs_context *ctx, const float *d_logits, int32_t rows, int64_t 
 }
 
 // src/engine.ts:1493-1515 (the lm_head GEMV; see lmhead_kernels.hip).
-int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32_t K,
-                const void *d_w, int32_t w_type, int32_t N, float *d_y, int64_t ldy,
-                hipStream_t stream) {
+int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const hs_weights *wt,
+                float *d_y, int64_t ldy, hipStream_t stream) {
   if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  if (!wt) return fail(HS_ERR_INVALID_ARGUMENT, "null weights");
+  const int32_t K = wt->cols, N = wt->rows, w_type = wt->type;
+  const void *d_w = wt->data;
   if (M < 0 || N < 0 || K <= 0)
     return fail(HS_ERR_INVALID_ARGUMENT, "need M >= 0, N >= 0, K > 0 (got %d, %d, %d)", M, N, K);
   if (M == 0 || N == 0) return HS_OK;
@@ -586,19 +589,31 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32
   if (ldx < K || ldy < N)
     return fail(HS_ERR_INVALID_ARGUMENT, "ldx %lld < K or ldy %lld < N", (long long)ldx, (long long)ldy);
   int bw = 0, bb = 0;
+  const bool planar = hs::tern_quant_bytes(w_type) > 0;
   switch (w_type) {
     case hs::kW_F32: bw = 32; bb = 128; break;   // as 32-weight units
     case hs::kW_Q4_0: bw = 32; bb = 18; break;
     case hs::kW_Q4_1: bw = 32; bb = 20; break;
     case hs::kW_Q4_K: bw = 256; bb = 144; break;
     case hs::kW_Q6_K: bw = 256; bb = 210; break;
+    case hs::kW_Q1_0: case hs::kW_PQ2_0: case hs::kW_PTQ1_0:
+      bw = 128; bb = hs::tern_quant_bytes(w_type); break;
     default: return fail(HS_ERR_UNSUPPORTED, "weight type %d is not supported", w_type);
   }
   if (K % bw)
     return fail(HS_ERR_INVALID_ARGUMENT, "K %d is not a multiple of the block size %d", K, bw);
   if (K > hs::kGemvMaxK) return fail(HS_ERR_UNSUPPORTED, "K %d above %d", K, hs::kGemvMaxK);
-  if ((reinterpret_cast<uintptr_t>(d_w) & 15u) || (reinterpret_cast<uintptr_t>(d_x) & 3u))
-    return fail(HS_ERR_INVALID_ARGUMENT, "w must be 16-byte and x 4-byte aligned");
+  if (planar && !wt->scales16)
+    return fail(HS_ERR_INVALID_ARGUMENT, "weight type %d needs its binary16 scales", w_type);
+  if (!planar && wt->scales16)
+    return fail(HS_ERR_INVALID_ARGUMENT, "scales16 is for types 41, 142 and 143 only");
+  if (wt->hadamard && K % 512)
+    return fail(HS_ERR_INVALID_ARGUMENT, "a Hadamard-folded weight needs K %% 512 == 0 (K = %d)", K);
+  const uintptr_t walign = planar ? (w_type == hs::kW_PTQ1_0 ? 3u : 15u) : 15u;
+  if ((reinterpret_cast<uintptr_t>(d_w) & walign) || (reinterpret_cast<uintptr_t>(d_x) & 3u) ||
+      (reinterpret_cast<uintptr_t>(wt->scales16) & 3u))
+    return fail(HS_ERR_INVALID_ARGUMENT,
+                "w must be 16-byte (PTQ1_0 quants 4-byte), scales and x 4-byte aligned");
   const int64_t row_bytes = (int64_t)(K / bw) * bb;
   // (Q6_K's slabs read up to 3 KiB past a row's start)
   if ((int64_t)N * row_bytes > (w_type == hs::kW_Q6_K ? 0xFFFF0000LL : 0xFFFFFF00LL))
@@ -608,6 +623,8 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32
   g.x = d_x;
   g.ldx = ldx;
   g.w = d_w;
+  g.scales = wt->scales16;
+  g.s_bytes = planar ? (uint32_t)((int64_t)N * (K / 128) * 2) : 0u;
   g.w_bytes = (uint32_t)(N * row_bytes);
   g.row_bytes = (uint32_t)row_bytes;
   g.y = d_y;
@@ -629,6 +646,17 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32
   DeviceGuard guard(ctx->device);
   int rc0 = enter_stream(ctx, stream);
   if (rc0) return rc0;
+  if (wt->hadamard) {   // src/engine.ts:1121-1145: the input is rotated first
+    HS_HIP(ctx->gemv_rot.ensure((size_t)M * (size_t)K * sizeof(float)));
+    float *rot = static_cast<float *>(ctx->gemv_rot.p);
+    const hipError_t e = hs::launch_hadamard(d_x, ldx, wt->signs, rot, M, K, stream);
+    if (e != hipSuccess) {
+      (void)leave_stream(ctx, stream, false);
+      return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+    }
+    g.x = rot;
+    g.ldx = K;
+  }
   if (w_type == hs::kW_Q6_K) {   // the hand-over slots of tiles cut between waves
     int cus = 0;
     HS_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device));
@@ -941,6 +969,7 @@ int hs_context_destroy(hs_context *ctx) {
     ctx->split_cnt.release();
     ctx->gemv_part.release();
     ctx->gemv_cnt.release();
+    ctx->gemv_rot.release();
     ctx->large_retry.release();
     ctx->large_replay.release();
     ctx->h_logits.release();
@@ -1000,12 +1029,32 @@ int hs_argmax_device(hs_context *ctx, const float *d_logits, int32_t rows, int64
                        static_cast<hipStream_t>(stream));
 }
 
+namespace {
+hs_weights raw_weights(int32_t K, const void *d_w, int32_t w_type, int32_t N) {
+  hs_weights w;
+  memset(&w, 0, sizeof w);
+  w.type = w_type;
+  w.rows = N;
+  w.cols = K;
+  w.data = d_w;
+  return w;
+}
+}  // namespace
+
 int hs_gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32_t K,
                    const void *d_w, int32_t w_type, int32_t N, float *d_y, int64_t ldy,
                    void *stream) {
   HS_LOCK(ctx);
-  return gemv_device(ctx, d_x, M, ldx, K, d_w, w_type, N, d_y, ldy,
-                     static_cast<hipStream_t>(stream));
+  if (hs::tern_quant_bytes(w_type) > 0)
+    return fail(HS_ERR_INVALID_ARGUMENT, "weight type %d is planar: use hs_gemv_device_ex", w_type);
+  const hs_weights w = raw_weights(K, d_w, w_type, N);
+  return gemv_device(ctx, d_x, M, ldx, &w, d_y, ldy, static_cast<hipStream_t>(stream));
+}
+
+int hs_gemv_device_ex(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx,
+                      const hs_weights *w, float *d_y, int64_t ldy, void *stream) {
+  HS_LOCK(ctx);
+  return gemv_device(ctx, d_x, M, ldx, w, d_y, ldy, static_cast<hipStream_t>(stream));
 }
 
 int hs_lm_head_sample_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32_t K,
@@ -1014,11 +1063,51 @@ int hs_lm_head_sample_device(hs_context *ctx, const float *d_x, int32_t M, int64
                              const hs_sample_config *configs, const double *d_uniforms,
                              int32_t *d_tokens, void *stream) {
   HS_LOCK(ctx);
+  if (hs::tern_quant_bytes(w_type) > 0)
+    return fail(HS_ERR_INVALID_ARGUMENT, "weight type %d is planar: use hs_lm_head_sample_device_ex",
+                w_type);
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  int rc = gemv_device(ctx, d_x, M, ldx, K, d_w, w_type, N, d_logits, ldl, st);
+  const hs_weights w = raw_weights(K, d_w, w_type, N);
+  int rc = gemv_device(ctx, d_x, M, ldx, &w, d_logits, ldl, st);
   if (rc) return rc;
   return sample_device(ctx, d_logits, M, ldl, N, d_hist_ids, d_hist_offsets, configs, d_uniforms,
                        d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr, st);
+}
+
+int hs_lm_head_sample_device_ex(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx,
+                                const hs_weights *w, float *d_logits, int64_t ldl,
+                                const int32_t *d_hist_ids, const int64_t *d_hist_offsets,
+                                const hs_sample_config *configs, const double *d_uniforms,
+                                int32_t *d_tokens, void *stream) {
+  HS_LOCK(ctx);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  int rc = gemv_device(ctx, d_x, M, ldx, w, d_logits, ldl, st);
+  if (rc) return rc;
+  return sample_device(ctx, d_logits, M, ldl, w->rows, d_hist_ids, d_hist_offsets, configs,
+                       d_uniforms, d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr, st);
+}
+
+// src/engine.ts:80-175 (createBlockSplitter): GGUF blocks of Q1_0 ([d][16 B
+// signs]), PQ2_0 ([d][32 B codes]) or PTQ1_0 ([24 B qs][2 B qh][d]) into the
+// planar quants and binary16 scales the GEMV reads.
+int hs_split_blocks(int32_t type, const void *blocks, int64_t n_blocks, void *quants,
+                    void *scales16) {
+  const int qb = hs::tern_quant_bytes(type);
+  if (qb == 0) return fail(HS_ERR_INVALID_ARGUMENT, "type %d has no planar form", type);
+  if (n_blocks < 0) return fail(HS_ERR_INVALID_ARGUMENT, "n_blocks must be >= 0");
+  if (n_blocks > 0 && (!blocks || !quants || !scales16))
+    return fail(HS_ERR_INVALID_ARGUMENT, "blocks, quants and scales16 must not be null");
+  const int bb = qb + 2;
+  const uint8_t *src = static_cast<const uint8_t *>(blocks);
+  uint8_t *q = static_cast<uint8_t *>(quants);
+  uint8_t *sc = static_cast<uint8_t *>(scales16);
+  const bool scale_last = type == hs::kW_PTQ1_0;
+  for (int64_t b = 0; b < n_blocks; ++b) {
+    const uint8_t *blk = src + b * bb;
+    memcpy(q + b * qb, scale_last ? blk : blk + 2, (size_t)qb);
+    memcpy(sc + b * 2, scale_last ? blk + qb : blk, 2);
+  }
+  return HS_OK;
 }
 
 // src/engine.ts:1626-1644 (one step of the decode loop) with the token

@@ -183,6 +183,12 @@ constexpr int kArgmaxMaxVocab = 1 << 28;
 // ---- lm_head GEMV (lmhead_kernels.hip)
 // GGML type ids of the weight formats (src/types.ts:4-15).
 constexpr int kW_F32 = 0, kW_Q4_0 = 2, kW_Q4_1 = 3, kW_Q4_K = 12, kW_Q6_K = 14;
+// 128-weight binary / ternary formats, planar (quants and binary16 scales
+// in two tensors, src/engine.ts:80-175): quant bytes per block
+constexpr int kW_Q1_0 = 41, kW_PQ2_0 = 142, kW_PTQ1_0 = 143;
+constexpr int tern_quant_bytes(int type) {
+  return type == kW_Q1_0 ? 16 : type == kW_PQ2_0 ? 32 : type == kW_PTQ1_0 ? 26 : 0;
+}
 constexpr int kGemvThreads = 256;
 constexpr int kGemvMaxK = 4096;       // x slices live in registers
 constexpr int kGemvTimedSlot = 7;     // its start/end events in a timed call
@@ -203,7 +209,16 @@ struct GemvArgs {
   float *part;
   uint32_t *tile_cnt;
   int32_t part_cap;          // at least the waves of one activation row
+  // Q1_0 / PQ2_0 / PTQ1_0: w holds the planar quants, scales the binary16
+  // block scales (N * K / 128 of each), s_bytes their size
+  const void *scales;
+  uint32_t s_bytes;
 };
+// The 512-wide Hadamard rotation of a hadamard-folded weight's input
+// (src/kernels.ts:177-227, mode 0): out[m][k] for m < M, k < K (K a multiple
+// of 512), from x [M][ldx] and optional +-1 signs [K].
+hipError_t launch_hadamard(const float *x, int64_t ldx, const float *signs, float *out, int M,
+                           int K, hipStream_t stream);
 constexpr int kGemvWavesPerCU = 16;   // Q6_K: the part_cap a CU needs
 // Block formats go through LDS in batches of row steps (a step: the rows of
 // one wave pass, 64 units): steps per batch and 16-byte reads per lane that

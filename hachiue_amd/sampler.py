@@ -36,7 +36,8 @@ EXPORTS = ("hs_abi_version", "hs_last_error", "hs_config_default", "hs_context_c
            "hs_context_destroy", "hs_sample_logits", "hs_sample_logits_batch",
            "hs_sample_batch_device", "hs_sample_batch_device_ex",
            "hs_sample_batch_device_noalloc", "hs_argmax_device",
-           "hs_argmax", "hs_gemv_device", "hs_lm_head_sample_device", "hs_decode_step_device",
+           "hs_argmax", "hs_gemv_device", "hs_gemv_device_ex", "hs_split_blocks",
+           "hs_lm_head_sample_device", "hs_lm_head_sample_device_ex", "hs_decode_step_device",
            "hs_context_set_timing", "hs_context_kernel_times")
 
 
@@ -44,6 +45,39 @@ class SamplerError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(f"{ERROR_NAMES.get(status, status)}: {message}")
         self.status = status
+
+
+class WeightsC(ctypes.Structure):
+    """hs_weights (include/hachiue_sampler.h): a weight tensor as the
+    reference's GPU holds it (src/engine.ts:736-800)."""
+    _fields_ = [("type", ctypes.c_int32), ("rows", ctypes.c_int32), ("cols", ctypes.c_int32),
+                ("hadamard", ctypes.c_int32), ("data", ctypes.c_void_p),
+                ("scales16", ctypes.c_void_p), ("signs", ctypes.c_void_p)]
+
+
+PLANAR_QUANT_BYTES = {41: 16, 142: 32, 143: 26}   # Q1_0, PQ2_0, PTQ1_0
+
+
+def split_blocks(wtype: int, blocks) -> tuple[np.ndarray, np.ndarray]:
+    """GGUF blocks of Q1_0 / PQ2_0 / PTQ1_0 -> (planar quants, binary16
+    scales as uint8), through hs_split_blocks (src/engine.ts:80-175)."""
+    qb = PLANAR_QUANT_BYTES[wtype]
+    raw = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+    n = raw.size // (qb + 2)
+    if n * (qb + 2) != raw.size:
+        raise ValueError("not a whole number of blocks")
+    q = np.zeros(max(n * qb, 1), np.uint8)
+    sc = np.zeros(max(n * 2, 1), np.uint8)
+    P = ctypes.POINTER(ctypes.c_uint8)
+    _check(lib().hs_split_blocks(int(wtype), raw.ctypes.data_as(P), n, q.ctypes.data_as(P),
+                                 sc.ctypes.data_as(P)))
+    return q[:n * qb], sc[:n * 2]
+
+
+def weights(wtype: int, N: int, K: int, d_data: int, d_scales16: int | None = None,
+            hadamard: bool = False, d_signs: int | None = None) -> WeightsC:
+    return WeightsC(int(wtype), int(N), int(K), 1 if hadamard else 0, d_data, d_scales16 or None,
+                    d_signs or None)
 
 
 class SampleConfigC(ctypes.Structure):
@@ -112,6 +146,10 @@ def _load() -> ctypes.CDLL:
     L.hs_gemv_device.argtypes = [vp, vp, i32, i64, i32, vp, i32, i32, vp, i64, vp]
     L.hs_lm_head_sample_device.argtypes = [vp, vp, i32, i64, i32, vp, i32, i32, vp, i64, vp, vp,
                                            P(SampleConfigC), vp, vp, vp]
+    L.hs_gemv_device_ex.argtypes = [vp, vp, i32, i64, P(WeightsC), vp, i64, vp]
+    L.hs_lm_head_sample_device_ex.argtypes = [vp, vp, i32, i64, P(WeightsC), vp, i64, vp, vp,
+                                              P(SampleConfigC), vp, vp, vp]
+    L.hs_split_blocks.argtypes = [i32, vp, i64, vp, vp]
     L.hs_decode_step_device.argtypes = [vp, vp, i32, i64, i32, vp, i64, vp, vp, vp, i32,
                                         P(SampleConfigC), vp, vp, vp]
     L.hs_context_set_timing.argtypes = [vp, ctypes.c_int]
@@ -327,6 +365,26 @@ class Sampler:
         st = stream.handle if isinstance(stream, hip.Stream) else stream
         _check(lib().hs_gemv_device(self._ctx, vp(d_x), int(M), int(ldx), int(K), vp(d_w),
                                     int(w_type), int(N), vp(d_y), int(ldy), st))
+
+    def gemv_device_ex(self, d_x: int, M: int, ldx: int, w: WeightsC, d_y: int, ldy: int,
+                       stream=None) -> None:
+        """y = x W^T for any hs_weights (planar Q1_0 / PQ2_0 / PTQ1_0, and
+        Hadamard-folded weights)."""
+        vp = ctypes.c_void_p
+        st = stream.handle if isinstance(stream, hip.Stream) else stream
+        _check(lib().hs_gemv_device_ex(self._ctx, vp(d_x), int(M), int(ldx), ctypes.byref(w),
+                                       vp(d_y), int(ldy), st))
+
+    def lm_head_sample_device_ex(self, d_x: int, M: int, ldx: int, w: WeightsC, d_logits: int,
+                                 ldl: int, d_hist_ids, d_hist_off, configs, d_uniforms: int,
+                                 d_tokens: int, stream=None) -> None:
+        """gemv_device_ex into d_logits, then sampling of its M rows."""
+        cfgs = configs if isinstance(configs, ctypes.Array) else _configs(configs, M)
+        vp = ctypes.c_void_p
+        st = stream.handle if isinstance(stream, hip.Stream) else stream
+        _check(lib().hs_lm_head_sample_device_ex(
+            self._ctx, vp(d_x), int(M), int(ldx), ctypes.byref(w), vp(d_logits), int(ldl),
+            vp(d_hist_ids or 0), vp(d_hist_off or 0), cfgs, vp(d_uniforms), vp(d_tokens), st))
 
     def lm_head_sample_device(self, d_x: int, M: int, ldx: int, K: int, d_w: int, w_type: int,
                               N: int, d_logits: int, ldl: int, d_hist_ids, d_hist_off, configs,

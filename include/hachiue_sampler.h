@@ -180,7 +180,9 @@ int hs_argmax(hs_context *ctx, const float *logits, int32_t rows,
 /* The logits producer in front of the sampler: hachiue's lm_head GEMV
  * (src/engine.ts:1493-1515, runMatmul of output.weight; WGSL pipelines
  * gemv_f32 / gemv_q4_0 / gemv_q4_1 / gemv_q4_k / gemv_q6_k,
- * src/kernels.ts:244-290, :717-1090).  y[m][n] = sum_k x[m][k] W[n][k] for
+ * src/kernels.ts:244-290, :717-1090; the planar Q1_0 / PQ2_0 / PTQ1_0 and
+ * Hadamard-folded weights go through hs_gemv_device_ex).
+ * y[m][n] = sum_k x[m][k] W[n][k] for
  * m < M, n < N; x is [M][ldx] binary32, y is [M][ldy] binary32, W is the
  * GGUF tensor's raw blocks of `w_type` (GGML ids: 0 F32, 2 Q4_0, 3 Q4_1,
  * 12 Q4_K, 14 Q6_K), N rows of K weights back to back, as the reference
@@ -190,6 +192,53 @@ int hs_argmax(hs_context *ctx, const float *logits, int32_t rows,
 int hs_gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx,
                    int32_t K, const void *d_w, int32_t w_type, int32_t N,
                    float *d_y, int64_t ldy, void *stream);
+
+/* A weight tensor as the reference's GPU holds it (GpuTensor,
+ * src/engine.ts:736-800): its GGML type, N rows of K weights, whether it
+ * was folded with the 512-wide Hadamard rotation (hadamardFolded,
+ * src/engine.ts:816-822), and its data:
+ *   - F32, Q4_0, Q4_1, Q4_K, Q6_K: `data` holds the raw GGUF blocks, rows
+ *     back to back, 16-byte aligned; `scales16` is NULL;
+ *   - Q1_0 (41), PQ2_0 (142), PTQ1_0 (143), 128 weights per block: the
+ *     planar form the reference uploads (src/engine.ts:80-175):
+ *     `data` holds every block's quant bytes (16, 32 or 26 per block; rows
+ *     of K / 128 blocks back to back; 16-byte aligned, PTQ1_0 4-byte),
+ *     `scales16` the blocks' binary16 scales in the same order (4-byte
+ *     aligned).  hs_split_blocks makes both from GGUF blocks.
+ * With `hadamard` set, the GEMV's input is rotated first, as
+ * src/engine.ts:1121-1145 does: each 512-block of x is multiplied by
+ * `signs` (K floats of +-1, or NULL for none; arch.hadamard's sign vector of
+ * width K), transformed by the Walsh-Hadamard butterflies and scaled by
+ * binary32(1/sqrt(512)) (src/kernels.ts:177-227); K must be a multiple of
+ * 512. */
+typedef struct hs_weights {
+  int32_t type;
+  int32_t rows;            /* N */
+  int32_t cols;            /* K */
+  int32_t hadamard;        /* nonzero: hadamardFolded */
+  const void *data;
+  const void *scales16;
+  const float *signs;
+} hs_weights;
+
+/* hs_gemv_device for any hs_weights (the only entry point for the planar
+ * types and for Hadamard-folded weights).  Planar types: every result lies
+ * within 2^-16 * sum_k |x_k w_k| of the exact product, like the others;
+ * their kernel holds x as four 7-bit limbs relative to each 128-block's
+ * largest |x|, so an element below about 2^-28 of that maximum counts as 0.
+ * A non-finite element of an x row makes every result of that row NaN.
+ * Asynchronous on `stream`; a folded weight's rotated input lives in the
+ * context's workspace. */
+int hs_gemv_device_ex(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx,
+                      const hs_weights *w, float *d_y, int64_t ldy, void *stream);
+
+/* GGUF blocks of Q1_0 ([binary16 d][16 B sign bits]), PQ2_0 ([d][32 B
+ * codes]) or PTQ1_0 ([24 B qs][2 B qh][d]) into planar quants
+ * (n_blocks * 16, 32 or 26 bytes) and binary16 scales (n_blocks * 2 bytes),
+ * on the host: the byte split of the reference's upload
+ * (src/engine.ts:80-175 createBlockSplitter). */
+int hs_split_blocks(int32_t type, const void *blocks, int64_t n_blocks, void *quants,
+                    void *scales16);
 
 /* lm_head and sampler in one call on one stream, with no host round trip in
  * between (the reference reads the logits back to the host, src/engine.ts:
@@ -203,6 +252,15 @@ int hs_lm_head_sample_device(hs_context *ctx, const float *d_x, int32_t M,
                              const hs_sample_config *configs,
                              const double *d_uniforms, int32_t *d_tokens,
                              void *stream);
+
+/* hs_lm_head_sample_device for any hs_weights (N = w->rows = vocab). */
+int hs_lm_head_sample_device_ex(hs_context *ctx, const float *d_x, int32_t M,
+                                int64_t ldx, const hs_weights *w, float *d_logits,
+                                int64_t ldl, const int32_t *d_hist_ids,
+                                const int64_t *d_hist_offsets,
+                                const hs_sample_config *configs,
+                                const double *d_uniforms, int32_t *d_tokens,
+                                void *stream);
 
 /* One step of the decode loop with the token history on the GPU
  * (src/engine.ts:1626-1644, whose tokenHistory is a host array, and whose

@@ -71,3 +71,27 @@ def test_timing_calls_reject_null_context():
     assert L.hs_context_set_timing(None, 1) == 1
     ms = (ctypes.c_double * 4)()
     assert L.hs_context_kernel_times(None, ms, 4, None) == 1
+
+
+def test_split_blocks_matches_the_block_layouts():
+    """hs_split_blocks (host) puts each block's quant bytes and binary16
+    scale where the planar GEMV reads them (src/engine.ts:80-175)."""
+    import numpy as np
+    rng = np.random.default_rng(1)
+    for wtype, qb, scale_at in ((41, 16, 0), (142, 32, 0), (143, 26, 26)):
+        blocks = rng.integers(0, 256, (7, qb + 2), dtype=np.uint8)
+        q, sc = sampler.split_blocks(wtype, blocks)
+        for b in range(7):
+            want_q = np.concatenate([blocks[b, :scale_at], blocks[b, scale_at + 2:]])
+            assert np.array_equal(q[b * qb:(b + 1) * qb], want_q)
+            assert np.array_equal(sc[2 * b:2 * b + 2], blocks[b, scale_at:scale_at + 2])
+    with pytest.raises(sampler.SamplerError) as e:
+        sampler._check(sampler.lib().hs_split_blocks(14, None, 1, None, None))
+    assert e.value.status == 1
+
+
+def test_gemv_ex_rejects_bad_weights_without_a_gpu():
+    L = sampler.lib()
+    w = sampler.weights(41, 10, 256, None)
+    rc = L.hs_gemv_device_ex(None, None, 1, 256, ctypes.byref(w), None, 10, None)
+    assert rc == 1 and b"null context" in L.hs_last_error()
