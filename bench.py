@@ -16,8 +16,9 @@ baseline (the JavaScript restatement of sampler.ts under Node on this host).
 Other paths (one JSON line each, same fields):
   --path greedy-route   the engine's greedy route: the WGSL-order argmax over
                         the workload's logits (hs_argmax_device)
-  --path lmhead         the lm_head GEMV (hs_gemv_device) over a synthetic
-                        vocab x hidden weight in GGUF blocks (--wfmt, --hidden)
+  --path lmhead         the lm_head GEMV (hs_gemv_device_ex) over a synthetic
+                        vocab x hidden weight (--wfmt f32|q4_0|q4_1|q4_k|q6_k in GGUF
+                        blocks, q1_0|pq2_0|ptq1_0 planar; --hidden; --hadamard)
 """
 from __future__ import annotations
 
@@ -174,6 +175,8 @@ def main() -> int:
     ap.add_argument("--path", default="sample", choices=["sample", "greedy-route", "lmhead", "decode"])
     ap.add_argument("--wfmt", default="q6_k", help="lm_head weight format (--path lmhead)")
     ap.add_argument("--hidden", type=int, default=2048, help="lm_head K (--path lmhead)")
+    ap.add_argument("--hadamard", action="store_true",
+                    help="Hadamard-folded lm_head: the input is rotated first (--path lmhead)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="end with one device-to-device copy of one input set (the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -392,25 +395,37 @@ def other_path(args) -> int:
                     "appended": int((lens == np.array([len(h) for h in ref.histories])).sum())}
         count = rows
     else:
+        from hachiue_amd.sampler import PLANAR_QUANT_BYTES, split_blocks, weights
         lh = workloads.make_lmhead(args.wfmt, args.hidden)
         rows, vocab, K = lh.x.shape[0], lh.vocab, lh.hidden
         sets = n_sets(lh.weights.nbytes)
-        d_in = [hip.DeviceArray.from_numpy(lh.weights.reshape(-1)) for _ in range(sets)]
+        planar = lh.wtype in PLANAR_QUANT_BYTES
+        if planar:   # the reference's upload: quants and binary16 scales apart
+            q, sc = split_blocks(lh.wtype, lh.weights)
+            d_in = [hip.DeviceArray.from_numpy(q) for _ in range(sets)]
+            d_sc = [hip.DeviceArray.from_numpy(sc) for _ in range(sets)]
+        else:
+            d_in = [hip.DeviceArray.from_numpy(lh.weights.reshape(-1)) for _ in range(sets)]
+            d_sc = [None] * sets
+        wts = [weights(lh.wtype, vocab, K, d_in[i].addr, d_sc[i].addr if d_sc[i] else None,
+                       args.hadamard) for i in range(sets)]
         d_x = hip.DeviceArray.from_numpy(lh.x)
         d_y = hip.DeviceArray((rows, vocab), np.float32)
         kernel, unit = "gemv_kernel", "logit rows/s"
         alg = lh.algorithmic_bytes()
-        desc = (f"lm_head GEMV: {vocab} x {K} {lh.fmt} weights ({lh.weights.nbytes} bytes, GGUF "
-                f"blocks), {rows} hidden state(s)")
+        desc = (f"lm_head GEMV: {vocab} x {K} {lh.fmt} weights ({lh.weights.nbytes} bytes, "
+                f"{'planar quants + binary16 scales' if planar else 'GGUF blocks'}"
+                f"{', Hadamard-folded' if args.hadamard else ''}), {rows} hidden state(s)")
 
         def step(i: int) -> None:
-            sampler.gemv_device(d_x.addr, rows, K, K, d_in[i % sets].addr, lh.wtype, vocab,
-                                d_y.addr, vocab, stream=stream)
+            sampler.gemv_device_ex(d_x.addr, rows, K, wts[i % sets], d_y.addr, vocab,
+                                   stream=stream)
 
         def check() -> dict:
             from oracle import pyoracle
             got = d_y.download().astype(np.float64)
-            exact, mag = pyoracle.gemv_exact(lh.wtype, lh.x, lh.weights, vocab)
+            xr = pyoracle.hadamard512(lh.x) if args.hadamard else lh.x
+            exact, mag = pyoracle.gemv_exact(lh.wtype, xr, lh.weights, vocab)
             rel = np.abs(got - exact) / np.maximum(mag, 1e-30)
             return {"logits": int(got.size), "within_2^-16_of_sum_abs": int((rel <= 2 ** -16).sum()),
                     "max_rel": float(rel.max())}

@@ -701,8 +701,9 @@ __global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_mfma_kernel(GemvArg
 // (PQ2_0) or the trit (PTQ1_0) (src/gguf.ts:93-147, src/kernels.ts:376-700).
 //
 // As for Q6_K, x is held as four int8 limbs, here per 128-weight block: with
-// 2^E above the block's largest |x|, a_t = rint(r_{t-1} 2^(6 + 7t - E)), so
-// x - sum_t a_t 2^(E - 6 - 7t) is below 2^(E - 28).  A block is eight
+// 2^E above the block's largest |x|, x is rounded to n 2^(E - 27) and the
+// limbs are n's balanced base-128 digits a_t (|a_t| <= 64), so
+// x - sum_t a_t 2^(E - 6 - 7t) is at most 2^(E - 28).  A block is eight
 // v_mfma_i32_16x16x64_i8 into one accumulator: B (64 x 16) holds the codes
 // of 16 rows, A (16 x 64) in row 4G + t limb t of lane group G's positions,
 // zero elsewhere.  The four lane groups G of a wave take four consecutive
@@ -721,8 +722,9 @@ __global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_mfma_kernel(GemvArg
 //          6 and 7 trit 4 of bytes 0..15 and 16..23 and the trits of the two
 //          tail bytes.
 namespace tm {
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
+// waves per workgroup: the x tables are built once per workgroup; PTQ1_0
+// (more registers) takes 8 so that three workgroups fit a CU
+template <int FMT> constexpr int waves() { return FMT == kW_PTQ1_0 ? 8 : 16; }
 constexpr int kLutBytes = 256 * 8;
 typedef int v4i __attribute__((ext_vector_type(4)));
 }  // namespace tm
@@ -745,35 +747,50 @@ __device__ __forceinline__ int tern_pos(int s, int w, int m) {
 
 size_t gemv_tern_lds_bytes(int K) {
   const int nb = K / 128;
-  // LUT | A operands [nb][8 MFMAs][4 limbs] | limb totals | limb scales |
-  // exponents | non-finite flag
-  return (size_t)tm::kLutBytes + (size_t)nb * 512 + (size_t)nb * 32 + (size_t)nb * 4 + 16;
+  // LUT | x staged | A operands [nb][8 MFMAs][4 limbs] | zeros (the A
+  // operand of the lanes outside their lane group) | limb totals | limb
+  // scales | exponents | non-finite flag
+  return (size_t)tm::kLutBytes + (size_t)K * 4 + (size_t)nb * 512 + 512 + (size_t)nb * 32 +
+         (size_t)nb * 4 + 16;
 }
 
 __device__ __forceinline__ uint32_t tern_bfi4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   return (a & 0xFFu) | (b & 0xFF00u) | (c & 0xFF0000u) | (d & 0xFF000000u);
 }
 
+// A lane's share of one block (its quant dwords and the dword holding its
+// binary16 scale), loaded a few items ahead of use.
+template <int FMT> struct TernSlot;
+template <> struct TernSlot<kW_Q1_0> { static constexpr int kDepth = 4; uint32_t q[4]; uint32_t sd; };
+template <> struct TernSlot<kW_PQ2_0> { static constexpr int kDepth = 2; uint32_t q[8]; uint32_t sd; };
+template <> struct TernSlot<kW_PTQ1_0> { static constexpr int kDepth = 2; uint32_t q[7]; uint32_t sd; };
+
 template <int FMT>
-__global__ __launch_bounds__(tm::kThreads) void gemv_tern_kernel(GemvArgs g) {
+__global__ __launch_bounds__(64 * tm::waves<FMT>()) void gemv_tern_kernel(GemvArgs g) {
   using tm::v4i;
   extern __shared__ uint4 tlds[];
   constexpr int QB = tern_quant_bytes(FMT);
   constexpr int C1 = FMT == kW_Q1_0 ? 2 : 1;
+  constexpr int D = TernSlot<FMT>::kDepth;
+  constexpr int NWV = tm::waves<FMT>(), NT = 64 * NWV;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int m = (int)blockIdx.y;
   const int K = g.K, nb = K / 128;
   uint8_t *base = reinterpret_cast<uint8_t *>(tlds);
   const uint2 *lut = reinterpret_cast<const uint2 *>(base);
-  uint32_t *aop = reinterpret_cast<uint32_t *>(base + tm::kLutBytes);   // [nb][8][4] x 4 dwords
-  v4i *atot = reinterpret_cast<v4i *>(base + tm::kLutBytes + (size_t)nb * 512);
+  float *xs = reinterpret_cast<float *>(base + tm::kLutBytes);
+  uint32_t *aop = reinterpret_cast<uint32_t *>(xs + K);   // [nb][8][4] x 4 dwords, then zeros
+  v4i *atot = reinterpret_cast<v4i *>(aop + (size_t)nb * 128 + 128);
   float4 *asc = reinterpret_cast<float4 *>(atot + nb);
   int *aexp = reinterpret_cast<int *>(asc + nb);
   int *bad = aexp + nb;
 
+  // ---- the limbs of activation row m, once per workgroup
+  const float *xm = g.x + (int64_t)m * g.ldx;
+  for (int i = tid; i < K; i += NT) xs[i] = xm[i];
   if constexpr (FMT == kW_PTQ1_0) {   // trits of every byte value (src/gguf.ts:111-144)
     uint2 *lw = reinterpret_cast<uint2 *>(base);
-    for (int v = tid; v < 256; v += tm::kThreads) {
+    for (int v = tid; v < 256; v += NT) {
       uint32_t t[5];
       uint32_t q = (uint32_t)v;
 #pragma unroll
@@ -784,11 +801,11 @@ __global__ __launch_bounds__(tm::kThreads) void gemv_tern_kernel(GemvArgs g) {
       lw[v] = make_uint2(t[0] | (t[1] << 8) | (t[2] << 16) | (t[3] << 24), t[4] * 0x01010101u);
     }
   }
-  // ---- the limbs of activation row m, once per workgroup
-  const float *xm = g.x + (int64_t)m * g.ldx;
   if (tid == 0) *bad = 0;
-  for (int b = wave; b < nb; b += tm::kWaves) {   // block exponents
-    const float v0 = xm[128 * b + lane], v1 = xm[128 * b + 64 + lane];
+  if (tid < 128) aop[(size_t)nb * 128 + tid] = 0u;
+  __syncthreads();
+  for (int b = wave; b < nb; b += NWV) {   // block exponents
+    const float v0 = xs[128 * b + lane], v1 = xs[128 * b + 64 + lane];
     float mx = fmaxf(fabsf(v0), fabsf(v1));
     const bool fin = __builtin_isfinite(v0) && __builtin_isfinite(v1);
 #pragma unroll
@@ -804,21 +821,27 @@ __global__ __launch_bounds__(tm::kThreads) void gemv_tern_kernel(GemvArgs g) {
     if (__ballot(!fin) && lane == 0) *bad = 1;
   }
   __syncthreads();
-  for (int it = tid; it < nb * 32; it += tm::kThreads) {   // item (b, s, w): 4 codes
+  for (int it = tid; it < nb * 32; it += NT) {   // item (b, s, w): 4 codes
     const int b = it >> 5, s = (it >> 2) & 7, w = it & 3;
     const int E = aexp[b];
     uint32_t limb[4] = {0u, 0u, 0u, 0u};
     int At[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int mm = 0; mm < 4; ++mm) {
-      float r = xm[128 * b + tern_pos<FMT>(s, w, mm)];
+      // x rounded to a multiple of 2^(E - 27): |n| <= 2^27, then its
+      // balanced base-128 digits, most significant first (|a_0| <= 64)
+      int n = (int)rintf(ldexpf(xs[128 * b + tern_pos<FMT>(s, w, mm)], 27 - E));
+      int a[4];
+#pragma unroll
+      for (int t = 3; t > 0; --t) {
+        a[t] = ((n + 64) & 127) - 64;
+        n = (n - a[t]) >> 7;
+      }
+      a[0] = n;
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const float a = rintf(ldexpf(r, 6 + 7 * t - E));
-        r -= ldexpf(a, E - 6 - 7 * t);   // exact: within half a step of r
-        const int ai = (int)a;
-        At[t] += ai;
-        limb[t] |= ((uint32_t)ai & 0xFFu) << (8 * mm);
+        At[t] += a[t];
+        limb[t] |= ((uint32_t)a[t] & 0xFFu) << (8 * mm);
       }
     }
 #pragma unroll
@@ -830,96 +853,143 @@ __global__ __launch_bounds__(tm::kThreads) void gemv_tern_kernel(GemvArgs g) {
   __syncthreads();
   const bool nonfinite = *bad != 0;
 
-  // ---- tiles of 16 rows, one wave each
-  // both resources cover their tensor rounded up to whole dwords: a dword
+  // ---- the wave's items: (tile of 16 rows, round r of four blocks), its
+  // tiles round-robin over the grid's waves; item z + D is requested as
+  // soon as item z is taken apart, so D items are in flight per wave.
+  // Both resources cover their tensor rounded up to whole dwords: a dword
   // read that straddles the limit would return 0 for its valid bytes too
-  // (the last PTQ1_0 block ends 2 bytes into a dword)
+  // (the last PTQ1_0 block ends 2 bytes into a dword).
   const rsrc_t rq = wrsrc(g.w, (g.w_bytes + 3u) & ~3u), rs = wrsrc(g.scales, (g.s_bytes + 3u) & ~3u);
   const int j = lane & 15, G = lane >> 4, tl = lane & 3;
   const bool a_live = ((lane & 15) >> 2) == G;
   const int ntiles = (g.N + 15) >> 4, nr = (nb + 3) >> 2;
-  const int nw = (int)gridDim.x * tm::kWaves;
-  for (int tile = (int)blockIdx.x * tm::kWaves + wave; tile < ntiles; tile += nw) {
+  const int nw = (int)gridDim.x * NWV;
+  const int first = (int)blockIdx.x * NWV + wave;
+  const int Z = first < ntiles ? ((ntiles - 1 - first) / nw + 1) * nr : 0;
+
+  auto load = [&](int z, TernSlot<FMT> &sl) {
+    const int tile = first + (z / nr) * nw, b = 4 * (z % nr) + G;
     const int row = tile * 16 + j;
-    float acc = 0.f;
-    for (int r = 0; r < nr; ++r) {
-      const int b = 4 * r + G;
-      const bool live = b < nb && row < g.N;
-      const uint32_t blk = (uint32_t)row * (uint32_t)nb + (uint32_t)b;
-      const uint32_t qo = live ? blk * (uint32_t)QB : 0xFFFFFFF0u;   // past the resource: zeros
-      const uint32_t so = live ? blk * 2u : 0xFFFFFFF0u;
-      const uint32_t dw = __builtin_amdgcn_raw_buffer_load_b32(rs, so & ~3u, 0, 0);
-      const float d = h2f(dw >> (8u * (so & 2u)));
-      v4i D = v4i{0, 0, 0, 0};
-      const v4i *ab = reinterpret_cast<const v4i *>(aop) + (size_t)(b < nb ? b : 0) * 32 + tl;
+    const bool live = z < Z && b < nb && row < g.N;
+    const uint32_t blk = (uint32_t)row * (uint32_t)nb + (uint32_t)b;
+    const uint32_t so = live ? (blk * 2u) & ~3u : 0xFFFFFFF0u;   // past the resource: zeros
+    sl.sd = __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0) >> (live ? 8u * (blk & 1u) * 2u : 0u);
+    const uint32_t qo = blk * (uint32_t)QB;
+    if constexpr (FMT == kW_Q1_0) {
+      const auto q = __builtin_amdgcn_raw_buffer_load_b128(rq, live ? qo : 0xFFFFFFF0u, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sl.q[i] = (uint32_t)q[i];
+    } else if constexpr (FMT == kW_PQ2_0) {
+      const auto q0 = __builtin_amdgcn_raw_buffer_load_b128(rq, live ? qo : 0xFFFFFFF0u, 0, 0);
+      const auto q1 = __builtin_amdgcn_raw_buffer_load_b128(rq, live ? qo + 16u : 0xFFFFFFF0u, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sl.q[i] = (uint32_t)q0[i];
+        sl.q[4 + i] = (uint32_t)q1[i];
+      }
+    } else {   // 26 bytes from an even offset: seven aligned dwords
+      const uint32_t a0 = qo & ~3u;
+#pragma unroll
+      for (int i = 0; i < 7; ++i)
+        sl.q[i] = __builtin_amdgcn_raw_buffer_load_b32(rq, live ? a0 + 4u * i : 0xFFFFFFF0u, 0, 0);
+    }
+  };
+
+  TernSlot<FMT> slot[D];
+#pragma unroll
+  for (int u = 0; u < D; ++u) load(u, slot[u]);
+  float acc = 0.f;
+  for (int z0 = 0; z0 < Z; z0 += D) {
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+      const int z = z0 + u;
+      const int tile = first + (z / nr) * nw, r = z % nr, b = 4 * r + G;
+      const int row = tile * 16 + j;
+      const bool bl = b < nb;
+      const float d = h2f(slot[u].sd);
+      v4i D0 = v4i{0, 0, 0, 0}, D1 = v4i{0, 0, 0, 0};
+      // this lane's A operand rows (limb tl of its lane group's block), or
+      // the zeros: one select per item, none per MFMA
+      const v4i *ab = reinterpret_cast<const v4i *>(aop) + (a_live && bl ? (size_t)b * 32 : (size_t)nb * 32) + tl;
       auto mfma = [&](int s, v4i B) {
-        const v4i al = ab[s * 4];
-        const v4i A = a_live && b < nb ? al : v4i{0, 0, 0, 0};
-        D = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, D, 0, 0, 0);
+        const v4i A = ab[s * 4];
+        if (s & 1)
+          D1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, D1, 0, 0, 0);
+        else
+          D0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(A, B, D0, 0, 0, 0);
       };
       if constexpr (FMT == kW_Q1_0) {
-        const auto q = __builtin_amdgcn_raw_buffer_load_b128(rq, qo, 0, 0);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-          const uint32_t wd = (uint32_t)q[s >> 1];
+          const uint32_t wd = slot[u].q[s >> 1];
           v4i B;
 #pragma unroll
           for (int w = 0; w < 4; ++w) B[w] = (int)((wd >> (4 * (s & 1) + w)) & 0x01010101u);
           mfma(s, B);
         }
       } else if constexpr (FMT == kW_PQ2_0) {
-        const auto q0 = __builtin_amdgcn_raw_buffer_load_b128(rq, qo, 0, 0);
-        const auto q1 = __builtin_amdgcn_raw_buffer_load_b128(rq, live ? qo + 16u : qo, 0, 0);
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-          const uint32_t wd = (uint32_t)(s < 4 ? q0[s & 3] : q1[s & 3]);
+          const uint32_t wd = slot[u].q[s];
           v4i B;
 #pragma unroll
           for (int w = 0; w < 4; ++w) B[w] = (int)((wd >> (2 * w)) & 0x03030303u);
           mfma(s, B);
         }
       } else {
-        // 26 bytes from an even offset: seven aligned dwords, realigned
-        const uint32_t a0 = qo & ~3u, sh = qo & 3u;
-        uint32_t dd[7];
-#pragma unroll
-        for (int i = 0; i < 7; ++i)
-          dd[i] = __builtin_amdgcn_raw_buffer_load_b32(rq, live ? a0 + 4u * i : 0xFFFFFFF0u, 0, 0);
+        const uint32_t sh = ((uint32_t)(row * nb + b) * (uint32_t)QB) & 3u;
         uint32_t q[7];
 #pragma unroll
-        for (int i = 0; i < 6; ++i) q[i] = __builtin_amdgcn_alignbyte(dd[i + 1], dd[i], sh);
-        q[6] = __builtin_amdgcn_alignbyte(0u, dd[6], sh);
-        uint2 e[26];
+        for (int i = 0; i < 6; ++i) q[i] = __builtin_amdgcn_alignbyte(slot[u].q[i + 1], slot[u].q[i], sh);
+        q[6] = __builtin_amdgcn_alignbyte(0u, slot[u].q[6], sh);
+        // bytes 0..15 (MFMAs 0..3 and 6), then bytes 16..25 (MFMAs 4, 5, 7)
+        {
+          uint2 e[16];
 #pragma unroll
-        for (int i = 0; i < 26; ++i) e[i] = lut[(q[i >> 2] >> (8 * (i & 3))) & 0xFFu];
+          for (int i = 0; i < 16; ++i) e[i] = lut[(q[i >> 2] >> (8 * (i & 3))) & 0xFFu];
 #pragma unroll
-        for (int s = 0; s < 6; ++s) {
-          const int b0 = s < 4 ? 4 * s : 16 + 4 * (s - 4);
-          mfma(s, v4i{(int)e[b0].x, (int)e[b0 + 1].x, (int)e[b0 + 2].x, (int)e[b0 + 3].x});
+          for (int s = 0; s < 4; ++s)
+            mfma(s, v4i{(int)e[4 * s].x, (int)e[4 * s + 1].x, (int)e[4 * s + 2].x,
+                        (int)e[4 * s + 3].x});
+          v4i B6;
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            B6[w] = (int)tern_bfi4(e[4 * w].y, e[4 * w + 1].y, e[4 * w + 2].y, e[4 * w + 3].y);
+          mfma(6, B6);
         }
-        v4i B6;
+        {
+          uint2 e[10];
 #pragma unroll
-        for (int w = 0; w < 4; ++w)
-          B6[w] = (int)tern_bfi4(e[4 * w].y, e[4 * w + 1].y, e[4 * w + 2].y, e[4 * w + 3].y);
-        mfma(6, B6);
-        mfma(7, v4i{(int)tern_bfi4(e[16].y, e[17].y, e[18].y, e[19].y),
-                    (int)tern_bfi4(e[20].y, e[21].y, e[22].y, e[23].y), (int)e[24].x,
-                    (int)e[25].x});
+          for (int i = 0; i < 10; ++i)
+            e[i] = lut[(q[(16 + i) >> 2] >> (8 * ((16 + i) & 3))) & 0xFFu];
+#pragma unroll
+          for (int s = 4; s < 6; ++s) {
+            const int b0 = 4 * (s - 4);
+            mfma(s, v4i{(int)e[b0].x, (int)e[b0 + 1].x, (int)e[b0 + 2].x, (int)e[b0 + 3].x});
+          }
+          mfma(7, v4i{(int)tern_bfi4(e[0].y, e[1].y, e[2].y, e[3].y),
+                      (int)tern_bfi4(e[4].y, e[5].y, e[6].y, e[7].y), (int)e[8].x, (int)e[9].x});
+        }
       }
-      if (b < nb) {
+      load(z + D, slot[u]);   // the slot is free: request the item D ahead
+      if (bl) {
         const v4i at = atot[b];
         const float4 sc = asc[b];
-        float val = (float)(C1 * D[0] - at[0]) * sc.x;
-        val = fmaf((float)(C1 * D[1] - at[1]), sc.y, val);
-        val = fmaf((float)(C1 * D[2] - at[2]), sc.z, val);
-        val = fmaf((float)(C1 * D[3] - at[3]), sc.w, val);
+        const v4i Dt = D0 + D1;
+        float val = (float)(C1 * Dt[0] - at[0]) * sc.x;
+        val = fmaf((float)(C1 * Dt[1] - at[1]), sc.y, val);
+        val = fmaf((float)(C1 * Dt[2] - at[2]), sc.z, val);
+        val = fmaf((float)(C1 * Dt[3] - at[3]), sc.w, val);
         acc = fmaf(d, val, acc);
       }
+      if (r == nr - 1) {   // the tile's last round: the four lane groups add up
+        acc += __shfl_xor(acc, 16);
+        acc += __shfl_xor(acc, 32);
+        if (lane < 16 && row < g.N && z < Z)
+          g.y[(int64_t)m * g.ldy + row] = nonfinite ? __builtin_nanf("") : acc;
+        acc = 0.f;
+      }
     }
-    acc += __shfl_xor(acc, 16);
-    acc += __shfl_xor(acc, 32);
-    if (lane < 16 && row < g.N)
-      g.y[(int64_t)m * g.ldy + row] = nonfinite ? __builtin_nanf("") : acc;
   }
 }
 
@@ -1039,10 +1109,10 @@ hipError_t launch_tern(GemvArgs g, hipStream_t stream, hipEvent_t *ev, hipEvent_
   const size_t lds = gemv_tern_lds_bytes(g.K);
   const int ntiles = (g.N + 15) / 16;
   const int res = resident_blocks(reinterpret_cast<const void *>(gemv_tern_kernel<FMT>),
-                                  (uint32_t)lds, tm::kThreads);
-  int blocks = (ntiles + tm::kWaves - 1) / tm::kWaves;
+                                  (uint32_t)lds, 64 * tm::waves<FMT>());
+  int blocks = (ntiles + tm::waves<FMT>() - 1) / tm::waves<FMT>();
   blocks = blocks < res ? blocks : res;
-  const dim3 grid((unsigned)blocks, (unsigned)g.M), block(tm::kThreads);
+  const dim3 grid((unsigned)blocks, (unsigned)g.M), block(64 * tm::waves<FMT>());
   if (ev)
     hipExtLaunchKernelGGL(gemv_tern_kernel<FMT>, grid, block, lds, stream, ev[0], ev[1], 0u, g);
   else if (done)

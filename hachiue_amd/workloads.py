@@ -173,7 +173,8 @@ NAMES = ("single", "batch64", "perrow256", "gumbel1024", "v262k512", "headline")
 
 # GGML weight type ids (src/types.ts:4-15) and (weights, bytes) per block.
 W_TYPES = {"f32": (0, 1, 4), "q4_0": (2, 32, 18), "q4_1": (3, 32, 20), "q4_k": (12, 256, 144),
-           "q6_k": (14, 256, 210)}
+           "q6_k": (14, 256, 210), "q1_0": (41, 128, 18), "pq2_0": (142, 128, 34),
+           "ptq1_0": (143, 128, 28)}
 
 
 @dataclass
@@ -214,4 +215,8 @@ def make_lmhead(fmt: str = "q6_k", hidden: int = 2048, vocab: int = V_QWEN, m: i
             np.uint8).reshape(vocab, nb, 2)
     if wtype == 14:
         raw[:, :, 208:210] = d
+    if wtype in (41, 142):
+        raw[:, :, 0:2] = d
+    if wtype == 143:
+        raw[:, :, 26:28] = d
     return LmHead(wtype, fmt, vocab, hidden, raw.reshape(vocab, nb * bb), x)
