@@ -556,15 +556,22 @@ __global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_mfma_kernel(GemvArg
   // slab z sits in ring buffer z % NB, its loads issued NB - 1 slabs earlier;
   // the first ones go out before the x tables are built
   for (int z = 0; z < items && z < NB - 1; ++z) issue(z, ring + z * kSlabBytes);
-  // limbs of this activation row, once per workgroup
+  // limbs of this activation row, once per workgroup; a non-finite element
+  // (whose limbs are undefined) makes the row's results NaN
+  __shared__ int nonfin;
+  if (tid == 0) nonfin = 0;
+  __syncthreads();
   const float *xm = g.x + (int64_t)m * g.ldx;
   for (int gi = tid; gi < NG; gi += q6m::kThreads) {
     float xv[16], mx = 0.f;
+    bool fin = true;
 #pragma unroll
     for (int b = 0; b < 16; ++b) {
       xv[b] = xm[16 * gi + b];
       mx = fmaxf(mx, fabsf(xv[b]));
+      fin = fin && __builtin_isfinite(xv[b]);
     }
+    if (!fin) nonfin = 1;
     int E = 0;
     (void)frexpf(mx, &E);   // mx < 2^E
     uint32_t limb[4][4];
@@ -598,6 +605,7 @@ __global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_mfma_kernel(GemvArg
                           ldexpf(1.f, E - 27));
   }
   __syncthreads();
+  const bool nan_out = nonfin != 0;
   for (int z = 0; z < items; ++z) {
     const uint8_t *cur = ring + (z % NB) * kSlabBytes;
     if (z + NB - 1 < items) {
@@ -664,7 +672,7 @@ __global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_mfma_kernel(GemvArg
       acc += __shfl_xor(acc, 16);
       acc += __shfl_xor(acc, 32);
       if (z < rfull * nsl || P == 1) {
-        if (lane < 16 && row < g.N) g.y[(int64_t)m * g.ldy + row] = acc;
+        if (lane < 16 && row < g.N) g.y[(int64_t)m * g.ldy + row] = nan_out ? __builtin_nanf("") : acc;
       } else {
         float *pm = g.part + ((int64_t)m * g.part_cap + wg) * 16;   // slot ptt * P + pidx == wg
         if (lane < 16)
@@ -682,7 +690,8 @@ __global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_mfma_kernel(GemvArg
             sum += lane < 16 ? __hip_atomic_load(p0p + q * 16 + lane, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT)
                              : 0.f;
-          if (lane < 16 && row < g.N) g.y[(int64_t)m * g.ldy + row] = sum;
+          if (lane < 16 && row < g.N)
+            g.y[(int64_t)m * g.ldy + row] = nan_out ? __builtin_nanf("") : sum;
           if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }

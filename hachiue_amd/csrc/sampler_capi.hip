@@ -67,9 +67,23 @@ int fail(int status, const char *fmt, ...) {
   return status;
 }
 
+// Failure injection for tests of the error paths: with HS_INJECT_HIP_FAILURE=n
+// in the environment when a context is created, the n-th HIP runtime call
+// checked through HS_HIP after that (0: the first) is not made and reports
+// hipErrorOutOfMemory instead; -1 (the default) injects nothing.
+std::atomic<int> g_inject{-1};
+
+bool inject_failure() {
+  int v = g_inject.load(std::memory_order_relaxed);
+  while (v >= 0) {
+    if (g_inject.compare_exchange_weak(v, v - 1, std::memory_order_relaxed)) return v == 0;
+  }
+  return false;
+}
+
 #define HS_HIP(call)                                                                \
   do {                                                                              \
-    hipError_t e_ = (call);                                                         \
+    hipError_t e_ = inject_failure() ? hipErrorOutOfMemory : (call);                \
     if (e_ != hipSuccess)                                                           \
       return fail(HS_ERR_HIP, "%s failed: %s", #call, hipGetErrorString(e_));       \
   } while (0)
@@ -308,15 +322,11 @@ int upload_plans(hs_context *ctx, const std::vector<hs::RowPlan> &plans, const R
   char *st = static_cast<char *>(ctx->plan_staging);
   memcpy(st, plans.data(), pbytes);
   int32_t *lists = reinterpret_cast<int32_t *>(st + pbytes);
-  memcpy(lists, rt.pf.data(), sizeof(int32_t) * rt.pf.size());
-  memcpy(lists + rt.pf.size(), rt.row.data(), sizeof(int32_t) * rt.row.size());
-  memcpy(lists + rt.pf.size() + rt.row.size(), rt.chunk.data(), sizeof(int32_t) * rt.chunk.size());
-  memcpy(lists + rt.pf.size() + rt.row.size() + rt.chunk.size(), rt.large.data(),
-         sizeof(int32_t) * rt.large.size());
-  memcpy(lists + rt.pf.size() + rt.row.size() + rt.chunk.size() + rt.large.size(), rt.mid.data(),
-         sizeof(int32_t) * rt.mid.size());
-  memcpy(lists + rt.pf.size() + rt.row.size() + rt.chunk.size() + rt.large.size() + rt.mid.size(),
-         rt.lfast.data(), sizeof(int32_t) * rt.lfast.size());
+  // the lists back to back (an empty list's data() may be null: no copy)
+  for (const std::vector<int32_t> *l : {&rt.pf, &rt.row, &rt.chunk, &rt.large, &rt.mid, &rt.lfast}) {
+    if (!l->empty()) memcpy(lists, l->data(), sizeof(int32_t) * l->size());
+    lists += l->size();
+  }
   HS_HIP(hipMemcpyAsync(ctx->plans.p, st, bytes, hipMemcpyHostToDevice, stream));
   HS_HIP(hipEventRecord(ctx->plan_done, stream));
   ctx->plan_pending = true;
@@ -345,16 +355,26 @@ int choose_split(const hs_context *ctx, int rows, int vocab) {
 }
 
 // The split rows' hand-over buffers for rows x split parts.
+// A buffer that holds zeros between calls (arrival counters), grown and
+// cleared together: a failed clear drops the buffer, so that the next call
+// allocates and clears it again instead of counting from stale values.
+int ensure_zeroed(DevBuf &b, size_t need) {
+  if (b.bytes >= need) return HS_OK;
+  HS_HIP(b.ensure(need));
+  const hipError_t e = inject_failure() ? hipErrorOutOfMemory : hipMemset(b.p, 0, b.bytes);
+  if (e != hipSuccess) {
+    b.release();
+    return fail(HS_ERR_HIP, "hipMemset(counters) failed: %s", hipGetErrorString(e));
+  }
+  return HS_OK;
+}
+
 int ensure_split(hs_context *ctx, int rows, int split) {
   if (split <= 1) return HS_OK;
   const size_t parts = (size_t)rows * (size_t)split;
   HS_HIP(ctx->split_list.ensure(parts * hs::kPartCap * sizeof(unsigned long long)));
   HS_HIP(ctx->split_meta.ensure(parts * sizeof(hs::SplitMeta)));
-  if (ctx->split_cnt.bytes < sizeof(uint32_t) * (size_t)rows) {
-    HS_HIP(ctx->split_cnt.ensure(sizeof(uint32_t) * (size_t)rows));
-    HS_HIP(hipMemset(ctx->split_cnt.p, 0, ctx->split_cnt.bytes));
-  }
-  return HS_OK;
+  return ensure_zeroed(ctx->split_cnt, sizeof(uint32_t) * (size_t)rows);
 }
 
 hs::Workspace split_workspace(const hs_context *ctx) {
@@ -450,10 +470,8 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   if (n_chunk > 0) {
     HS_HIP(ctx->cand.ensure((size_t)n_chunk * (size_t)S * hs::kChunkCap * sizeof(uint2)));
     HS_HIP(ctx->info.ensure((size_t)n_chunk * (size_t)S * sizeof(hs::ChunkInfo)));
-    if (ctx->cand_count.bytes < sizeof(int32_t) * (size_t)n_chunk) {
-      HS_HIP(ctx->cand_count.ensure(sizeof(int32_t) * (size_t)n_chunk));
-      HS_HIP(hipMemset(ctx->cand_count.p, 0, ctx->cand_count.bytes));
-    }
+    const int rz = ensure_zeroed(ctx->cand_count, sizeof(int32_t) * (size_t)n_chunk);
+    if (rz) return rz;
   }
   if (n_lfast > 0) HS_HIP(ctx->large_retry.ensure(sizeof(int32_t) * (size_t)n_lfast));
   if (n_large > 0) HS_HIP(ctx->large_replay.ensure(sizeof(hs::ReplayReq) * (size_t)n_large));
@@ -663,10 +681,8 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const
     g.part_cap = cus * hs::kGemvWavesPerCU;
     const size_t slots = (size_t)g.part_cap * (size_t)M;
     HS_HIP(ctx->gemv_part.ensure(slots * 16 * sizeof(float)));
-    if (ctx->gemv_cnt.bytes < slots * sizeof(uint32_t)) {
-      HS_HIP(ctx->gemv_cnt.ensure(slots * sizeof(uint32_t)));
-      HS_HIP(hipMemset(ctx->gemv_cnt.p, 0, ctx->gemv_cnt.bytes));
-    }
+    const int rz = ensure_zeroed(ctx->gemv_cnt, slots * sizeof(uint32_t));
+    if (rz) return rz;
     g.part = static_cast<float *>(ctx->gemv_part.p);
     g.tile_cnt = static_cast<uint32_t *>(ctx->gemv_cnt.p);
   }
@@ -879,6 +895,7 @@ int hs_context_create(int device, hs_context **out) {
     return fail(HS_ERR_HIP, "no HIP device available (%s)", hipGetErrorString(e));
   if (device < 0 || device >= n)
     return fail(HS_ERR_INVALID_ARGUMENT, "device %d out of range [0, %d)", device, n);
+  if (const char *env = getenv("HS_INJECT_HIP_FAILURE")) g_inject.store(atoi(env));
   DeviceGuard guard(device);
   {
     std::lock_guard<std::mutex> lk(g_prep_mu);

@@ -307,3 +307,17 @@ def test_lm_head_then_sample_planar_folded(sampler):
     res = o.sample_batch(ref, N, ids, off, cfgs, u)
     assert tokens.tolist() == res.token.tolist()
     assert np.array_equal(pen.view(np.uint32), ref.view(np.uint32))
+
+
+def test_gemv_q6k_nonfinite_input(sampler):
+    """The Q6_K matrix-core kernel holds x as integer limbs: a row of x with a
+    NaN or an infinity gives NaN for every result of that row."""
+    wtype, K, N = o.W_Q6_K, 512, 40
+    rng = np.random.default_rng(6)
+    w = random_blocks(wtype, N, K, rng)
+    x = rng.standard_normal((3, K)).astype(np.float32)
+    x[1, 300] = np.nan
+    x[2, 7] = -np.inf
+    y = run_gemv(sampler, wtype, x, w, N)
+    assert np.all(np.isnan(y[1])) and np.all(np.isnan(y[2]))
+    check(wtype, x[:1], w, N, y[:1])
