@@ -257,9 +257,11 @@ hs::RowPlan plan_row(const hs_sample_config &c, int vocab) {
 }
 
 // The large-k kernel takes penalised logits: its rows' penalties run in the
-// pre-pass, like the presence / frequency rows of the other kernels.
-bool in_prepass(const hs::RowPlan &p) {
-  return (p.pen & hs::kPenPF) || (p.pen && p.mode == hs::kModeLarge);
+// pre-pass, like the presence / frequency rows of the row and chunk kernels.
+// The mid kernel applies its presence / frequency rows' penalties itself
+// (`mid`: the row is routed to it).
+bool in_prepass(const hs::RowPlan &p, bool mid) {
+  return ((p.pen & hs::kPenPF) && !mid) || (p.pen && p.mode == hs::kModeLarge);
 }
 
 int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_rows,
@@ -274,7 +276,6 @@ int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_r
   for (int r = 0; r < rows; ++r) {
     const hs::RowPlan p = plan_row(cfgs[r], vocab);
     out[(size_t)r] = p;
-    if (in_prepass(p)) rt.pf.push_back(r);
     if (p.mode == hs::kModeLarge) {
       (two_pass_large(p, vocab) ? rt.lfast : rt.large).push_back(r);
       continue;
@@ -292,6 +293,10 @@ int build_plans(const hs_sample_config *cfgs, int rows, int vocab, int row_min_r
     for (int32_t r : rt.row) (out[(size_t)r].mode == hs::kModeSmall ? rt.mid : keep).push_back(r);
     rt.row.swap(keep);
   }
+  std::vector<char> mid((size_t)rows, 0);
+  for (int32_t r : rt.mid) mid[(size_t)r] = 1;
+  for (int r = 0; r < rows; ++r)
+    if (in_prepass(out[(size_t)r], mid[(size_t)r] != 0)) rt.pf.push_back(r);
   return HS_OK;
 }
 
@@ -721,7 +726,6 @@ void build_plans_fixed(const hs_sample_config *cfgs, int rows, int vocab, hs::Ro
   for (int r = 0; r < rows; ++r) {
     const hs::RowPlan p = plan_row(cfgs[r], vocab);
     plans[r] = p;
-    n_pf += in_prepass(p);
     n_lfast += two_pass_large(p, vocab);
     n_large += p.mode == hs::kModeLarge && !two_pass_large(p, vocab);
     n_mid += p.mode == hs::kModeGeneric;
@@ -733,14 +737,18 @@ void build_plans_fixed(const hs_sample_config *cfgs, int rows, int vocab, hs::Ro
     n_row -= n_small;
     n_mid += n_small;
   }
+  auto to_mid = [&](const hs::RowPlan &p) {
+    return p.mode == hs::kModeGeneric || (merge && p.mode == hs::kModeSmall);
+  };
+  for (int r = 0; r < rows; ++r) n_pf += in_prepass(plans[r], to_mid(plans[r]));
   int32_t *pf = lists, *row = pf + n_pf, *large = row + n_row, *mid = large + n_large;
   int32_t *lfast = mid + n_mid;
   for (int r = 0; r < rows; ++r) {
     const hs::RowPlan &p = plans[r];
-    if (in_prepass(p)) *pf++ = r;
+    if (in_prepass(p, to_mid(p))) *pf++ = r;
     if (two_pass_large(p, vocab)) *lfast++ = r;
     else if (p.mode == hs::kModeLarge) *large++ = r;
-    else if (p.mode == hs::kModeGeneric || (merge && p.mode == hs::kModeSmall)) *mid++ = r;
+    else if (to_mid(p)) *mid++ = r;
     else *row++ = r;
   }
   n[0] = n_pf;

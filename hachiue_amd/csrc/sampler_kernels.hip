@@ -495,26 +495,24 @@ __device__ __forceinline__ uint32_t pen_hash(int id) {
   return ((uint32_t)id * 2654435761u) >> (32 - kPenBits);
 }
 
-__global__ __launch_bounds__(kPenThreads) void pen_kernel(LaunchArgs a, Workspace ws) {
-  extern __shared__ uint32_t pdyn[];
+// One row's penalties in place, by the whole workgroup of NT threads: `pdyn`
+// holds pen_smem_bytes() of LDS, `full` is a shared flag.  The row's stores
+// are issued when it returns; the caller orders them before any later read.
+template <int NT>
+__device__ __forceinline__ void pen_row(const HistRow h, const RowPlan P, float *rowp, int V,
+                                        uint32_t *pdyn, int32_t &full) {
   int32_t *keys = reinterpret_cast<int32_t *>(pdyn);   // kPenSlots ids (-1: empty)
   uint32_t *cnts = pdyn + kPenSlots;                    // kPenSlots counts | rep bit
-  __shared__ int32_t full;
   const int tid = threadIdx.x;
-  const int row = ws.pf_list[blockIdx.x];
-  const RowPlan P = ws.plans[row];
-  float *rowp = a.logits + (int64_t)row * a.stride;
-  const int V = a.vocab;
-  const HistRow h = hist_row(a, row);
   const int64_t hl = h.n;
   const int64_t rep0 = (P.pen & kPenRep) ? hl - (hl < 128 ? hl : 128) : hl;   // history.slice(-128)
   const bool pf = (P.pen & kPenPF) != 0;
-  for (int i = tid; i < kPenSlots; i += kPenThreads) { keys[i] = -1; cnts[i] = 0; }
+  for (int i = tid; i < kPenSlots; i += NT) { keys[i] = -1; cnts[i] = 0; }
   if (tid == 0) full = 0;
   __syncthreads();
   // the repetition-only entries (before rep0 without presence / frequency)
   // are not counted: their count is not used
-  for (int64_t t = pf ? tid : rep0 + tid; t < hl; t += kPenThreads) {
+  for (int64_t t = pf ? tid : rep0 + tid; t < hl; t += NT) {
     const int id = h.p[hist_pos(h, t)];
     if (id < 0 || id >= V) continue;
     uint32_t h = pen_hash(id);
@@ -533,7 +531,7 @@ __global__ __launch_bounds__(kPenThreads) void pen_kernel(LaunchArgs a, Workspac
   }
   __syncthreads();
   if (!full) {
-    for (int i = tid; i < kPenSlots; i += kPenThreads) {
+    for (int i = tid; i < kPenSlots; i += NT) {
       const int id = keys[i];
       if (id < 0) continue;
       const uint32_t c = cnts[i];
@@ -547,22 +545,30 @@ __global__ __launch_bounds__(kPenThreads) void pen_kernel(LaunchArgs a, Workspac
   for (int lo = 0; lo < V; lo += kPenRange) {
     const int hi = min(lo + kPenRange, V);
     __syncthreads();
-    for (int i = tid; i < kPenRange; i += kPenThreads) counts[i] = 0;
-    for (int i = tid; i < kPenRange / 32; i += kPenThreads) repbits[i] = 0;
+    for (int i = tid; i < kPenRange; i += NT) counts[i] = 0;
+    for (int i = tid; i < kPenRange / 32; i += NT) repbits[i] = 0;
     __syncthreads();
-    for (int64_t t = pf ? tid : rep0 + tid; t < hl; t += kPenThreads) {
+    for (int64_t t = pf ? tid : rep0 + tid; t < hl; t += NT) {
       const int id = h.p[hist_pos(h, t)];
       if (id < lo || id >= hi) continue;
       atomicAdd(&counts[id - lo], 1u);
       if (t >= rep0) atomicOr(&repbits[(id - lo) >> 5], 1u << ((id - lo) & 31));
     }
     __syncthreads();
-    for (int o = tid; o < hi - lo; o += kPenThreads) {
+    for (int o = tid; o < hi - lo; o += NT) {
       const uint32_t n = counts[o];
       const bool rep = (repbits[o >> 5] >> (o & 31)) & 1u;
       if (n) rowp[lo + o] = penalise(rowp[lo + o], rep, pf ? n : 0u, P);
     }
   }
+}
+
+__global__ __launch_bounds__(kPenThreads) void pen_kernel(LaunchArgs a, Workspace ws) {
+  extern __shared__ uint32_t pdyn[];
+  __shared__ int32_t full;
+  const int row = ws.pf_list[blockIdx.x];
+  pen_row<kPenThreads>(hist_row(a, row), ws.plans[row], a.logits + (int64_t)row * a.stride,
+                       a.vocab, pdyn, full);
 }
 
 size_t pen_smem_bytes() {
@@ -2246,6 +2252,13 @@ __device__ __forceinline__ void mid_step(float (&v)[kRowNV][4], int fb, int tid,
   if ((tid & 63) == 0 && m) atomicMax(top_key, m);
 }
 
+// the penalty prologue's table and range buffer fit below the bitmap
+static_assert((size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + (size_t)kMidBins * 4 >=
+                  (size_t)kPenSlots * 8 &&
+              (size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + (size_t)kMidBins * 4 >=
+                  (size_t)(kPenRange + kPenRange / 32) * 4,
+              "mid kernel LDS too small for the penalty prologue");
+
 size_t mid_smem_bytes(int vocab) {
   const size_t words = ((size_t)vocab + 31) / 32;
   return (size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + (size_t)kMidBins * 4 + words * 4;
@@ -2272,6 +2285,19 @@ __global__ __launch_bounds__(kRowThreads) void mid_kernel(LaunchArgs a, Workspac
   const int V = a.vocab;
   const int nr = row_rounds(V);
 
+  // Presence / frequency rows: the row's penalties (the repetition penalty
+  // included) are applied in place first, as pen_kernel does, in the LDS
+  // the stream has not taken yet (the candidate, sort and histogram arrays
+  // hold pen_smem_bytes()); the stores complete before any read of the row.
+  if (load_scalar(&ws.plans[row].pen) & kPenPF) {
+    __shared__ int32_t pen_full;
+    pen_row<kRowThreads>(hist_row(a, row), ws.plans[row], rowp, V,
+                         reinterpret_cast<uint32_t *>(mdyn), pen_full);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+
   // history ids first, then rounds 0 and 1 (as in row_kernel)
   const HistTail ht = hist_tail(a, row, tid);
   const int hraw = ht.id, hist_n = ht.n;
@@ -2297,7 +2323,7 @@ __global__ __launch_bounds__(kRowThreads) void mid_kernel(LaunchArgs a, Workspac
   const int k = load_scalar(&plan->k);
   const int penbits = load_scalar(&plan->pen);
   const double prep = load_scalar(&plan->rep);
-  // presence / frequency rows were penalised in place by pen_kernel
+  // presence / frequency rows were penalised in place above
   const bool rep = (penbits & kPenRep) && !(penbits & kPenPF);
   if (tid == 0) { ms.top_key = 0; ms.n_f = 0; ms.ovf = 0; ms.n_sel = 0; }
   for (int i = tid; i < kMidBins; i += kRowThreads) hist[i] = 0;
