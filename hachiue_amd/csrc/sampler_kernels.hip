@@ -383,9 +383,45 @@ __device__ void bitonic_reg(unsigned long long *a, int P2) {
   __syncthreads();
 }
 
-// Sorts the first n packed candidates of `a` descending (n <= kSortCap).
+// Bitonic sort of P2 packed candidates (a power of two, 64 < P2 <= NT) by
+// the first P2 threads, one each; the other waves only take the barriers.
+// Partners in other waves meet in LDS, alternately in `a` and `b` (P2
+// entries each), so each such step needs one barrier.  The result is in `a`
+// after a barrier.
 template <int NT>
-__device__ void sort_packed(unsigned long long *a, int n) {
+__device__ void bitonic_small(unsigned long long *a, unsigned long long *b, int P2) {
+  const int tid = threadIdx.x;
+  const bool act = tid < P2;   // whole waves: P2 is a multiple of 64
+  unsigned long long x = act ? a[tid] : 0ull;
+  int flip = 0;
+  for (int size = 2; size <= P2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const bool keep_max = ((tid & stride) == 0) == ((tid & size) == 0);
+      if (stride >= 64) {
+        unsigned long long *buf = flip ? b : a;
+        flip ^= 1;
+        if (act) buf[tid] = x;
+        __syncthreads();
+        if (act) {
+          const unsigned long long y = buf[tid ^ stride];
+          x = keep_max ? (y > x ? y : x) : (y < x ? y : x);
+        }
+      } else if (act) {
+        const unsigned long long y = __shfl_xor(x, stride);
+        x = keep_max ? (y > x ? y : x) : (y < x ? y : x);
+      }
+    }
+  }
+  __syncthreads();   // every read of the last exchange buffer is done
+  if (act) a[tid] = x;
+  __syncthreads();
+}
+
+// Sorts the first n packed candidates of `a` descending (n <= kSortCap).
+// `b`, when given, is a second buffer of kSortCap entries for the exchanges
+// of n <= NT candidates.
+template <int NT>
+__device__ void sort_packed(unsigned long long *a, int n, unsigned long long *b = nullptr) {
   int P2 = 1;
   while (P2 < n) P2 <<= 1;
   for (int i = n + threadIdx.x; i < P2; i += NT) a[i] = 0ull;
@@ -398,10 +434,89 @@ __device__ void sort_packed(unsigned long long *a, int n) {
       if (lane < P2) a[lane] = x;
     }
     __syncthreads();
+  } else if (b && P2 <= NT) {
+    bitonic_small<NT>(a, b, P2);
   } else {
     static_assert(kSortCap % NT == 0, "sort_packed: kSortCap must be a multiple of NT");
     bitonic_reg<NT, kSortCap / NT>(a, P2);
   }
+}
+
+// Sorts the first n (<= kSortCap) packed candidates of `a` descending, all
+// distinct, every key in [lo, hi]: a counting sort over kBinSortBins bins
+// that split [lo, hi] evenly (a bin index monotone in the key), then each
+// candidate's rank inside its bin by comparison with the bin's others.
+// Six barriers, against about sixty for the bitonic network.  A bin with more
+// than kBinSortMax candidates (values clustered or equal) sends the whole
+// list to sort_packed instead.  `cnt` holds kBinSortBins + 32 words and `tmp`
+// kSortCap entries of LDS, apart from `a`.
+constexpr int kBinSortBins = 4096;
+constexpr int kBinSortMax = 32;
+template <int NT>
+__device__ void sort_binned(unsigned long long *a, int n, uint32_t lo, uint32_t hi, uint32_t *cnt,
+                            unsigned long long *tmp) {
+  constexpr int NB = kBinSortBins, E = kSortCap / NT, PT = NB / NT;
+  static_assert(kSortCap % NT == 0 && NB % NT == 0 && PT == 4, "sort_binned: layout");
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (n <= 64) {
+    sort_packed<NT>(a, n);
+    return;
+  }
+  uint32_t *wsum = cnt + NB;      // NT / 64 words
+  uint32_t *crowd = cnt + NB + 16;
+  for (int i = tid; i < NB; i += NT) cnt[i] = 0u;
+  if (tid == 0) *crowd = 0u;
+  __syncthreads();
+  // bin (descending: bin 0 holds the largest keys) and place in it; the
+  // binary32 product rounds monotonically, so the bin never decreases with
+  // the key
+  const float scale = (float)NB / ((float)(hi - lo) + 1.0f);
+  unsigned long long x[E];
+  int bn[E], sl[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = tid + NT * e;
+    x[e] = 0ull;
+    bn[e] = 0;
+    sl[e] = 0;
+    if (i < n) {
+      x[e] = a[i];
+      const uint32_t key = cand_key(x[e]);
+      const int up = min(NB - 1, (int)((float)(key > lo ? key - lo : 0u) * scale));
+      bn[e] = NB - 1 - up;
+      sl[e] = (int)atomicAdd(&cnt[bn[e]], 1u);
+    }
+  }
+  __syncthreads();
+  // bin starts: exclusive prefix sum in place, PT bins per thread
+  {
+    const uint4 c = reinterpret_cast<const uint4 *>(cnt)[tid];
+    const uint32_t s = c.x + c.y + c.z + c.w;
+    const uint32_t mx = max(max(c.x, c.y), max(c.z, c.w));
+    const uint32_t ex = block_scan_incl<NT>(s, wsum) - s;   // one barrier inside
+    reinterpret_cast<uint4 *>(cnt)[tid] = make_uint4(ex, ex + c.x, ex + c.x + c.y, ex + c.x + c.y + c.z);
+    if (__ballot(mx > (uint32_t)kBinSortMax) && lane == 0) *crowd = 1u;
+  }
+  __syncthreads();
+  if (*crowd) {   // uniform: every thread reads the flag after the barrier
+    sort_packed<NT>(a, n, tmp);
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (tid + NT * e < n) tmp[cnt[bn[e]] + sl[e]] = x[e];
+  __syncthreads();
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    if (tid + NT * e < n) {
+      const int s = (int)cnt[bn[e]];
+      const int t = bn[e] + 1 < NB ? (int)cnt[bn[e] + 1] : n;
+      int rank = 0;
+      for (int j = s; j < t; ++j) rank += tmp[j] > x[e] ? 1 : 0;
+      a[s + rank] = x[e];
+    }
+  }
+  __syncthreads();
 }
 
 // ---------------------------------------------------------------- histories
@@ -511,31 +626,57 @@ __device__ __forceinline__ void pen_row(const HistRow h, const RowPlan P, float 
   if (tid == 0) full = 0;
   __syncthreads();
   // the repetition-only entries (before rep0 without presence / frequency)
-  // are not counted: their count is not used
-  for (int64_t t = pf ? tid : rep0 + tid; t < hl; t += NT) {
-    const int id = h.p[hist_pos(h, t)];
-    if (id < 0 || id >= V) continue;
-    uint32_t h = pen_hash(id);
-    int probe = 0;
-    for (; probe < kPenProbe; ++probe) {
-      const int old = atomicCAS(&keys[h], -1, id);
-      if (old == -1 || old == id) break;
-      h = (h + 1) & (kPenSlots - 1);
+  // are not counted: their count is not used.  Four ids per thread are
+  // requested before any is inserted.
+  bool over = false;
+  for (int64_t t0 = pf ? 0 : rep0; t0 < hl; t0 += 4 * NT) {
+    int ids[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int64_t t = t0 + tid + NT * c;
+      ids[c] = t < hl ? h.p[hist_pos(h, t)] : -1;
     }
-    if (probe == kPenProbe) {
-      full = 1;
-      break;
+#pragma unroll 1
+    for (int c = 0; c < 4; ++c) {
+      const int64_t t = t0 + tid + NT * c;
+      const int id = c == 0 ? ids[0] : c == 1 ? ids[1] : c == 2 ? ids[2] : ids[3];
+      if (over || id < 0 || id >= V) continue;
+      uint32_t hs = pen_hash(id);
+      int probe = 0;
+      for (; probe < kPenProbe; ++probe) {
+        const int old = atomicCAS(&keys[hs], -1, id);
+        if (old == -1 || old == id) break;
+        hs = (hs + 1) & (kPenSlots - 1);
+      }
+      if (probe == kPenProbe) {
+        over = true;
+        continue;
+      }
+      atomicAdd(&cnts[hs], 1u);
+      if (t >= rep0) atomicOr(&cnts[hs], 0x80000000u);
     }
-    atomicAdd(&cnts[h], 1u);
-    if (t >= rep0) atomicOr(&cnts[h], 0x80000000u);
+    if (over) break;
   }
+  if (over) full = 1;
   __syncthreads();
   if (!full) {
-    for (int i = tid; i < kPenSlots; i += NT) {
-      const int id = keys[i];
-      if (id < 0) continue;
-      const uint32_t c = cnts[i];
-      rowp[id] = penalise(rowp[id], (c >> 31) != 0, pf ? (c & 0x7FFFFFFFu) : 0u, P);
+    // every read of this thread's slots before any write (no write can
+    // alias a later read: the slots hold distinct ids)
+    constexpr int SPT = kPenSlots / NT;
+    static_assert(kPenSlots % NT == 0, "pen_row: slots per thread");
+    int sid[SPT];
+    float raw[SPT];
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      sid[i] = keys[tid + NT * i];
+      raw[i] = sid[i] >= 0 ? rowp[sid[i]] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      if (sid[i] >= 0) {
+        const uint32_t c = cnts[tid + NT * i];
+        rowp[sid[i]] = penalise(raw[i], (c >> 31) != 0, pf ? (c & 0x7FFFFFFFu) : 0u, P);
+      }
     }
     return;
   }
@@ -2418,7 +2559,9 @@ __global__ __launch_bounds__(kRowThreads) void mid_kernel(LaunchArgs a, Workspac
   uint32_t T = 0;
   int n_sel = 0;
   if (!overflow) {
-    sort_packed<kRowThreads>(srt, n);   // ends with a barrier
+    // every entry's key is in [lo, top_key] (the penalised and tail logits
+    // may exceed top_key: they share the top bin)
+    sort_binned<kRowThreads>(srt, n, lo, ms.top_key, hist, cbuf);   // ends with a barrier
     if (n >= k) {
       T = cand_key(srt[k - 1]);
       if (tid == 0) ms.n_sel = k;
