@@ -363,10 +363,17 @@ int choose_split(const hs_context *ctx, int rows, int vocab) {
 // A buffer that holds zeros between calls (arrival counters), grown and
 // cleared together: a failed clear drops the buffer, so that the next call
 // allocates and clears it again instead of counting from stale values.
-int ensure_zeroed(DevBuf &b, size_t need) {
+// Grows a counter buffer and clears it on the call's stream, ahead of the
+// call's kernels (a blocking-stream hipMemset would not be ordered with the
+// context's non-blocking stream, and the first kernels could count into
+// memory not yet cleared).  The clear is a fill kernel, not a memset node.
+int ensure_zeroed(DevBuf &b, size_t need, hipStream_t stream) {
   if (b.bytes >= need) return HS_OK;
   HS_HIP(b.ensure(need));
-  const hipError_t e = inject_failure() ? hipErrorOutOfMemory : hipMemset(b.p, 0, b.bytes);
+  const hipError_t e = inject_failure()
+                           ? hipErrorOutOfMemory
+                           : hs::launch_fill_u32(static_cast<uint32_t *>(b.p),
+                                                 (int64_t)(b.bytes / sizeof(uint32_t)), 0u, stream);
   if (e != hipSuccess) {
     b.release();
     return fail(HS_ERR_HIP, "hipMemset(counters) failed: %s", hipGetErrorString(e));
@@ -374,12 +381,12 @@ int ensure_zeroed(DevBuf &b, size_t need) {
   return HS_OK;
 }
 
-int ensure_split(hs_context *ctx, int rows, int split) {
+int ensure_split(hs_context *ctx, int rows, int split, hipStream_t stream) {
   if (split <= 1) return HS_OK;
   const size_t parts = (size_t)rows * (size_t)split;
   HS_HIP(ctx->split_list.ensure(parts * hs::kPartCap * sizeof(unsigned long long)));
   HS_HIP(ctx->split_meta.ensure(parts * sizeof(hs::SplitMeta)));
-  return ensure_zeroed(ctx->split_cnt, sizeof(uint32_t) * (size_t)rows);
+  return ensure_zeroed(ctx->split_cnt, sizeof(uint32_t) * (size_t)rows, stream);
 }
 
 hs::Workspace split_workspace(const hs_context *ctx) {
@@ -475,14 +482,14 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   if (n_chunk > 0) {
     HS_HIP(ctx->cand.ensure((size_t)n_chunk * (size_t)S * hs::kChunkCap * sizeof(uint2)));
     HS_HIP(ctx->info.ensure((size_t)n_chunk * (size_t)S * sizeof(hs::ChunkInfo)));
-    const int rz = ensure_zeroed(ctx->cand_count, sizeof(int32_t) * (size_t)n_chunk);
+    const int rz = ensure_zeroed(ctx->cand_count, sizeof(int32_t) * (size_t)n_chunk, stream);
     if (rz) return rz;
   }
   if (n_lfast > 0) HS_HIP(ctx->large_retry.ensure(sizeof(int32_t) * (size_t)n_lfast));
   if (n_large > 0) HS_HIP(ctx->large_replay.ensure(sizeof(hs::ReplayReq) * (size_t)n_large));
   // small batches split each row of the row kernel over several workgroups
   const int split = choose_split(ctx, n_row, vocab);
-  int rc = ensure_split(ctx, n_row, split);
+  int rc = ensure_split(ctx, n_row, split, stream);
   if (rc) return rc;
   rc = upload_plans(ctx, plans, rt, vocab, stream);
   if (rc) return rc;
@@ -572,7 +579,7 @@ int argmax_device(hs_context *ctx, const float *d_logits, int32_t rows, int64_t 
   const int split = choose_split(ctx, rows, vocab);
   if ((int64_t)rows * split > 0x7FFFFFFF)
     return fail(HS_ERR_UNSUPPORTED, "rows %d too many", rows);
-  int rc = ensure_split(ctx, rows, split);
+  int rc = ensure_split(ctx, rows, split, stream);
   if (rc) return rc;
   hs::Workspace ws = split_workspace(ctx);
   hs::LaunchArgs a;
@@ -686,7 +693,7 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const
     g.part_cap = cus * hs::kGemvWavesPerCU;
     const size_t slots = (size_t)g.part_cap * (size_t)M;
     HS_HIP(ctx->gemv_part.ensure(slots * 16 * sizeof(float)));
-    const int rz = ensure_zeroed(ctx->gemv_cnt, slots * sizeof(uint32_t));
+    const int rz = ensure_zeroed(ctx->gemv_cnt, slots * sizeof(uint32_t), stream);
     if (rz) return rz;
     g.part = static_cast<float *>(ctx->gemv_part.p);
     g.tile_cnt = static_cast<uint32_t *>(ctx->gemv_cnt.p);

@@ -896,6 +896,14 @@ struct RowScratch {          // LDS arrays of at least k entries each
   int32_t *rsid;
 };
 
+// atomicMin(dst, i) for the first lane of the wave whose pred holds, i rising
+// with the lane: one LDS atomic per wave instead of one per qualifying lane
+// (they all hit one word and would be serialised).
+__device__ __forceinline__ void first_min(bool pred, int i, int32_t *dst) {
+  const unsigned long long b = __ballot(pred);
+  if (b && lane_id() == __ffsll((long long)b) - 1) atomicMin(dst, i);
+}
+
 // Block-parallel tail of src/sampler.ts:79-117 over n >= 2 sorted candidate
 // keys s.skey[0, n) (descending), by NT threads.  Leaves the probabilities in
 // s.sprob and f.cutoff, f.pick.
@@ -931,12 +939,11 @@ __device__ __forceinline__ void tail_block(int n, const RowPlan &P, double u, Ro
     const float prob = (float)((double)(float)s.sp[i] / sum);
     s.sprob[i] = prob;
     const double pd = (double)prob;
-    if (!(pd == 0.0 || (pd >= 0x1p-29 && pd <= 1.0))) atomicMin(&f.m, i);
+    first_min(!(pd == 0.0 || (pd >= 0x1p-29 && pd <= 1.0)), i, &f.m);
   }
   __syncthreads();
   const double thr = P.min_p * (double)s.sprob[0];
-  for (int i = tid; i < n; i += NT)
-    if (i > 0 && (double)s.sprob[i] < thr) atomicMin(&f.f1, i);
+  for (int i = tid; i < n; i += NT) first_min(i > 0 && (double)s.sprob[i] < thr, i, &f.f1);
   const int m = f.m;
   // exact prefix sums over [0, m), into s.sp
   double carry = 0;
@@ -953,10 +960,8 @@ __device__ __forceinline__ void tail_block(int n, const RowPlan &P, double u, Ro
       tot += f.wtot[w];
     }
     c += add;
-    if (i < m) {
-      s.sp[i] = c;
-      if (c >= P.top_p) atomicMin(&f.f2, i);
-    }
+    if (i < m) s.sp[i] = c;
+    first_min(i < m && c >= P.top_p, i, &f.f2);
     carry = tot;
     exact = exact && tot < 2.0;
   }
@@ -988,8 +993,7 @@ __device__ __forceinline__ void tail_block(int n, const RowPlan &P, double u, Ro
   const double kept = s.sp[cut - 1];   // keptSum equals cumProb at cutoff - 1
   const double r0 = u * kept;
   if (cut <= mm) {
-    for (int i = tid; i < cut; i += NT)
-      if (s.sp[i] >= r0) atomicMin(&f.hit, i);
+    for (int i = tid; i < cut; i += NT) first_min(s.sp[i] >= r0, i, &f.hit);
     __syncthreads();
     if (tid == 0) f.pick = f.hit < cut ? f.hit : cut - 1;
   } else if (tid == 0) {
@@ -1021,14 +1025,14 @@ __device__ __forceinline__ void finish_row(const LaunchArgs &a, const RowPlan &P
   if (!need_replay) {
     n = n_sel < k ? n_sel : k;
     boundary_tie = n_sel > k;
-    for (int i = tid; i < n; i += NT) {
-      s.skey[i] = cand_key(srt[i]);
-      s.sids[i] = (int32_t)cand_idx(srt[i]);
-    }
-    __syncthreads();
     int tie = 0;
-    for (int i = tid; i + 1 < n; i += NT) tie |= s.skey[i] == s.skey[i + 1];
-    internal_tie = __syncthreads_or(tie) != 0;
+    for (int i = tid; i < n; i += NT) {
+      const uint32_t key = cand_key(srt[i]);
+      s.skey[i] = key;
+      s.sids[i] = (int32_t)cand_idx(srt[i]);
+      if (i + 1 < n) tie |= key == cand_key(srt[i + 1]);
+    }
+    internal_tie = __syncthreads_or(tie) != 0;   // also completes skey, sids
     if (closed_form) { boundary_tie = false; internal_tie = false; }
     // the candidate outputs must carry the reference's exact order
     if ((boundary_tie || internal_tie) && a.want_cands) need_replay = true;
@@ -2563,13 +2567,18 @@ __global__ __launch_bounds__(kRowThreads) void mid_kernel(LaunchArgs a, Workspac
     // may exceed top_key: they share the top bin)
     sort_binned<kRowThreads>(srt, n, lo, ms.top_key, hist, cbuf);   // ends with a barrier
     if (n >= k) {
+      // past the last entry equal to T (sorted: a binary search by every
+      // thread, usually settled by the first read)
       T = cand_key(srt[k - 1]);
-      if (tid == 0) ms.n_sel = k;
-      __syncthreads();
-      for (int i = k + tid; i < n; i += kRowThreads)   // the last entry equal to T
-        if (cand_key(srt[i]) == T && (i + 1 == n || cand_key(srt[i + 1]) != T)) ms.n_sel = i + 1;
-      __syncthreads();
-      n_sel = ms.n_sel;
+      int lo_i = k, hi_i = n;   // srt[lo_i - 1] == T; srt[hi_i] < T or hi_i == n
+      if (k < n && cand_key(srt[k]) == T) {
+        lo_i = k + 1;
+        while (lo_i < hi_i) {
+          const int mid = (lo_i + hi_i) >> 1;
+          if (cand_key(srt[mid]) == T) lo_i = mid + 1; else hi_i = mid;
+        }
+      }
+      n_sel = lo_i;
     } else {
       n_sel = n;
     }
