@@ -622,20 +622,26 @@ __device__ __forceinline__ void pen_row(const HistRow h, const RowPlan P, float 
   const int64_t hl = h.n;
   const int64_t rep0 = (P.pen & kPenRep) ? hl - (hl < 128 ? hl : 128) : hl;   // history.slice(-128)
   const bool pf = (P.pen & kPenPF) != 0;
-  for (int i = tid; i < kPenSlots; i += NT) { keys[i] = -1; cnts[i] = 0; }
-  if (tid == 0) full = 0;
-  __syncthreads();
   // the repetition-only entries (before rep0 without presence / frequency)
   // are not counted: their count is not used.  Four ids per thread are
-  // requested before any is inserted.
-  bool over = false;
-  for (int64_t t0 = pf ? 0 : rep0; t0 < hl; t0 += 4 * NT) {
-    int ids[4];
+  // requested before any is inserted, the first four before the table is
+  // cleared.
+  const int64_t tstart = pf ? 0 : rep0;
+  int ids[4];
+  auto request = [&](int64_t t0) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int64_t t = t0 + tid + NT * c;
       ids[c] = t < hl ? h.p[hist_pos(h, t)] : -1;
     }
+  };
+  request(tstart);
+  for (int i = tid; i < kPenSlots; i += NT) { keys[i] = -1; cnts[i] = 0; }
+  if (tid == 0) full = 0;
+  __syncthreads();
+  bool over = false;
+  for (int64_t t0 = tstart; t0 < hl; t0 += 4 * NT) {
+    if (t0 != tstart) request(t0);
 #pragma unroll 1
     for (int c = 0; c < 4; ++c) {
       const int64_t t = t0 + tid + NT * c;

@@ -94,3 +94,27 @@ def test_timing_slot(sampler):
         sampler.set_timing(False)
     assert calls == 1 and ms["argmax_kernel"] > 0
     assert all(v == 0 for k, v in ms.items() if k != "argmax_kernel")
+
+
+@pytest.mark.parametrize("path", ["sample", "argmax"])
+def test_first_call_on_fresh_split_context(path):
+    """The first call on a new context grows and clears the split rows'
+    arrival counters; that clear must be ordered before the call's kernels on
+    the context's own (non-blocking) stream, or a row can count into stale
+    memory and never complete (its token stays 0).  Several fresh contexts,
+    each used once, on a row whose answer is not 0."""
+    from tests.conftest import _context
+    x = np.full((1, 151936), -1.0, np.float32)
+    x[0, 123457] = 5.0
+    for i in range(6):
+        s = _context({"HS_ROW_SPLIT": "4"})
+        try:
+            print(f"[gpu] fresh split context {i}: {path}", flush=True)
+            if path == "argmax":
+                got = s.argmax(x.copy())
+            else:
+                got = s.sample_logits_batch(x.copy(), x.shape[1], None, [dict(temperature=0.0)],
+                                            np.zeros(1))
+            assert got.tolist() == [123457]
+        finally:
+            s.close()
