@@ -172,9 +172,12 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-parity", action="store_true")
-    ap.add_argument("--path", default="sample", choices=["sample", "greedy-route", "lmhead", "decode"])
+    ap.add_argument("--path", default="sample",
+                    choices=["sample", "greedy-route", "lmhead", "lmhead-sample", "decode"])
     ap.add_argument("--wfmt", default="q6_k", help="lm_head weight format (--path lmhead)")
     ap.add_argument("--hidden", type=int, default=2048, help="lm_head K (--path lmhead)")
+    ap.add_argument("--lm-greedy", action="store_true",
+                    help="--path lmhead-sample: greedy rows (temperature 0, repetition 1.1)")
     ap.add_argument("--hadamard", action="store_true",
                     help="Hadamard-folded lm_head: the input is rotated first (--path lmhead)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -430,6 +433,45 @@ def other_path(args) -> int:
             return {"logits": int(got.size), "within_2^-16_of_sum_abs": int((rel <= 2 ** -16).sum()),
                     "max_rel": float(rel.max())}
         count = rows
+        if args.path == "lmhead-sample":
+            # the lm_head and the sampler on its rows (one launch when every
+            # row takes k <= 64 with at most the repetition penalty): the
+            # headline's sampling, a 64-id history per hidden state
+            from hachiue_amd.sampler import make_configs
+            rng = np.random.default_rng(5)
+            hist = rng.integers(0, vocab, (rows, 64)).astype(np.int32)
+            off = np.arange(rows + 1, dtype=np.int64) * 64
+            cfg = [dict(temperature=0.0 if args.lm_greedy else 0.7, topK=40, topP=0.9,
+                        repetitionPenalty=1.1)] * rows
+            cfgs = make_configs(cfg, rows)
+            u = rng.random(rows)
+            d_ids, d_off = hip.DeviceArray.from_numpy(hist.reshape(-1)), hip.DeviceArray.from_numpy(off)
+            d_u, d_t = hip.DeviceArray.from_numpy(u), hip.DeviceArray(rows, np.int32)
+            unit = "sampled rows/s"
+            desc = desc.replace("lm_head GEMV:", "lm_head GEMV + greedy (repetition 1.1 over 64 ids):"
+                                if args.lm_greedy else
+                                "lm_head GEMV + sampling (top-k 40, top-p 0.9, "
+                                "repetition 1.1 over 64 ids, temperature 0.7):")
+
+            def step_on(ctx, i: int) -> None:
+                ctx.lm_head_sample_device_ex(d_x.addr, rows, K, wts[i % sets], d_y.addr, vocab,
+                                             d_ids.addr, d_off.addr, cfgs, d_u.addr, d_t.addr,
+                                             stream=stream)
+
+            def step(i: int) -> None:
+                step_on(sampler, i)
+
+            def check() -> dict:
+                from oracle import pyoracle
+                pen = d_y.download()
+                tok = d_t.download()
+                sampler.gemv_device_ex(d_x.addr, rows, K, wts[0], d_y.addr, vocab, stream=stream)
+                stream.synchronize()
+                raw = d_y.download()
+                res = pyoracle.sample_batch(raw, vocab, hist.reshape(-1), off, cfg, u)
+                return {"rows": rows, "tokens_equal": int((tok == res.token).sum()),
+                        "penalised_logits_equal": bool(np.array_equal(pen.view(np.uint32),
+                                                                      raw.view(np.uint32)))}
 
     step(0)
     stream.synchronize()
@@ -456,6 +498,26 @@ def other_path(args) -> int:
     kms, calls = sampler.kernel_times()
     sampler.set_timing(False)
     kms_avg = kms[kernel] / max(calls, 1)
+    two_launch = None
+    if args.path == "lmhead-sample":   # the same call on a context that always takes two launches
+        os.environ["HS_LMHEAD_FUSE"] = "0"
+        try:
+            other = Sampler(0)
+        finally:
+            del os.environ["HS_LMHEAD_FUSE"]
+        for i in range(args.warmup):
+            step_on(other, i)
+        hip.synchronize()
+        e0, e1 = hip.Event(), hip.Event()
+        e0.record(stream)
+        for i in range(args.steps):
+            step_on(other, i)
+        e1.record(stream)
+        e1.synchronize()
+        two_launch = round(e0.elapsed_ms(e1) / args.steps, 5)
+        other.close()
+        log(f"[bench] lmhead-sample: one launch {total_ms / args.steps * 1e3:.2f} us per step, "
+            f"two launches {two_launch * 1e3:.2f} us")
     if args.copy_probe and sets > 1:   # a copy of known size for the counters' scale
         d_in[1].copy_from(d_in[0])
         hip.synchronize()
@@ -479,6 +541,9 @@ def other_path(args) -> int:
         "cpu_baseline": None,
         "parity": parity,
     }
+    if two_launch is not None:
+        line["ms_per_step_two_launches"] = two_launch
+        line["kernels_ms"] = {k: round(v / max(calls, 1), 5) for k, v in kms.items() if v > 0}
     print(json.dumps(line), flush=True)
     sampler.close()
     return 0

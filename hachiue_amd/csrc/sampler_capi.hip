@@ -138,6 +138,9 @@ struct hs_context {
   DevBuf split_list, split_meta, split_cnt;   // split rows (split_cnt: zero between calls)
   DevBuf gemv_part, gemv_cnt;   // Q6_K GEMV tiles cut between waves (gemv_cnt: zero between calls)
   DevBuf gemv_rot;              // the Hadamard-rotated input of a folded weight
+  DevBuf fuse_rows, fuse_pool;  // lm_head GEMV that samples its rows: counters (zero
+                                //   between calls), the merge tree's lists
+  bool fuse = true;             // HS_LMHEAD_FUSE=0 at creation: always two launches
   DevBuf large_retry;           // two-pass large-k rows handed back
   DevBuf large_replay;          // slot-history replays asked for by the large-k kernel
   int64_t cand_count_rows = 0;     // rows whose counter is known to be zero
@@ -606,15 +609,22 @@ int argmax_device(hs_context *ctx, const float *d_logits, int32_t rows, int64_t 
 }
 
 // src/engine.ts:1493-1515 (the lm_head GEMV; see lmhead_kernels.hip).
-int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const hs_weights *wt,
-                float *d_y, int64_t ldy, hipStream_t stream) {
+// The checks and arguments of an lm_head GEMV call, on the call's stream
+// (entered: enter_stream ran).  A Hadamard-folded weight's input is rotated
+// here, into the workspace.  *skip: nothing to compute (M or N is 0).
+int gemv_setup(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const hs_weights *wt,
+               float *d_y, int64_t ldy, hipStream_t stream, hs::GemvArgs &g, bool *skip) {
+  *skip = false;
   if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
   if (!wt) return fail(HS_ERR_INVALID_ARGUMENT, "null weights");
   const int32_t K = wt->cols, N = wt->rows, w_type = wt->type;
   const void *d_w = wt->data;
   if (M < 0 || N < 0 || K <= 0)
     return fail(HS_ERR_INVALID_ARGUMENT, "need M >= 0, N >= 0, K > 0 (got %d, %d, %d)", M, N, K);
-  if (M == 0 || N == 0) return HS_OK;
+  if (M == 0 || N == 0) {
+    *skip = true;
+    return HS_OK;
+  }
   if (!d_x || !d_w || !d_y) return fail(HS_ERR_INVALID_ARGUMENT, "x, w and y must not be null");
   if (ldx < K || ldy < N)
     return fail(HS_ERR_INVALID_ARGUMENT, "ldx %lld < K or ldy %lld < N", (long long)ldx, (long long)ldy);
@@ -648,7 +658,6 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const
   // (Q6_K's slabs read up to 3 KiB past a row's start)
   if ((int64_t)N * row_bytes > (w_type == hs::kW_Q6_K ? 0xFFFF0000LL : 0xFFFFFF00LL))
     return fail(HS_ERR_UNSUPPORTED, "weights of %lld bytes above 4 GiB", (long long)(N * row_bytes));
-  hs::GemvArgs g;
   memset(&g, 0, sizeof g);
   g.x = d_x;
   g.ldx = ldx;
@@ -673,20 +682,6 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const
   const int64_t wpb = hs::kGemvThreads / 64;
   g.blocks = (int32_t)std::min<int64_t>((steps + wpb - 1) / wpb, 1 << 20);
   if (M > 65535) return fail(HS_ERR_UNSUPPORTED, "M %d above 65535", M);
-  DeviceGuard guard(ctx->device);
-  int rc0 = enter_stream(ctx, stream);
-  if (rc0) return rc0;
-  if (wt->hadamard) {   // src/engine.ts:1121-1145: the input is rotated first
-    HS_HIP(ctx->gemv_rot.ensure((size_t)M * (size_t)K * sizeof(float)));
-    float *rot = static_cast<float *>(ctx->gemv_rot.p);
-    const hipError_t e = hs::launch_hadamard(d_x, ldx, wt->signs, rot, M, K, stream);
-    if (e != hipSuccess) {
-      (void)leave_stream(ctx, stream, false);
-      return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
-    }
-    g.x = rot;
-    g.ldx = K;
-  }
   if (w_type == hs::kW_Q6_K) {   // the hand-over slots of tiles cut between waves
     int cus = 0;
     HS_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device));
@@ -698,22 +693,51 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const
     g.part = static_cast<float *>(ctx->gemv_part.p);
     g.tile_cnt = static_cast<uint32_t *>(ctx->gemv_cnt.p);
   }
-  hipEvent_t *ev = nullptr;
-  if (ctx->timing) {
-    hs_context::TimedCall tc{};
-    tc.mask = 1u << hs::kGemvTimedSlot;
-    for (int i = 0; i < 2; ++i) {
-      if (ctx->ev_free.empty()) {
-        hipEvent_t x;
-        HS_HIP(hipEventCreate(&x));
-        ctx->ev_free.push_back(x);
-      }
-      tc.ev[2 * hs::kGemvTimedSlot + i] = ctx->ev_free.back();
-      ctx->ev_free.pop_back();
-    }
-    ctx->timed.push_back(tc);
-    ev = ctx->timed.back().ev + 2 * hs::kGemvTimedSlot;
+  if (wt->hadamard) {   // src/engine.ts:1121-1145: the input is rotated first
+    HS_HIP(ctx->gemv_rot.ensure((size_t)M * (size_t)K * sizeof(float)));
+    float *rot = static_cast<float *>(ctx->gemv_rot.p);
+    const hipError_t e = hs::launch_hadamard(d_x, ldx, wt->signs, rot, M, K, stream);
+    if (e != hipSuccess) return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+    g.x = rot;
+    g.ldx = K;
   }
+  return HS_OK;
+}
+
+// Start/end events of timing slot `slot` for the call's one kernel, when
+// timing is on (null otherwise).
+int timed_slot(hs_context *ctx, int slot, hipEvent_t **ev) {
+  *ev = nullptr;
+  if (!ctx->timing) return HS_OK;
+  hs_context::TimedCall tc{};
+  tc.mask = 1u << slot;
+  for (int i = 0; i < 2; ++i) {
+    if (ctx->ev_free.empty()) {
+      hipEvent_t x;
+      HS_HIP(hipEventCreate(&x));
+      ctx->ev_free.push_back(x);
+    }
+    tc.ev[2 * slot + i] = ctx->ev_free.back();
+    ctx->ev_free.pop_back();
+  }
+  ctx->timed.push_back(tc);
+  *ev = ctx->timed.back().ev + 2 * slot;
+  return HS_OK;
+}
+
+int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const hs_weights *wt,
+                float *d_y, int64_t ldy, hipStream_t stream) {
+  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  DeviceGuard guard(ctx->device);
+  int rc = enter_stream(ctx, stream);
+  if (rc) return rc;
+  hs::GemvArgs g;
+  bool skip = false;
+  rc = gemv_setup(ctx, d_x, M, ldx, wt, d_y, ldy, stream, g, &skip);
+  if (rc || skip) return rc;   // nothing was enqueued
+  hipEvent_t *ev = nullptr;
+  rc = timed_slot(ctx, hs::kGemvTimedSlot, &ev);
+  if (rc) return rc;
   const hipError_t e = hs::launch_gemv(g, stream, ev, ctx->done_ev);
   if (e != hipSuccess) {
     (void)leave_stream(ctx, stream, false);
@@ -935,6 +959,7 @@ int hs_context_create(int device, hs_context **out) {
   ctx->device = device;
   if (const char *env = getenv("HS_ROW_KERNEL_MIN_ROWS")) ctx->row_min_rows = atoi(env);
   if (const char *env = getenv("HS_ROW_SPLIT")) ctx->row_split = atoi(env);
+  if (const char *env = getenv("HS_LMHEAD_FUSE")) ctx->fuse = atoi(env) != 0;
   e = hipEventCreateWithFlags(&ctx->plan_done, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->done_ev, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->na_upload_ev, hipEventDisableTiming);
@@ -1106,17 +1131,89 @@ int hs_lm_head_sample_device(hs_context *ctx, const float *d_x, int32_t M, int64
                        d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr, st);
 }
 
+namespace {
+
+// The lm_head GEMV and the sampler on its M rows: one launch of the planar
+// GEMV that samples its own rows when every row is greedy or takes k <= 64
+// candidates with at most the repetition penalty (and the vocabulary fits
+// its per-wave record); otherwise the GEMV, then hs_sample_batch_device.
+// Either way the logits hold the penalised values afterwards.
+int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const hs_weights *w,
+                   float *d_logits, int64_t ldl, const int32_t *d_hist_ids,
+                   const int64_t *d_hist_offsets, const hs_sample_config *configs,
+                   const double *d_uniforms, int32_t *d_tokens, hipStream_t st) {
+  if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
+  if (!w) return fail(HS_ERR_INVALID_ARGUMENT, "null weights");
+  bool fused = ctx->fuse && hs::tern_quant_bytes(w->type) > 0 && M > 0 && w->rows > 0 && configs &&
+               d_uniforms && d_tokens && (d_hist_ids == nullptr) == (d_hist_offsets == nullptr);
+  std::vector<hs::RowPlan> plans;
+  Routing rt;
+  if (fused) {
+    try {
+      int rc = build_plans(configs, M, w->rows, ctx->row_min_rows, plans, rt);
+      if (rc) return rc;
+    } catch (const std::bad_alloc &) {
+      return fail(HS_ERR_OUT_OF_MEMORY, "host allocation failed");
+    }
+    for (const hs::RowPlan &p : plans)
+      if ((p.mode != hs::kModeGreedy && p.mode != hs::kModeSmall) || (p.pen & hs::kPenPF))
+        fused = false;
+  }
+  if (fused) {
+    DeviceGuard guard(ctx->device);
+    int rc = enter_stream(ctx, st);
+    if (rc) return rc;
+    hs::GemvArgs g;
+    bool skip = false;
+    rc = gemv_setup(ctx, d_x, M, ldx, w, d_logits, ldl, st, g, &skip);
+    if (rc) return rc;
+    const int blocks = skip ? 0 : hs::tern_sample_grid(g);
+    if (blocks > 0) {
+      const size_t nl = (size_t)M * blocks;
+      HS_HIP(ctx->fuse_pool.ensure(nl * 64 * sizeof(unsigned long long) + nl * sizeof(uint32_t)));
+      // counters: zero between calls (each is reset by the workgroup that counts last)
+      rc = ensure_zeroed(ctx->fuse_rows, (size_t)M * sizeof(hs::FuseRow), st);
+      if (rc) return rc;
+      rc = upload_plans(ctx, plans, rt, w->rows, st);
+      if (rc) return rc;
+      hs::FuseArgs f;
+      f.plans = static_cast<const hs::RowPlan *>(ctx->plans.p);
+      f.hist_ids = d_hist_ids;
+      f.hist_off = d_hist_offsets;
+      f.uniforms = d_uniforms;
+      f.tokens = d_tokens;
+      f.rows = static_cast<hs::FuseRow *>(ctx->fuse_rows.p);
+      f.list = static_cast<unsigned long long *>(ctx->fuse_pool.p);
+      f.disc = reinterpret_cast<uint32_t *>(f.list + nl * 64);
+      f.blocks = blocks;
+      hipEvent_t *ev = nullptr;
+      rc = timed_slot(ctx, hs::kGemvTimedSlot, &ev);
+      if (rc) return rc;
+      const hipError_t e = hs::launch_tern_sample(g, f, st, ev, ctx->done_ev);
+      if (e != hipSuccess) {
+        (void)leave_stream(ctx, st, false);
+        return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+      }
+      return leave_stream(ctx, st, ev == nullptr);
+    }
+    if (g.x != d_x) (void)leave_stream(ctx, st, false);   // the rotation was enqueued
+  }
+  int rc = gemv_device(ctx, d_x, M, ldx, w, d_logits, ldl, st);
+  if (rc) return rc;
+  return sample_device(ctx, d_logits, M, ldl, w->rows, d_hist_ids, d_hist_offsets, configs,
+                       d_uniforms, d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr, st);
+}
+
+}  // namespace
+
 int hs_lm_head_sample_device_ex(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx,
                                 const hs_weights *w, float *d_logits, int64_t ldl,
                                 const int32_t *d_hist_ids, const int64_t *d_hist_offsets,
                                 const hs_sample_config *configs, const double *d_uniforms,
                                 int32_t *d_tokens, void *stream) {
   HS_LOCK(ctx);
-  const hipStream_t st = static_cast<hipStream_t>(stream);
-  int rc = gemv_device(ctx, d_x, M, ldx, w, d_logits, ldl, st);
-  if (rc) return rc;
-  return sample_device(ctx, d_logits, M, ldl, w->rows, d_hist_ids, d_hist_offsets, configs,
-                       d_uniforms, d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr, st);
+  return lm_head_sample(ctx, d_x, M, ldx, w, d_logits, ldl, d_hist_ids, d_hist_offsets, configs,
+                        d_uniforms, d_tokens, static_cast<hipStream_t>(stream));
 }
 
 // src/engine.ts:80-175 (createBlockSplitter): GGUF blocks of Q1_0 ([d][16 B

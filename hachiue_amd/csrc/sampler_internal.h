@@ -258,4 +258,34 @@ hipError_t prepare_kernels();   // per device, once: raise dynamic LDS limits
 size_t row_smem_bytes(int vocab);
 size_t mid_smem_bytes(int vocab);
 
+// ---- the planar lm_head GEMV that samples its own rows (one launch)
+// Workgroups of `kernel` resident at once on the current GPU (cached).
+int resident_blocks(const void *kernel, uint32_t lds, int threads);
+// Per activation row, zero between calls (the workgroup that completes the
+// row resets it).
+struct FuseRow {
+  unsigned long long best;   // greedy: packed maximum of the row
+  uint32_t arrived;          // workgroups done
+  uint32_t pad;
+};
+static_assert(sizeof(FuseRow) == 16, "FuseRow layout");
+constexpr int kFuseTiles = 8;     // 16-row tiles a wave of the fused GEMV records
+constexpr int kFuseStage = 1024;  // entries the last workgroup ranks
+struct FuseArgs {
+  const RowPlan *plans;      // [M]: greedy or k <= 64, repetition penalty only
+  const int32_t *hist_ids;   // packed lists (hist_off[m], hist_off[m + 1]) or null
+  const int64_t *hist_off;
+  const double *uniforms;    // [M]
+  int32_t *tokens;           // [M]
+  FuseRow *rows;             // [M]
+  unsigned long long *list;  // [M][blocks][64] each workgroup's top 64
+  uint32_t *disc;            // [M][blocks] and the largest key it left out
+  int32_t blocks;            // workgroups per activation row
+};
+hipError_t launch_tern_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
+                              hipEvent_t *ev, hipEvent_t done);
+// Its workgroups per activation row, or 0 when N needs more tiles per wave
+// than it records (then the two-launch path is used).
+int tern_sample_grid(const GemvArgs &g);
+
 }  // namespace hs

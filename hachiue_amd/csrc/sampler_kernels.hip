@@ -47,6 +47,7 @@
 #include <math.h>
 
 #include "hachiue_sampler.h"
+#include "tern_gemv.h"
 
 namespace hs {
 
@@ -1677,7 +1678,9 @@ __device__ __forceinline__ TailState tail_decide(const LaunchArgs &a, const RowP
   return st;
 }
 
-// The replay when needed, then the token and the optional outputs.
+// The replay when needed, then the token and the optional outputs (RB:
+// the replay's logits in flight per lane).
+template <int RB = 16>
 __device__ __forceinline__ void tail_finish(const LaunchArgs &a, const RowPlan &P, int row,
                                             const float *rowp, TailState st, double u,
                                             float *rsv, int32_t *rsid, double *sp,
@@ -1687,7 +1690,7 @@ __device__ __forceinline__ void tail_finish(const LaunchArgs &a, const RowPlan &
   bool replayed = false;
   if (st.need) {
     if (acquire_replay) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    replay_row<16>(rowp, a.vocab, k, rsv, rsid, bkey);
+    replay_row<RB>(rowp, a.vocab, k, rsv, rsid, bkey);
     const bool filled = lane < k && rsid[lane] >= 0;
     unsigned long long x = filled ? pack_cand(f2key(rsv[lane]), (uint32_t)lane) : 0ull;
     x = wave_sort_desc64(x);   // value descending, slot ascending (stable sort)
@@ -1717,11 +1720,12 @@ __device__ __forceinline__ void tail_finish(const LaunchArgs &a, const RowPlan &
   }
 }
 
+template <int RB = 16>
 __device__ __forceinline__ void finish_wave(const LaunchArgs &a, const RowPlan &P, int row, const float *rowp,
                             unsigned long long F, bool extra_ties, bool force_replay, double u,
                             float *rsv, int32_t *rsid, double *sp, bool acquire_replay = false) {
   const TailState st = tail_decide(a, P, F, extra_ties, force_replay, u, sp);
-  tail_finish(a, P, row, rowp, st, u, rsv, rsid, sp, acquire_replay, nullptr);
+  tail_finish<RB>(a, P, row, rowp, st, u, rsv, rsid, sp, acquire_replay, nullptr);
 }
 
 size_t row_smem_bytes(int vocab) {
@@ -4574,6 +4578,488 @@ __global__ __launch_bounds__(kRowThreads) void argmax_kernel(LaunchArgs a, Works
   }
 }
 
+// ---------------------------------------------------------------- lm_head GEMV that samples its rows
+//
+// One launch for the planar lm_head (src/engine.ts:1493-1515) and the
+// sampler on its rows, for rows that are greedy or take k <= 64 candidates
+// with at most the repetition penalty (hachiue's defaults: topK 20).  In the
+// GEMV's loop a tile's results are only written as logits and recorded in
+// the wave's LDS buffer.  After the loop each wave penalises its recorded
+// results where the row's history asks for it (src/sampler.ts:24-33: the
+// last 128 ids, each distinct id once; the logit is written again) and keeps
+// their top 64; the workgroup merges its waves' lists and publishes its own
+// top 64, with the largest key it left out (`disc`).  The last workgroup to
+// count itself in takes as a bound the 64th largest of the lists' first J
+// entries (J = 1 with 64 or more lists: the workgroups' maxima, distinct
+// logits, so the row has at least 64 at or above it), gathers the entries at
+// or above it (a few dozen on common rows), ranks them, and runs the row
+// kernel's tail (wave_tail, with the slot replay over the written logits
+// when equal values decide the draw).
+// Exactness, as for split rows: every logit of the row's top k (k <= 64) is
+// in its wave's and its workgroup's top 64, and at or above the bound; a
+// value equal to the k-th largest left out of a list shows as that list's
+// disc, which flags the boundary tie.  More than kFuseStage entries at or
+// above the bound (many equal values) send the row to the replay.  Greedy
+// rows keep the packed maximum instead.  No workgroup waits for another:
+// each publishes with agent-scope stores, waits for them, then counts
+// itself in; the one that counts last reads.
+
+constexpr int kFuseSetSlots = 256;   // repetition ids of a row (at most 128)
+__device__ __forceinline__ uint32_t fuse_hash(int id) {
+  return ((uint32_t)id * 2654435761u) >> 24;
+}
+__device__ __forceinline__ bool fuse_in_set(const int32_t *set, int id) {
+  uint32_t h = fuse_hash(id);
+  for (int probe = 0; probe < kFuseSetSlots; ++probe) {
+    const int v = set[h];
+    if (v == id) return true;
+    if (v < 0) return false;
+    h = (h + 1) & (kFuseSetSlots - 1);
+  }
+  return false;
+}
+
+struct FuseSmem {
+  int32_t rset[kFuseSetSlots];
+  unsigned long long best[16];
+  uint32_t disc, bound, key64, lo, hi;
+  int32_t last, nf, bin, nmore;
+  unsigned long long top[64];
+  float rsv[64];
+  int32_t rsid[64];
+  double sp[64];
+};
+
+// The epilogue the GEMV body calls with each tile's results (tern_gemv.h):
+// the logit is written through (the last workgroup may replay the row),
+// except at the row's repetition ids, written once penalised after the loop,
+// and (value bits, row) recorded in the wave's buffer; row ~0u marks no
+// result.
+struct RecordEpi {
+  float *y;
+  uint2 *wbuf;          // kFuseTiles * 16 entries
+  const int32_t *rset;  // the repetition ids, or null
+  int nt;               // tiles recorded (wave-uniform)
+  __device__ __forceinline__ void out(int lane, int row, float v, bool valid) {
+    if (valid && !(rset && fuse_in_set(rset, row))) store_agent(y + row, v);
+    // (the body calls past the wave's last tile with nothing valid; the
+    // launch gives no wave more than kFuseTiles tiles)
+    if (!__ballot(valid) || nt >= kFuseTiles) return;
+    if (lane < 16)
+      wbuf[nt * 16 + lane] = make_uint2(__float_as_uint(v), valid ? (uint32_t)row : ~0u);
+    ++nt;
+  }
+};
+
+constexpr int kFuseLoad = 2048;   // list entries the last workgroup loads at first
+constexpr int kFuseBins = 1024;
+// LDS: the GEMV body's, the waves' result buffers, then the histogram and
+// the candidates; the last workgroup's loads reuse the body's and the
+// buffers' (at least kFuseLoad entries).
+__host__ __device__ inline size_t fuse_extra_off(int K, int nw) {
+  const size_t rec = gemv_tern_lds_bytes(K) + (size_t)nw * kFuseTiles * 16 * sizeof(uint2);
+  const size_t ld = (size_t)kFuseLoad * sizeof(unsigned long long);
+  return rec > ld ? rec : ld;
+}
+size_t tern_sample_lds_bytes(int K, int nw) {
+  return fuse_extra_off(K, nw) + kFuseBins * sizeof(uint32_t) + (size_t)kFuseStage * sizeof(unsigned long long);
+}
+
+// The top 64 of the n packed candidates at src (0: none) into fs.top
+// (descending, zeros past the count), the 65th's key into fs.key64 and the
+// largest key of the others into fs.disc.  The 64th largest key is bounded
+// from below by a histogram of the keys over [their least, their largest]
+// (kFuseBins bins, each bin's keys above the previous bin's): the entries in
+// the bins from the top down to where 64 are reached are compacted into
+// `cand` and ranked by comparison (a few dozen on common rows).  False when
+// more than `cap` reach it (many equal keys).  Every thread calls it.
+template <int NT>
+__device__ bool block_top64(const unsigned long long *src, int n, uint32_t *bins,
+                            unsigned long long *cand, int cap, FuseSmem &fs) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (tid == 0) { fs.lo = ~0u; fs.hi = 0u; fs.bin = -1; fs.nf = 0; fs.key64 = 0u; fs.disc = 0u; }
+  for (int i = tid; i < kFuseBins; i += NT) bins[i] = 0u;
+  for (int i = tid; i < 64; i += NT) fs.top[i] = 0ull;
+  __syncthreads();
+  {
+    uint32_t lo = ~0u, hi = 0u;
+    for (int i = tid; i < n; i += NT) {
+      const uint32_t kx = cand_key(src[i]);
+      if (kx) { lo = kx < lo ? kx : lo; hi = kx > hi ? kx : hi; }
+    }
+    lo = ~wave_max_u32(~lo);
+    hi = wave_max_u32(hi);
+    if (lane == 0 && hi) { atomicMin(&fs.lo, lo); atomicMax(&fs.hi, hi); }
+  }
+  __syncthreads();
+  const uint32_t klo = fs.lo, khi = fs.hi;
+  const float bscale = (float)kFuseBins / ((float)(khi - klo) + 1.0f);
+  auto bin_of = [&](uint32_t kx) { return min(kFuseBins - 1, (int)((float)(kx - klo) * bscale)); };
+  if (khi)
+    for (int i = tid; i < n; i += NT) {
+      const uint32_t kx = cand_key(src[i]);
+      if (kx) atomicAdd(&bins[bin_of(kx)], 1u);
+    }
+  __syncthreads();
+  if (tid < 64 && khi) {   // wave 0: from the top bin down to where 64 keys are reached
+    uint32_t cum = 0;
+    for (int top = kFuseBins - 1; top >= 0; top -= 64) {
+      const int bb = top - lane;
+      const uint32_t cnt = bb >= 0 ? bins[bb] : 0u;
+      const uint32_t incl = wave_scan_incl(cnt);
+      const uint32_t tot = readlane_u32(incl, 63);
+      if (cum + tot >= 64u) {
+        const unsigned long long mk = __ballot(cum + incl >= 64u);
+        if (lane == 0) fs.bin = top - (__ffsll((long long)mk) - 1);
+        break;
+      }
+      cum += tot;
+    }
+  }
+  __syncthreads();
+  const int bstar = fs.bin < 0 ? 0 : fs.bin;   // fewer than 64 keys: all of them
+  uint32_t dm = 0u;
+  for (int i0 = 0; i0 < n; i0 += NT) {
+    const int i = i0 + tid;
+    const unsigned long long x = i < n ? src[i] : 0ull;
+    const uint32_t kx = cand_key(x);
+    const bool keep = kx != 0u && bin_of(kx) >= bstar;
+    if (kx && !keep) dm = kx > dm ? kx : dm;
+    const unsigned long long bl = __ballot(keep);
+    if (bl) {
+      int base = 0;
+      if (lane == 0) base = atomicAdd(&fs.nf, __popcll(bl));
+      base = __shfl(base, 0);
+      const int p = base + (int)lanes_below(bl);
+      if (keep && p < cap) cand[p] = x;
+    }
+  }
+  dm = wave_max_u32(dm);
+  if (lane == 0 && dm) atomicMax(&fs.disc, dm);
+  __syncthreads();
+  const int nc = fs.nf;
+  if (nc > cap) return false;
+  for (int i = tid; i < nc; i += NT) {
+    const unsigned long long xi = cand[i];
+    int rank = 0;
+    for (int j = 0; j < nc; ++j) rank += cand[j] > xi ? 1 : 0;
+    if (rank < 64) fs.top[rank] = xi;
+    if (rank == 64) fs.key64 = cand_key(xi);
+  }
+  __syncthreads();
+  return true;
+}
+
+// Counts the calling workgroup in at *cnt (after its published stores
+// completed); true in the one that counts `of`, which also zeroes *cnt for
+// the next call.  Every thread calls it.
+__device__ __forceinline__ bool fuse_arrive(uint32_t *cnt, uint32_t of, FuseSmem &fs) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    fs.last = old == of - 1;
+    if (fs.last) store_agent(cnt, 0u);
+  }
+  __syncthreads();
+  return fs.last != 0;
+}
+
+// (one 16-wave workgroup per CU, where the plain GEMV fits two: its
+// epilogue's scalar registers.  Bounding them to fit two was measured slower:
+// the GEMV part is no faster and the last workgroup gets twice the lists.)
+template <int FMT>
+__global__ __launch_bounds__(64 * tm::waves<FMT>()) void gemv_tern_sample_kernel(GemvArgs g,
+                                                                                   FuseArgs f) {
+  constexpr int NW = tm::waves<FMT>(), NT = 64 * NW;
+  extern __shared__ uint4 tlds[];
+  __shared__ FuseSmem fs;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m = (int)blockIdx.y;
+  const RowPlan *plan = f.plans + m;
+  const int mode = load_scalar(&plan->mode);
+  const bool rep = (load_scalar(&plan->pen) & kPenRep) != 0;
+  float *y = g.y + (int64_t)m * g.ldy;
+
+  // the row's repetition set: history.slice(-128), ids in [0, N)
+  if (tid < kFuseSetSlots) fs.rset[tid] = -1;
+  if (tid == 0) fs.disc = 0u;
+  __syncthreads();
+  if (rep && f.hist_off && tid < 128) {
+    const int64_t h0 = f.hist_off[m], n = f.hist_off[m + 1] - h0;
+    const int64_t j = n - (n < 128 ? n : 128) + tid;
+    if (j < n) {
+      const int id = f.hist_ids[h0 + j];
+      if (id >= 0 && id < g.N) {
+        uint32_t h = fuse_hash(id);
+        for (int probe = 0; probe < kFuseSetSlots; ++probe) {
+          const int old = atomicCAS(&fs.rset[h], -1, id);
+          if (old == -1 || old == id) break;
+          h = (h + 1) & (kFuseSetSlots - 1);
+        }
+      }
+    }
+  }
+  // (the body's first barrier completes the set)
+
+  uint2 *wbuf = reinterpret_cast<uint2 *>(reinterpret_cast<uint8_t *>(tlds) + gemv_tern_lds_bytes(g.K)) +
+                wave * kFuseTiles * 16;
+  RecordEpi epi{y, wbuf, rep ? fs.rset : nullptr, 0};
+  tern_gemv_body<FMT>(g, tlds, epi);
+
+  // ---- this wave's results as packed candidates in its buffer (penalties
+  // applied; unused slots 0), or its maximum
+  const bool greedy = mode == kModeGreedy;
+  const double prep = load_scalar(&plan->rep);
+  const int ne = epi.nt * 16;
+  unsigned long long *cb = reinterpret_cast<unsigned long long *>(wbuf);   // the same slots
+  unsigned long long best = 0ull;
+  for (int e = lane; e < kFuseTiles * 16; e += 64) {
+    unsigned long long c = 0ull;
+    if (e < ne) {
+      const uint2 r = wbuf[e];
+      float v = __uint_as_float(r.x);
+      if (r.y != ~0u) {
+        if (rep && fuse_in_set(fs.rset, (int)r.y)) {
+          RowPlan pr{};
+          pr.rep = prep;
+          pr.pen = kPenRep;
+          v = penalise(v, true, 0u, pr);
+          store_agent(y + r.y, v);
+        }
+        const uint32_t key = f2key(v);
+        c = key ? pack_cand(key, r.y) : 0ull;
+      }
+    }
+    if (greedy) best = c > best ? c : best;
+    else cb[e] = c;
+  }
+  __syncthreads();   // every wave is done with the body's LDS and its buffer
+  FuseRow *fr = f.rows + m;
+  unsigned long long *buf = reinterpret_cast<unsigned long long *>(tlds);
+  uint32_t *bins = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(tlds) + fuse_extra_off(g.K, NW));
+  unsigned long long *xcand = reinterpret_cast<unsigned long long *>(bins + kFuseBins);   // kFuseStage
+  LaunchArgs a{};
+  a.logits = g.y;
+  a.stride = g.ldy;
+  a.rows = g.M;
+  a.vocab = g.N;
+  a.uniforms = f.uniforms;
+  a.tokens = f.tokens;
+
+  if (greedy) {   // the packed maximum; the last workgroup writes the token
+    const unsigned long long b = wave_max64(best);
+    if (lane == 0) fs.best[wave] = b;
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long bb = 0ull;
+      for (int w = 0; w < NW; ++w) bb = fs.best[w] > bb ? fs.best[w] : bb;
+      if (bb) __hip_atomic_fetch_max(&fr->best, bb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (!fuse_arrive(&fr->arrived, gridDim.x, fs)) return;
+    if (tid == 0) {
+      const unsigned long long bb = load_agent(&fr->best);
+      write_greedy(a, m, load_agent(y), bb);
+      store_agent(&fr->best, 0ull);
+    }
+    return;
+  }
+
+  // ---- the workgroup's top 64, published (its disc: the largest key left
+  // out; ~0u marks a workgroup whose candidates did not fit, the row is
+  // then replayed)
+  const unsigned long long *wsrc = reinterpret_cast<const unsigned long long *>(
+      reinterpret_cast<uint8_t *>(tlds) + gemv_tern_lds_bytes(g.K));
+  const bool fit = block_top64<NT>(wsrc, NW * kFuseTiles * 16, bins, xcand, kFuseStage, fs);
+  const int64_t r0 = (int64_t)m * f.blocks;
+  if (wave == 0) {
+    store_agent(f.list + (r0 + blockIdx.x) * 64 + lane, fit ? fs.top[lane] : 0ull);
+    const uint32_t d = fs.disc > fs.key64 ? fs.disc : fs.key64;
+    if (lane == 0) store_agent(f.disc + r0 + blockIdx.x, fit ? d : ~0u);
+  }
+  if (!fuse_arrive(&fr->arrived, (uint32_t)f.blocks, fs)) return;
+
+  // ---- the row, by the last workgroup.  The first J entries of every list
+  // (J = 4, or more when there are fewer than 16 lists, so that J * B >= 64)
+  // are distinct logits of the row, so the 64th
+  // largest of them bounds the row's 64th largest from below.  It is found
+  // by a histogram over [their least key, their largest key] (kFuseBins
+  // bins, each bin's keys above the previous bin's), then the least loaded
+  // key in the bins from the top down to where 64 are reached.  Every entry
+  // at or above it is then among the loaded ones, or in a list whose J-th
+  // entry reaches it (read whole).
+  const int B = f.blocks;
+  const unsigned long long *lists = f.list + r0 * 64;
+  const int J = min(64, max(4, (64 + B - 1) / B));   // J * B <= kFuseLoad: the launch checks
+  const int nk = B * J;
+  unsigned long long *ld = buf;                                         // kFuseLoad entries
+  unsigned long long *cand = xcand;                                     // kFuseStage entries
+  if (tid == 0) { fs.bound = ~0u; fs.disc = 0u; fs.nf = 0; fs.key64 = 0u; fs.lo = ~0u; fs.hi = 0u; fs.bin = -1; }
+  for (int i = tid; i < kFuseBins; i += NT) bins[i] = 0u;
+  __syncthreads();
+  {
+    uint32_t lo = ~0u, hi = 0u, dm = 0u;
+    for (int t = tid; t < nk; t += NT) {
+      const int i = t / J, j = t - i * J;
+      const unsigned long long x = load_agent(lists + (int64_t)i * 64 + j);
+      ld[t] = x;
+      const uint32_t kx = cand_key(x);
+      if (kx) { lo = kx < lo ? kx : lo; hi = kx > hi ? kx : hi; }
+      if (j == 0) {
+        const uint32_t d = load_agent(f.disc + r0 + i);
+        dm = d > dm ? d : dm;
+      }
+    }
+    lo = ~wave_max_u32(~lo);
+    hi = wave_max_u32(hi);
+    dm = wave_max_u32(dm);
+    if (lane == 0) {
+      if (dm) atomicMax(&fs.disc, dm);
+      if (hi) { atomicMin(&fs.lo, lo); atomicMax(&fs.hi, hi); }
+    }
+  }
+  __syncthreads();
+  const uint32_t klo = fs.lo, khi = fs.hi;
+  const float bscale = (float)kFuseBins / ((float)(khi - klo) + 1.0f);
+  auto bin_of = [&](uint32_t kx) { return min(kFuseBins - 1, (int)((float)(kx - klo) * bscale)); };
+  if (khi) {
+    for (int t = tid; t < nk; t += NT) {
+      const uint32_t kx = cand_key(ld[t]);
+      if (kx) atomicAdd(&bins[bin_of(kx)], 1u);
+    }
+  }
+  __syncthreads();
+  if (wave == 0 && khi) {   // from the top bin down to where 64 keys are reached
+    uint32_t cum = 0;
+    for (int top = kFuseBins - 1; top >= 0; top -= 64) {
+      const int bb = top - lane;
+      const uint32_t cnt = bb >= 0 ? bins[bb] : 0u;
+      const uint32_t incl = wave_scan_incl(cnt);
+      const uint32_t tot = readlane_u32(incl, 63);
+      if (cum + tot >= 64u) {
+        const unsigned long long mk = __ballot(cum + incl >= 64u);
+        if (lane == 0) fs.bin = top - (__ffsll((long long)mk) - 1);
+        break;
+      }
+      cum += tot;
+    }
+  }
+  __syncthreads();
+  const int bstar = fs.bin;   // -1: fewer than 64 loaded keys, every entry counts
+  if (bstar >= 0) {
+    for (int t = tid; t < nk; t += NT) {
+      const uint32_t kx = cand_key(ld[t]);
+      if (kx && bin_of(kx) >= bstar) atomicMin(&fs.bound, kx);
+    }
+  }
+  __syncthreads();
+  const uint32_t bound = bstar >= 0 ? fs.bound : 1u;
+  auto add = [&](bool keep, unsigned long long x) {
+    const unsigned long long bl = __ballot(keep);
+    if (!bl) return;
+    int base = 0;
+    if (lane == 0) base = atomicAdd(&fs.nf, __popcll(bl));
+    base = __shfl(base, 0);
+    const int p = base + (int)lanes_below(bl);
+    if (keep && p < kFuseStage) cand[p] = x;
+  };
+  for (int t0 = 0; t0 < nk; t0 += NT) {
+    const int t = t0 + tid;
+    const unsigned long long x = t < nk ? ld[t] : 0ull;
+    add(x != 0ull && cand_key(x) >= bound, x);
+  }
+  // lists whose J-th entry reaches the bound: the rest of the list (rare)
+  uint32_t *more = bins;   // the histogram is no longer needed
+  if (tid == 0) fs.nmore = 0;
+  __syncthreads();
+  if (J < 64)
+    for (int i = tid; i < B; i += NT)
+      if (cand_key(ld[i * J + J - 1]) >= bound) more[atomicAdd(&fs.nmore, 1)] = (uint32_t)i;
+  __syncthreads();
+  for (int q = wave; q < fs.nmore; q += NW) {
+    const int i = (int)more[q];
+    const unsigned long long x = lane >= J ? load_agent(lists + (int64_t)i * 64 + lane) : 0ull;
+    add(x != 0ull && cand_key(x) >= bound, x);
+  }
+  __syncthreads();
+  const int nf = fs.nf;
+  const bool ovf = nf > kFuseStage || fs.disc == ~0u;
+  const int n = ovf ? 0 : nf;
+  unsigned long long *stage = cand;
+  // the top 64 and the 65th (ranks by comparison: n is small)
+  for (int i = tid; i < 64; i += NT) fs.top[i] = 0ull;
+  __syncthreads();
+  for (int i = tid; i < n; i += NT) {
+    const unsigned long long xi = stage[i];
+    int rank = 0;
+    for (int j = 0; j < n; ++j) rank += stage[j] > xi ? 1 : 0;
+    if (rank < 64) fs.top[rank] = xi;
+    if (rank == 64) fs.key64 = cand_key(xi);
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  const unsigned long long F = fs.top[lane];
+  RowPlan P{};
+  P.temperature = load_scalar(&plan->temperature);
+  P.top_p = load_scalar(&plan->top_p);
+  P.min_p = load_scalar(&plan->min_p);
+  P.k = load_scalar(&plan->k);
+  const uint32_t Tk = cand_key(__shfl(F, P.k - 1));
+  const bool extra = Tk != 0u && (fs.key64 == Tk || fs.disc == Tk);
+  // (a replay here is rare: fewer logits in flight keep the GEMV's registers)
+  finish_wave<4>(a, P, m, y, F, extra, ovf, f.uniforms[m], fs.rsv, fs.rsid, fs.sp, true);
+}
+
+// The fused kernel's grid: as the GEMV's (tiles over resident workgroups);
+// 0 when a wave would get more than kFuseTiles tiles.
+template <int FMT>
+int tern_sample_blocks(const GemvArgs &g, size_t lds) {
+  constexpr int nw = tm::waves<FMT>();
+  const int ntiles = (g.N + 15) / 16;
+  const int res = resident_blocks(reinterpret_cast<const void *>(gemv_tern_sample_kernel<FMT>),
+                                  (uint32_t)lds, 64 * nw);
+  int blocks = (ntiles + nw - 1) / nw;
+  blocks = blocks < res ? blocks : res;
+  const int J = min(64, max(4, (64 + blocks - 1) / blocks));
+  return (ntiles + blocks * nw - 1) / (blocks * nw) <= kFuseTiles && blocks * J <= kFuseLoad &&
+                 blocks <= kFuseBins
+             ? blocks
+             : 0;
+}
+
+int tern_sample_grid(const GemvArgs &g) {
+  switch (g.type) {
+    case kW_Q1_0: return tern_sample_blocks<kW_Q1_0>(g, tern_sample_lds_bytes(g.K, tm::waves<kW_Q1_0>()));
+    case kW_PQ2_0: return tern_sample_blocks<kW_PQ2_0>(g, tern_sample_lds_bytes(g.K, tm::waves<kW_PQ2_0>()));
+    case kW_PTQ1_0: return tern_sample_blocks<kW_PTQ1_0>(g, tern_sample_lds_bytes(g.K, tm::waves<kW_PTQ1_0>()));
+    default: return 0;
+  }
+}
+
+hipError_t launch_tern_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
+                              hipEvent_t *ev, hipEvent_t done) {
+  auto go = [&](auto kern, int nw, int blocks) {
+    if (blocks < 1) return hipErrorInvalidValue;
+    const size_t lds = tern_sample_lds_bytes(g.K, nw);
+    const dim3 grid((unsigned)blocks, (unsigned)g.M), block(64 * nw);
+    if (ev)
+      hipExtLaunchKernelGGL(kern, grid, block, lds, stream, ev[0], ev[1], 0u, g, f);
+    else if (done)
+      hipExtLaunchKernelGGL(kern, grid, block, lds, stream, nullptr, done, 0u, g, f);
+    else
+      hipLaunchKernelGGL(kern, grid, block, lds, stream, g, f);
+    return hipGetLastError();
+  };
+  const int blocks = tern_sample_grid(g);
+  if (blocks != f.blocks) return hipErrorInvalidValue;   // the workspace was sized for another grid
+  switch (g.type) {
+    case kW_Q1_0: return go(gemv_tern_sample_kernel<kW_Q1_0>, tm::waves<kW_Q1_0>(), blocks);
+    case kW_PQ2_0: return go(gemv_tern_sample_kernel<kW_PQ2_0>, tm::waves<kW_PQ2_0>(), blocks);
+    case kW_PTQ1_0: return go(gemv_tern_sample_kernel<kW_PTQ1_0>, tm::waves<kW_PTQ1_0>(), blocks);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 // ---------------------------------------------------------------- launch
 
 hipError_t prepare_kernels() {
@@ -4600,6 +5086,15 @@ hipError_t prepare_kernels() {
   if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mid_kernel<false>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, mid_smem)) != hipSuccess)
     return e;
+  {
+    const void *tk[3] = {reinterpret_cast<const void *>(&gemv_tern_sample_kernel<kW_Q1_0>),
+                         reinterpret_cast<const void *>(&gemv_tern_sample_kernel<kW_PQ2_0>),
+                         reinterpret_cast<const void *>(&gemv_tern_sample_kernel<kW_PTQ1_0>)};
+    for (const void *fk : tk)
+      if ((e = hipFuncSetAttribute(fk, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)tern_sample_lds_bytes(kGemvMaxK, 16))) != hipSuccess)
+        return e;
+  }
   if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&finalize_kernel),
                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)finalize_smem_bytes())) != hipSuccess)
