@@ -425,8 +425,10 @@ int begin_timed(hs_context *ctx, const hs::LaunchArgs &a, hipEvent_t **ev) {
 // A failed launch may have left counters of earlier kernels of the call
 // raised: clear them for the next call.
 void reset_counters(hs_context *ctx, hipStream_t stream) {
-  if (ctx->cand_count.p) (void)hipMemsetAsync(ctx->cand_count.p, 0, ctx->cand_count.bytes, stream);
-  if (ctx->split_cnt.p) (void)hipMemsetAsync(ctx->split_cnt.p, 0, ctx->split_cnt.bytes, stream);
+  for (DevBuf *b : {&ctx->cand_count, &ctx->split_cnt})
+    if (b->p)
+      (void)hs::launch_fill_u32(static_cast<uint32_t *>(b->p),
+                                (int64_t)(b->bytes / sizeof(uint32_t)), 0u, stream);
 }
 
 int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_stride,

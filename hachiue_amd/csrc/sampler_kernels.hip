@@ -3982,6 +3982,9 @@ struct FastWalk {
   double ssum[16];                     // the located bucket in 16 parts: probability,
   uint32_t scnt[16];                   //   logits
   unsigned long long few[64];          // the logits of the located part
+  double fewp[64];                     //   and their probabilities (wave walk)
+  unsigned long long srt[64];          // the wave walk's ranked logits,
+  double srp[64];                      //   and their probabilities
   int res_id, res_pos;
   double res_cum;
 };
@@ -4200,6 +4203,167 @@ __device__ __forceinline__ FastLoc fast_locate(int glo, int ghi, double c_start,
   return r;
 }
 
+// fast_locate by one wave, without a barrier, for ranges of at most 64
+// buckets: the same steps (bucket sums, the located bucket, its 16 parts
+// when it holds more than 64 logits, the walk through the part holding the
+// target) over the probabilities in sm.pb.  The walk orders at most 64
+// logits by rank (the count of larger packed keys; keys are distinct) instead
+// of a sorting network.  Every lane returns the result; id -2: a part of more
+// than 64 logits (or more than 64 logits above m0), which the block version
+// sorts whole.  Its scratch is the bucket array's (FastWalk), as the block
+// version's.
+constexpr int kFWaveList = 1024;   // gathered logits the wave walks scan
+__device__ __forceinline__ FastLoc fast_locate_wave(int glo, int ghi, double c_start,
+                                                    double target, int nl, float cz, float m0cz,
+                                                    float m0, FastSmem &sm) {
+  FastWalk &w = *reinterpret_cast<FastWalk *>(sm.mass);
+  const int lane = lane_id();
+  const int span = ghi - glo + 1;
+  FastLoc r{-1, 0, 0.0};
+  auto bucket_of = [&](unsigned long long c) {
+    const float v = key2f(cand_key(c));
+    return v > m0 ? -1 : fast_bucket(v, cz, m0cz);
+  };
+  auto part_of = [&](unsigned long long c, int bq) {
+    const float q = fast_q(key2f(cand_key(c)), cz, m0cz);
+    return (int)fminf(fmaxf((q - (float)bq) * 16.0f, 0.0f), 15.0f);
+  };
+  // LDS operations of one wave take effect in issue order: no waits needed.
+  // Loops read four entries per lane before using any.
+  w.bsum[lane] = 0.0;
+  w.bcnt[lane] = 0u;
+  for (int base = 0; base < nl; base += 256) {
+    unsigned long long c[4];
+    double p[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = base + 64 * k + lane;
+      c[k] = i < nl ? sm.buf[i] : 0ull;
+      p[k] = i < nl ? sm.pb[i] : 0.0;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int b = base + 64 * k + lane < nl ? bucket_of(c[k]) : glo - 1;
+      if (b >= glo && b <= ghi) {
+        atomicAdd(&w.bsum[b - glo], p[k]);
+        atomicAdd(&w.bcnt[b - glo], 1u);
+      }
+    }
+  }
+  const double bs = lane < span ? w.bsum[lane] : 0.0;
+  const uint32_t bc = lane < span ? w.bcnt[lane] : 0u;
+  const double incl = wave_scan_incl_f64(bs);
+  const uint32_t cincl = wave_scan_incl(bc);
+  const double up = __shfl_up(incl, 1);
+  const double before = c_start + (lane > 0 ? up : 0.0);
+  const unsigned long long hb = __ballot(lane < span && bc > 0 && before + bs >= target);
+  if (!hb) return r;
+  const int lb = __builtin_ctzll(hb);
+  const double cb = readlane_f64(before, lb);
+  const int nb = (int)readlane_u32(bc, lb);
+  const int kb = (int)readlane_u32(cincl, lb) - nb;
+  const int bq = glo + lb;
+  // the located bucket's logits and probabilities, in list order
+  int n = 0;
+  for (int base = 0; base < nl; base += 256) {
+    unsigned long long c[4];
+    double p[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = base + 64 * k + lane;
+      c[k] = i < nl ? sm.buf[i] : 0ull;
+      p[k] = i < nl ? sm.pb[i] : 0.0;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const bool in = base + 64 * k + lane < nl && bucket_of(c[k]) == bq;
+      const unsigned long long m = __ballot(in);
+      if (in) {
+        const int o = n + (int)lanes_below(m);
+        w.one[o] = c[k];
+        w.pone[o] = p[k];
+      }
+      n += __popcll(m);
+    }
+  }
+  double cs = cb;
+  int ks = kb, ns = nb;
+  const unsigned long long *fx = w.one;
+  const double *fp = w.pone;
+  if (nb > 64) {
+    if (bq < 0) { r.id = -2; return r; }
+    // 16 parts by (q - bq) * 16, as the block version cuts them
+    if (lane < 16) { w.ssum[lane] = 0.0; w.scnt[lane] = 0u; }
+    for (int base = 0; base < nb; base += 256) {
+      unsigned long long c[4];
+      double p[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int i = base + 64 * k + lane;
+        c[k] = i < nb ? w.one[i] : 0ull;
+        p[k] = i < nb ? w.pone[i] : 0.0;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (base + 64 * k + lane < nb) {
+          const int part = part_of(c[k], bq);
+          atomicAdd(&w.ssum[part], p[k]);
+          atomicAdd(&w.scnt[part], 1u);
+        }
+      }
+    }
+    const double pm = lane < 16 ? w.ssum[lane] : 0.0;
+    const uint32_t pc = lane < 16 ? w.scnt[lane] : 0u;
+    const double pincl = wave_scan_incl_f64(pm) + cb;
+    const uint32_t ci = wave_scan_incl(pc);
+    const unsigned long long hp = __ballot(lane < 16 && pc > 0 && pincl >= target);
+    if (!hp) { r.id = -2; return r; }   // the block version walks the whole bucket
+    const int L = __builtin_ctzll(hp);
+    const int np = (int)readlane_u32(pc, L);
+    if (np > 64) { r.id = -2; return r; }
+    cs = readlane_f64(pincl - pm, L);
+    ks = kb + (int)readlane_u32(ci, L) - np;
+    ns = np;
+    int f = 0;
+    for (int base = 0; base < nb; base += 64) {
+      const int i = base + lane;
+      const unsigned long long c = i < nb ? w.one[i] : 0ull;
+      const bool in = i < nb && part_of(c, bq) == L;
+      const unsigned long long m = __ballot(in);
+      if (in) {
+        const int o = f + (int)lanes_below(m);
+        w.few[o] = c;
+        w.fewp[o] = w.pone[i];
+      }
+      f += __popcll(m);
+    }
+    fx = w.few;
+    fp = w.fewp;
+  }
+  // the walk: value descending, index ascending (packed key descending)
+  const unsigned long long x = lane < ns ? fx[lane] : 0ull;
+  const double px = lane < ns ? fp[lane] : 0.0;
+  int rank = 0;
+  for (int j = 0; j < ns; ++j) {
+    const unsigned long long y =
+        ((unsigned long long)readlane_u32((uint32_t)(x >> 32), j) << 32) | readlane_u32((uint32_t)x, j);
+    rank += y > x ? 1 : 0;
+  }
+  if (lane < ns) {
+    w.srt[rank] = x;
+    w.srp[rank] = px;
+  }
+  const unsigned long long xs = lane < ns ? w.srt[lane] : 0ull;
+  const double c = wave_scan_incl_f64(lane < ns ? w.srp[lane] : 0.0) + cs;
+  const unsigned long long hit = __ballot(lane < ns && c >= target);
+  if (!hit) return r;
+  const int L = __builtin_ctzll(hit);
+  r.id = (int)readlane_u32(cand_idx(xs), L);
+  r.pos = ks + L;
+  r.cum = readlane_f64(c, L);
+  return r;
+}
+
 // One row of the two-pass path; false (block-uniform) hands it back.
 __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P, int row,
                                            FastSmem &sm) {
@@ -4395,20 +4559,53 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
   const int ng = sm.nbuf;
   const int nl = ng + ntop;
   if (nl > kFCap || g0hi - g0lo + 1 > kFSpan || g1hi - g1lo + 1 > kFSpan) return false;
-  for (int i = tid; i < ntop; i += kFT) sm.buf[ng + i] = sm.top[i];
-  __syncthreads();
-  // the gathered logits' probabilities as the reference rounds them
+  // the list above m0 joins the gathered logits; their probabilities as the
+  // reference rounds them
   for (int i = tid; i < nl; i += kFT) {
-    const float v = key2f(cand_key(sm.buf[i]));
-    sm.pb[i] = (double)(float)((double)(float)exp(((double)v - md) * it) / S);
+    const unsigned long long c = i < ng ? sm.buf[i] : sm.top[i - ng];
+    if (i >= ng) sm.buf[i] = c;
+    sm.pb[i] = (double)(float)((double)(float)exp(((double)key2f(cand_key(c)) - md) * it) / S);
   }
   // the ranges' cumulative starts, read before the walks reuse the buckets
   const double c0 = fast_start(g0lo, top_total, scale, sm);
   const double c1 = two ? fast_start(g1lo, top_total, scale, sm) : 0.0;
   __syncthreads();
+  auto finish = [&](const FastLoc &l1, const FastLoc &l2) {
+    const int pos1 = (g0lo < 0 ? 0 : ntop + (int)below) + l1.pos;
+    if (tid == 0) {
+      put_token(a, row, l2.id);
+      if (a.cand_count_out) a.cand_count_out[row] = (int)n_f;
+      if (a.cutoff_out) a.cutoff_out[row] = pos1 + 1;
+      if (a.row_flags) a.row_flags[row] = HS_ROW_LARGE | HS_ROW_TWO_PASS;
+    }
+  };
 
   // 5. src/sampler.ts:93-117 on the gathered ranges: the top-p crossing
-  // (keptSum = cumProb through it), then the draw r = u keptSum
+  // (keptSum = cumProb through it), then the draw r = u keptSum.  Short lists
+  // and narrow ranges: wave 0 alone, while the other waves wait at one
+  // barrier (1: done, -1: hand the row back, 0: the block walks below).
+  if (nl <= kFWaveList && g0hi - g0lo < 64 && g1hi - g1lo < 64) {
+    if (tid < 64) {
+      int res = -1;
+      const FastLoc l1 = fast_locate_wave(g0lo, g0hi, c0, tp, nl, cz, m0cz, m0, sm);
+      if (l1.id == -2) {
+        res = 0;
+      } else if (l1.id >= 0) {
+        const double r = u * l1.cum;
+        if (r == r) {
+          const FastLoc l2 =
+              two ? fast_locate_wave(g1lo, g1hi, c1, r, nl, cz, m0cz, m0, sm)
+                  : fast_locate_wave(g0lo, g0hi, c0, r, nl, cz, m0cz, m0, sm);
+          res = l2.id == -2 ? 0 : l2.id >= 0 ? 1 : -1;
+          if (res == 1) finish(l1, l2);
+        }
+      }
+      if (tid == 0) sm.flag = res;
+    }
+    __syncthreads();
+    const int res = sm.flag;
+    if (res != 0) return res > 0;
+  }
   const FastLoc l1 = fast_locate(g0lo, g0hi, c0, tp, nl, cz, m0cz, m0, md, it, S, sm);
   if (l1.id < 0) return false;
   const double r = u * l1.cum;
@@ -4416,19 +4613,13 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
   const FastLoc l2 = two ? fast_locate(g1lo, g1hi, c1, r, nl, cz, m0cz, m0, md, it, S, sm)
                          : fast_locate(g0lo, g0hi, c0, r, nl, cz, m0cz, m0, md, it, S, sm);
   if (l2.id < 0) return false;
-  const int pos1 = (g0lo < 0 ? 0 : ntop + (int)below) + l1.pos;
-  if (tid == 0) {
-    put_token(a, row, l2.id);
-    if (a.cand_count_out) a.cand_count_out[row] = (int)n_f;
-    if (a.cutoff_out) a.cutoff_out[row] = pos1 + 1;
-    if (a.row_flags) a.row_flags[row] = HS_ROW_LARGE | HS_ROW_TWO_PASS;
-  }
+  finish(l1, l2);
   return true;
 }
 
 // Rows of lfast_list; a row it cannot finish is marked in large_retry for
 // large_kernel.  Unaligned rows and calls that want candidate outputs are
-// all handed back.  Four waves per SIMD: two workgroups per CU.
+// all handed back.  Four waves per SIMD: one workgroup per CU.
 __global__ __launch_bounds__(kFT, 4) void large_fast_kernel(LaunchArgs a, Workspace ws) {
   extern __shared__ unsigned long long ldyn[];
   const int row = ws.lfast_list[blockIdx.x];

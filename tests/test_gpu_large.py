@@ -100,6 +100,24 @@ def test_two_pass_distributions(sampler, name):
     assert not got.flags[3] & HS_ROW_TWO_PASS
 
 
+@pytest.mark.parametrize("step", [1 / 64, 1 / 16])
+def test_two_pass_block_walks(sampler, step):
+    """Logits on a grid of `step` (N(0, 2.5^2), T 1, top-p 0.9): near the
+    top-p crossing (v ~ 3) each grid value is held by about 180 (1/64) or 720
+    (1/16) logits, so the located bucket's part holds more than 64 equal
+    values (1/64) or the gathered list exceeds what one wave walks (1/16).
+    Those walks take the whole workgroup's sort; draws near the top take the
+    one-wave walk.  Tokens against the oracle."""
+    rng = np.random.default_rng(int(1 / step))
+    rows, vocab = 32, 151936
+    logits = (np.round(rng.standard_normal((rows, vocab)) * 2.5 / step) * step).astype(np.float32)
+    cfg = dict(temperature=1.0, topK=float("inf"), topP=0.9)
+    u = rng.random(rows)
+    got, _ = _check(sampler, logits, vocab, None, None, [cfg] * rows, u, 64,
+                    f"two-pass grid {step}", want_cands=False)
+    assert ((got.flags & HS_ROW_LARGE) != 0).all()
+
+
 def test_partial_large_k(sampler):
     rng = np.random.default_rng(11)
     rows, vocab = 24, 151936
