@@ -45,6 +45,9 @@ constexpr int kPenBits = 13;
 constexpr int kPenSlots = 1 << kPenBits;         // table slots (64 KiB with the counts)
 constexpr int kPenProbe = 64;                    // probes per insert before the range fallback
 constexpr int kPenRange = 16384;                 // ids per range of the fallback
+constexpr int kMidEarly = 2048;                  // mid kernel: a presence / frequency row's
+                                                 //   listed (deferred) penalised ids
+constexpr int kMidLdsMax = 152 * 1024;           // mid kernel: dynamic LDS ceiling
 
 constexpr int kSmallK = 64;                      // wave-select paths
 constexpr int kMaxK = 1024;                      // largest k of the select paths

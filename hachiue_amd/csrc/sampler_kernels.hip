@@ -614,35 +614,100 @@ __device__ __forceinline__ uint32_t pen_hash(int id) {
 // One row's penalties in place, by the whole workgroup of NT threads: `pdyn`
 // holds pen_smem_bytes() of LDS, `full` is a shared flag.  The row's stores
 // are issued when it returns; the caller orders them before any later read.
+// on_write(id, value) sees every logit written.
+struct PenNoHook {
+  __device__ __forceinline__ void operator()(int, float) const {}
+};
+// The history entries pen_row counts start here: the repetition-only entries
+// (before the last 128 without presence / frequency) are not counted, their
+// count is not used.
+__device__ __forceinline__ int64_t pen_start(const HistRow &h, const RowPlan &P) {
+  const int64_t hl = h.n;
+  const int64_t rep0 = (P.pen & kPenRep) ? hl - (hl < 128 ? hl : 128) : hl;   // history.slice(-128)
+  return (P.pen & kPenPF) ? 0 : rep0;
+}
+
+// Thread tid's four history ids of the batch at t0 (-1 past the history).
 template <int NT>
-__device__ __forceinline__ void pen_row(const HistRow h, const RowPlan P, float *rowp, int V,
-                                        uint32_t *pdyn, int32_t &full) {
+__device__ __forceinline__ void pen_request(const HistRow &h, int64_t t0, int (&ids)[4]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int64_t t = t0 + tid + NT * c;
+    ids[c] = t < h.n ? h.p[hist_pos(h, t)] : -1;
+  }
+}
+
+// The table's penalised logits rewritten in place (every read of a thread's
+// slots before any of its writes: no write can alias a later read, the slots
+// hold distinct ids; every value before any store: a wait for a read issued
+// before a store also waits for that store, so the stores go out back to
+// back).
+template <int NT, typename OnWrite = PenNoHook>
+__device__ __forceinline__ void pen_apply(const uint32_t *pdyn, const RowPlan &P, float *rowp,
+                                          OnWrite on_write = {}) {
+  const int32_t *keys = reinterpret_cast<const int32_t *>(pdyn);
+  const uint32_t *cnts = pdyn + kPenSlots;
+  const int tid = threadIdx.x;
+  const bool pf = (P.pen & kPenPF) != 0;
+  constexpr int SPT = kPenSlots / NT;
+  static_assert(kPenSlots % NT == 0, "pen_apply: slots per thread");
+  int sid[SPT];
+  float raw[SPT];
+#pragma unroll
+  for (int i = 0; i < SPT; ++i) {
+    sid[i] = keys[tid + NT * i];
+    raw[i] = sid[i] >= 0 ? rowp[sid[i]] : 0.f;
+  }
+  float pv[SPT];
+#pragma unroll
+  for (int i = 0; i < SPT; ++i) {
+    const uint32_t c = sid[i] >= 0 ? cnts[tid + NT * i] : 0u;
+    pv[i] = penalise(raw[i], (c >> 31) != 0, pf ? (c & 0x7FFFFFFFu) : 0u, P);
+    if (sid[i] >= 0) on_write(sid[i], pv[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < SPT; ++i)
+    if (sid[i] >= 0) rowp[sid[i]] = pv[i];
+}
+
+struct PenNoSlot {
+  __device__ __forceinline__ void operator()(int, uint32_t) const {}
+};
+
+// With `pre`, the caller has requested the first batch of ids (pen_request
+// at pen_start) before reads of its own, whose waits then do not hold up the
+// table.  With DEFER, a row whose distinct ids fit the table is not
+// rewritten: on_slot(id, count word) sees each distinct id (count | rep bit
+// 31), the table stays in pdyn, and the result is true; the caller applies
+// the penalties (pen_apply, or from what on_slot kept).  Otherwise the row is
+// rewritten in place and the result is false.
+template <int NT, bool DEFER = false, typename OnWrite = PenNoHook, typename OnSlot = PenNoSlot>
+__device__ __forceinline__ bool pen_row(const HistRow h, const RowPlan P, float *rowp, int V,
+                                        uint32_t *pdyn, int32_t &full, OnWrite on_write = {},
+                                        int (*pre)[4] = nullptr, OnSlot on_slot = {}) {
   int32_t *keys = reinterpret_cast<int32_t *>(pdyn);   // kPenSlots ids (-1: empty)
   uint32_t *cnts = pdyn + kPenSlots;                    // kPenSlots counts | rep bit
   const int tid = threadIdx.x;
   const int64_t hl = h.n;
   const int64_t rep0 = (P.pen & kPenRep) ? hl - (hl < 128 ? hl : 128) : hl;   // history.slice(-128)
   const bool pf = (P.pen & kPenPF) != 0;
-  // the repetition-only entries (before rep0 without presence / frequency)
-  // are not counted: their count is not used.  Four ids per thread are
-  // requested before any is inserted, the first four before the table is
-  // cleared.
-  const int64_t tstart = pf ? 0 : rep0;
+  // Four ids per thread are requested before any is inserted, the first four
+  // before the table is cleared.
+  const int64_t tstart = pen_start(h, P);
   int ids[4];
-  auto request = [&](int64_t t0) {
+  auto request = [&](int64_t t0) { pen_request<NT>(h, t0, ids); };
+  if (pre) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int64_t t = t0 + tid + NT * c;
-      ids[c] = t < hl ? h.p[hist_pos(h, t)] : -1;
-    }
-  };
-  request(tstart);
+    for (int c = 0; c < 4; ++c) ids[c] = (*pre)[c];
+  } else {
+    request(tstart);
+  }
   for (int i = tid; i < kPenSlots; i += NT) { keys[i] = -1; cnts[i] = 0; }
   if (tid == 0) full = 0;
   __syncthreads();
   bool over = false;
-  for (int64_t t0 = tstart; t0 < hl; t0 += 4 * NT) {
-    if (t0 != tstart) request(t0);
+  auto insert = [&](int64_t t0) {
 #pragma unroll 1
     for (int c = 0; c < 4; ++c) {
       const int64_t t = t0 + tid + NT * c;
@@ -662,30 +727,25 @@ __device__ __forceinline__ void pen_row(const HistRow h, const RowPlan P, float 
       atomicAdd(&cnts[hs], 1u);
       if (t >= rep0) atomicOr(&cnts[hs], 0x80000000u);
     }
-    if (over) break;
+  };
+  // the first batch outside the loop: its wait counts the caller's later
+  // reads exactly (a batch requested inside a loop is waited for with every
+  // read before it)
+  insert(tstart);
+  for (int64_t t0 = tstart + 4 * NT; t0 < hl && !over; t0 += 4 * NT) {
+    request(t0);
+    insert(t0);
   }
   if (over) full = 1;
   __syncthreads();
   if (!full) {
-    // every read of this thread's slots before any write (no write can
-    // alias a later read: the slots hold distinct ids)
-    constexpr int SPT = kPenSlots / NT;
-    static_assert(kPenSlots % NT == 0, "pen_row: slots per thread");
-    int sid[SPT];
-    float raw[SPT];
-#pragma unroll
-    for (int i = 0; i < SPT; ++i) {
-      sid[i] = keys[tid + NT * i];
-      raw[i] = sid[i] >= 0 ? rowp[sid[i]] : 0.f;
+    if (DEFER) {
+      for (int i = tid; i < kPenSlots; i += NT)
+        if (keys[i] >= 0) on_slot(keys[i], cnts[i]);
+      return true;
     }
-#pragma unroll
-    for (int i = 0; i < SPT; ++i) {
-      if (sid[i] >= 0) {
-        const uint32_t c = cnts[tid + NT * i];
-        rowp[sid[i]] = penalise(raw[i], (c >> 31) != 0, pf ? (c & 0x7FFFFFFFu) : 0u, P);
-      }
-    }
-    return;
+    pen_apply<NT>(pdyn, P, rowp, on_write);
+    return false;
   }
   // too many distinct ids: count by id ranges (the table's LDS reused)
   uint32_t *counts = pdyn;                  // kPenRange
@@ -706,9 +766,14 @@ __device__ __forceinline__ void pen_row(const HistRow h, const RowPlan P, float 
     for (int o = tid; o < hi - lo; o += NT) {
       const uint32_t n = counts[o];
       const bool rep = (repbits[o >> 5] >> (o & 31)) & 1u;
-      if (n) rowp[lo + o] = penalise(rowp[lo + o], rep, pf ? n : 0u, P);
+      if (n) {
+        const float pv = penalise(rowp[lo + o], rep, pf ? n : 0u, P);
+        rowp[lo + o] = pv;
+        on_write(lo + o, pv);
+      }
     }
   }
+  return false;
 }
 
 __global__ __launch_bounds__(kPenThreads) void pen_kernel(LaunchArgs a, Workspace ws) {
@@ -2352,17 +2417,20 @@ __device__ __forceinline__ uint32_t append_hist_rd(const float (&v)[NV][4], int 
 // The largest bin edge t with at least k counted keys >= t, searching down
 // from the bin of `top` (the largest counted key); 0 when fewer than k are
 // counted.  Counts read while other waves still add are lower bounds of the
-// final ones, so the result is a lower bound of the row's k-th largest.
+// final ones, so the result is a lower bound of the row's k-th largest.  A
+// bin may hold a negative count (a left-out logit taken out before the
+// stream counts it, or never counted): counts stay lower bounds, read as
+// signed.
 __device__ __forceinline__ uint32_t hist_bound(const uint32_t *hist, uint32_t top, int k) {
   const int lane = lane_id();
-  uint32_t cum = 0;
+  int cum = 0;
   for (int base = (int)(top >> kMidShift); base >= 0; base -= 64) {
     const int b = base - lane;
     const uint32_t c = b >= 0 ? __atomic_load_n(hist + b, __ATOMIC_RELAXED) : 0u;
-    const uint32_t incl = wave_scan_incl(c);   // lane 0 holds the highest bin
-    const uint32_t tot = readlane_u32(incl, 63);
-    if (cum + tot >= (uint32_t)k) {
-      const unsigned long long mk = __ballot(cum + incl >= (uint32_t)k);
+    const int incl = (int)wave_scan_incl(c);   // lane 0 holds the highest bin
+    const int tot = (int)readlane_u32((uint32_t)incl, 63);
+    if (cum + tot >= k) {
+      const unsigned long long mk = __ballot(cum + incl >= k);
       const int L = __ffsll((long long)mk) - 1;
       return (uint32_t)(base - L) << kMidShift;
     }
@@ -2389,10 +2457,10 @@ __device__ __forceinline__ void compact_seg(unsigned long long *seg, int &cnt, u
 
 // One round of the mid kernel: the bound from the histogram (dropping the
 // segment's entries below it when it rose), then the round's candidates.
-__device__ __forceinline__ void mid_step(float (&v)[kRowNV][4], int fb, int tid, int lim, int V,
-                                         int k, bool rep, const uint32_t *bitmap, uint32_t *hist,
-                                         uint32_t *top_key, unsigned long long *seg, int &cnt,
-                                         uint32_t &theta, float &xf, bool &lost) {
+__device__ __forceinline__ void mid_step(float (&v)[kRowNV][4], int fb, int tid, int lim,
+                                         int k, uint32_t *hist, uint32_t *top_key,
+                                         unsigned long long *seg, int &cnt, uint32_t &theta,
+                                         float &xf, bool &lost) {
   const uint32_t t =
       hist_bound(hist, (uint32_t)uniform_i32((int)__atomic_load_n(top_key, __ATOMIC_RELAXED)), k);
   if (t > theta) {
@@ -2402,7 +2470,6 @@ __device__ __forceinline__ void mid_step(float (&v)[kRowNV][4], int fb, int tid,
     compact_seg(seg, cnt, theta);
   }
   clip_rd<kRowNV>(v, fb, tid, lim);
-  if (rep) mask_penalised<kRowNV>(v, fb, tid, V, bitmap);
   const uint32_t m = wave_max_u32(append_hist_rd<kRowNV>(v, fb, tid, xf, seg, cnt, hist));
   if ((tid & 63) == 0 && m) atomicMax(top_key, m);
 }
@@ -2414,15 +2481,29 @@ static_assert((size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + (size_t)kMidBins 
                   (size_t)(kPenRange + kPenRange / 32) * 4,
               "mid kernel LDS too small for the penalty prologue");
 
-size_t mid_smem_bytes(int vocab) {
+// The mid kernel's LDS: the stream's arrays, the bitmap, then the early list
+// of a presence / frequency row (ids and values, 8 bytes each) in what remains
+// of kMidLdsMax, at most kMidEarly.
+__host__ __device__ __forceinline__ size_t mid_base_bytes(int vocab) {
   const size_t words = ((size_t)vocab + 31) / 32;
   return (size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + (size_t)kMidBins * 4 + words * 4;
 }
+__host__ __device__ __forceinline__ int mid_early_cap(int vocab) {
+  const size_t base = mid_base_bytes(vocab);
+  const size_t fit = base < (size_t)kMidLdsMax ? ((size_t)kMidLdsMax - base) / 8 : 0;
+  return (int)(fit < (size_t)kMidEarly ? fit : (size_t)kMidEarly);
+}
+static_assert((size_t)kRowCandCap * 8 + (size_t)kSortCap * 8 + (size_t)kMidBins * 4 +
+                      (size_t)kRowMaxVocab / 8 <= (size_t)kMidLdsMax,
+              "mid kernel LDS");
+
+size_t mid_smem_bytes(int vocab) { return mid_base_bytes(vocab) + 8 * (size_t)mid_early_cap(vocab); }
 
 struct MidSmem {
   TailSmem tail;
   uint32_t top_key;
-  int32_t n_f, ovf, n_sel;
+  int32_t n_f, ovf, n_sel, pen_full;
+  float tl[3];   // the tail logits (VEC)
 };
 
 template <bool VEC>
@@ -2440,46 +2521,106 @@ __global__ __launch_bounds__(kRowThreads) void mid_kernel(LaunchArgs a, Workspac
   const int V = a.vocab;
   const int nr = row_rounds(V);
 
-  // Presence / frequency rows: the row's penalties (the repetition penalty
-  // included) are applied in place first, as pen_kernel does, in the LDS
-  // the stream has not taken yet (the candidate, sort and histogram arrays
-  // hold pen_smem_bytes()); the stores complete before any read of the row.
-  if (load_scalar(&ws.plans[row].pen) & kPenPF) {
-    __shared__ int32_t pen_full;
-    pen_row<kRowThreads>(hist_row(a, row), ws.plans[row], rowp, V,
-                         reinterpret_cast<uint32_t *>(mdyn), pen_full);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __syncthreads();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  }
+  const RowPlan *plan = ws.plans + row;
+  const int penbits = load_scalar(&plan->pen);
+  const bool pf = (penbits & kPenPF) != 0;
+  // the penalties' part of the plan, by scalar reads (a vector read issued
+  // after the rounds' reads would wait for them)
+  RowPlan pp{};
+  pp.pen = penbits;
+  pp.rep = load_scalar(&plan->rep);
+  pp.pres = load_scalar(&plan->pres);
+  pp.freq = load_scalar(&plan->freq);
 
-  // history ids first, then rounds 0 and 1 (as in row_kernel)
-  const HistTail ht = hist_tail(a, row, tid);
+  // Reads in this order: a presence / frequency row's first history ids, the
+  // repetition set's ids, the tail logits, rounds 0 and 1 (a wait for one
+  // read waits for the reads before it, not after).
+  const HistRow hrow = hist_row(a, row);
+  int pids[4] = {-1, -1, -1, -1};
+  if (pf) pen_request<kRowThreads>(hrow, pen_start(hrow, pp), pids);
+  const HistTail ht = pf ? HistTail{-1, 0} : hist_tail(a, row, tid);
   const int hraw = ht.id, hist_n = ht.n;
   RowSrc src;
   src.lim = VEC ? (V & ~3) : V;
   src.x4 = make_rsrc(rowp, 4u * (uint32_t)(V & ~3));
   src.x1 = make_rsrc(rowp, 4u * (uint32_t)V);
+  // the fewer than four logits past the last whole float4 (thread 0), kept
+  // in LDS once they arrive
+  float tl[3] = {0.f, 0.f, 0.f};
+  auto load_tail = [&]() {
+    if (VEC) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        const int e = src.lim + q;
+        tl[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+            src.x1, (tid == 0 && e < V ? e : V) * 4, 0, 0));
+      }
+    }
+  };
+  load_tail();
   float v0[kR0NV][4], va[kRowNV][4], vb[kRowNV][4];
   load_rd<kR0NV, VEC>(v0, src, 0, tid);
   load_rd<kRowNV, VEC>(vb, src, round_base(1), tid);
-  float tl[3] = {0.f, 0.f, 0.f};
-  if (VEC) {
-#pragma unroll
-    for (int q = 0; q < 3; ++q) {
-      const int e = src.lim + q;
-      tl[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-          src.x1, (tid == 0 && e < V ? e : V) * 4, 0, 0));
-    }
-  }
   __builtin_amdgcn_sched_barrier(0);
 
-  const RowPlan *plan = ws.plans + row;
   const int k = load_scalar(&plan->k);
-  const int penbits = load_scalar(&plan->pen);
-  const double prep = load_scalar(&plan->rep);
-  // presence / frequency rows were penalised in place above
-  const bool rep = (penbits & kPenRep) && !(penbits & kPenPF);
+  const int words = (V + 31) >> 5;
+  const int ecap = mid_early_cap(V);
+  int32_t *eid = reinterpret_cast<int32_t *>(bitmap + words);   // the penalised ids, and
+  uint32_t *eaux = reinterpret_cast<uint32_t *>(eid + ecap);     //   their count words, then values
+  __shared__ int32_t n_early;
+  int ne = 0;                    // penalised ids listed
+  float praw[2] = {0.f, 0.f};    // logits of list entries tid and tid + kRowThreads
+  static_assert(kMidEarly <= 2 * kRowThreads, "two list entries per thread");
+
+  // Presence / frequency rows: the row's distinct history ids are counted as
+  // pen_kernel counts them, in the LDS the stream has not taken yet (the
+  // candidate, sort and histogram arrays hold pen_smem_bytes()), while rounds
+  // 0 and 1 are in flight, into a list (eid: id, eaux: count | rep bit 31)
+  // and the bitmap.  The stream leaves the listed ids out; their logits are
+  // requested now and needed only at the end of the row, where their
+  // penalties are applied, stored in place and joined.  A row whose ids do
+  // not fit the table or the list is rewritten in place now, waits for its
+  // stores and reads rounds 0 and 1 again, unmasked.
+  if (pf) {
+    for (int i = tid; i < words; i += kRowThreads) bitmap[i] = 0u;
+    if (tid == 0) n_early = 0;
+    __syncthreads();
+    auto slot = [&](int id, uint32_t cw) {
+      const int p = atomicAdd(&n_early, 1);
+      if (p < ecap) {
+        eid[p] = id;
+        eaux[p] = cw;
+      }
+      atomicOr(&bitmap[id >> 5], 1u << (id & 31));
+    };
+    const bool deferred = pen_row<kRowThreads, true>(
+        hrow, pp, rowp, V, reinterpret_cast<uint32_t *>(mdyn), ms.pen_full, PenNoHook{}, &pids,
+        slot);
+    __syncthreads();   // the list and the bitmap are complete
+    ne = n_early;
+    if (!deferred || ne > ecap) {   // (uniform)
+      if (deferred) pen_apply<kRowThreads>(reinterpret_cast<const uint32_t *>(mdyn), pp, rowp);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __syncthreads();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      load_tail();
+      load_rd<kR0NV, VEC>(v0, src, 0, tid);
+      load_rd<kRowNV, VEC>(vb, src, round_base(1), tid);
+      ne = 0;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const int i = tid + c * kRowThreads;
+        const int id = i < ne ? eid[i] : V;   // (past the row: 0, no read)
+        praw[c] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(src.x1, id * 4, 0, 0));
+      }
+    }
+  }
+  // the ids the stream leaves out: the repetition set (rows without presence
+  // / frequency), or a presence / frequency row's penalised ids
+  const bool rep = (penbits & kPenRep) && !pf;
+  const bool mask = rep || ne > 0;
   if (tid == 0) { ms.top_key = 0; ms.n_f = 0; ms.ovf = 0; ms.n_sel = 0; }
   for (int i = tid; i < kMidBins; i += kRowThreads) hist[i] = 0;
   unsigned long long *seg = cbuf + wave * kSegCap;
@@ -2488,7 +2629,6 @@ __global__ __launch_bounds__(kRowThreads) void mid_kernel(LaunchArgs a, Workspac
 
   int pid = -1;
   if (rep) {
-    const int words = (V + 31) >> 5;
     for (int i = tid; i < words; i += kRowThreads) bitmap[i] = 0;
     __syncthreads();
     const int hid = tid < hist_n ? hraw : -1;
@@ -2503,7 +2643,7 @@ __global__ __launch_bounds__(kRowThreads) void mid_kernel(LaunchArgs a, Workspac
 
   // ---- round 0 is counted whole; the bound follows from the histogram
   clip_rd<kR0NV>(v0, 0, tid, src.lim);
-  if (rep) mask_penalised<kR0NV>(v0, 0, tid, V, bitmap);
+  if (mask) mask_penalised<kR0NV>(v0, 0, tid, V, bitmap);
   uint32_t k0[kR0NV][4];
   {
     const uint32_t m0 = wave_max_u32(hist_keys<kR0NV>(v0, k0, hist));
@@ -2513,18 +2653,42 @@ __global__ __launch_bounds__(kRowThreads) void mid_kernel(LaunchArgs a, Workspac
   load_rd<kRowNV, VEC>(va, src, round_base(2), tid);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();   // round 0 counted
+  // the tail logits, kept in LDS until the end (their reads, issued before
+  // round 0's, are done: no wait)
+  if (VEC && tid == 0) {
+#pragma unroll
+    for (int q = 0; q < 3; ++q) ms.tl[q] = tl[q];
+  }
   uint32_t theta = hist_bound(hist, ms.top_key, k);
   float xf = key_floor(theta ? theta : 1u);
   append_keys<kR0NV>(k0, 0, tid, theta ? theta : 1u, seg, cnt);
+  if (mask) {   // (uniform)
+    // The left-out ids after round 0 (the repetition set, or a deferring
+    // row's listed ids) are streamed with their raw logits, which later
+    // rounds may count: each is taken out of its bin first (before any wave
+    // counts a later round).  Counted or not, the counts stay lower bounds of
+    // the other logits' counts, and the raw entries are dropped at the end.
+    const int e01 = 4 * round_base(1);
+    auto take_out = [&](int id, float raw) {
+      const uint32_t key = f2key(raw);
+      if (id >= e01 && id < src.lim && key) atomicSub(&hist[key >> kMidShift], 1u);
+    };
+    if (pid >= 0) take_out(pid, pval);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int i = tid + c * kRowThreads;
+      if (i < ne) take_out(eid[i], praw[c]);
+    }
+    __syncthreads();
+  }
 
   // ---- rounds >= 1
   for (int r = 1; r < nr; r += 2) {
-    mid_step(vb, round_base(r), tid, src.lim, V, k, rep, bitmap, hist, &ms.top_key, seg, cnt,
-             theta, xf, lost);
+    mid_step(vb, round_base(r), tid, src.lim, k, hist, &ms.top_key, seg, cnt, theta, xf, lost);
     load_rd<kRowNV, VEC>(vb, src, round_base(r + 2), tid);   // past the row near its end
     if (r + 1 >= nr) break;
-    mid_step(va, round_base(r + 1), tid, src.lim, V, k, rep, bitmap, hist, &ms.top_key, seg, cnt,
-             theta, xf, lost);
+    mid_step(va, round_base(r + 1), tid, src.lim, k, hist, &ms.top_key, seg, cnt, theta, xf,
+             lost);
     load_rd<kRowNV, VEC>(va, src, round_base(r + 3), tid);
   }
   lost = lost || cnt > kSegCap;
@@ -2533,12 +2697,34 @@ __global__ __launch_bounds__(kRowThreads) void mid_kernel(LaunchArgs a, Workspac
   float pv = 0.f;
   if (pid >= 0) {
     RowPlan pr;
-    pr.rep = prep;
+    pr.rep = load_scalar(&plan->rep);   // (read again: not held through the stream)
     pr.pen = kPenRep;
     pv = penalise(pval, true, 0u, pr);
     rowp[pid] = pv;
   }
+  // a presence / frequency row's listed penalties (src/sampler.ts:24-33 and
+  // the presence / frequency extension, as pen_kernel applies them), stored
+  // in place; the fence makes the stores seen by a replay's reads
+  if (ne > 0) {
+    RowPlan pe{};   // (read again: not held through the stream)
+    pe.pen = load_scalar(&plan->pen);
+    pe.rep = load_scalar(&plan->rep);
+    pe.pres = load_scalar(&plan->pres);
+    pe.freq = load_scalar(&plan->freq);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int i = tid + c * kRowThreads;
+      if (i < ne) {
+        const uint32_t cw = eaux[i];
+        const float v = penalise(praw[c], (cw >> 31) != 0, cw & 0x7FFFFFFFu, pe);
+        eaux[i] = __float_as_uint(v);
+        rowp[eid[i]] = v;
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __syncthreads();   // every wave's counts are in
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   theta = hist_bound(hist, ms.top_key, k);
   const uint32_t lo = theta ? theta : 1u;
   xf = key_floor(lo);
@@ -2556,15 +2742,26 @@ __global__ __launch_bounds__(kRowThreads) void mid_kernel(LaunchArgs a, Workspac
   if (lost) {
     if (lane == 0) ms.ovf = 1;
   } else {
-    for (int i = lane; i < cnt; i += 64) join(cand_key(seg[i]) >= lo, seg[i]);
+    // (the raw entries of left-out ids are dropped)
+    for (int i = lane; i < cnt; i += 64) {
+      const unsigned long long c = seg[i];
+      const uint32_t id = cand_idx(c);
+      join(cand_key(c) >= lo && !(mask && ((bitmap[id >> 5] >> (id & 31)) & 1u)), c);
+    }
   }
   join(pid >= 0 && pv >= xf, pack_cand(f2key(pv), (uint32_t)pid));
+  for (int i0 = 0; i0 < ne; i0 += kRowThreads) {   // (a presence / frequency row's listed ids)
+    const int i = i0 + tid;
+    const float ev = i < ne ? __uint_as_float(eaux[i]) : 0.f;
+    join(i < ne && ev >= xf, pack_cand(f2key(ev), (uint32_t)(i < ne ? eid[i] : 0)));
+  }
   if (VEC && src.lim < V) {
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
       const int e = src.lim + q;
-      const bool ok = tid == 0 && e < V && !(rep && ((bitmap[e >> 5] >> (e & 31)) & 1u));
-      join(ok && tl[q] >= xf, pack_cand(f2key(tl[q]), (uint32_t)e));
+      const bool ok = tid == 0 && e < V && !(mask && ((bitmap[e >> 5] >> (e & 31)) & 1u));
+      const float t = ms.tl[q];
+      join(ok && t >= xf, pack_cand(f2key(t), (uint32_t)e));
     }
   }
   __syncthreads();
@@ -5270,7 +5467,7 @@ hipError_t prepare_kernels() {
     if ((e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, row_smem)) !=
         hipSuccess)
       return e;
-  const int mid_smem = (int)mid_smem_bytes(kRowMaxVocab);
+  const int mid_smem = kMidLdsMax;
   if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mid_kernel<true>),
                                hipFuncAttributeMaxDynamicSharedMemorySize, mid_smem)) != hipSuccess)
     return e;

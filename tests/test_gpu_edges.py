@@ -179,6 +179,39 @@ def test_penalty_history_beyond_the_table(any_sampler):
     _run(any_sampler, cases, V)
 
 
+@pytest.mark.parametrize("stride", [151940, 151937])
+def test_mid_penalties_long_histories(any_sampler, stride):
+    """Presence / frequency rows of the mid kernel (64 < k <= 1024).  The
+    history is counted while the first rounds load, its ids are left out of
+    the stream's counts and their penalised logits joined at the end, unless
+    its distinct ids overflow the list (2048) or the table (then counted by
+    id ranges): that row is rewritten in place and read again.  Short and
+    long histories, repeated ids.
+    The histories hit the row's top logits (in round 0, later rounds and the
+    last logit past the whole float4s), so the penalties change the candidate
+    set.  Aligned rows (the last logit read apart from the float4s) and
+    unaligned ones.  Candidate ids, probabilities and penalised logits
+    against the oracle."""
+    V = 151937
+    r = _rng(21)
+    row = (r.standard_normal(V) * 2.5).astype(np.float32)
+    row[V - 1] = 11.0
+    row[100] = 10.5                                       # in round 0
+    top = [int(i) for i in np.argsort(-row)[:1500]]
+    short = top[:300] + list(r.integers(0, V, 1200))      # 1500 entries
+    listed = list(r.choice(top, 3000)) + [V - 1, 100]     # > 2048 entries, <= 1500 distinct
+    over_list = [int(i) for i in r.choice(V, 4000, replace=False)] + top[:600] * 2
+    over_table = list(r.integers(0, V, 20000)) + top[:200]
+    pf = dict(temperature=0.8, topK=300, topP=0.95, presencePenalty=0.5, frequencyPenalty=0.2)
+    cases = [(row, short, pf, 0.3),
+             (row, listed, pf, 0.6),
+             (row, listed, dict(pf, repetitionPenalty=1.3, topK=1000, topP=0.99), 0.9),
+             (row, over_list, pf, 0.45),
+             (row, over_table, dict(pf, repetitionPenalty=1.1), 0.2),
+             (row, listed, dict(temperature=0.0, presencePenalty=2.0, frequencyPenalty=0.1), 0.5)]
+    _run(any_sampler, cases, V, stride=stride, cap=1024, label="mid penalties")
+
+
 @pytest.mark.parametrize("vocab,pad", [(151669, 0), (1001, 3), (4097, 1), (1, 0), (2, 5), (3, 0),
                                        (151937, 3), (50257, 3), (32003, 1), (6, 2), (7, 1)])
 def test_ragged_vocab_and_stride(any_sampler, vocab, pad):
