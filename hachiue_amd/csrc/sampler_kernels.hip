@@ -85,6 +85,14 @@ __device__ __forceinline__ unsigned long long pack_cand(uint32_t key, uint32_t i
 __device__ __forceinline__ uint32_t cand_key(unsigned long long c) { return (uint32_t)(c >> 32); }
 __device__ __forceinline__ uint32_t cand_idx(unsigned long long c) { return 0xFFFFFFFFu - (uint32_t)c; }
 
+// Wave-uniform read of memory the kernel never writes, through the scalar
+// cache (constant address space): it completes independently of the vector
+// loads queued before it.
+template <typename T>
+__device__ __forceinline__ T load_scalar(const T *p) {
+  return *(const __attribute__((address_space(4))) T *)(p);
+}
+
 // ---------------------------------------------------------------- wave helpers
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63); }
@@ -535,16 +543,20 @@ struct HistRow {
 __device__ __forceinline__ HistRow hist_row(const LaunchArgs &a, int row) {
   HistRow h{a.hist_ids, 0, 0, 0};
   if (a.hist_cap > 0) {
-    int64_t len = a.hist_len[row];
+    // (the scalar cache, invalidated when a kernel starts: a decode step
+    // reads the row's length here and its own workgroup writes it at the end)
+    int64_t len = load_scalar(a.hist_len + row);
     if (len < 0) len = 0;
     h.p = a.hist_ids + (int64_t)row * a.hist_cap;
     h.n = len < a.hist_cap ? len : a.hist_cap;
     h.start = (len - h.n) % a.hist_cap;
     h.cap = a.hist_cap;
   } else if (a.hist_off) {
-    const int64_t h0 = a.hist_off[row];
+    // (through the scalar cache: the offsets are not written while a kernel
+    // runs, and the vector reads are not held up by them)
+    const int64_t h0 = load_scalar(a.hist_off + row);
     h.p = a.hist_ids + h0;
-    h.n = a.hist_off[row + 1] - h0;
+    h.n = load_scalar(a.hist_off + row + 1) - h0;
   }
   return h;
 }
@@ -1410,14 +1422,6 @@ __device__ __forceinline__ float rd_max(const float (&v)[NV][4]) {
 }
 
 
-// Wave-uniform read of memory the kernel never writes, through the scalar
-// cache (constant address space): it completes independently of the vector
-// loads queued before it.
-template <typename T>
-__device__ __forceinline__ T load_scalar(const T *p) {
-  return *(const __attribute__((address_space(4))) T *)(p);
-}
-
 // Maximum of one key per lane over the wave (DPP row shifts and row
 // broadcasts, then lane 63), returned wave-uniform.
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
@@ -1952,18 +1956,21 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   float *rowp = rowfull + eoff;
   const int nr = row_rounds(V);
 
-  // The last <= 128 history ids, one per thread of waves 0-1, are requested
-  // before the stream: a wave's reads complete in order.
-  const HistTail ht = hist_tail(a, row, tid);
-  const int hraw = ht.id, hist_n = ht.n;
+  // Round 0 is requested first; the last <= 128 history ids (one per thread
+  // of waves 0-1; their offsets come through the scalar cache) right after
+  // it, so that they arrive with round 0 (a wave's reads complete in order);
+  // then round 1.  Round 2 follows as soon as round 0 has arrived, so the
+  // bound below is computed while rounds 1 and 2 stream.
   RowSrc src;
   src.lim = VEC ? (V & ~3) : V;
   src.x4 = make_rsrc(rowp, 4u * (uint32_t)(V & ~3));
   src.x1 = make_rsrc(rowp, 4u * (uint32_t)V);
-  // rounds 0 and 1 go out together; round 2 follows as soon as round 0 has
-  // arrived, so the bound below is computed while rounds 1 and 2 stream
   float v0[kR0NV][4], va[kRowNV][4], vb[kRowNV][4];
   load_rd<kR0NV, VEC>(v0, src, 0, tid);
+  __builtin_amdgcn_sched_barrier(0);
+  const HistTail ht = hist_tail(a, row, tid);
+  const int hraw = ht.id, hist_n = ht.n;
+  __builtin_amdgcn_sched_barrier(0);
   load_rd<kRowNV, VEC>(vb, src, round_base(1), tid);   // past the row when nr == 1
   // the logits past the last whole float4 (VEC only), read by thread 0
   float tl[3] = {0.f, 0.f, 0.f};
