@@ -4580,13 +4580,6 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
   const int iters = (nfull + U * kFT - 1) / (U * kFT);
   const double it = 1.0 / P.temperature;
 
-  // the only plain loads (before the buffer reads: a wait for a later load
-  // would wait for every read before it)
-  const double u = a.uniforms[row];
-  const float vtail = tid < (V & 3) ? rowp[4 * nfull + tid] : -INFINITY;
-  for (int i = tid; i < kFB; i += kFT) sm.mass[i] = 0.0;
-  if (tid == 0) { sm.ntop = 0; sm.nbuf = 0; }
-
   f32x4 A[U], B[U];
   // pass 1 reads cached (pass 2 reads the row again), pass 2 non-temporal
   auto load = [&](f32x4 (&t)[U], int c, auto policy) {
@@ -4601,9 +4594,19 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
   using cached = std::integral_constant<int, 0>;
   using nontemporal = std::integral_constant<int, kReadNT>;
   // every read is unconditional (past the row a buffer read returns 0 and
-  // touches no memory), so the compiler keeps both buffers in flight
+  // touches no memory), so the compiler keeps both buffers in flight.  The
+  // first two chunks go out first; the uniform comes through the scalar
+  // cache, and the logits past the last whole float4 (needed after pass 1)
+  // are read after the chunks, then the LDS is cleared.
   load(A, 0, cached{});
   load(B, 1, cached{});
+  __builtin_amdgcn_sched_barrier(0);
+  const double u = load_scalar(a.uniforms + row);
+  const float vtail = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+      make_rsrc(rowp, 4u * (uint32_t)V), (tid < (V & 3) ? 4 * nfull + tid : V) * 4, 0, 0));
+  const float vt = tid < (V & 3) ? vtail : -INFINITY;
+  for (int i = tid; i < kFB; i += kFT) sm.mass[i] = 0.0;
+  if (tid == 0) { sm.ntop = 0; sm.nbuf = 0; }
   // m0: the largest of the first 4 U kFT logits (NaN is never > anything)
   float mx = -INFINITY;
 #pragma unroll
@@ -4665,7 +4668,7 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
   load(B, 1, nontemporal{});
   if (tid < (V & 3)) {   // the logits past the last whole float4
     const int e = 4 * nfull + tid;
-    const float v = vtail;
+    const float v = vt;
     if (v > -INFINITY) {
       ++nf;
       if (v > m0) {
@@ -4758,7 +4761,7 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
     scan(B, c + 1);
     load(B, c + 3, nontemporal{});
   }
-  if (tid < (V & 3)) gather(vtail, 4 * nfull + tid);
+  if (tid < (V & 3)) gather(vt, 4 * nfull + tid);
   const uint32_t below = fast_block_sum(below0, reinterpret_cast<uint32_t *>(sm.ured));
   const int ng = sm.nbuf;
   const int nl = ng + ntop;
