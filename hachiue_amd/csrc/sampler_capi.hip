@@ -1161,6 +1161,8 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
       if ((p.mode != hs::kModeGreedy && p.mode != hs::kModeSmall) || (p.pen & hs::kPenPF))
         fused = false;
   }
+  bool greedy = fused;   // every row greedy: the GEMV keeps the argmax alone
+  for (const hs::RowPlan &p : plans) greedy = greedy && p.mode == hs::kModeGreedy;
   if (fused) {
     DeviceGuard guard(ctx->device);
     int rc = enter_stream(ctx, st);
@@ -1169,10 +1171,11 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
     bool skip = false;
     rc = gemv_setup(ctx, d_x, M, ldx, w, d_logits, ldl, st, g, &skip);
     if (rc) return rc;
-    const int blocks = skip ? 0 : hs::tern_sample_grid(g);
+    const int blocks = skip ? 0 : greedy ? hs::tern_argmax_grid(g) : hs::tern_sample_grid(g);
     if (blocks > 0) {
-      const size_t nl = (size_t)M * blocks;
-      HS_HIP(ctx->fuse_pool.ensure(nl * 64 * sizeof(unsigned long long) + nl * sizeof(uint32_t)));
+      const size_t nl = greedy ? 0 : (size_t)M * blocks;
+      if (!greedy)
+        HS_HIP(ctx->fuse_pool.ensure(nl * 64 * sizeof(unsigned long long) + nl * sizeof(uint32_t)));
       // counters: zero between calls (each is reset by the workgroup that counts last)
       rc = ensure_zeroed(ctx->fuse_rows, (size_t)M * sizeof(hs::FuseRow), st);
       if (rc) return rc;
@@ -1185,13 +1188,14 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
       f.uniforms = d_uniforms;
       f.tokens = d_tokens;
       f.rows = static_cast<hs::FuseRow *>(ctx->fuse_rows.p);
-      f.list = static_cast<unsigned long long *>(ctx->fuse_pool.p);
-      f.disc = reinterpret_cast<uint32_t *>(f.list + nl * 64);
+      f.list = greedy ? nullptr : static_cast<unsigned long long *>(ctx->fuse_pool.p);
+      f.disc = greedy ? nullptr : reinterpret_cast<uint32_t *>(f.list + nl * 64);
       f.blocks = blocks;
       hipEvent_t *ev = nullptr;
       rc = timed_slot(ctx, hs::kGemvTimedSlot, &ev);
       if (rc) return rc;
-      const hipError_t e = hs::launch_tern_sample(g, f, st, ev, ctx->done_ev);
+      const hipError_t e = greedy ? hs::launch_tern_argmax(g, f, st, ev, ctx->done_ev)
+                                  : hs::launch_tern_sample(g, f, st, ev, ctx->done_ev);
       if (e != hipSuccess) {
         (void)leave_stream(ctx, st, false);
         return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));

@@ -5163,6 +5163,25 @@ __device__ __forceinline__ bool fuse_arrive(uint32_t *cnt, uint32_t of, FuseSmem
   return fs.last != 0;
 }
 
+// Row m's repetition set (src/sampler.ts:24-33: history.slice(-128), ids
+// in [0, N)) into rset (kFuseSetSlots slots, -1 when empty, cleared by the
+// caller beforehand), by threads 0-127.
+__device__ __forceinline__ void fuse_rep_set(const FuseArgs &f, int m, int N, int32_t *rset) {
+  const int tid = threadIdx.x;
+  if (!f.hist_off || tid >= 128) return;
+  const int64_t h0 = f.hist_off[m], n = f.hist_off[m + 1] - h0;
+  const int64_t j = n - (n < 128 ? n : 128) + tid;
+  if (j >= n) return;
+  const int id = f.hist_ids[h0 + j];
+  if (id < 0 || id >= N) return;
+  uint32_t h = fuse_hash(id);
+  for (int probe = 0; probe < kFuseSetSlots; ++probe) {
+    const int old = atomicCAS(&rset[h], -1, id);
+    if (old == -1 || old == id) break;
+    h = (h + 1) & (kFuseSetSlots - 1);
+  }
+}
+
 // (one 16-wave workgroup per CU, where the plain GEMV fits two: its
 // epilogue's scalar registers.  Bounding them to fit two was measured slower:
 // the GEMV part is no faster and the last workgroup gets twice the lists.)
@@ -5183,21 +5202,7 @@ __global__ __launch_bounds__(64 * tm::waves<FMT>()) void gemv_tern_sample_kernel
   if (tid < kFuseSetSlots) fs.rset[tid] = -1;
   if (tid == 0) fs.disc = 0u;
   __syncthreads();
-  if (rep && f.hist_off && tid < 128) {
-    const int64_t h0 = f.hist_off[m], n = f.hist_off[m + 1] - h0;
-    const int64_t j = n - (n < 128 ? n : 128) + tid;
-    if (j < n) {
-      const int id = f.hist_ids[h0 + j];
-      if (id >= 0 && id < g.N) {
-        uint32_t h = fuse_hash(id);
-        for (int probe = 0; probe < kFuseSetSlots; ++probe) {
-          const int old = atomicCAS(&fs.rset[h], -1, id);
-          if (old == -1 || old == id) break;
-          h = (h + 1) & (kFuseSetSlots - 1);
-        }
-      }
-    }
-  }
+  if (rep) fuse_rep_set(f, m, g.N, fs.rset);
   // (the body's first barrier completes the set)
 
   uint2 *wbuf = reinterpret_cast<uint2 *>(reinterpret_cast<uint8_t *>(tlds) + gemv_tern_lds_bytes(g.K)) +
@@ -5434,6 +5439,116 @@ int tern_sample_grid(const GemvArgs &g) {
   }
 }
 
+// Every row greedy (src/sampler.ts:36-46 at temperature <= 0): the GEMV
+// whose epilogue stores each logit (its repetition penalty applied, as
+// pen_kernel does) and keeps each lane's packed maximum (value, then the
+// smallest index); no record buffer, the plain GEMV's LDS and grid.  The
+// workgroup's maximum goes to the row's word by an atomic maximum; the last
+// workgroup to count in writes the token.
+struct ArgmaxEpi {
+  float *y;
+  const int32_t *rset;   // the repetition ids, or null
+  double rep;
+  unsigned long long best;
+  __device__ __forceinline__ void out(int, int row, float v, bool valid) {
+    if (!valid) return;
+    if (rset && fuse_in_set(rset, row)) {
+      RowPlan pr{};
+      pr.rep = rep;
+      pr.pen = kPenRep;
+      v = penalise(v, true, 0u, pr);
+    }
+    store_agent(y + row, v);
+    const uint32_t key = f2key(v);
+    const unsigned long long c = key ? pack_cand(key, (uint32_t)row) : 0ull;
+    best = c > best ? c : best;
+  }
+};
+
+template <int FMT>
+__global__ __launch_bounds__(64 * tm::waves<FMT>())
+void gemv_tern_argmax_kernel(GemvArgs g, FuseArgs f) {
+  constexpr int NW = tm::waves<FMT>();
+  extern __shared__ uint4 tlds[];
+  __shared__ int32_t rset[kFuseSetSlots];
+  __shared__ unsigned long long wbest[NW];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m = (int)blockIdx.y;
+  const RowPlan *plan = f.plans + m;
+  const bool rep = (load_scalar(&plan->pen) & kPenRep) != 0;
+  float *y = g.y + (int64_t)m * g.ldy;
+  if (tid < kFuseSetSlots) rset[tid] = -1;
+  __syncthreads();
+  if (rep) fuse_rep_set(f, m, g.N, rset);
+  // (the body's first barrier completes the set)
+  ArgmaxEpi epi{y, rep ? rset : nullptr, load_scalar(&plan->rep), 0ull};
+  tern_gemv_body<FMT>(g, tlds, epi);
+  const unsigned long long b = wave_max64(epi.best);
+  if (lane == 0) wbest[wave] = b;
+  __syncthreads();
+  FuseRow *fr = f.rows + m;
+  if (tid == 0) {
+    unsigned long long bb = 0ull;
+    for (int w = 0; w < NW; ++w) bb = wbest[w] > bb ? wbest[w] : bb;
+    if (bb) __hip_atomic_fetch_max(&fr->best, bb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // counted in after the stores and the maximum completed
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t old =
+        __hip_atomic_fetch_add(&fr->arrived, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old == gridDim.x - 1) {
+      store_agent(&fr->arrived, 0u);
+      LaunchArgs a{};
+      a.logits = g.y;
+      a.stride = g.ldy;
+      a.rows = g.M;
+      a.vocab = g.N;
+      a.uniforms = f.uniforms;
+      a.tokens = f.tokens;
+      const unsigned long long bb = load_agent(&fr->best);
+      write_greedy(a, m, load_agent(y), bb);
+      store_agent(&fr->best, 0ull);
+    }
+  }
+}
+
+int tern_argmax_grid(const GemvArgs &g) {
+  const int nw = g.type == kW_Q1_0 ? tm::waves<kW_Q1_0>()
+                 : g.type == kW_PQ2_0 ? tm::waves<kW_PQ2_0>() : tm::waves<kW_PTQ1_0>();
+  const void *k = g.type == kW_Q1_0 ? reinterpret_cast<const void *>(gemv_tern_argmax_kernel<kW_Q1_0>)
+                  : g.type == kW_PQ2_0 ? reinterpret_cast<const void *>(gemv_tern_argmax_kernel<kW_PQ2_0>)
+                                       : reinterpret_cast<const void *>(gemv_tern_argmax_kernel<kW_PTQ1_0>);
+  const int res = resident_blocks(k, (uint32_t)gemv_tern_lds_bytes(g.K), 64 * nw);
+  const int ntiles = (g.N + 15) / 16;
+  const int blocks = (ntiles + nw - 1) / nw;
+  return blocks < res ? blocks : res;
+}
+
+hipError_t launch_tern_argmax(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
+                              hipEvent_t *ev, hipEvent_t done) {
+  auto go = [&](auto kern, int nw) {
+    const int blocks = tern_argmax_grid(g);
+    if (blocks < 1) return hipErrorInvalidValue;
+    const size_t lds = gemv_tern_lds_bytes(g.K);
+    const dim3 grid((unsigned)blocks, (unsigned)g.M), block(64 * nw);
+    if (ev)
+      hipExtLaunchKernelGGL(kern, grid, block, lds, stream, ev[0], ev[1], 0u, g, f);
+    else if (done)
+      hipExtLaunchKernelGGL(kern, grid, block, lds, stream, nullptr, done, 0u, g, f);
+    else
+      hipLaunchKernelGGL(kern, grid, block, lds, stream, g, f);
+    return hipGetLastError();
+  };
+  switch (g.type) {
+    case kW_Q1_0: return go(gemv_tern_argmax_kernel<kW_Q1_0>, tm::waves<kW_Q1_0>());
+    case kW_PQ2_0: return go(gemv_tern_argmax_kernel<kW_PQ2_0>, tm::waves<kW_PQ2_0>());
+    case kW_PTQ1_0: return go(gemv_tern_argmax_kernel<kW_PTQ1_0>, tm::waves<kW_PTQ1_0>());
+    default: return hipErrorInvalidValue;
+  }
+}
+
 hipError_t launch_tern_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
                               hipEvent_t *ev, hipEvent_t done) {
   auto go = [&](auto kern, int nw, int blocks) {
@@ -5491,6 +5606,13 @@ hipError_t prepare_kernels() {
     for (const void *fk : tk)
       if ((e = hipFuncSetAttribute(fk, hipFuncAttributeMaxDynamicSharedMemorySize,
                                    (int)tern_sample_lds_bytes(kGemvMaxK, 16))) != hipSuccess)
+        return e;
+    const void *ak[3] = {reinterpret_cast<const void *>(&gemv_tern_argmax_kernel<kW_Q1_0>),
+                         reinterpret_cast<const void *>(&gemv_tern_argmax_kernel<kW_PQ2_0>),
+                         reinterpret_cast<const void *>(&gemv_tern_argmax_kernel<kW_PTQ1_0>)};
+    for (const void *fk : ak)
+      if ((e = hipFuncSetAttribute(fk, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                   (int)gemv_tern_lds_bytes(kGemvMaxK))) != hipSuccess)
         return e;
   }
   if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&finalize_kernel),
