@@ -4086,6 +4086,7 @@ struct FastSmem {
   unsigned long long ured[kFT / 64];
   double top_m, top_s;                 // the list's maximum and exp sum
   int ntop, nbuf, hit, flag;
+  int next1, next2;                    // the passes' next unit
 };
 
 size_t large_fast_smem_bytes() { return sizeof(FastSmem); }
@@ -4572,46 +4573,65 @@ __device__ __forceinline__ FastLoc fast_locate_wave(int glo, int ghi, double c_s
 __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P, int row,
                                            FastSmem &sm) {
   constexpr int U = 4;   // float4 per thread per buffer; two buffers in flight
-  const int tid = threadIdx.x;
+  constexpr int kW = kFT / 64;   // waves
+  constexpr int kUnit = U * 64;  // float4 of one wave's buffer
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float *rowp = a.logits + (int64_t)row * a.stride;
   const int V = a.vocab;
   const int nfull = V >> 2;
   const rsrc_t r4 = make_rsrc(rowp, 16u * (uint32_t)nfull);
-  const int iters = (nfull + U * kFT - 1) / (U * kFT);
+  const int nunits = (nfull + kUnit - 1) / kUnit;
   const double it = 1.0 / P.temperature;
 
+  // Each pass hands the row out in units of kUnit float4 (4 KB): a wave's
+  // first two are fixed (units w and kW + w), the rest come from an LDS
+  // counter, one unit ahead, so that every wave streams until the row ends.
+  // (With fixed shares the youngest waves of a CU ended each pass up to
+  // 13 us after the others.)
   f32x4 A[U], B[U];
   // pass 1 reads cached (pass 2 reads the row again), pass 2 non-temporal
-  auto load = [&](f32x4 (&t)[U], int c, auto policy) {
+  auto load = [&](f32x4 (&t)[U], int n, auto policy) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const auto x = __builtin_amdgcn_raw_buffer_load_b128(r4, (c * U * kFT + u * kFT + tid) * 16, 0,
+      const auto x = __builtin_amdgcn_raw_buffer_load_b128(r4, (n * kUnit + u * 64 + lane) * 16, 0,
                                                            decltype(policy)::value);
       t[u] = f32x4{__uint_as_float(x[0]), __uint_as_float(x[1]), __uint_as_float(x[2]),
                    __uint_as_float(x[3])};
     }
   };
+  // (lane 0 holds the unit; it is broadcast where used, a unit later, so
+  // that no wave waits for its LDS operations at the grab)
+  // (an increment below 2^32 - 1 is a plain add; unlike atomicAdd it is left
+  // alone by the compiler's wave aggregation, which waits for the result)
+  auto grab = [&](int *ctr) {
+    int n = 0;
+    if (lane == 0)
+      n = (int)__builtin_amdgcn_atomic_inc32(reinterpret_cast<uint32_t *>(ctr), 0xFFFFFFFFu,
+                                             __ATOMIC_RELAXED, "workgroup");
+    return n;
+  };
   using cached = std::integral_constant<int, 0>;
   using nontemporal = std::integral_constant<int, kReadNT>;
   // every read is unconditional (past the row a buffer read returns 0 and
   // touches no memory), so the compiler keeps both buffers in flight.  The
-  // first two chunks go out first; the uniform comes through the scalar
+  // first two units go out first; the uniform comes through the scalar
   // cache, and the logits past the last whole float4 (needed after pass 1)
-  // are read after the chunks, then the LDS is cleared.
-  load(A, 0, cached{});
-  load(B, 1, cached{});
+  // are read after the units, then the LDS is cleared.
+  load(A, wave, cached{});
+  load(B, kW + wave, cached{});
   __builtin_amdgcn_sched_barrier(0);
   const double u = load_scalar(a.uniforms + row);
   const float vtail = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
       make_rsrc(rowp, 4u * (uint32_t)V), (tid < (V & 3) ? 4 * nfull + tid : V) * 4, 0, 0));
   const float vt = tid < (V & 3) ? vtail : -INFINITY;
   for (int i = tid; i < kFB; i += kFT) sm.mass[i] = 0.0;
-  if (tid == 0) { sm.ntop = 0; sm.nbuf = 0; }
-  // m0: the largest of the first 4 U kFT logits (NaN is never > anything)
+  if (tid == 0) { sm.ntop = 0; sm.nbuf = 0; sm.next1 = 2 * kW; sm.next2 = 2 * kW; }
+  // m0: the largest of the first 4 U kFT logits, units 0 to kW - 1 (NaN is
+  // never > anything)
   float mx = -INFINITY;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    if (u * kFT + tid < nfull) {
+    if (wave * kUnit + u * 64 + lane < nfull) {
 #pragma unroll
       for (int c = 0; c < 4; ++c) mx = A[u][c] > mx ? A[u][c] : mx;
     }
@@ -4650,22 +4670,31 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
       atomicAdd(&sm.mass[fast_bucket_q(q)], (double)(cand && !(v > m0) ? w : 0.0f));
     }
   };
-  auto process = [&](const f32x4 (&t)[U], int c) {
+  auto process = [&](const f32x4 (&t)[U], int n) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int i = c * U * kFT + u * kFT + tid;
+      const int i = n * kUnit + u * 64 + lane;
       if (i < nfull) add4(t[u], 4 * i);
     }
   };
-  for (int c = 0; c < iters; c += 2) {
-    process(A, c);
-    load(A, c + 2, cached{});
-    process(B, c + 1);   // (past the row: every element skipped)
-    load(B, c + 3, cached{});
+  {
+    // units are taken in increasing order: once A's is past the row, so is B's
+    int ua = wave, ub = kW + wave, nx = grab(&sm.next1);
+    for (;;) {
+      process(A, ua);
+      ua = __builtin_amdgcn_readfirstlane(nx);
+      nx = grab(&sm.next1);
+      load(A, ua, cached{});
+      process(B, ub);
+      ub = __builtin_amdgcn_readfirstlane(nx);
+      nx = grab(&sm.next1);
+      load(B, ub, cached{});
+      if (ua >= nunits) break;
+    }
   }
   // pass 2's first reads go out now, under the analysis below
-  load(A, 0, nontemporal{});
-  load(B, 1, nontemporal{});
+  load(A, wave, nontemporal{});
+  load(B, kW + wave, nontemporal{});
   if (tid < (V & 3)) {   // the logits past the last whole float4
     const int e = 4 * nfull + tid;
     const float v = vt;
@@ -4735,33 +4764,70 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
 
   // 4. gather the ranges' logits (the list above m0 joins them all).  This
   // is the row's last read: non-temporal.
+  // The bucket tests run on q itself: b = trunc(clamp(q, 0, kFB - 1)) and
+  // both ranges end below kFB - 1, so b < lo iff q < lo (lo > 0), and
+  // lo <= b <= hi iff lo' <= q < hi + 1, lo' = lo or -Infinity for lo <= 0.
+  // A NaN fails v <= m0; -Infinity gives q = +Infinity, in no test.
+  const float fb0 = g0lo > 0 ? (float)g0lo : -INFINITY;
+  const float fh0 = g0hi >= 0 ? (float)(g0hi + 1) : -INFINITY;
+  const float fb1 = g1lo > 0 ? (float)g1lo : -INFINITY;
+  const float fh1 = g1hi >= 0 ? (float)(g1hi + 1) : -INFINITY;
   uint32_t below0 = 0;   // candidates v <= m0 in buckets before g0lo
-  auto gather = [&](float v, int e) {
-    if (!(v > -INFINITY) || v > m0) return;
-    const int b = fast_bucket(v, cz, m0cz);
-    below0 += b < g0lo;
-    if ((b >= g0lo && b <= g0hi) || (b >= g1lo && b <= g1hi)) {
-      const int slot = atomicAdd(&sm.nbuf, 1);
-      if (slot < kFCap) sm.buf[slot] = pack_cand(f2key(v), (uint32_t)e);
-    }
-  };
-  auto scan = [&](const f32x4 (&t)[U], int c) {
+  // four logits per lane, without a branch per logit: the wave appends all
+  // of a float4's gathered logits with one LDS atomic
+  // (one ballot per comparison, combined as scalar masks: a ballot of a
+  // combined condition costs two more vector instructions per logit)
+  auto gather4 = [&](const f32x4 &t, int e, bool valid) {
+    const unsigned long long mv = __builtin_amdgcn_ballot_w64(valid);
+    unsigned long long m[4];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = c * U * kFT + u * kFT + tid;
-      if (i < nfull) {
-        gather(t[u][0], 4 * i); gather(t[u][1], 4 * i + 1); gather(t[u][2], 4 * i + 2);
-        gather(t[u][3], 4 * i + 3);
+    for (int c = 0; c < 4; ++c) {
+      const float v = t[c];
+      const float q = fast_q(v, cz, m0cz);
+      const bool le = v <= m0;
+      below0 += (valid & le & (q < fb0)) ? 1u : 0u;
+      const unsigned long long ok = mv & __builtin_amdgcn_ballot_w64(le);
+      m[c] = ok & ((__builtin_amdgcn_ballot_w64(q >= fb0) & __builtin_amdgcn_ballot_w64(q < fh0)) |
+                   (__builtin_amdgcn_ballot_w64(q >= fb1) & __builtin_amdgcn_ballot_w64(q < fh1)));
+    }
+    asm volatile("" : "+v"(below0));   // (counted here, not after the append below)
+    if (__builtin_expect((m[0] | m[1] | m[2] | m[3]) != 0ull, 0)) {
+      const int n0 = __popcll(m[0]), n1 = __popcll(m[1]), n2 = __popcll(m[2]);
+      int base = 0;
+      if (lane_id() == 0) base = atomicAdd(&sm.nbuf, n0 + n1 + n2 + __popcll(m[3]));
+      base = __builtin_amdgcn_readfirstlane(base);
+      const int off[4] = {base, base + n0, base + n0 + n1, base + n0 + n1 + n2};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if ((m[c] >> lane_id()) & 1ull) {
+          const int slot = off[c] + (int)lanes_below(m[c]);
+          if (slot < kFCap) sm.buf[slot] = pack_cand(f2key(t[c]), (uint32_t)(e + c));
+        }
       }
     }
   };
-  for (int c = 0; c < iters; c += 2) {
-    scan(A, c);
-    load(A, c + 2, nontemporal{});
-    scan(B, c + 1);
-    load(B, c + 3, nontemporal{});
+  auto scan = [&](const f32x4 (&t)[U], int n) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = n * kUnit + u * 64 + lane;
+      gather4(t[u], 4 * i, i < nfull);
+    }
+  };
+  {
+    int ua = wave, ub = kW + wave, nx = grab(&sm.next2);
+    for (;;) {
+      scan(A, ua);
+      ua = __builtin_amdgcn_readfirstlane(nx);
+      nx = grab(&sm.next2);
+      load(A, ua, nontemporal{});
+      scan(B, ub);
+      ub = __builtin_amdgcn_readfirstlane(nx);
+      nx = grab(&sm.next2);
+      load(B, ub, nontemporal{});
+      if (ua >= nunits) break;
+    }
   }
-  if (tid < (V & 3)) gather(vt, 4 * nfull + tid);
+  gather4(f32x4{vt, -INFINITY, -INFINITY, -INFINITY}, 4 * nfull + tid, tid < (V & 3));
   const uint32_t below = fast_block_sum(below0, reinterpret_cast<uint32_t *>(sm.ured));
   const int ng = sm.nbuf;
   const int nl = ng + ntop;
