@@ -2392,31 +2392,42 @@ __device__ __forceinline__ void append_keys(const uint32_t (&kk)[NV][4], int fb,
 }
 
 // append_rd that also counts every appended logit; returns the largest key
-// appended.
+// appended.  The round's logits >= xf go to the segment as they pass (their
+// value bits in place of the key); the keys, the bins and the maximum are
+// then computed over the entries the round appended with every lane busy,
+// where a row of many candidates would otherwise run that work per
+// component with one or two lanes active.  (Entries past kSegCap are not
+// counted: the counts stay lower bounds, and such a segment loses the row.)
 template <int NV>
 __device__ __forceinline__ uint32_t append_hist_rd(const float (&v)[NV][4], int fb, int tid, float xf,
                                                    unsigned long long *seg, int &cnt,
                                                    uint32_t *hist) {
-  uint32_t m = 0;
+  const int c0 = cnt;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const float mx = fmaxf(fmaxf(v[j][0], v[j][1]), fmaxf(v[j][2], v[j][3]));
-    if (!__ballot(mx >= xf)) continue;
+    if (!__builtin_amdgcn_ballot_w64(mx >= xf)) continue;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const bool pass = v[j][q] >= xf;
-      const unsigned long long b = __ballot(pass);
+      const unsigned long long b = __builtin_amdgcn_ballot_w64(v[j][q] >= xf);
       if (b) {
         const int p = cnt + (int)lanes_below(b);
-        if (pass) {
-          const uint32_t key = f2key(v[j][q]);
-          if (p < kSegCap) seg[p] = pack_cand(key, (uint32_t)(slot_elem(fb, tid, j) + q));
-          atomicAdd(&hist[key >> kMidShift], 1u);
-          m = key > m ? key : m;
-        }
+        if (v[j][q] >= xf && p < kSegCap)
+          seg[p] = ((unsigned long long)__float_as_uint(v[j][q]) << 32) |
+                   (uint32_t)pack_cand(0u, (uint32_t)(slot_elem(fb, tid, j) + q));
         cnt = uniform_i32(cnt + __popcll(b));
       }
     }
+  }
+  // (a wave's LDS operations take effect in issue order)
+  uint32_t m = 0;
+  const int c1 = cnt < kSegCap ? cnt : kSegCap;
+  for (int i = c0 + lane_id(); i < c1; i += 64) {
+    const unsigned long long e = seg[i];
+    const uint32_t key = f2key(__uint_as_float((uint32_t)(e >> 32)));
+    seg[i] = ((unsigned long long)key << 32) | (uint32_t)e;
+    atomicAdd(&hist[key >> kMidShift], 1u);
+    m = key > m ? key : m;
   }
   return m;
 }
