@@ -4059,9 +4059,9 @@ __global__ __launch_bounds__(kLT) void large_replay_kernel(LaunchArgs a, Workspa
 // candidate outputs: the common form of "top-p only" sampling.  Two passes
 // over the row instead of the general path's four to six:
 //
-//  1. (HBM) m0 = the maximum of the first 32768 logits.  Every candidate
+//  1. (HBM) m0 = the maximum of the first 16384 logits.  Every candidate
 //     v <= m0 adds w = 2^(q * -log2(e) / 256) to bucket floor(q) of an LDS
-//     histogram (binary64 sums), q = (m0 - v) * 256 / T in binary32 (one
+//     histogram (64-bit fixed-point sums), q = (m0 - v) * 256 / T in binary32 (one
 //     fma, shared by the bucket and the weight); the few v > m0 go to a list
 //     of their own.  m = max(m0, list), S = e^((m0 - m)/T) * sum + the
 //     list's exp((v - m)/T).
@@ -4654,6 +4654,22 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
         m0cz < INFINITY))
     return false;   // (uniform: every thread read the same values)
   const float kq = -1.4426950408889634f / kFBScale;   // w = 2^(q kq) = e^((v - m0) / T)
+  // The buckets sum w in fixed point, floor(w 2^sx) as 64-bit integers: LDS
+  // adds of 64-bit integers run far faster than binary64 ones (the pass took
+  // 28 us per row with binary64 adds).  w <= 1 (up to a rounding of q below
+  // 0) and V < 2^nb, so sx = 63 - nb keeps every sum below 2^64; each weight
+  // loses less than 2^-sx, which the margins below add.
+  const int nbits = 32 - __clz(V);
+  const int sx = 63 - nbits;
+  const float sc_hi = __builtin_ldexpf(1.0f, sx - 32), sc_all = __builtin_ldexpf(1.0f, sx);
+  // floor(w 2^sx): the high word floor(w 2^(sx-32)), the low word the rest
+  // (both exact in binary32: w has 24 significant bits)
+  auto fixw = [&](float w) {
+    const float hf = floorf(w * sc_hi);
+    const uint32_t lo = (uint32_t)fmaf(hf, -4294967296.0f, w * sc_all);
+    return ((unsigned long long)(uint32_t)hf << 32) | lo;
+  };
+  unsigned long long *massx = reinterpret_cast<unsigned long long *>(sm.mass);
 
   // Per logit, without a branch: every one adds to some bucket (0 for those
   // that do not belong: NaN, -Infinity, and the rare v > m0, which go to
@@ -4678,7 +4694,7 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
       nf += cand ? 1u : 0u;
       const float q = fast_q(v, cz, m0cz);
       const float w = __builtin_amdgcn_exp2f(q * kq);
-      atomicAdd(&sm.mass[fast_bucket_q(q)], (double)(cand && !(v > m0) ? w : 0.0f));
+      atomicAdd(&massx[fast_bucket_q(q)], fixw(cand && !(v > m0) ? w : 0.0f));
     }
   };
   auto process = [&](const f32x4 (&t)[U], int n) {
@@ -4716,7 +4732,7 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
         if (slot < kFTop) sm.top[slot] = pack_cand(f2key(v), (uint32_t)e);
       } else {
         const float q = fast_q(v, cz, m0cz);
-        atomicAdd(&sm.mass[fast_bucket_q(q)], (double)__builtin_amdgcn_exp2f(q * kq));
+        atomicAdd(&massx[fast_bucket_q(q)], fixw(__builtin_amdgcn_exp2f(q * kq)));
       }
     }
   }
@@ -4743,6 +4759,17 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
     for (int d = 32; d > 0; d >>= 1) st += __shfl_xor(st, d);
     if (tid == 0) { sm.top_m = mdw; sm.top_s = st; }
   }
+  {
+    // the sums back to binary64, each wave over the buckets it owns in
+    // fast_prefix (a wave's LDS operations take effect in issue order)
+    const double unit = __builtin_ldexp(1.0, -sx);
+    constexpr int per = kFB / (kFT / 64);
+#pragma unroll
+    for (int i = 0; i < per / 64; ++i) {
+      const int b = per * wave + 64 * i + lane;
+      sm.mass[b] = (double)massx[b] * unit;
+    }
+  }
   fast_prefix(sm);   // (its barriers publish top_m, top_s)
   const float m = (float)sm.top_m;
   const double md = (double)m;
@@ -4756,12 +4783,14 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
 
   // 3. the bucket ranges of the top-p crossing and of the draw
   const double tp = P.top_p;
-  const int b1lo = fast_first_reaching(tp - kFEps, top_total, scale, sm);
-  const int b1hi = fast_first_reaching(tp + kFEps, top_total, scale, sm);
+  // (the fixed point's loss, n_f 2^-sx, bounds its error in probability: S >= 1)
+  const double eps = kFEps + (double)n_f * __builtin_ldexp(1.0, -sx);
+  const int b1lo = fast_first_reaching(tp - eps, top_total, scale, sm);
+  const int b1hi = fast_first_reaching(tp + eps, top_total, scale, sm);
   if (!(tp == tp) || b1hi >= kFB - 1) return false;   // no crossing, or in the clamped tail
-  const double k_hi = fast_start(b1hi + 1, top_total, scale, sm) + kFEps;
-  const double r_lo = u * (tp > 0.0 ? tp : 0.0) - 2 * kFEps;
-  const double r_hi = u * k_hi + kFEps;
+  const double k_hi = fast_start(b1hi + 1, top_total, scale, sm) + eps;
+  const double r_lo = u * (tp > 0.0 ? tp : 0.0) - 2 * eps;
+  const double r_hi = u * k_hi + eps;
   if (!(r_lo == r_lo) || !(r_hi == r_hi)) return false;
   int b2lo = fast_first_reaching(r_lo, top_total, scale, sm);
   int b2hi = fast_first_reaching(r_hi, top_total, scale, sm);
