@@ -23,7 +23,8 @@
 // rows handed back [kMaxRows] | slot-replay requests [kMaxRows] | split-row
 // hand-over lists
 // [kSplitCUs][kPartCap] | their meta data [kSplitCUs] | the split rows'
-// arrival counters [kSplitCUs] (zero between calls).
+// arrival counters [kSplitCUs] (zero between calls) | one region of the
+// device-memory slot replay: keys [kRowMaxVocab], ids [kRowMaxVocab].
 namespace na {
 constexpr int kMaxRows = 2048;
 constexpr size_t kPlansOff = 0;
@@ -40,11 +41,14 @@ constexpr size_t kSplitMetaOff = kSplitListOff + kSplitListBytes;
 constexpr size_t kSplitMetaBytes = sizeof(hs::SplitMeta) * hs::kSplitCUs;
 constexpr size_t kSplitCntOff = kSplitMetaOff + kSplitMetaBytes;
 constexpr size_t kSplitCntBytes = sizeof(uint32_t) * hs::kSplitCUs;
-constexpr size_t kBytes = kSplitCntOff + kSplitCntBytes;
+constexpr size_t kRKeysOff = (kSplitCntOff + kSplitCntBytes + 255) / 256 * 256;
+constexpr size_t kRSlotBytes = sizeof(uint32_t) * hs::kRowMaxVocab;
+constexpr size_t kRIdsOff = kRKeysOff + kRSlotBytes;
+constexpr size_t kBytes = kRIdsOff + kRSlotBytes;
 static_assert(kListsOff % 256 == 0 && kRetryOff % 256 == 0 && kReplayOff % 256 == 0 &&
                   kSplitListOff % 256 == 0 &&
                   kSplitMetaOff % 256 == 0 &&
-                  kSplitCntOff % 256 == 0,
+                  kSplitCntOff % 256 == 0 && kRKeysOff % 256 == 0 && kRIdsOff % 256 == 0,
               "scratch layout alignment");
 constexpr int kMaxDevices = 64;
 }  // namespace na
@@ -143,6 +147,7 @@ struct hs_context {
   bool fuse = true;             // HS_LMHEAD_FUSE=0 at creation: always two launches
   DevBuf large_retry;           // two-pass large-k rows handed back
   DevBuf large_replay;          // slot-history replays asked for by the large-k kernel
+  DevBuf replay_slots;          // the device-memory replay's regions: keys, then ids
   int64_t cand_count_rows = 0;     // rows whose counter is known to be zero
   // plan upload cache
   std::vector<hs::RowPlan> last_plans;
@@ -179,7 +184,8 @@ struct hs_context {
   bool na_pending = false;
   hs_sample_config *na_last = nullptr;
   int na_rows = -1, na_vocab = -1;
-  int na_count[5] = {0, 0, 0, 0, 0};   // pf, row, large, mid, two-pass large
+  int na_count[6] = {0, 0, 0, 0, 0, 0};   // pf, row, large, mid, two-pass large; and
+                                           //   whether a large row has k > kReplayMaxK
   uint64_t na_gen = 0;
 };
 
@@ -492,6 +498,18 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   }
   if (n_lfast > 0) HS_HIP(ctx->large_retry.ensure(sizeof(int32_t) * (size_t)n_lfast));
   if (n_large > 0) HS_HIP(ctx->large_replay.ensure(sizeof(hs::ReplayReq) * (size_t)n_large));
+  // a large-k row whose slots exceed the LDS replay's, or candidate outputs
+  // longer than it orders, may need the device-memory replay: one region of
+  // vocab keys and vocab ids per workgroup of it
+  int replay_dev = 0;
+  {
+    bool big = (d_cand_ids || d_cand_probs) && cand_stride > hs::kReplayCands;
+    for (int32_t r : rt.large) big |= plans[(size_t)r].k > hs::kReplayMaxK;
+    if (big && n_large > 0) {
+      replay_dev = std::min(n_large, hs::kReplayDevBlocks);
+      HS_HIP(ctx->replay_slots.ensure((size_t)replay_dev * (size_t)vocab * 8));
+    }
+  }
   // small batches split each row of the row kernel over several workgroups
   const int split = choose_split(ctx, n_row, vocab);
   int rc = ensure_split(ctx, n_row, split, stream);
@@ -510,6 +528,10 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   ws.lfast_list = lists + n_pf + n_row + n_chunk + n_large + n_mid;
   ws.large_retry = static_cast<int32_t *>(ctx->large_retry.p);
   ws.large_replay = static_cast<hs::ReplayReq *>(ctx->large_replay.p);
+  if (replay_dev > 0) {
+    ws.replay_keys = static_cast<uint32_t *>(ctx->replay_slots.p);
+    ws.replay_ids = reinterpret_cast<int32_t *>(ws.replay_keys + (size_t)replay_dev * vocab);
+  }
   ws.cand = static_cast<uint2 *>(ctx->cand.p);
   ws.cand_count = static_cast<int32_t *>(ctx->cand_count.p);
   ws.info = static_cast<hs::ChunkInfo *>(ctx->info.p);
@@ -531,6 +553,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   a.n_large = n_large;
   a.n_mid = n_mid;
   a.n_lfast = n_lfast;
+  a.replay_dev = replay_dev;
   a.hist_ids = d_hist_ids;
   a.hist_off = d_hist_offsets;
   a.hist_len = d_hist_len;
@@ -750,17 +773,19 @@ int gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const
 
 // Plans and routing lists written into fixed arrays (no allocation): the
 // lists pf | row | large | mid | two-pass large back to back, in row order,
-// their lengths in n[0..4].  Routing as build_plans with every row on the one-pass kernels
-// (vocab <= kRowMaxVocab): rows with k <= 64 join the mid kernel's launch
-// when it has rows.
+// their lengths in n[0..4], and in n[5] whether a row of the large list has
+// more slots than the LDS replay holds.  Routing as build_plans with every
+// row on the one-pass kernels (vocab <= kRowMaxVocab): rows with k <= 64
+// join the mid kernel's launch when it has rows.
 void build_plans_fixed(const hs_sample_config *cfgs, int rows, int vocab, hs::RowPlan *plans,
-                       int32_t *lists, int n[5]) {
-  int n_pf = 0, n_row = 0, n_large = 0, n_mid = 0, n_small = 0, n_lfast = 0;
+                       int32_t *lists, int n[6]) {
+  int n_pf = 0, n_row = 0, n_large = 0, n_mid = 0, n_small = 0, n_lfast = 0, big = 0;
   for (int r = 0; r < rows; ++r) {
     const hs::RowPlan p = plan_row(cfgs[r], vocab);
     plans[r] = p;
     n_lfast += two_pass_large(p, vocab);
     n_large += p.mode == hs::kModeLarge && !two_pass_large(p, vocab);
+    big |= p.mode == hs::kModeLarge && !two_pass_large(p, vocab) && p.k > hs::kReplayMaxK;
     n_mid += p.mode == hs::kModeGeneric;
     n_row += p.mode == hs::kModeGreedy || p.mode == hs::kModeSmall;
     n_small += p.mode == hs::kModeSmall;
@@ -789,6 +814,7 @@ void build_plans_fixed(const hs_sample_config *cfgs, int rows, int vocab, hs::Ro
   n[2] = n_large;
   n[3] = n_mid;
   n[4] = n_lfast;
+  n[5] = big;
 }
 
 // hs_sample_batch_device with the device's `scratch` array as its workspace:
@@ -815,6 +841,13 @@ int sample_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows, int64_
       !ctx->na_staging || !ctx->na_last)
     return fail(HS_ERR_UNSUPPORTED, "no scratch workspace on device %d", ctx->device);
   DeviceGuard guard(ctx->device);
+  // The call blocks on its last upload's event when the configs change and
+  // reads plans from the shared scratch that later calls rewrite: it cannot
+  // be captured into a graph.  Checked before anything is enqueued.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HS_HIP(hipStreamIsCapturing(stream, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(HS_ERR_UNSUPPORTED, "the no-allocation entry point cannot be captured into a graph");
   int rc = enter_stream(ctx, stream);
   if (rc) return rc;
   if (vocab <= 0) {   // src/sampler.ts: no logit is read; every path returns 0
@@ -835,17 +868,35 @@ int sample_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows, int64_
       HS_HIP(hipEventSynchronize(ctx->na_upload_ev));
       ctx->na_pending = false;
     }
+    // Invalidate first: once the scratch may hold new plans, no context
+    // (this one included) may take the `same` path on its old bookkeeping,
+    // even if a copy below fails.
+    ++gen;
+    ctx->na_gen = ~0ull;
+    ctx->na_rows = -1;
     char *st = static_cast<char *>(ctx->na_staging);
     hs::RowPlan *plans = reinterpret_cast<hs::RowPlan *>(st);
     int32_t *lists = reinterpret_cast<int32_t *>(st + na::kPlansBytes);
     build_plans_fixed(configs, rows, vocab, plans, lists, ctx->na_count);
     const int nl = ctx->na_count[0] + ctx->na_count[1] + ctx->na_count[2] + ctx->na_count[3] +
                    ctx->na_count[4];
-    HS_HIP(hipMemcpyAsync(base + na::kPlansOff, plans, sizeof(hs::RowPlan) * (size_t)rows,
-                          hipMemcpyHostToDevice, stream));
-    HS_HIP(hipMemcpyAsync(base + na::kListsOff, lists, sizeof(int32_t) * (size_t)nl,
-                          hipMemcpyHostToDevice, stream));
-    HS_HIP(hipEventRecord(ctx->na_upload_ev, stream));
+    // a failure after the first copy was issued waits for the stream, so
+    // that no copy still reads the staging when the next call refills it
+    hipError_t ue = inject_failure() ? hipErrorOutOfMemory
+                                     : hipMemcpyAsync(base + na::kPlansOff, plans,
+                                                      sizeof(hs::RowPlan) * (size_t)rows,
+                                                      hipMemcpyHostToDevice, stream);
+    if (ue != hipSuccess)
+      return fail(HS_ERR_HIP, "hipMemcpyAsync(plans) failed: %s", hipGetErrorString(ue));
+    ue = inject_failure() ? hipErrorOutOfMemory
+                          : hipMemcpyAsync(base + na::kListsOff, lists, sizeof(int32_t) * (size_t)nl,
+                                           hipMemcpyHostToDevice, stream);
+    if (ue == hipSuccess)
+      ue = inject_failure() ? hipErrorOutOfMemory : hipEventRecord(ctx->na_upload_ev, stream);
+    if (ue != hipSuccess) {
+      (void)hipStreamSynchronize(stream);
+      return fail(HS_ERR_HIP, "plan upload failed: %s", hipGetErrorString(ue));
+    }
     ctx->na_pending = true;
     memcpy(ctx->na_last, configs, cbytes);
     ctx->na_rows = rows;
@@ -854,6 +905,7 @@ int sample_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows, int64_
   }
   const int n_pf = ctx->na_count[0], n_row = ctx->na_count[1], n_large = ctx->na_count[2],
             n_mid = ctx->na_count[3], n_lfast = ctx->na_count[4];
+  const int replay_dev = n_large > 0 && ctx->na_count[5] ? 1 : 0;
   // small batches split each row of the row kernel (at most kSplitCUs parts)
   int split = choose_split(ctx, n_row, vocab);
   while (split > 1 && (int64_t)n_row * split > hs::kSplitCUs) --split;
@@ -873,6 +925,8 @@ int sample_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows, int64_
   ws.split_list = reinterpret_cast<unsigned long long *>(base + na::kSplitListOff);
   ws.split_meta = reinterpret_cast<hs::SplitMeta *>(base + na::kSplitMetaOff);
   ws.split_cnt = reinterpret_cast<uint32_t *>(base + na::kSplitCntOff);
+  ws.replay_keys = reinterpret_cast<uint32_t *>(base + na::kRKeysOff);
+  ws.replay_ids = reinterpret_cast<int32_t *>(base + na::kRIdsOff);
 
   hs::LaunchArgs a;
   memset(&a, 0, sizeof a);
@@ -889,6 +943,7 @@ int sample_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows, int64_
   a.n_large = n_large;
   a.n_mid = n_mid;
   a.n_lfast = n_lfast;
+  a.replay_dev = replay_dev;
   a.hist_ids = d_hist_ids;
   a.hist_off = d_hist_offsets;
   a.uniforms = d_uniforms;
@@ -1031,6 +1086,7 @@ int hs_context_destroy(hs_context *ctx) {
     ctx->gemv_rot.release();
     ctx->large_retry.release();
     ctx->large_replay.release();
+    ctx->replay_slots.release();
     ctx->h_logits.release();
     ctx->h_hist.release();
     ctx->h_off.release();
@@ -1412,7 +1468,7 @@ int hs_sample_logits_batch(hs_context *ctx, float *logits, int32_t rows, int64_t
       return fail(HS_ERR_UNSUPPORTED,
                   "row %d: top-k above %d with equal logits at the drawn position; the "
                   "reference orders them by its slot history, which this build replays up to "
-                  "that top-k only", r, hs::kReplayMaxK);
+                  "that top-k only", r, hs::kReplayDevMaxK);
   return HS_OK;
 }
 

@@ -101,17 +101,28 @@ struct SplitMeta {
 };
 static_assert(sizeof(SplitMeta) == 24, "SplitMeta layout");
 
-// What a large-k row leaves for large_replay_kernel when equal values make
+// What a large-k row leaves for the slot replays when equal values make
 // its order depend on the reference's slot history (k < the finite count).
 struct ReplayReq {
-  int32_t need;              // bit 0: the token; bit 1: the candidate ids
+  int32_t need;              // bit 0: the token; bit 1: the candidate ids;
+                             //   bit 2 (kReplayDev): slots in device memory
   uint32_t xkey;             // the drawn value's key
   int32_t pos;               // the drawn position (value descending)
   int32_t mo;                // candidate positions to write
+  uint32_t ckey;             // key at candidate position mo - 1
+  int32_t pad;
 };
-static_assert(sizeof(ReplayReq) == 16, "ReplayReq layout");
-constexpr int kReplayMaxK = 16384;     // slots the replay holds in LDS
+static_assert(sizeof(ReplayReq) == 24, "ReplayReq layout");
+constexpr int kReplayMaxK = 16384;     // slots the LDS replay holds
 constexpr int kReplayCands = 1024;     // candidate positions it can order
+// The replay with its slots in device memory (large_replay_dev_kernel): any
+// k up to kReplayDevMaxK, kReplayDevCands candidate positions, at most
+// kReplayDevBlocks workgroups, each with its own region of vocab keys and
+// vocab ids in the workspace.
+constexpr int kReplayDev = 4;
+constexpr int kReplayDevMaxK = 1 << 19;
+constexpr int kReplayDevCands = 8192;
+constexpr int kReplayDevBlocks = 16;
 
 struct Workspace {
   RowPlan *plans;            // [rows]
@@ -123,6 +134,8 @@ struct Workspace {
   const int32_t *lfast_list; // rows of the two-pass large-k kernel (k = vocab, no min-p)
   int32_t *large_retry;      // [n_lfast] 1: the two-pass kernel handed the row back
   ReplayReq *large_replay;   // [n_large] slot-history replays asked for by large_row
+  uint32_t *replay_keys;     // [replay_dev][vocab] slots of the device-memory replay
+  int32_t *replay_ids;       // [replay_dev][vocab]
   uint2 *cand;               // [n_chunk][S][kChunkCap] (key, index)
   int32_t *cand_count;       // [n_chunk]
   ChunkInfo *info;           // [n_chunk][S]
@@ -144,6 +157,7 @@ struct LaunchArgs {
   int32_t n_lfast;           // rows of the two-pass large-k kernel
   int32_t n_argmax;          // rows of the GPU greedy route (a call of its own)
   int32_t split;             // row / argmax kernel: workgroups per row (1: whole rows)
+  int32_t replay_dev;        // workgroups of the device-memory slot replay (0: not launched)
   const int32_t *hist_ids;
   const int64_t *hist_off;   // packed lists: row r is hist_ids[off[r], off[r+1])
   const int64_t *hist_len;   // rings (hist_cap > 0): row r is hist_ids[r * cap, +cap),
@@ -169,15 +183,16 @@ struct LaunchArgs {
 // ev[2i] and ev[2i + 1] receive the start and end of kernel i's dispatch
 // (0 penalty pre-pass, 1 row kernel, 2 chunk kernel, 3 finalize, 4 large-k
 // kernel, 5 mid kernel, 6 GPU greedy-route argmax, 8 two-pass large-k kernel,
-// 9 the large-k slot replay;
+// 9 the large-k slot replay, 10 the device-memory slot replay;
 // 7 is the lm_head GEMV, launched apart), for the kernels that launch only:
 // launched_kernels() says which.  The large-k kernel launches whenever a row
 // has k > 1024: it also takes the rows the two-pass kernel hands back.
-constexpr int kTimedKernels = 10;
+constexpr int kTimedKernels = 11;
 inline unsigned launched_kernels(const LaunchArgs &a) {
   return (a.n_pf > 0 ? 1u : 0u) | (a.n_row > 0 ? 2u : 0u) | (a.n_chunk > 0 ? 12u : 0u) |
          (a.n_large + a.n_lfast > 0 ? 16u : 0u) | (a.n_mid > 0 ? 32u : 0u) |
-         (a.n_argmax > 0 ? 64u : 0u) | (a.n_lfast > 0 ? 256u : 0u) | (a.n_large > 0 ? 512u : 0u);
+         (a.n_argmax > 0 ? 64u : 0u) | (a.n_lfast > 0 ? 256u : 0u) | (a.n_large > 0 ? 512u : 0u) |
+         (a.n_large > 0 && a.replay_dev > 0 ? 1024u : 0u);
 }
 // Largest vocabulary of the GPU greedy route (byte offsets of a row stay
 // below 2^31).

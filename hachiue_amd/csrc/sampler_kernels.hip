@@ -3597,8 +3597,11 @@ __device__ __forceinline__ LargeLoc large_locate(const LargeRow &L, int mode, do
 // The general large-k path for one row: any k > 1024, min-p, candidate
 // outputs, and the rows the two-pass path below hands back.
 // With k below the finite count, an equal-value group whose order decides
-// the token or the candidate list is left to large_replay_kernel through
-// *req (k <= kReplayMaxK); beyond that the row reports HS_ROW_UNSUPPORTED.
+// the token or the candidate list is left to a slot replay through *req:
+// large_replay_kernel (slots in LDS) for k <= kReplayMaxK and at most
+// kReplayCands candidate positions, large_replay_dev_kernel (slots in device
+// memory) up to k = kReplayDevMaxK and kReplayDevCands positions; beyond
+// those the row reports HS_ROW_UNSUPPORTED.
 __device__ __forceinline__ void large_row(const LaunchArgs &a, const RowPlan &P, int row,
                                           LargeSmem &sm, ReplayReq *req) {
   const int tid = threadIdx.x;
@@ -3764,10 +3767,11 @@ __device__ __forceinline__ void large_row(const LaunchArgs &a, const RowPlan &P,
     lpick = large_locate(L, kByPos, 0.0, 0u, sm);
   }
   const bool ambiguous = L.T != 0u && lpick.tie;   // slot history orders equal values
-  const bool replay = ambiguous && k <= kReplayMaxK;
+  const bool replay = ambiguous && k <= kReplayDevMaxK;
   uint32_t flags = HS_ROW_LARGE;
   if (ambiguous) flags |= HS_ROW_TIES | (replay ? HS_ROW_REPLAYED : HS_ROW_UNSUPPORTED);
   int need = replay ? 1 : 0, need_mo = 0;
+  uint32_t need_ckey = 0;
   if (tid == 0) {
     if (!replay) put_token(a, row, ambiguous ? -1 : lpick.id);
     if (a.cand_count_out) a.cand_count_out[row] = n;
@@ -3820,20 +3824,25 @@ __device__ __forceinline__ void large_row(const LaunchArgs &a, const RowPlan &P,
     }
     if (rest > 1 || (kend == L.T && L.teq > L.tin)) tie = 1;
     if (__syncthreads_or(tie) && L.T) {
-      if (k <= kReplayMaxK && mo <= kReplayCands && !too_long) {
+      if (k <= kReplayDevMaxK && mo <= kReplayDevCands && !too_long) {
         need |= 2;
         need_mo = mo;
+        need_ckey = kend;
         flags |= HS_ROW_TIES | HS_ROW_REPLAYED;
       } else {
         flags |= HS_ROW_UNSUPPORTED | HS_ROW_TIES;
       }
     }
   }
+  // slots beyond the LDS replay's, or more positions than it orders: the
+  // device-memory replay
+  if (need && (k > kReplayMaxK || need_mo > kReplayCands)) need |= kReplayDev;
   if (tid == 0) {
     if (a.row_flags) a.row_flags[row] = flags;
     req->xkey = lpick.key;
     req->pos = lpick.pos;
     req->mo = need_mo;
+    req->ckey = need_ckey;
     req->need = need;
   }
 }
@@ -3885,7 +3894,7 @@ __global__ __launch_bounds__(kLT) void large_replay_kernel(LaunchArgs a, Workspa
   extern __shared__ unsigned long long rdyn[];
   ReplaySmem &sm = *reinterpret_cast<ReplaySmem *>(rdyn);
   const ReplayReq req = ws.large_replay[blockIdx.x];
-  if (!req.need) return;
+  if (!req.need || (req.need & kReplayDev)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int row = ws.large_list[blockIdx.x];
   const int k = ws.plans[row].k;
@@ -4049,6 +4058,234 @@ __global__ __launch_bounds__(kLT) void large_replay_kernel(LaunchArgs a, Workspa
     const int cs = a.cand_stride;
     for (int i = tid; i < mo; i += kLT)
       a.cand_ids[(int64_t)row * cs + i] = sm.ids[cand_idx(sm.queue[i])];
+  }
+}
+
+// ---------------------------------------------------------------- large-k slot replay, slots in device memory
+
+// The same replay of src/sampler.ts:50-69 for the rows whose k slots do not
+// fit in LDS (k > kReplayMaxK, up to kReplayDevMaxK), or whose candidate
+// outputs need more ordered positions than the LDS replay takes.  The slots'
+// keys and ids live in the workgroup's region of the workspace; the min tree
+// above them (lvl1 over 64 slots, lvl2 over 64 lvl1 entries, a root over at
+// most 128 lvl2 entries) stays in LDS.  The lane that writes a slot is the
+// lane that reads it back (slot & 63), so every read of a slot written
+// during the replay is ordered after that write by the thread's own program
+// order.  The grid holds at most kReplayDevBlocks workgroups, each taking
+// the requesting rows whose rank among them is its index modulo the grid,
+// one after the other: the workspace needs one region per workgroup, not
+// one per row.
+struct ReplayDevSmem {
+  unsigned long long lvl1[kReplayDevMaxK / 64];
+  unsigned long long lvl2[kReplayDevMaxK / 4096];
+  unsigned long long buf[kReplayDevCands];   // the chunk's entering logits, then the sort
+  int32_t rows[kLT];                         // this workgroup's rows of a list chunk
+  uint32_t wsum[kLT / 64];
+  int32_t fill_end, res;
+  unsigned long long root;
+};
+size_t replay_dev_smem_bytes() { return sizeof(ReplayDevSmem); }
+
+__device__ void replay_dev_row(const LaunchArgs &a, const Workspace &ws, const ReplayReq &req,
+                               int row, uint32_t *keys, int32_t *ids, ReplayDevSmem &sm) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int k = ws.plans[row].k;
+  const float *rowp = a.logits + (int64_t)row * a.stride;
+  const int V = a.vocab;
+  constexpr unsigned long long kNone = ~0ull;
+  auto scan = [&](uint32_t x, uint32_t &total) {
+    const uint32_t incl = block_scan_incl<kLT>(x, sm.wsum);
+    uint32_t t = 0;
+    for (int w = 0; w < kLT / 64; ++w) t += sm.wsum[w];
+    total = t;
+    __syncthreads();   // before wsum is used again
+    return incl;
+  };
+
+  // 1. the first k finite logits fill slots 0..k-1 in index order: thread t
+  // counts the finite logits of its span, a block prefix gives its first slot
+  if (tid == 0) sm.fill_end = V;
+  const int span = (V + kLT - 1) / kLT;
+  const int e0 = min(V, tid * span), e1 = min(V, e0 + span);
+  uint32_t nfin = 0;
+  for (int e = e0; e < e1; ++e) nfin += f2key(rowp[e]) != 0u;
+  uint32_t total;
+  uint32_t slot = scan(nfin, total) - nfin;
+  for (int e = e0; e < e1 && slot < (uint32_t)k; ++e) {
+    const uint32_t key = f2key(rowp[e]);
+    if (key) {
+      keys[slot] = key;
+      ids[slot] = e;
+      if (slot == (uint32_t)k - 1) sm.fill_end = e + 1;
+      ++slot;
+    }
+  }
+  const int filled = total < (uint32_t)k ? (int)total : k;
+  for (int s = filled + tid; s < k; s += kLT) { keys[s] = 0u; ids[s] = -1; }
+  __syncthreads();
+  const int nl1 = (k + 63) >> 6, nl2 = (nl1 + 63) >> 6;   // nl2 <= 128
+  for (int b = wave; b < nl1; b += kLT / 64) {
+    const int sl = 64 * b + lane;
+    const unsigned long long m = wave_min64(sl < k ? slot_pack(keys[sl], (uint32_t)sl) : kNone);
+    if (lane == 0) sm.lvl1[b] = m;
+  }
+  __syncthreads();
+  for (int c = wave; c < nl2; c += kLT / 64) {
+    const int i = 64 * c + lane;
+    const unsigned long long m = wave_min64(i < nl1 ? sm.lvl1[i] : kNone);
+    if (lane == 0) sm.lvl2[c] = m;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const unsigned long long x0 = lane < nl2 ? sm.lvl2[lane] : kNone;
+    const unsigned long long x1 = lane + 64 < nl2 ? sm.lvl2[lane + 64] : kNone;
+    const unsigned long long m = wave_min64(x0 < x1 ? x0 : x1);
+    if (lane == 0) sm.root = m;
+  }
+  __syncthreads();
+
+  // 2. the rest of the row, in index order: the logits above the chunk's
+  // starting minimum queue up, and wave 0 takes them one by one
+  const int start = sm.fill_end;
+  for (int base = start; base < V; base += kLT) {
+    const uint32_t lo = (uint32_t)(sm.root >> 32);
+    const int e = base + tid;
+    const uint32_t key = e < V ? f2key(rowp[e]) : 0u;
+    const bool enter = key > lo;
+    const uint32_t incl = scan(enter ? 1u : 0u, total);
+    if (enter) sm.buf[incl - 1] = slot_pack(key, (uint32_t)e);
+    const int nq = (int)total;
+    __syncthreads();
+    if (wave == 0) {
+      unsigned long long top = sm.root;
+      for (int q = 0; q < nq; ++q) {
+        const unsigned long long item = sm.buf[q];
+        const uint32_t kv = (uint32_t)(item >> 32);
+        if (kv <= (uint32_t)(top >> 32)) continue;   // not above the current minimum
+        const int s = (int)(uint32_t)top;
+        const int b1 = s >> 6, sl = 64 * b1 + lane;
+        if (sl == s) {
+          keys[s] = kv;
+          ids[s] = (int32_t)(uint32_t)item;
+        }
+        const uint32_t ks = sl == s ? kv : (sl < k ? keys[sl] : 0u);
+        const unsigned long long m1 = wave_min64(sl < k ? slot_pack(ks, (uint32_t)sl) : kNone);
+        const int b2 = b1 >> 6, i1 = 64 * b2 + lane;
+        const unsigned long long m2 =
+            wave_min64(i1 < nl1 ? (i1 == b1 ? m1 : sm.lvl1[i1]) : kNone);
+        const unsigned long long y0 = lane < nl2 ? (lane == b2 ? m2 : sm.lvl2[lane]) : kNone;
+        const unsigned long long y1 =
+            lane + 64 < nl2 ? (lane + 64 == b2 ? m2 : sm.lvl2[lane + 64]) : kNone;
+        const unsigned long long m3 = wave_min64(y0 < y1 ? y0 : y1);
+        if (lane == 0) {
+          sm.lvl1[b1] = m1;
+          sm.lvl2[b2] = m2;
+        }
+        top = m3;
+      }
+      if (lane == 0) sm.root = top;
+    }
+    __syncthreads();
+  }
+
+  // 3. the token: the member of the drawn value at its rank in slot order
+  const int sspan = (k + kLT - 1) / kLT;
+  const int s0 = min(k, tid * sspan), s1 = min(k, s0 + sspan);
+  if (req.need & 1) {
+    uint32_t above = 0, eq = 0;
+    for (int s = s0; s < s1; ++s) {
+      const uint32_t key = keys[s];
+      above += key > req.xkey;
+      eq += key == req.xkey;
+    }
+    uint32_t n_above, n_eq;
+    (void)scan(above, n_above);
+    const uint32_t incl = scan(eq, n_eq);
+    const int j = req.pos - (int)n_above;     // rank in the group
+    if (tid == 0) sm.res = -1;
+    __syncthreads();
+    uint32_t seen = incl - eq;
+    if (j >= 0 && (uint32_t)j >= seen && (uint32_t)j < incl) {
+      for (int s = s0; s < s1; ++s) {
+        if (keys[s] == req.xkey) {
+          if (seen == (uint32_t)j) { sm.res = ids[s]; break; }
+          ++seen;
+        }
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      put_token(a, row, sm.res);
+      if (sm.res < 0 && a.row_flags) a.row_flags[row] |= HS_ROW_UNSUPPORTED;
+    }
+    __syncthreads();
+  }
+
+  // 4. the candidate ids of positions 0..mo-1 (value descending, slot
+  // ascending): the slots above X = the key at position mo - 1, and the
+  // first of those equal to X in slot order, sorted
+  if ((req.need & 2) && a.cand_ids) {
+    const int mo = req.mo;
+    const uint32_t X = req.ckey;   // >= 1: a finite logit's key
+    int P2 = 1;
+    while (P2 < mo) P2 <<= 1;
+    for (int i = tid; i < P2; i += kLT) sm.buf[i] = 0ull;
+    uint32_t gt = 0, eq = 0;
+    for (int s = s0; s < s1; ++s) {
+      const uint32_t key = keys[s];
+      gt += key > X;
+      eq += key == X;
+    }
+    uint32_t n_gt, n_eq;
+    const uint32_t ig = scan(gt, n_gt);   // its barriers order the clearing above
+    const uint32_t ie = scan(eq, n_eq);
+    uint32_t pg = ig - gt, pe = ie - eq;
+    for (int s = s0; s < s1; ++s) {
+      const uint32_t key = keys[s];
+      if (key > X) {
+        if (pg < (uint32_t)mo) sm.buf[pg] = pack_cand(key, (uint32_t)s);
+        ++pg;
+      } else if (key == X) {
+        if (n_gt + pe < (uint32_t)mo) sm.buf[n_gt + pe] = pack_cand(key, (uint32_t)s);
+        ++pe;
+      }
+    }
+    __syncthreads();
+    block_sort_desc<kLT>(sm.buf, P2);
+    const int cs = a.cand_stride;
+    for (int i = tid; i < mo; i += kLT) {
+      const unsigned long long c = sm.buf[i];   // 0: no slot (never, for a consistent request)
+      a.cand_ids[(int64_t)row * cs + i] = c ? ids[cand_idx(c)] : -1;
+    }
+  }
+  __syncthreads();   // the region and LDS are reused by the next row
+}
+
+__global__ __launch_bounds__(kLT) void large_replay_dev_kernel(LaunchArgs a, Workspace ws) {
+  extern __shared__ unsigned long long rdyn[];
+  ReplayDevSmem &sm = *reinterpret_cast<ReplayDevSmem *>(rdyn);
+  const int tid = threadIdx.x, G = (int)gridDim.x, g = (int)blockIdx.x;
+  uint32_t *keys = ws.replay_keys + (int64_t)g * a.vocab;
+  int32_t *ids = ws.replay_ids + (int64_t)g * a.vocab;
+  int seen = 0;   // requesting rows in the list chunks before this one
+  for (int c0 = 0; c0 < a.n_large; c0 += kLT) {
+    const int i = c0 + tid;
+    const bool f = i < a.n_large && (ws.large_replay[i].need & kReplayDev) != 0;
+    const uint32_t incl = block_scan_incl<kLT>(f ? 1u : 0u, sm.wsum);
+    uint32_t total = 0;
+    for (int w = 0; w < kLT / 64; ++w) total += sm.wsum[w];
+    // this workgroup's ranks in the chunk: r = seen + incl - 1 with r % G == g
+    const int r = seen + (int)incl - 1;
+    const int first = seen + ((g - seen % G) + G) % G;   // the first such rank >= seen
+    if (f && r % G == g) sm.rows[(r - first) / G] = i;
+    const int mine = first < seen + (int)total ? (seen + (int)total - 1 - first) / G + 1 : 0;
+    seen += (int)total;
+    __syncthreads();
+    for (int j = 0; j < mine; ++j) {
+      const int li = sm.rows[j];
+      replay_dev_row(a, ws, ws.large_replay[li], ws.large_list[li], keys, ids, sm);
+    }
+    __syncthreads();   // sm.rows and wsum are rewritten by the next chunk
   }
 }
 
@@ -5733,6 +5970,10 @@ hipError_t prepare_kernels() {
                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                (int)replay_smem_bytes())) != hipSuccess)
     return e;
+  if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&large_replay_dev_kernel),
+                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                               (int)replay_dev_smem_bytes())) != hipSuccess)
+    return e;
   return hipFuncSetAttribute(reinterpret_cast<const void *>(&large_kernel),
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)large_smem_bytes());
 }
@@ -5826,7 +6067,8 @@ hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t s
                          hipEvent_t *ev, hipEvent_t done) {
   hipError_t e;
   // the last kernel of the call records `done`
-  const int last = a.n_argmax > 0 ? 6 : a.n_large > 0 ? 9 : a.n_lfast > 0 ? 4
+  const int last = a.n_argmax > 0 ? 6 : a.n_large > 0 && a.replay_dev > 0 ? 10
+                 : a.n_large > 0 ? 9 : a.n_lfast > 0 ? 4
                  : a.n_chunk > 0 ? 3 : a.n_mid > 0 ? 5 : a.n_row > 0 ? 1 : 0;
   auto dn = [&](int slot) { return slot == last ? done : nullptr; };
   if (a.n_pf > 0) {
@@ -5877,6 +6119,11 @@ hipError_t launch_sample(const LaunchArgs &a, const Workspace &ws, hipStream_t s
   if (a.n_large > 0) {   // rows of large_list that asked for the slot replay
     e = launch_one(large_replay_kernel, dim3((unsigned)a.n_large), dim3(kLT), replay_smem_bytes(),
                    stream, ev, 9, dn(9), a, ws);
+    if (e != hipSuccess) return e;
+  }
+  if (a.n_large > 0 && a.replay_dev > 0) {   // the replays whose slots live in device memory
+    e = launch_one(large_replay_dev_kernel, dim3((unsigned)a.replay_dev), dim3(kLT),
+                   replay_dev_smem_bytes(), stream, ev, 10, dn(10), a, ws);
     if (e != hipSuccess) return e;
   }
   if (a.n_argmax > 0) {

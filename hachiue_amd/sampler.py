@@ -241,7 +241,7 @@ class Sampler:
 
     KERNELS = ("pen_kernel", "row_kernel", "chunk_kernel", "finalize_kernel", "large_kernel",
                "mid_kernel", "argmax_kernel", "gemv_kernel", "large_fast_kernel",
-               "large_replay_kernel")
+               "large_replay_kernel", "large_replay_dev_kernel")
 
     def kernel_times(self):
         """({kernel: total device ms}, calls) since the last query."""

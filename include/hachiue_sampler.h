@@ -60,12 +60,15 @@ typedef struct hs_sample_config {
 #define HS_ROW_REPLAYED     0x2u /* exact replace-min replay was needed (ties) */
 #define HS_ROW_TIES         0x4u /* equal values among or at the candidates */
 #define HS_ROW_SINGLE       0x8u /* 0 or 1 candidate: no draw consumed */
-#define HS_ROW_UNSUPPORTED 0x10u /* top-k > 16384 below the finite count with a group
-                                    of equal values at the drawn position (or in the
-                                    candidate outputs, also for more than 1024 of
-                                    them): the reference orders it by its slot
-                                    history, which this build replays for top-k up
-                                    to 16384 only; token is -1 */
+#define HS_ROW_UNSUPPORTED 0x10u /* top-k > 524288 (a vocab above that) below the
+                                    finite count with a group of equal values at
+                                    the drawn position: the reference orders it by
+                                    its slot history, which this build replays for
+                                    top-k up to 524288; token is -1.  Also set
+                                    (token kept) when candidate outputs would need
+                                    more than 8192 slot-ordered positions or more
+                                    than 2048 positions above the last listed
+                                    value on the top-k > 1024 path */
 #define HS_ROW_LARGE       0x20u /* top-k > 1024 path: binary64 sums in another order
                                     than the reference's (probabilities within 1e-5) */
 #define HS_ROW_TWO_PASS    0x40u /* with HS_ROW_LARGE: a top-k = vocab row finished by
@@ -136,18 +139,22 @@ int hs_sample_batch_device_ex(hs_context *ctx, float *d_logits, int32_t rows,
                               void *stream);
 
 /* hs_sample_batch_device without any allocation.  No counterpart in the
- * reference: it is for callers that cannot allocate during the call (code
- * under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc).  Same arguments, semantics and outputs as
- * hs_sample_batch_device; the workspace is one static device array per GPU
- * (about 350 KB, held until the process ends, its address taken once per
- * device when the first context on it is created), and the plans are staged
- * through pinned memory the context set up at creation.  The call makes no
- * hipMalloc, hipFree, host allocation or hipMemset.  Limits: rows <= 2048 and
- * vocab <= 524288 (HS_ERR_UNSUPPORTED beyond).  Every call on one GPU shares
- * that GPU's array: calls that overlap on one GPU through different contexts
- * race (calls on one context are serialised as usual).  Kernel timing
- * (hs_context_set_timing) does not cover this entry point. */
+ * reference: it is for callers that cannot allocate during the call (tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, semantics
+ * and outputs as hs_sample_batch_device; the workspace is one static device
+ * array per GPU (about 4.5 MB: 350 KB of plans, lists and hand-over buffers
+ * and one 4 MB region of the large-k slot replay; held until the process
+ * ends, its address taken once per device when the first context on it is
+ * created), and the plans are staged through pinned memory the context set
+ * up at creation.  The call makes no hipMalloc, hipFree, host allocation or
+ * hipMemset.  Limits: rows <= 2048 and vocab <= 524288 (HS_ERR_UNSUPPORTED
+ * beyond).  It must not be captured into a HIP graph: it may wait for its
+ * previous plan upload, and a replay would read plans that later calls have
+ * rewritten (a call on a capturing stream returns HS_ERR_UNSUPPORTED).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU through different contexts race (calls on one context are serialised
+ * as usual).  Kernel timing (hs_context_set_timing) does not cover this
+ * entry point. */
 int hs_sample_batch_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows,
                                    int64_t row_stride, int32_t vocab,
                                    const int32_t *d_hist_ids,
@@ -304,7 +311,8 @@ int hs_decode_step_device(hs_context *ctx, float *d_logits, int32_t rows,
  * (ms[0] presence/frequency pre-pass, ms[1] row kernel, ms[2] chunk kernel,
  * ms[3] finalize, ms[4] large-k kernel, ms[5] mid-k kernel, ms[6] greedy-route
  * argmax, ms[7] lm_head GEMV, ms[8] two-pass large-k kernel, ms[9] large-k
- * slot replay; a kernel a call did not launch adds 0)
+ * slot replay in LDS, ms[10] large-k slot replay in device memory; a kernel
+ * a call did not launch adds 0)
  * and the number of
  * timed calls, and resets the totals. */
 int hs_context_set_timing(hs_context *ctx, int enable);

@@ -143,15 +143,46 @@ def test_decode_rejects_bad_arguments(sampler):
     st.free()
 
 
+def test_decode_large_k_ties_resolved(sampler):
+    """Large-k rows whose draw lands in a group of equal logits are resolved
+    by the slot replay (its slots in LDS at k = 5000, in device memory at
+    k = 20000) inside a decode step: the tokens, histories and lengths equal
+    the oracle's decode loop."""
+    V = 40000
+    logits = np.zeros((3, V), np.float32)
+    logits[1] = np.round(np.random.default_rng(3).standard_normal(V) * 2)
+    logits[2] = np.random.default_rng(4).standard_normal(V).astype(np.float32)
+    cfgs = [dict(temperature=1.0, topK=5000.0, topP=0.95),
+            dict(temperature=0.8, topK=20000.0, topP=0.9),
+            dict(temperature=0.0)]
+    uni = np.array([0.999, 0.37, 0.5])
+    st = DecodeState(sampler, [[1, 2], [3], [4]], [], ring_cap=128)
+    d_l = hip.DeviceArray.from_numpy(logits)
+    d_u = hip.DeviceArray.from_numpy(uni)
+    d_t = hip.DeviceArray(3, np.int32)
+    print("[gpu] decode large-k ties", flush=True)
+    st.step(d_l.addr, V, V, cfgs, d_u.addr, d_t.addr)
+    hip.synchronize()
+    tok = d_t.download().tolist()
+    want = o.sample_batch(logits.copy(), V, None, None, cfgs, uni).token
+    assert tok == list(want)
+    assert st.lengths().tolist() == [3, 2, 2]
+    assert st.history(0).tolist() == [1, 2, tok[0]]
+    assert st.history(1).tolist() == [3, tok[1]]
+    assert st.finished().tolist() == [False, False, False]
+    st.free()
+
+
 def test_decode_unresolved_row_keeps_state(sampler):
-    """A large-k row whose draw lands in a group of equal logits is left
-    unresolved by the sampler (HS_ROW_UNSUPPORTED, token -1); in a decode step
-    that row reports -1 and keeps its history, length and done flag, while the
-    other rows advance."""
-    V = 20000
+    """A row the sampler leaves unresolved (HS_ROW_UNSUPPORTED, token -1:
+    top-k above the replay's 2^19 slots on a vocabulary larger than that,
+    with the draw in a group of equal logits) reports -1 in a decode step
+    and keeps its history, length and done flag, while the other row
+    advances."""
+    V = 600000
     logits = np.zeros((2, V), np.float32)
     logits[1] = np.random.default_rng(3).standard_normal(V).astype(np.float32)
-    cfgs = [dict(temperature=1.0, topK=5000.0, topP=0.95), dict(temperature=0.0)]
+    cfgs = [dict(temperature=1.0, topK=550000.0, topP=0.95), dict(temperature=0.0)]
     st = DecodeState(sampler, [[1, 2], [3]], [], ring_cap=128)
     d_l = hip.DeviceArray.from_numpy(logits)
     d_u = hip.DeviceArray.from_numpy(np.array([0.999, 0.5]))
@@ -162,13 +193,9 @@ def test_decode_unresolved_row_keeps_state(sampler):
     tok = d_t.download().tolist()
     want = o.sample_batch(logits.copy(), V, None, None, cfgs, np.array([0.999, 0.5])).token
     assert tok[1] == want[1]
-    if tok[0] == -1:   # unresolved: the row's state stays as it was
-        assert st.lengths().tolist() == [2, 2]
-        assert st.history(0).tolist() == [1, 2]
-    else:
-        assert tok[0] == want[0]
-        assert st.lengths().tolist() == [3, 2]
-        assert st.history(0).tolist() == [1, 2, tok[0]]
+    assert tok[0] == -1
+    assert st.lengths().tolist() == [2, 2]
+    assert st.history(0).tolist() == [1, 2]
     assert st.finished().tolist() == [False, False]
     assert st.history(1).tolist() == [3, tok[1]]
     st.free()
