@@ -4298,8 +4298,8 @@ __global__ __launch_bounds__(kLT) void large_replay_dev_kernel(LaunchArgs a, Wor
 //
 //  1. (HBM) m0 = the maximum of the first 16384 logits.  Every candidate
 //     v <= m0 adds w = 2^(q * -log2(e) / 256) to bucket floor(q) of an LDS
-//     histogram (64-bit fixed-point sums), q = (m0 - v) * 256 / T in binary32 (one
-//     fma, shared by the bucket and the weight); the few v > m0 go to a list
+//     histogram (64-bit fixed-point sums), q = (m0 - v) * 256 / T in binary32
+//     (shared by the bucket and the weight); the few v > m0 go to a list
 //     of their own.  m = max(m0, list), S = e^((m0 - m)/T) * sum + the
 //     list's exp((v - m)/T).
 //  2. From the buckets' cumulative probabilities the kernel picks the bucket
@@ -4341,14 +4341,18 @@ size_t large_fast_smem_bytes() { return sizeof(FastSmem); }
 static_assert(kFT * 8 == kFB, "each thread owns eight buckets");
 
 // Bucket of a candidate v <= m0 from q = (m0 - v) * 256 / T, computed once
-// per logit with one rounding (fma): q never increases with v, so neither
-// does the bucket; clamped to the last bucket.
-__device__ __forceinline__ float fast_q(float v, float cz, float m0cz) { return fmaf(v, -cz, m0cz); }
+// per logit as (m0 - v) * cz: two roundings, each relative to q itself, so
+// q's error vanishes where the weights matter (small q).  (A product m0 * cz
+// rounded once per row and an fma would shift every q by the same error, up
+// to half an ulp of m0 * cz: a common bias of all bucket weights that grows
+// with m0 / T.)  q never increases with v, so neither does the bucket;
+// clamped to the last bucket.
+__device__ __forceinline__ float fast_q(float v, float cz, float m0) { return (m0 - v) * cz; }
 __device__ __forceinline__ int fast_bucket_q(float q) {
   return (int)fminf(fmaxf(q, 0.0f), (float)(kFB - 1));
 }
-__device__ __forceinline__ int fast_bucket(float v, float cz, float m0cz) {
-  return fast_bucket_q(fast_q(v, cz, m0cz));
+__device__ __forceinline__ int fast_bucket(float v, float cz, float m0) {
+  return fast_bucket_q(fast_q(v, cz, m0));
 }
 
 template <typename T>
@@ -4458,7 +4462,7 @@ struct FastLoc {
 // exactly per bucket (binary64 sums of binary32 values), only the located
 // bucket's logits are sorted, and the walk through them is a block prefix sum.
 __device__ __forceinline__ FastLoc fast_locate(int glo, int ghi, double c_start, double target,
-                                               int nl, float cz, float m0cz, float m0, double md,
+                                               int nl, float cz, float m0, double md,
                                                double it, double S, FastSmem &sm) {
   FastWalk &w = *reinterpret_cast<FastWalk *>(sm.mass);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -4468,7 +4472,7 @@ __device__ __forceinline__ FastLoc fast_locate(int glo, int ghi, double c_start,
   __syncthreads();
   for (int i = tid; i < nl; i += kFT) {
     const float v = key2f(cand_key(sm.buf[i]));
-    const int b = v > m0 ? -1 : fast_bucket(v, cz, m0cz);
+    const int b = v > m0 ? -1 : fast_bucket(v, cz, m0);
     if (b >= glo && b <= ghi) {
       atomicAdd(&w.bsum[b - glo], sm.pb[i]);
       atomicAdd(&w.bcnt[b - glo], 1u);
@@ -4516,7 +4520,7 @@ __device__ __forceinline__ FastLoc fast_locate(int glo, int ghi, double c_start,
   const int bq = glo + lb;   // the bucket (-1: the list above m0)
   for (int i = tid; i < nl; i += kFT) {
     const float v = key2f(cand_key(sm.buf[i]));
-    const int b = v > m0 ? -1 : fast_bucket(v, cz, m0cz);
+    const int b = v > m0 ? -1 : fast_bucket(v, cz, m0);
     if (b == bq) w.one[atomicAdd(&sm.nbuf, 1)] = sm.buf[i];
   }
   if (tid < 16) { w.ssum[tid] = 0.0; w.scnt[tid] = 0u; }
@@ -4534,7 +4538,7 @@ __device__ __forceinline__ FastLoc fast_locate(int glo, int ghi, double c_start,
   const unsigned long long *few = w.one;
   if (nb > 64 && bq >= 0) {
     for (int i = tid; i < nb; i += kFT) {
-      const float q = fast_q(key2f(cand_key(w.one[i])), cz, m0cz);
+      const float q = fast_q(key2f(cand_key(w.one[i])), cz, m0);
       const int part = (int)fminf(fmaxf((q - (float)bq) * 16.0f, 0.0f), 15.0f);
       atomicAdd(&w.ssum[part], prob(w.one[i]));
       atomicAdd(&w.scnt[part], 1u);
@@ -4572,7 +4576,7 @@ __device__ __forceinline__ FastLoc fast_locate(int glo, int ghi, double c_start,
       if (tid == 0) sm.nbuf = 0;
       __syncthreads();
       for (int i = tid; i < nb; i += kFT) {
-        const float q = fast_q(key2f(cand_key(w.one[i])), cz, m0cz);
+        const float q = fast_q(key2f(cand_key(w.one[i])), cz, m0);
         if ((int)fminf(fmaxf((q - (float)bq) * 16.0f, 0.0f), 15.0f) == L)
           w.few[atomicAdd(&sm.nbuf, 1)] = w.one[i];
       }
@@ -4667,18 +4671,18 @@ __device__ __forceinline__ FastLoc fast_locate(int glo, int ghi, double c_start,
 // version's.
 constexpr int kFWaveList = 1024;   // gathered logits the wave walks scan
 __device__ __forceinline__ FastLoc fast_locate_wave(int glo, int ghi, double c_start,
-                                                    double target, int nl, float cz, float m0cz,
-                                                    float m0, FastSmem &sm) {
+                                                    double target, int nl, float cz, float m0,
+                                                    FastSmem &sm) {
   FastWalk &w = *reinterpret_cast<FastWalk *>(sm.mass);
   const int lane = lane_id();
   const int span = ghi - glo + 1;
   FastLoc r{-1, 0, 0.0};
   auto bucket_of = [&](unsigned long long c) {
     const float v = key2f(cand_key(c));
-    return v > m0 ? -1 : fast_bucket(v, cz, m0cz);
+    return v > m0 ? -1 : fast_bucket(v, cz, m0);
   };
   auto part_of = [&](unsigned long long c, int bq) {
-    const float q = fast_q(key2f(cand_key(c)), cz, m0cz);
+    const float q = fast_q(key2f(cand_key(c)), cz, m0);
     return (int)fminf(fmaxf((q - (float)bq) * 16.0f, 0.0f), 15.0f);
   };
   // LDS operations of one wave take effect in issue order: no waits needed.
@@ -4886,9 +4890,7 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
   }
   const float m0 = fast_block_max(mx, sm.dred);   // (its barriers order the clears above)
   const float cz = (float)(it * (double)kFBScale);
-  const float m0cz = m0 * cz;
-  if (!(m0 > -INFINITY && m0 < INFINITY && cz > 0.0f && cz < INFINITY && m0cz > -INFINITY &&
-        m0cz < INFINITY))
+  if (!(m0 > -INFINITY && m0 < INFINITY && cz > 0.0f && cz < INFINITY))
     return false;   // (uniform: every thread read the same values)
   const float kq = -1.4426950408889634f / kFBScale;   // w = 2^(q kq) = e^((v - m0) / T)
   // The buckets sum w in fixed point, floor(w 2^sx) as 64-bit integers: LDS
@@ -4929,7 +4931,7 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
       const float v = t[c];
       const bool cand = v > -INFINITY;
       nf += cand ? 1u : 0u;
-      const float q = fast_q(v, cz, m0cz);
+      const float q = fast_q(v, cz, m0);
       const float w = __builtin_amdgcn_exp2f(q * kq);
       atomicAdd(&massx[fast_bucket_q(q)], fixw(cand && !(v > m0) ? w : 0.0f));
     }
@@ -4968,7 +4970,7 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
         const int slot = atomicAdd(&sm.ntop, 1);
         if (slot < kFTop) sm.top[slot] = pack_cand(f2key(v), (uint32_t)e);
       } else {
-        const float q = fast_q(v, cz, m0cz);
+        const float q = fast_q(v, cz, m0);
         atomicAdd(&massx[fast_bucket_q(q)], fixw(__builtin_amdgcn_exp2f(q * kq)));
       }
     }
@@ -5060,7 +5062,7 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const float v = t[c];
-      const float q = fast_q(v, cz, m0cz);
+      const float q = fast_q(v, cz, m0);
       const bool le = v <= m0;
       below0 += (valid & le & (q < fb0)) ? 1u : 0u;
       const unsigned long long ok = mv & __builtin_amdgcn_ballot_w64(le);
@@ -5137,15 +5139,15 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
   if (nl <= kFWaveList && g0hi - g0lo < 64 && g1hi - g1lo < 64) {
     if (tid < 64) {
       int res = -1;
-      const FastLoc l1 = fast_locate_wave(g0lo, g0hi, c0, tp, nl, cz, m0cz, m0, sm);
+      const FastLoc l1 = fast_locate_wave(g0lo, g0hi, c0, tp, nl, cz, m0, sm);
       if (l1.id == -2) {
         res = 0;
       } else if (l1.id >= 0) {
         const double r = u * l1.cum;
         if (r == r) {
           const FastLoc l2 =
-              two ? fast_locate_wave(g1lo, g1hi, c1, r, nl, cz, m0cz, m0, sm)
-                  : fast_locate_wave(g0lo, g0hi, c0, r, nl, cz, m0cz, m0, sm);
+              two ? fast_locate_wave(g1lo, g1hi, c1, r, nl, cz, m0, sm)
+                  : fast_locate_wave(g0lo, g0hi, c0, r, nl, cz, m0, sm);
           res = l2.id == -2 ? 0 : l2.id >= 0 ? 1 : -1;
           if (res == 1) finish(l1, l2);
         }
@@ -5156,12 +5158,12 @@ __device__ __forceinline__ bool large_fast(const LaunchArgs &a, const RowPlan &P
     const int res = sm.flag;
     if (res != 0) return res > 0;
   }
-  const FastLoc l1 = fast_locate(g0lo, g0hi, c0, tp, nl, cz, m0cz, m0, md, it, S, sm);
+  const FastLoc l1 = fast_locate(g0lo, g0hi, c0, tp, nl, cz, m0, md, it, S, sm);
   if (l1.id < 0) return false;
   const double r = u * l1.cum;
   if (!(r == r)) return false;
-  const FastLoc l2 = two ? fast_locate(g1lo, g1hi, c1, r, nl, cz, m0cz, m0, md, it, S, sm)
-                         : fast_locate(g0lo, g0hi, c0, r, nl, cz, m0cz, m0, md, it, S, sm);
+  const FastLoc l2 = two ? fast_locate(g1lo, g1hi, c1, r, nl, cz, m0, md, it, S, sm)
+                         : fast_locate(g0lo, g0hi, c0, r, nl, cz, m0, md, it, S, sm);
   if (l2.id < 0) return false;
   finish(l1, l2);
   return true;

@@ -52,11 +52,15 @@ def test_gumbel_full_batch_two_pass(sampler):
     assert two.mean() > 0.99
 
 
-@pytest.mark.parametrize("name", ["gumbel", "normal", "low_t", "high_t", "penalised"])
+@pytest.mark.parametrize("name", ["gumbel", "normal", "low_t", "high_t", "penalised",
+                                  "shifted_t02", "shifted_t01"])
 def test_two_pass_distributions(sampler, name):
     """The two-pass kernel over other logit shapes and temperatures, with
     rows it must hand back (sorted ascending, so nearly every logit lies
-    above the first chunk's maximum) mixed in."""
+    above the first chunk's maximum) mixed in.  The shifted cases put the
+    maximum near 30 at T 0.2 and 0.1 (m0 / T of 150 to 300), where a
+    per-row rounding of m0 / T shared by every bucket weight would move the
+    bucket sums by more than the tolerated 1e-6."""
     rng = np.random.default_rng(len(name))
     rows, vocab = 40, 151936
     hist_ids = hist_off = None
@@ -72,6 +76,12 @@ def test_two_pass_distributions(sampler, name):
     elif name == "high_t":
         logits = rng.gumbel(size=(rows, vocab)).astype(np.float32)
         cfg = dict(temperature=1.5, topK=float("inf"), topP=0.99)
+    elif name == "shifted_t02":
+        logits = (rng.standard_normal((rows, vocab)) * 2 + 20).astype(np.float32)
+        cfg = dict(temperature=0.2, topK=float("inf"), topP=0.95)
+    elif name == "shifted_t01":
+        logits = (rng.gumbel(size=(rows, vocab)) + 20).astype(np.float32)
+        cfg = dict(temperature=0.1, topK=float("inf"), topP=0.99)
     else:
         wl = workloads.make("v262k512", 4, rows=rows, vocab=vocab)
         logits, hist_ids, hist_off = wl.logits, wl.hist_ids, wl.hist_off
