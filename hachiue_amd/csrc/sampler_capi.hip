@@ -118,6 +118,47 @@ struct DevBuf {
   }
 };
 
+// Grow-only pinned host buffer (hipHostMalloc: the device reads and writes it
+// directly, and copies from it are truly asynchronous).
+struct PinBuf {
+  void *p = nullptr;
+  size_t bytes = 0;
+  hipError_t ensure(size_t need) {
+    if (need <= bytes) return hipSuccess;
+    if (p) {
+      (void)hipHostFree(p);
+      p = nullptr;
+      bytes = 0;
+    }
+    size_t b = need + need / 4;
+    hipError_t e = hipHostMalloc(&p, b);
+    if (e != hipSuccess) { p = nullptr; return e; }
+    bytes = b;
+    return hipSuccess;
+  }
+  void release() {
+    if (p) (void)hipHostFree(p);
+    p = nullptr;
+    bytes = 0;
+  }
+};
+
+// Host entry points stage a logits block of at most this size through the
+// context's pinned buffer (larger blocks are copied from the caller's memory
+// directly).
+constexpr size_t kPinLogitsMax = size_t(64) << 20;
+// Up to this size, a host call whose rows all stream their logits once (no
+// top-k above 1024) lets the kernels read the pinned staging directly and
+// write the tokens and penalised logits back into it: no copy to device
+// memory and none back.
+constexpr size_t kZeroCopyMax = size_t(4) << 20;
+constexpr size_t pin_align(size_t b) { return (b + 255) / 256 * 256; }
+
+// Routing of rows to kernels, uploaded next to the plans.
+struct Routing {
+  std::vector<int32_t> pf, row, chunk, large, mid, lfast;
+};
+
 std::mutex g_prep_mu;
 std::vector<int> g_prepared;
 // per device: the address of `scratch` on that device (set once, at the
@@ -151,16 +192,18 @@ struct hs_context {
   int64_t cand_count_rows = 0;     // rows whose counter is known to be zero
   // plan upload cache
   std::vector<hs::RowPlan> last_plans;
+  std::vector<hs::RowPlan> call_plans;   // the current call's plans and routing
+  Routing call_rt;                       //   (kept to reuse their storage)
   int last_vocab = -1;
   void *plan_staging = nullptr;          // pinned
   size_t plan_staging_bytes = 0;
   hipEvent_t plan_done = nullptr;
   bool plan_pending = false;
   // host entry points
-  DevBuf h_logits, h_hist, h_off, h_u, h_tok;
-  DevBuf h_gidx, h_gval;          // the penalised entries copied back
-  std::vector<int64_t> gidx;      // their offsets in the logits block
-  std::vector<float> gval;
+  DevBuf h_logits, h_small, h_tok;  // logits block; uniforms | offsets | history ids
+  PinBuf h_pin;                   // staging of the same, the penalised entries' offsets,
+                                  //   and the outputs the device writes back
+  std::vector<int64_t> gidx;      // offsets of the penalised entries in the logits block
   hipStream_t stream = nullptr;
   // per-kernel timing diagnostics
   bool timing = false;
@@ -227,11 +270,6 @@ int64_t resolve_k(double top_k, int64_t vocab) {
   const double k = m > 1.0 ? m : 1.0;
   return (int64_t)floor(k);
 }
-
-// Routing of rows to kernels, uploaded next to the plans.
-struct Routing {
-  std::vector<int32_t> pf, row, chunk, large, mid, lfast;
-};
 
 // k = vocab (no slot is ever evicted) and no min-p: the two-pass large-k
 // kernel's rows.
@@ -477,8 +515,8 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   if (S * hs::kChunkCap > 0x7FFFFFFF / 2 || (int64_t)rows * S > 0x7FFFFFFF)
     return fail(HS_ERR_UNSUPPORTED, "vocab %d x rows %d too large", vocab, rows);
 
-  std::vector<hs::RowPlan> plans;
-  Routing rt;
+  std::vector<hs::RowPlan> &plans = ctx->call_plans;
+  Routing &rt = ctx->call_rt;
   try {
     int rc = build_plans(configs, rows, vocab, ctx->row_min_rows, plans, rt);
     if (rc) return rc;
@@ -958,6 +996,55 @@ int sample_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows, int64_
   return leave_stream(ctx, stream, true);
 }
 
+// hs_sample_logits_batch for small blocks whose rows all stream their logits
+// once: the kernels read the logits, uniforms and histories from the
+// context's pinned buffer and write the tokens and the penalised logits
+// there (device access to pinned host memory), so the call makes no copy to
+// or from device memory.  ctx->gidx lists the penalised entries.
+int sample_host_zero_copy(hs_context *ctx, float *logits, size_t lbytes, int32_t rows,
+                          int64_t row_stride, int32_t vocab, const int32_t *hist_ids,
+                          const int64_t *hist_offsets, int64_t hist_total,
+                          const hs_sample_config *configs, const double *uniforms,
+                          int32_t *tokens_out) {
+  hipStream_t st = ctx->stream;
+  const size_t s_u = sizeof(double) * rows;
+  const size_t s_off = hist_offsets ? sizeof(int64_t) * (size_t)(rows + 1) : 0;
+  const size_t s_hist = sizeof(int32_t) * (size_t)hist_total;
+  const size_t o_u = pin_align(lbytes);
+  const size_t o_off = o_u + pin_align(s_u);
+  const size_t o_hist = o_off + pin_align(s_off);
+  const size_t o_tok = o_hist + pin_align(s_hist);
+  HS_HIP(ctx->h_pin.ensure(o_tok + sizeof(int32_t) * rows));
+  char *pin = static_cast<char *>(ctx->h_pin.p);
+  memcpy(pin, logits, lbytes);
+  memcpy(pin + o_u, uniforms, s_u);
+  if (hist_offsets) {
+    memcpy(pin + o_off, hist_offsets, s_off);
+    if (hist_total > 0) memcpy(pin + o_hist, hist_ids, s_hist);
+  }
+  float *p_logits = reinterpret_cast<float *>(pin);
+  const int rc = sample_device(
+      ctx, p_logits, rows, row_stride, vocab,
+      hist_offsets ? reinterpret_cast<const int32_t *>(pin + o_hist) : nullptr,
+      hist_offsets ? reinterpret_cast<const int64_t *>(pin + o_off) : nullptr, configs,
+      reinterpret_cast<const double *>(pin + o_u), reinterpret_cast<int32_t *>(pin + o_tok), 0,
+      nullptr, nullptr, nullptr, nullptr, nullptr, st);
+  // the pinned buffer is free again only once the stream has drained
+  const hipError_t es = hipStreamSynchronize(st);
+  if (rc) return rc;
+  if (es != hipSuccess)
+    return fail(HS_ERR_HIP, "hipStreamSynchronize failed: %s", hipGetErrorString(es));
+  memcpy(tokens_out, pin + o_tok, sizeof(int32_t) * rows);
+  for (const int64_t g : ctx->gidx) logits[g] = p_logits[g];
+  for (int r = 0; r < rows; ++r)
+    if (tokens_out[r] < 0)
+      return fail(HS_ERR_UNSUPPORTED,
+                  "row %d: top-k above %d with equal logits at the drawn position; the "
+                  "reference orders them by its slot history, which this build replays up to "
+                  "that top-k only", r, hs::kReplayDevMaxK);
+  return HS_OK;
+}
+
 }  // namespace
 
 // Every entry point that uses a context holds its mutex for the whole call.
@@ -1088,12 +1175,9 @@ int hs_context_destroy(hs_context *ctx) {
     ctx->large_replay.release();
     ctx->replay_slots.release();
     ctx->h_logits.release();
-    ctx->h_hist.release();
-    ctx->h_off.release();
-    ctx->h_u.release();
+    ctx->h_small.release();
     ctx->h_tok.release();
-    ctx->h_gidx.release();
-    ctx->h_gval.release();
+    ctx->h_pin.release();
     if (ctx->plan_staging) (void)hipHostFree(ctx->plan_staging);
     if (ctx->plan_done) (void)hipEventDestroy(ctx->plan_done);
     if (ctx->done_ev) (void)hipEventDestroy(ctx->done_ev);
@@ -1353,17 +1437,29 @@ int hs_argmax(hs_context *ctx, const float *logits, int32_t rows, int64_t row_st
   DeviceGuard guard(ctx->device);
   hipStream_t st = ctx->stream;
   const size_t lbytes = sizeof(float) * ((size_t)(rows - 1) * (size_t)row_stride + (size_t)vocab);
+  const bool stage = lbytes <= kPinLogitsMax;
+  const size_t o_tok = stage ? pin_align(lbytes) : 0;
   HS_HIP(ctx->h_logits.ensure(lbytes));
   HS_HIP(ctx->h_tok.ensure(sizeof(int32_t) * rows));
-  HS_HIP(hipMemcpyAsync(ctx->h_logits.p, logits, lbytes, hipMemcpyHostToDevice, st));
+  HS_HIP(ctx->h_pin.ensure(o_tok + sizeof(int32_t) * rows));
+  char *pin = static_cast<char *>(ctx->h_pin.p);
+  if (stage) memcpy(pin, logits, lbytes);
+  HS_HIP(hipMemcpyAsync(ctx->h_logits.p, stage ? static_cast<const void *>(pin) : logits, lbytes,
+                        hipMemcpyHostToDevice, st));
   int rc = argmax_device(ctx, static_cast<float *>(ctx->h_logits.p), rows, row_stride, vocab,
                          static_cast<int32_t *>(ctx->h_tok.p), st);
   if (rc) {
     (void)hipStreamSynchronize(st);
     return rc;
   }
-  HS_HIP(hipMemcpyAsync(tokens_out, ctx->h_tok.p, sizeof(int32_t) * rows, hipMemcpyDeviceToHost, st));
-  HS_HIP(hipStreamSynchronize(st));
+  const hipError_t e = inject_failure() ? hipErrorOutOfMemory
+                                        : hipMemcpyAsync(pin + o_tok, ctx->h_tok.p,
+                                                         sizeof(int32_t) * rows,
+                                                         hipMemcpyDeviceToHost, st);
+  const hipError_t es = hipStreamSynchronize(st);   // the staging is free again either way
+  if (e != hipSuccess) return fail(HS_ERR_HIP, "token copy failed: %s", hipGetErrorString(e));
+  if (es != hipSuccess) return fail(HS_ERR_HIP, "hipStreamSynchronize failed: %s", hipGetErrorString(es));
+  memcpy(tokens_out, pin + o_tok, sizeof(int32_t) * rows);
   return HS_OK;
 }
 
@@ -1397,34 +1493,11 @@ int hs_sample_logits_batch(hs_context *ctx, float *logits, int32_t rows, int64_t
   DeviceGuard guard(ctx->device);
   hipStream_t st = ctx->stream;
   const size_t lbytes = sizeof(float) * ((size_t)(rows - 1) * (size_t)row_stride + (size_t)vocab);
-  HS_HIP(ctx->h_logits.ensure(lbytes));
-  HS_HIP(ctx->h_u.ensure(sizeof(double) * rows));
-  HS_HIP(ctx->h_tok.ensure(sizeof(int32_t) * rows));
-  HS_HIP(hipMemcpyAsync(ctx->h_logits.p, logits, lbytes, hipMemcpyHostToDevice, st));
-  HS_HIP(hipMemcpyAsync(ctx->h_u.p, uniforms, sizeof(double) * rows, hipMemcpyHostToDevice, st));
-  int32_t *d_ids = nullptr;
-  int64_t *d_off = nullptr;
-  if (hist_offsets) {
-    HS_HIP(ctx->h_off.ensure(sizeof(int64_t) * (rows + 1)));
-    HS_HIP(ctx->h_hist.ensure(sizeof(int32_t) * (size_t)(hist_total > 0 ? hist_total : 1)));
-    d_ids = static_cast<int32_t *>(ctx->h_hist.p);
-    d_off = static_cast<int64_t *>(ctx->h_off.p);
-    if (hist_total > 0)
-      HS_HIP(hipMemcpyAsync(d_ids, hist_ids, sizeof(int32_t) * hist_total, hipMemcpyHostToDevice, st));
-    HS_HIP(hipMemcpyAsync(d_off, hist_offsets, sizeof(int64_t) * (rows + 1), hipMemcpyHostToDevice, st));
-  }
-  int rc = sample_device(ctx, static_cast<float *>(ctx->h_logits.p), rows, row_stride, vocab, d_ids,
-                         d_off, configs, static_cast<double *>(ctx->h_u.p),
-                         static_cast<int32_t *>(ctx->h_tok.p), 0, nullptr, nullptr, nullptr, nullptr,
-                         nullptr, st);
-  if (rc) {
-    (void)hipStreamSynchronize(st);
-    return rc;
-  }
   // The reference writes the penalised values back (src/sampler.ts:30).
   // Only history ids change: the last 128 of a row for the repetition
-  // penalty, all of them with presence / frequency.  Those entries are
-  // gathered on the device and copied back, not the whole block.
+  // penalty, all of them with presence / frequency.  Their offsets are listed
+  // here, and a kernel gathers those entries (and the tokens) into the pinned
+  // buffer after sampling: no copy of the whole block back.
   try {
     ctx->gidx.clear();
     for (int r = 0; r < rows && hist_offsets; ++r) {
@@ -1439,30 +1512,75 @@ int hs_sample_logits_batch(hs_context *ctx, float *logits, int32_t rows, int64_t
         if (id >= 0 && id < vocab) ctx->gidx.push_back((int64_t)r * row_stride + id);
       }
     }
-    ctx->gval.resize(ctx->gidx.size());
   } catch (const std::bad_alloc &) {
-    (void)hipStreamSynchronize(st);
     return fail(HS_ERR_OUT_OF_MEMORY, "host allocation failed");
   }
   const int64_t ng = (int64_t)ctx->gidx.size();
-  HS_HIP(hipMemcpyAsync(tokens_out, ctx->h_tok.p, sizeof(int32_t) * rows, hipMemcpyDeviceToHost, st));
-  if (ng > 0) {
-    HS_HIP(ctx->h_gidx.ensure(sizeof(int64_t) * (size_t)ng));
-    HS_HIP(ctx->h_gval.ensure(sizeof(float) * (size_t)ng));
-    HS_HIP(hipMemcpyAsync(ctx->h_gidx.p, ctx->gidx.data(), sizeof(int64_t) * (size_t)ng,
-                          hipMemcpyHostToDevice, st));
-    const hipError_t e = hs::launch_gather_f32(static_cast<const float *>(ctx->h_logits.p),
-                                               static_cast<const int64_t *>(ctx->h_gidx.p),
-                                               static_cast<float *>(ctx->h_gval.p), ng, st);
-    if (e != hipSuccess) {
-      (void)hipStreamSynchronize(st);
-      return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
-    }
-    HS_HIP(hipMemcpyAsync(ctx->gval.data(), ctx->h_gval.p, sizeof(float) * (size_t)ng,
-                          hipMemcpyDeviceToHost, st));
+  bool zero_copy = lbytes <= kZeroCopyMax;
+  for (int r = 0; r < rows && zero_copy; ++r)
+    zero_copy = plan_row(configs[r], vocab).mode != hs::kModeLarge;
+  if (zero_copy) return sample_host_zero_copy(ctx, logits, lbytes, rows, row_stride, vocab, hist_ids,
+                                              hist_offsets, hist_total, configs, uniforms,
+                                              tokens_out);
+  // pinned layout: [logits (when staged)] [uniforms | offsets | history ids]
+  // [gathered offsets] [gathered values] [tokens]; the device copy of the
+  // middle part has the same layout, so one copy moves it
+  const bool stage = lbytes <= kPinLogitsMax;
+  const size_t o_small = stage ? pin_align(lbytes) : 0;
+  const size_t s_u = sizeof(double) * rows;
+  const size_t s_off = hist_offsets ? sizeof(int64_t) * (size_t)(rows + 1) : 0;
+  const size_t s_hist = sizeof(int32_t) * (size_t)hist_total;
+  const size_t r_off = pin_align(s_u), r_hist = r_off + pin_align(s_off);
+  const size_t small_bytes = r_hist + s_hist;
+  const size_t o_gidx = o_small + pin_align(small_bytes);
+  const size_t o_gval = o_gidx + pin_align(sizeof(int64_t) * (size_t)ng);
+  const size_t o_tok = o_gval + pin_align(sizeof(float) * (size_t)ng);
+  HS_HIP(ctx->h_logits.ensure(lbytes));
+  HS_HIP(ctx->h_small.ensure(small_bytes));
+  HS_HIP(ctx->h_tok.ensure(sizeof(int32_t) * rows));
+  HS_HIP(ctx->h_pin.ensure(o_tok + sizeof(int32_t) * rows));
+  char *pin = static_cast<char *>(ctx->h_pin.p);
+  char *small = pin + o_small;
+  if (stage) memcpy(pin, logits, lbytes);
+  memcpy(small, uniforms, s_u);
+  if (hist_offsets) {
+    memcpy(small + r_off, hist_offsets, s_off);
+    if (hist_total > 0) memcpy(small + r_hist, hist_ids, s_hist);
   }
+  if (ng > 0) memcpy(pin + o_gidx, ctx->gidx.data(), sizeof(int64_t) * (size_t)ng);
+  // from the first copy on, every return waits for the stream first: the
+  // pinned buffer must not be refilled while a copy still reads it
+  auto bail = [&](int rc) {
+    (void)hipStreamSynchronize(st);
+    return rc;
+  };
+  HS_HIP(hipMemcpyAsync(ctx->h_logits.p, stage ? static_cast<const void *>(pin) : logits, lbytes,
+                        hipMemcpyHostToDevice, st));
+  hipError_t e = inject_failure() ? hipErrorOutOfMemory
+                                  : hipMemcpyAsync(ctx->h_small.p, small, small_bytes,
+                                                   hipMemcpyHostToDevice, st);
+  if (e != hipSuccess)
+    return bail(fail(HS_ERR_HIP, "input copy failed: %s", hipGetErrorString(e)));
+  char *dsmall = static_cast<char *>(ctx->h_small.p);
+  const int32_t *d_ids = hist_offsets ? reinterpret_cast<const int32_t *>(dsmall + r_hist) : nullptr;
+  const int64_t *d_off = hist_offsets ? reinterpret_cast<const int64_t *>(dsmall + r_off) : nullptr;
+  int rc = sample_device(ctx, static_cast<float *>(ctx->h_logits.p), rows, row_stride, vocab, d_ids,
+                         d_off, configs, reinterpret_cast<const double *>(dsmall),
+                         static_cast<int32_t *>(ctx->h_tok.p), 0, nullptr, nullptr, nullptr, nullptr,
+                         nullptr, st);
+  if (rc) return bail(rc);
+  e = inject_failure() ? hipErrorOutOfMemory
+                       : hs::launch_gather_out(static_cast<const float *>(ctx->h_logits.p),
+                                               reinterpret_cast<const int64_t *>(pin + o_gidx),
+                                               reinterpret_cast<float *>(pin + o_gval), ng,
+                                               static_cast<const int32_t *>(ctx->h_tok.p),
+                                               reinterpret_cast<int32_t *>(pin + o_tok), rows, st);
+  if (e != hipSuccess)
+    return bail(fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e)));
   HS_HIP(hipStreamSynchronize(st));
-  for (int64_t i = 0; i < ng; ++i) logits[ctx->gidx[i]] = ctx->gval[i];
+  memcpy(tokens_out, pin + o_tok, sizeof(int32_t) * rows);
+  const float *gval = reinterpret_cast<const float *>(pin + o_gval);
+  for (int64_t i = 0; i < ng; ++i) logits[ctx->gidx[i]] = gval[i];
   for (int r = 0; r < rows; ++r)
     if (tokens_out[r] < 0)
       return fail(HS_ERR_UNSUPPORTED,

@@ -266,7 +266,8 @@ struct DecodeArgs {
 constexpr int kMaxStopIds = 1024;
 hipError_t launch_decode_append(const DecodeArgs &d, hipStream_t stream);
 hipError_t launch_fill_u32(uint32_t *p, int64_t n, uint32_t v, hipStream_t stream);
-hipError_t launch_gather_f32(const float *src, const int64_t *idx, float *dst, int64_t n,
+hipError_t launch_gather_out(const float *src, const int64_t *idx, float *dst, int64_t n,
+                             const int32_t *tok, int32_t *tok_dst, int32_t rows,
                              hipStream_t stream);
 // `done`, when not null and `ev` is null, is recorded at the end of the
 // call's last kernel (hipExtLaunchKernelGGL's stop event: no marker packet).

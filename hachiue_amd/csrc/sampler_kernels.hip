@@ -6028,19 +6028,24 @@ __global__ __launch_bounds__(256) void decode_append_kernel(DecodeArgs d) {
   d.len[r] = len + 1;
 }
 
-// dst[i] = src[idx[i]] for i < n: the penalised logits a host call copies
-// back, instead of whole rows.
-__global__ __launch_bounds__(256) void gather_f32_kernel(const float *src, const int64_t *idx,
-                                                         float *dst, int64_t n) {
+// What a host call copies back, written straight into its pinned buffer:
+// dst[i] = src[idx[i]] for i < n (the penalised logits; idx is read from the
+// pinned buffer too) and tok_dst[r] = tok[r] for r < rows.
+__global__ __launch_bounds__(256) void gather_out_kernel(const float *src, const int64_t *idx,
+                                                         float *dst, int64_t n, const int32_t *tok,
+                                                         int32_t *tok_dst, int32_t rows) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) dst[i] = src[idx[i]];
+  else if (i < n + rows) tok_dst[i - n] = tok[i - n];
 }
 
-hipError_t launch_gather_f32(const float *src, const int64_t *idx, float *dst, int64_t n,
+hipError_t launch_gather_out(const float *src, const int64_t *idx, float *dst, int64_t n,
+                             const int32_t *tok, int32_t *tok_dst, int32_t rows,
                              hipStream_t stream) {
-  if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(gather_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
-                     src, idx, dst, n);
+  const int64_t total = n + rows;
+  if (total <= 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_out_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream,
+                     src, idx, dst, n, tok, tok_dst, rows);
   return hipGetLastError();
 }
 
