@@ -2279,21 +2279,37 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     __syncthreads();
     if (lane == 0 && disc) atomicMax(&rs.key64, disc);
     __syncthreads();
-    if (wave != 0) return;
-    if (!overflow) {
-      F = c;
-      const uint32_t Tk = cand_key(__shfl(F, k - 1));
-      // the union's 65th, or a part's own 65th, equal to the row's k-th
-      // largest: more values equal to it may exist beyond F
-      extra = Tk != 0u && (rs.key64 == Tk || __ballot(lane < S && k64 == Tk) != 0);
-    }
     RowPlan P;
     P.temperature = temperature;
     P.top_p = top_p;
     P.min_p = min_p;
     P.k = k;
-    finish_wave(a, P, row, rowfull, F, extra, overflow, u, rsv, rsid,
-                reinterpret_cast<double *>(top), true);
+    // Wave 0 draws; when the slot replay is needed, the whole workgroup
+    // first records the largest logit of every 64-logit block of the row, as
+    // for a whole row, after acquiring the other parts' penalised write-backs
+    // at agent scope.  The other waves wait for the decision.
+    TailState st;
+    if (wave == 0) {
+      if (!overflow) {
+        F = c;
+        const uint32_t Tk = cand_key(__shfl(F, k - 1));
+        // the union's 65th, or a part's own 65th, equal to the row's k-th
+        // largest: more values equal to it may exist beyond F
+        extra = Tk != 0u && (rs.key64 == Tk || __ballot(lane < S && k64 == Tk) != 0);
+      }
+      st = tail_decide(a, P, F, extra, overflow, u, reinterpret_cast<double *>(top));
+      if (lane == 0) rs.tie = st.need ? 1 : 0;
+    }
+    __syncthreads();
+    const uint32_t *bkey = nullptr;
+    if (rs.tie) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      block_keys<kRowThreads>(rowfull, a.vocab, reinterpret_cast<uint32_t *>(cbuf));
+      __syncthreads();
+      bkey = reinterpret_cast<const uint32_t *>(cbuf);
+    }
+    if (wave != 0) return;
+    tail_finish(a, P, row, rowfull, st, u, rsv, rsid, reinterpret_cast<double *>(top), true, bkey);
     return;
   }
   if (!overflow && n_all <= kRowThreads) {
