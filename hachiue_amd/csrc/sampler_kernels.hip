@@ -817,87 +817,107 @@ template <int BLK>
 __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, float *sv, int32_t *sid,
                                            const uint32_t *bkey = nullptr) {
   const int lane = lane_id();
-  // k <= 64: slot j lives in lane j's registers with its rank rk among the
-  // slots by (value, slot index), binary32 order (-0 == +0); the slot of
-  // rank 0 is the reference's minimum (the smallest index among equal
-  // minima).  An entering logit takes that slot; its new rank is the number
-  // of other slots below it, and the slots it passes move down by one.
+  // k <= 64: the slots live in lanes 0..k-1 sorted by (value, slot index):
+  // lane j holds a value's key rk (f2key: -0 == +0; an empty slot, -Infinity,
+  // is 0), its slot rs and its logit's index rid, and lane 0 holds the
+  // reference's minimum (the smallest slot among equal minima), key mk in
+  // slot mi.  A logit enters iff its key is above mk (NaN and -Infinity have
+  // key 0 and never do) and takes slot mi; its position p is the number of
+  // other slots below it, lanes 1..p move down one lane (a wave shift by
+  // DPP) and the new slot goes to lane p.  The next minimum is lane 0.
   const bool in_regs = k <= 64;
-  float rv = lane < k ? -INFINITY : INFINITY;
+  uint32_t rk = lane < k ? 0u : 0xFFFFFFFFu;
   int32_t rid = -1;
-  int rk = lane < k ? lane : 64;
-  auto take_min = [&](float vL, int idx, float &mv, int &mi) {
-    const bool less = lane < k && lane != mi && (rv < vL || (rv == vL && lane < mi));
-    const int r = __popcll(__ballot(less));
-    if (lane == mi) {
-      rv = vL;
-      rid = idx;
-      rk = r;
-    } else if (rk >= 1 && rk <= r) {
-      rk -= 1;
+  int rs = lane;
+  uint32_t mk = 0;
+  int mi = 0;
+  auto take_min = [&](uint32_t kL, int idx) {
+    const bool less = lane >= 1 && lane < k && (rk < kL || (rk == kL && rs < mi));
+    const int p = __popcll(__ballot(less));
+    // lane j <- lane j + 1 (wave_shl:1)
+    const uint32_t nk = (uint32_t)__builtin_amdgcn_update_dpp((int)rk, (int)rk, 0x130, 0xF, 0xF, false);
+    const int ns = __builtin_amdgcn_update_dpp(rs, rs, 0x130, 0xF, 0xF, false);
+    const int ni = __builtin_amdgcn_update_dpp(rid, rid, 0x130, 0xF, 0xF, false);
+    const bool low = lane < p, at = lane == p;
+    rk = low ? nk : (at ? kL : rk);
+    rid = low ? ni : (at ? idx : rid);
+    rs = low ? ns : (at ? mi : rs);
+    mk = (uint32_t)__builtin_amdgcn_readfirstlane((int)rk);
+    mi = __builtin_amdgcn_readfirstlane(rs);
+  };
+  // the logits of one 64-logit group (lane = logit) whose keys kx are above
+  // the minimum at the group's start, in index order, one scalar test each
+  auto scan64 = [&](uint32_t kx, int base) {
+    unsigned long long cm = __ballot(kx > mk);
+    while (cm) {
+      const int L = (int)__ffsll((long long)cm) - 1;
+      cm &= cm - 1;
+      const uint32_t kL = readlane_u32(kx, L);
+      if (kL > mk) take_min(kL, base + L);
     }
-    mi = (int)__ffsll((long long)__ballot(lane < k && rk == 0)) - 1;
-    mv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rv), mi));
+  };
+  auto store_slots = [&]() {
+    if (lane < k) {
+      sv[rs] = rid >= 0 ? key2f(rk) : -INFINITY;
+      sid[rs] = rid;
+    }
   };
   if (bkey && in_regs) {
     // bkey[b]: key of the largest logit of block b (64 logits).  A block
     // whose largest logit is not above the current minimum holds no logit
-    // that enters, so it is not read.  Windows of 64 blocks; of a window's
-    // blocks that can hold one (against the minimum at the window's start),
-    // BLK at a time are read together, then scanned in order.
-    float mv = -INFINITY;
-    int mi = 0;
+    // that enters, so it is not read.  Batches of up to BLK such blocks (in
+    // index order, tested against the minimum when the batch is formed) are
+    // read together, and the next batch's reads are issued before the
+    // current batch is scanned: the scan of one batch hides the latency of
+    // the next one's reads.
     const int nb = (vocab + 63) >> 6;
-    for (int b = 0; b < nb; b += 64) {
-      const uint32_t kb = b + lane < nb ? bkey[b + lane] : 0u;
-      unsigned long long m = __ballot(kb > f2key(mv));
-      while (m) {
-        unsigned long long mm = m;
-        float x[BLK];
-        uint32_t ok = 0;   // bit q: x[q] is a logit of the row
-        // (the reads are only issued here; nothing uses them before the scan)
+    int wb = -64;                      // window of 64 blocks being taken
+    unsigned long long wm = 0;         // its blocks still to take
+    auto form = [&](float (&x)[BLK], int (&blk)[BLK]) {
+      int n = 0;
 #pragma unroll
-        for (int q = 0; q < BLK; ++q) {
-          const int t = mm ? (int)__ffsll((long long)mm) - 1 : -1;
-          if (mm) mm &= mm - 1;
-          const int e = (b + t) * 64 + lane;
-          const bool in = t >= 0 && e < vocab;
-          x[q] = rowp[in ? e : 0];   // always a read inside the row
-          ok |= (in ? 1u : 0u) << q;
+      for (int q = 0; q < BLK; ++q) {
+        while (!wm && wb + 64 < nb) {
+          wb += 64;
+          const uint32_t kb = wb + lane < nb ? bkey[wb + lane] : 0u;
+          wm = __ballot(kb > mk);
         }
-        unsigned long long m2 = m;
-#pragma unroll
-        for (int q = 0; q < BLK; ++q) {
-          if (m2) {
-            const int t = (int)__ffsll((long long)m2) - 1;
-            m2 &= m2 - 1;
-            const int base = (b + t) * 64;
-            int done = -1;
-            for (;;) {
-              const unsigned long long bl = __ballot(((ok >> q) & 1u) && x[q] > mv && lane > done);
-              if (!bl) break;
-              const int L = __ffsll((long long)bl) - 1;
-              const float vL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[q]), L));
-              take_min(vL, base + L, mv, mi);
-              done = L;
-            }
-          }
+        blk[q] = -1;
+        if (wm) {
+          blk[q] = wb + (int)__ffsll((long long)wm) - 1;
+          wm &= wm - 1;
+          ++n;
         }
-        m = mm;
+        const int e = blk[q] * 64 + lane;
+        x[q] = rowp[blk[q] >= 0 && e < vocab ? e : 0];   // always a read inside the row
       }
+      return n;
+    };
+    auto scan = [&](const float (&x)[BLK], const int (&blk)[BLK]) {
+#pragma unroll
+      for (int q = 0; q < BLK; ++q) {
+        if (blk[q] >= 0) {
+          const int e = blk[q] * 64 + lane;
+          scan64(e < vocab ? f2key(x[q]) : 0u, blk[q] * 64);
+        }
+      }
+    };
+    float xa[BLK], xb[BLK];
+    int ba[BLK], bb[BLK];
+    int na = form(xa, ba);
+    while (na > 0) {
+      const int nb2 = form(xb, bb);
+      scan(xa, ba);
+      if (nb2 == 0) break;
+      na = form(xa, ba);
+      scan(xb, bb);
     }
-    if (lane < k) {
-      sv[lane] = rv;
-      sid[lane] = rid;
-    }
+    store_slots();
     return;
   }
-  if (!in_regs)
-    for (int j = lane; j < k; j += 64) { sv[j] = -INFINITY; sid[j] = -1; }
-  float mv = -INFINITY;
-  int mi = 0;
-  // the reads of a step are only issued when the step before is scanned
-  // (nothing uses them earlier); `ok` marks the lanes inside the row
+  // the whole row, 64 * BLK logits per step; the reads of a step are only
+  // issued when the step before is scanned (nothing uses them earlier);
+  // `ok` marks the lanes inside the row
   float nx[BLK];
   uint32_t nok = 0;
 #pragma unroll
@@ -906,6 +926,31 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
     nx[q] = rowp[e < vocab ? e : 0];   // always a read inside the row
     nok |= (e < vocab ? 1u : 0u) << q;
   }
+  if (in_regs) {
+    for (int base = 0; base < vocab; base += 64 * BLK) {
+      float x[BLK];
+#pragma unroll
+      for (int q = 0; q < BLK; ++q) x[q] = nx[q];
+      const uint32_t ok = nok;
+      if (base + 64 * BLK < vocab) {
+        nok = 0;
+#pragma unroll
+        for (int q = 0; q < BLK; ++q) {
+          const int e = base + 64 * BLK + q * 64 + lane;
+          nx[q] = rowp[e < vocab ? e : 0];
+          nok |= (e < vocab ? 1u : 0u) << q;
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < BLK; ++q) scan64(((ok >> q) & 1u) ? f2key(x[q]) : 0u, base + q * 64);
+    }
+    store_slots();
+    return;
+  }
+  // k > 64: the slots in LDS, the first minimum found by a wave search
+  for (int j = lane; j < k; j += 64) { sv[j] = -INFINITY; sid[j] = -1; }
+  float mv = -INFINITY;
+  int mj = 0;
   for (int base = 0; base < vocab; base += 64 * BLK) {
     float x[BLK];
 #pragma unroll
@@ -928,19 +973,14 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
         if (!b) break;
         const int L = __ffsll((long long)b) - 1;
         const float vL = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x[q]), L));
-        if (in_regs) {
-          take_min(vL, base + q * 64 + L, mv, mi);
-          done = L;
-          continue;
-        }
         // a wave's LDS accesses complete in program order, so every lane's
         // rescan below observes this store
-        if (lane == 0) { sv[mi] = vL; sid[mi] = base + q * 64 + L; }
+        if (lane == 0) { sv[mj] = vL; sid[mj] = base + q * 64 + L; }
         float bv = INFINITY;
         int bj = 0x7FFFFFFF;
         for (int j = lane; j < k; j += 64) {
-          const float s = sv[j];
-          if (bj == 0x7FFFFFFF || s < bv) { bv = s; bj = j; }
+          const float sj = sv[j];
+          if (bj == 0x7FFFFFFF || sj < bv) { bv = sj; bj = j; }
         }
 #pragma unroll
         for (int m = 32; m > 0; m >>= 1) {
@@ -951,14 +991,10 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
           if (take) { bv = ov; bj = oj; }
         }
         mv = bv;
-        mi = bj;
+        mj = bj;
         done = L;
       }
     }
-  }
-  if (in_regs && lane < k) {
-    sv[lane] = rv;
-    sid[lane] = rid;
   }
 }
 
