@@ -837,10 +837,10 @@ template <int FMT>
 hipError_t launch_tern(GemvArgs g, hipStream_t stream, hipEvent_t *ev, hipEvent_t done) {
   const size_t lds = gemv_tern_lds_bytes(g.K);
   const int ntiles = (g.N + 15) / 16;
+  // one workgroup per CU (its LDS holds two out), at most one per tile
   const int res = resident_blocks(reinterpret_cast<const void *>(gemv_tern_kernel<FMT>),
                                   (uint32_t)lds, 64 * tm::waves<FMT>());
-  int blocks = (ntiles + tm::waves<FMT>() - 1) / tm::waves<FMT>();
-  blocks = blocks < res ? blocks : res;
+  const int blocks = ntiles < res ? ntiles : res;
   const dim3 grid((unsigned)blocks, (unsigned)g.M), block(64 * tm::waves<FMT>());
   if (ev)
     hipExtLaunchKernelGGL(gemv_tern_kernel<FMT>, grid, block, lds, stream, ev[0], ev[1], 0u, g);

@@ -5437,8 +5437,7 @@ struct RecordEpi {
   int nt;               // tiles recorded (wave-uniform)
   __device__ __forceinline__ void out(int lane, int row, float v, bool valid) {
     if (valid && !(rset && fuse_in_set(rset, row))) store_agent(y + row, v);
-    // (the body calls past the wave's last tile with nothing valid; the
-    // launch gives no wave more than kFuseTiles tiles)
+    // (the launch gives no wave more than kFuseTiles tiles)
     if (!__ballot(valid) || nt >= kFuseTiles) return;
     if (lane < 16)
       wbuf[nt * 16 + lane] = make_uint2(__float_as_uint(v), valid ? (uint32_t)row : ~0u);
@@ -5579,9 +5578,7 @@ __device__ __forceinline__ void fuse_rep_set(const FuseArgs &f, int m, int N, in
   }
 }
 
-// (one 16-wave workgroup per CU, where the plain GEMV fits two: its
-// epilogue's scalar registers.  Bounding them to fit two was measured slower:
-// the GEMV part is no faster and the last workgroup gets twice the lists.)
+// (one 16-wave workgroup per CU, as the plain GEMV)
 template <int FMT>
 __global__ __launch_bounds__(64 * tm::waves<FMT>()) void gemv_tern_sample_kernel(GemvArgs g,
                                                                                    FuseArgs f) {
@@ -5810,18 +5807,17 @@ __global__ __launch_bounds__(64 * tm::waves<FMT>()) void gemv_tern_sample_kernel
   finish_wave<4>(a, P, m, y, F, extra, ovf, f.uniforms[m], fs.rsv, fs.rsid, fs.sp, true);
 }
 
-// The fused kernel's grid: as the GEMV's (tiles over resident workgroups);
-// 0 when a wave would get more than kFuseTiles tiles.
+// The fused kernel's grid: as the GEMV's (one workgroup per CU, at most one
+// per tile); 0 when a wave would get more than kFuseTiles tiles.
 template <int FMT>
 int tern_sample_blocks(const GemvArgs &g, size_t lds) {
   constexpr int nw = tm::waves<FMT>();
   const int ntiles = (g.N + 15) / 16;
   const int res = resident_blocks(reinterpret_cast<const void *>(gemv_tern_sample_kernel<FMT>),
                                   (uint32_t)lds, 64 * nw);
-  int blocks = (ntiles + nw - 1) / nw;
-  blocks = blocks < res ? blocks : res;
+  const int blocks = ntiles < res ? ntiles : res;
   const int J = min(64, max(4, (64 + blocks - 1) / blocks));
-  return (ntiles + blocks * nw - 1) / (blocks * nw) <= kFuseTiles && blocks * J <= kFuseLoad &&
+  return tern_out_tiles_max(g.N, g.K, blocks, nw) <= kFuseTiles && blocks * J <= kFuseLoad &&
                  blocks <= kFuseBins
              ? blocks
              : 0;
@@ -5919,8 +5915,7 @@ int tern_argmax_grid(const GemvArgs &g) {
                                        : reinterpret_cast<const void *>(gemv_tern_argmax_kernel<kW_PTQ1_0>);
   const int res = resident_blocks(k, (uint32_t)gemv_tern_lds_bytes(g.K), 64 * nw);
   const int ntiles = (g.N + 15) / 16;
-  const int blocks = (ntiles + nw - 1) / nw;
-  return blocks < res ? blocks : res;
+  return ntiles < res ? ntiles : res;
 }
 
 hipError_t launch_tern_argmax(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
