@@ -24,7 +24,8 @@
 // hand-over lists
 // [kSplitCUs][kPartCap] | their meta data [kSplitCUs] | the split rows'
 // arrival counters [kSplitCUs] (zero between calls) | one region of the
-// device-memory slot replay: keys [kRowMaxVocab], ids [kRowMaxVocab].
+// device-memory slot replay: keys [kRowMaxVocab], ids [kRowMaxVocab], the
+// minima of each 64 slots [kRowMaxVocab / 64].
 namespace na {
 constexpr int kMaxRows = 2048;
 constexpr size_t kPlansOff = 0;
@@ -44,11 +45,14 @@ constexpr size_t kSplitCntBytes = sizeof(uint32_t) * hs::kSplitCUs;
 constexpr size_t kRKeysOff = (kSplitCntOff + kSplitCntBytes + 255) / 256 * 256;
 constexpr size_t kRSlotBytes = sizeof(uint32_t) * hs::kRowMaxVocab;
 constexpr size_t kRIdsOff = kRKeysOff + kRSlotBytes;
-constexpr size_t kBytes = kRIdsOff + kRSlotBytes;
+constexpr size_t kRLvl1Off = kRIdsOff + kRSlotBytes;
+constexpr size_t kRLvl1Bytes = sizeof(unsigned long long) * (hs::kRowMaxVocab / 64);
+constexpr size_t kBytes = kRLvl1Off + kRLvl1Bytes;
 static_assert(kListsOff % 256 == 0 && kRetryOff % 256 == 0 && kReplayOff % 256 == 0 &&
                   kSplitListOff % 256 == 0 &&
                   kSplitMetaOff % 256 == 0 &&
-                  kSplitCntOff % 256 == 0 && kRKeysOff % 256 == 0 && kRIdsOff % 256 == 0,
+                  kSplitCntOff % 256 == 0 && kRKeysOff % 256 == 0 && kRIdsOff % 256 == 0 &&
+                  kRLvl1Off % 256 == 0,
               "scratch layout alignment");
 constexpr int kMaxDevices = 64;
 }  // namespace na
@@ -545,7 +549,8 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
     for (int32_t r : rt.large) big |= plans[(size_t)r].k > hs::kReplayMaxK;
     if (big && n_large > 0) {
       replay_dev = std::min(n_large, hs::kReplayDevBlocks);
-      HS_HIP(ctx->replay_slots.ensure((size_t)replay_dev * (size_t)vocab * 8));
+      HS_HIP(ctx->replay_slots.ensure((size_t)replay_dev * ((size_t)vocab * 8 +
+                                                           (size_t)(vocab + 63) / 64 * 8)));
     }
   }
   // small batches split each row of the row kernel over several workgroups
@@ -569,6 +574,7 @@ int sample_device(hs_context *ctx, float *d_logits, int32_t rows, int64_t row_st
   if (replay_dev > 0) {
     ws.replay_keys = static_cast<uint32_t *>(ctx->replay_slots.p);
     ws.replay_ids = reinterpret_cast<int32_t *>(ws.replay_keys + (size_t)replay_dev * vocab);
+    ws.replay_lvl1 = reinterpret_cast<unsigned long long *>(ws.replay_ids + (size_t)replay_dev * vocab);
   }
   ws.cand = static_cast<uint2 *>(ctx->cand.p);
   ws.cand_count = static_cast<int32_t *>(ctx->cand_count.p);
@@ -965,6 +971,7 @@ int sample_device_noalloc(hs_context *ctx, float *d_logits, int32_t rows, int64_
   ws.split_cnt = reinterpret_cast<uint32_t *>(base + na::kSplitCntOff);
   ws.replay_keys = reinterpret_cast<uint32_t *>(base + na::kRKeysOff);
   ws.replay_ids = reinterpret_cast<int32_t *>(base + na::kRIdsOff);
+  ws.replay_lvl1 = reinterpret_cast<unsigned long long *>(base + na::kRLvl1Off);
 
   hs::LaunchArgs a;
   memset(&a, 0, sizeof a);

@@ -117,10 +117,10 @@ constexpr int kReplayMaxK = 16384;     // slots the LDS replay holds
 constexpr int kReplayCands = 1024;     // candidate positions it can order
 // The replay with its slots in device memory (large_replay_dev_kernel): any
 // k up to kReplayDevMaxK, kReplayDevCands candidate positions, at most
-// kReplayDevBlocks workgroups, each with its own region of vocab keys and
-// vocab ids in the workspace.
+// kReplayDevBlocks workgroups, each with its own region of vocab keys, vocab
+// ids and ceil(vocab / 64) first-level minima in the workspace.
 constexpr int kReplayDev = 4;
-constexpr int kReplayDevMaxK = 1 << 19;
+constexpr int kReplayDevMaxK = 1 << 24;
 constexpr int kReplayDevCands = 8192;
 constexpr int kReplayDevBlocks = 16;
 
@@ -136,6 +136,7 @@ struct Workspace {
   ReplayReq *large_replay;   // [n_large] slot-history replays asked for by large_row
   uint32_t *replay_keys;     // [replay_dev][vocab] slots of the device-memory replay
   int32_t *replay_ids;       // [replay_dev][vocab]
+  unsigned long long *replay_lvl1;  // [replay_dev][ceil(vocab / 64)] minima of 64 slots
   uint2 *cand;               // [n_chunk][S][kChunkCap] (key, index)
   int32_t *cand_count;       // [n_chunk]
   ChunkInfo *info;           // [n_chunk][S]

@@ -4118,18 +4118,20 @@ __global__ __launch_bounds__(kLT) void large_replay_kernel(LaunchArgs a, Workspa
 // The same replay of src/sampler.ts:50-69 for the rows whose k slots do not
 // fit in LDS (k > kReplayMaxK, up to kReplayDevMaxK), or whose candidate
 // outputs need more ordered positions than the LDS replay takes.  The slots'
-// keys and ids live in the workgroup's region of the workspace; the min tree
-// above them (lvl1 over 64 slots, lvl2 over 64 lvl1 entries, a root over at
-// most 128 lvl2 entries) stays in LDS.  The lane that writes a slot is the
-// lane that reads it back (slot & 63), so every read of a slot written
-// during the replay is ordered after that write by the thread's own program
-// order.  The grid holds at most kReplayDevBlocks workgroups, each taking
+// keys and ids, and the first level of the min tree above them (lvl1, the
+// minimum of each 64 slots), live in the workgroup's region of the
+// workspace; lvl2 (over 64 lvl1 entries) and lvl3 (over 64 lvl2 entries,
+// at most 64 of them) stay in LDS, and the root is the minimum of lvl3.
+// The lane that writes a slot or a lvl1 entry is the lane that reads it
+// back (its index & 63), so every read of one written during the replay is
+// ordered after that write by the thread's own program order.  The grid
+// holds at most kReplayDevBlocks workgroups, each taking
 // the requesting rows whose rank among them is its index modulo the grid,
 // one after the other: the workspace needs one region per workgroup, not
 // one per row.
 struct ReplayDevSmem {
-  unsigned long long lvl1[kReplayDevMaxK / 64];
   unsigned long long lvl2[kReplayDevMaxK / 4096];
+  unsigned long long lvl3[64];
   unsigned long long buf[kReplayDevCands];   // the chunk's entering logits, then the sort
   int32_t rows[kLT];                         // this workgroup's rows of a list chunk
   uint32_t wsum[kLT / 64];
@@ -4137,9 +4139,11 @@ struct ReplayDevSmem {
   unsigned long long root;
 };
 size_t replay_dev_smem_bytes() { return sizeof(ReplayDevSmem); }
+static_assert(kReplayDevMaxK <= 64 * 64 * 64 * 64, "lvl3 holds at most 64 entries");
 
 __device__ void replay_dev_row(const LaunchArgs &a, const Workspace &ws, const ReplayReq &req,
-                               int row, uint32_t *keys, int32_t *ids, ReplayDevSmem &sm) {
+                               int row, uint32_t *keys, int32_t *ids,
+                               unsigned long long *lvl1, ReplayDevSmem &sm) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int k = ws.plans[row].k;
   const float *rowp = a.logits + (int64_t)row * a.stride;
@@ -4175,23 +4179,26 @@ __device__ void replay_dev_row(const LaunchArgs &a, const Workspace &ws, const R
   const int filled = total < (uint32_t)k ? (int)total : k;
   for (int s = filled + tid; s < k; s += kLT) { keys[s] = 0u; ids[s] = -1; }
   __syncthreads();
-  const int nl1 = (k + 63) >> 6, nl2 = (nl1 + 63) >> 6;   // nl2 <= 128
+  const int nl1 = (k + 63) >> 6, nl2 = (nl1 + 63) >> 6, nl3 = (nl2 + 63) >> 6;   // nl3 <= 64
   for (int b = wave; b < nl1; b += kLT / 64) {
     const int sl = 64 * b + lane;
     const unsigned long long m = wave_min64(sl < k ? slot_pack(keys[sl], (uint32_t)sl) : kNone);
-    if (lane == 0) sm.lvl1[b] = m;
+    if (lane == (b & 63)) lvl1[b] = m;   // the lane that reads it in the replay
   }
   __syncthreads();
   for (int c = wave; c < nl2; c += kLT / 64) {
     const int i = 64 * c + lane;
-    const unsigned long long m = wave_min64(i < nl1 ? sm.lvl1[i] : kNone);
+    const unsigned long long m = wave_min64(i < nl1 ? lvl1[i] : kNone);
     if (lane == 0) sm.lvl2[c] = m;
   }
   __syncthreads();
   if (wave == 0) {
-    const unsigned long long x0 = lane < nl2 ? sm.lvl2[lane] : kNone;
-    const unsigned long long x1 = lane + 64 < nl2 ? sm.lvl2[lane + 64] : kNone;
-    const unsigned long long m = wave_min64(x0 < x1 ? x0 : x1);
+    for (int d = 0; d < nl3; ++d) {
+      const int i = 64 * d + lane;
+      const unsigned long long m = wave_min64(i < nl2 ? sm.lvl2[i] : kNone);
+      if (lane == 0) sm.lvl3[d] = m;
+    }
+    const unsigned long long m = wave_min64(lane < nl3 ? sm.lvl3[lane] : kNone);
     if (lane == 0) sm.root = m;
   }
   __syncthreads();
@@ -4220,20 +4227,23 @@ __device__ void replay_dev_row(const LaunchArgs &a, const Workspace &ws, const R
           keys[s] = kv;
           ids[s] = (int32_t)(uint32_t)item;
         }
-        const uint32_t ks = sl == s ? kv : (sl < k ? keys[sl] : 0u);
-        const unsigned long long m1 = wave_min64(sl < k ? slot_pack(ks, (uint32_t)sl) : kNone);
         const int b2 = b1 >> 6, i1 = 64 * b2 + lane;
-        const unsigned long long m2 =
-            wave_min64(i1 < nl1 ? (i1 == b1 ? m1 : sm.lvl1[i1]) : kNone);
-        const unsigned long long y0 = lane < nl2 ? (lane == b2 ? m2 : sm.lvl2[lane]) : kNone;
-        const unsigned long long y1 =
-            lane + 64 < nl2 ? (lane + 64 == b2 ? m2 : sm.lvl2[lane + 64]) : kNone;
-        const unsigned long long m3 = wave_min64(y0 < y1 ? y0 : y1);
+        // both device reads go out before the first minimum
+        const uint32_t ks = sl == s ? kv : (sl < k ? keys[sl] : 0u);
+        const unsigned long long l1 = i1 < nl1 && i1 != b1 ? lvl1[i1] : kNone;
+        const unsigned long long m1 = wave_min64(sl < k ? slot_pack(ks, (uint32_t)sl) : kNone);
+        const unsigned long long m2 = wave_min64(i1 == b1 ? m1 : l1);
+        if (i1 == b1) lvl1[b1] = m1;
+        const int b3 = b2 >> 6, i2 = 64 * b3 + lane;
+        const unsigned long long m3 =
+            wave_min64(i2 < nl2 ? (i2 == b2 ? m2 : sm.lvl2[i2]) : kNone);
+        const unsigned long long m4 =
+            wave_min64(lane < nl3 ? (lane == b3 ? m3 : sm.lvl3[lane]) : kNone);
         if (lane == 0) {
-          sm.lvl1[b1] = m1;
           sm.lvl2[b2] = m2;
+          sm.lvl3[b3] = m3;
         }
-        top = m3;
+        top = m4;
       }
       if (lane == 0) sm.root = top;
     }
@@ -4319,6 +4329,7 @@ __global__ __launch_bounds__(kLT) void large_replay_dev_kernel(LaunchArgs a, Wor
   const int tid = threadIdx.x, G = (int)gridDim.x, g = (int)blockIdx.x;
   uint32_t *keys = ws.replay_keys + (int64_t)g * a.vocab;
   int32_t *ids = ws.replay_ids + (int64_t)g * a.vocab;
+  unsigned long long *lvl1 = ws.replay_lvl1 + (int64_t)g * ((a.vocab + 63) / 64);
   int seen = 0;   // requesting rows in the list chunks before this one
   for (int c0 = 0; c0 < a.n_large; c0 += kLT) {
     const int i = c0 + tid;
@@ -4335,7 +4346,7 @@ __global__ __launch_bounds__(kLT) void large_replay_dev_kernel(LaunchArgs a, Wor
     __syncthreads();
     for (int j = 0; j < mine; ++j) {
       const int li = sm.rows[j];
-      replay_dev_row(a, ws, ws.large_replay[li], ws.large_list[li], keys, ids, sm);
+      replay_dev_row(a, ws, ws.large_replay[li], ws.large_list[li], keys, ids, lvl1, sm);
     }
     __syncthreads();   // sm.rows and wsum are rewritten by the next chunk
   }

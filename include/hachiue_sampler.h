@@ -60,11 +60,11 @@ typedef struct hs_sample_config {
 #define HS_ROW_REPLAYED     0x2u /* exact replace-min replay was needed (ties) */
 #define HS_ROW_TIES         0x4u /* equal values among or at the candidates */
 #define HS_ROW_SINGLE       0x8u /* 0 or 1 candidate: no draw consumed */
-#define HS_ROW_UNSUPPORTED 0x10u /* top-k > 524288 (a vocab above that) below the
-                                    finite count with a group of equal values at
-                                    the drawn position: the reference orders it by
-                                    its slot history, which this build replays for
-                                    top-k up to 524288; token is -1.  Also set
+#define HS_ROW_UNSUPPORTED 0x10u /* top-k > 16777216 (a vocab above that) below
+                                    the finite count with a group of equal values
+                                    at the drawn position: the reference orders it
+                                    by its slot history, which this build replays
+                                    for top-k up to 16777216; token is -1.  Also set
                                     (token kept) when candidate outputs would need
                                     more than 8192 slot-ordered positions or more
                                     than 2048 positions above the last listed

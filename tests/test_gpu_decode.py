@@ -173,16 +173,41 @@ def test_decode_large_k_ties_resolved(sampler):
     st.free()
 
 
-def test_decode_unresolved_row_keeps_state(sampler):
-    """A row the sampler leaves unresolved (HS_ROW_UNSUPPORTED, token -1:
-    top-k above the replay's 2^19 slots on a vocabulary larger than that,
-    with the draw in a group of equal logits) reports -1 in a decode step
-    and keeps its history, length and done flag, while the other row
-    advances."""
+def test_decode_large_k_ties_beyond_2_19_resolved(sampler):
+    """Top-k above 2^19 on a vocabulary larger than that, with the draw in
+    a group of equal logits: the device-memory replay orders the group
+    (src/sampler.ts:55-74), and the decode step appends the oracle's token."""
     V = 600000
     logits = np.zeros((2, V), np.float32)
     logits[1] = np.random.default_rng(3).standard_normal(V).astype(np.float32)
     cfgs = [dict(temperature=1.0, topK=550000.0, topP=0.95), dict(temperature=0.0)]
+    uni = np.array([0.999, 0.5])
+    st = DecodeState(sampler, [[1, 2], [3]], [], ring_cap=128)
+    d_l = hip.DeviceArray.from_numpy(logits)
+    d_u = hip.DeviceArray.from_numpy(uni)
+    d_t = hip.DeviceArray(2, np.int32)
+    print("[gpu] decode large-k ties beyond 2^19", flush=True)
+    st.step(d_l.addr, V, V, cfgs, d_u.addr, d_t.addr)
+    hip.synchronize()
+    tok = d_t.download().tolist()
+    want = o.sample_batch(logits.copy(), V, None, None, cfgs, uni).token
+    assert tok == list(want)
+    assert st.lengths().tolist() == [3, 2]
+    assert st.history(0).tolist() == [1, 2, tok[0]]
+    assert st.history(1).tolist() == [3, tok[1]]
+    st.free()
+
+
+def test_decode_unresolved_row_keeps_state(sampler):
+    """A row the sampler leaves unresolved (HS_ROW_UNSUPPORTED, token -1:
+    top-k above the replay's 2^24 slots on a vocabulary larger than that,
+    with the draw in a group of equal logits) reports -1 in a decode step
+    and keeps its history, length and done flag, while the other row
+    advances."""
+    V = (1 << 24) + 1024
+    logits = np.zeros((2, V), np.float32)
+    logits[1, ::4099] = np.random.default_rng(3).standard_normal(logits[1, ::4099].size)
+    cfgs = [dict(temperature=1.0, topK=float((1 << 24) + 1), topP=0.95), dict(temperature=0.0)]
     st = DecodeState(sampler, [[1, 2], [3]], [], ring_cap=128)
     d_l = hip.DeviceArray.from_numpy(logits)
     d_u = hip.DeviceArray.from_numpy(np.array([0.999, 0.5]))
@@ -191,8 +216,9 @@ def test_decode_unresolved_row_keeps_state(sampler):
     st.step(d_l.addr, V, V, cfgs, d_u.addr, d_t.addr)
     hip.synchronize()
     tok = d_t.download().tolist()
-    want = o.sample_batch(logits.copy(), V, None, None, cfgs, np.array([0.999, 0.5])).token
-    assert tok[1] == want[1]
+    # the greedy row alone through the oracle
+    want = o.sample_batch(logits[1:].copy(), V, None, None, cfgs[1:], np.array([0.5])).token
+    assert tok[1] == want[0]
     assert tok[0] == -1
     assert st.lengths().tolist() == [2, 2]
     assert st.history(0).tolist() == [1, 2]

@@ -209,6 +209,22 @@ def test_large_k_ties_replayed(sampler, k):
         assert (got.flags & HS_ROW_REPLAYED).any()
 
 
+def test_large_k_ties_beyond_2_19(sampler):
+    """Top-k above 2^19 on a 600000-logit vocabulary of coarse values (a few
+    dozen distinct ones): the device-memory replay's four-level min tree,
+    tokens and candidate ids equal to the oracle's."""
+    rng = np.random.default_rng(11)
+    rows, vocab = 2, 600000
+    logits = np.round(rng.standard_normal((rows, vocab)) * 3).astype(np.float32)
+    configs = [dict(temperature=1.0, topK=550000, topP=0.9),
+               dict(temperature=0.7, topK=530000, topP=0.99)]
+    u = np.array([0.999, 0.31])
+    for want in (True, False):
+        got, _ = _check(sampler, logits, vocab, None, None, configs, u, 64,
+                        "ties k > 2^19", want_cands=want)
+        assert (got.flags & HS_ROW_REPLAYED).all()
+
+
 @pytest.mark.parametrize("k,cap", [(5000, 2000), (30000, 1500)])
 def test_large_k_ties_long_candidate_lists(sampler, k, cap):
     """More candidate positions with ties than the LDS replay orders (1024):
