@@ -187,9 +187,13 @@ struct hs_context {
   DevBuf split_list, split_meta, split_cnt;   // split rows (split_cnt: zero between calls)
   DevBuf gemv_part, gemv_cnt;   // Q6_K GEMV tiles cut between waves (gemv_cnt: zero between calls)
   DevBuf gemv_rot;              // the Hadamard-rotated input of a folded weight
-  DevBuf fuse_rows, fuse_pool;  // lm_head GEMV that samples its rows: counters (zero
-                                //   between calls), the merge tree's lists
-  bool fuse = true;             // HS_LMHEAD_FUSE=0 at creation: always two launches
+  DevBuf fuse_rows, fuse_pool, fuse_hist;   // lm_head GEMV that samples its rows: counters
+                                //   (zero between calls), the waves' two largest, the
+                                //   rows' key histograms (zero between calls)
+  // HS_LMHEAD_FUSE at creation: 0 always two launches; 1 (default) one
+  // launch for qualifying rows on planar lm_heads and for all-greedy calls
+  // on Q6_K ones; 2 also for Q6_K sampling rows
+  int fuse = 1;
   DevBuf large_retry;           // two-pass large-k rows handed back
   DevBuf large_replay;          // slot-history replays asked for by the large-k kernel
   DevBuf replay_slots;          // the device-memory replay's regions: keys, then ids
@@ -1110,7 +1114,7 @@ int hs_context_create(int device, hs_context **out) {
   ctx->device = device;
   if (const char *env = getenv("HS_ROW_KERNEL_MIN_ROWS")) ctx->row_min_rows = atoi(env);
   if (const char *env = getenv("HS_ROW_SPLIT")) ctx->row_split = atoi(env);
-  if (const char *env = getenv("HS_LMHEAD_FUSE")) ctx->fuse = atoi(env) != 0;
+  if (const char *env = getenv("HS_LMHEAD_FUSE")) ctx->fuse = atoi(env);
   e = hipEventCreateWithFlags(&ctx->plan_done, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->done_ev, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->na_upload_ev, hipEventDisableTiming);
@@ -1263,37 +1267,24 @@ int hs_gemv_device_ex(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx,
   return gemv_device(ctx, d_x, M, ldx, w, d_y, ldy, static_cast<hipStream_t>(stream));
 }
 
-int hs_lm_head_sample_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32_t K,
-                             const void *d_w, int32_t w_type, int32_t N, float *d_logits,
-                             int64_t ldl, const int32_t *d_hist_ids, const int64_t *d_hist_offsets,
-                             const hs_sample_config *configs, const double *d_uniforms,
-                             int32_t *d_tokens, void *stream) {
-  HS_LOCK(ctx);
-  if (hs::tern_quant_bytes(w_type) > 0)
-    return fail(HS_ERR_INVALID_ARGUMENT, "weight type %d is planar: use hs_lm_head_sample_device_ex",
-                w_type);
-  const hipStream_t st = static_cast<hipStream_t>(stream);
-  const hs_weights w = raw_weights(K, d_w, w_type, N);
-  int rc = gemv_device(ctx, d_x, M, ldx, &w, d_logits, ldl, st);
-  if (rc) return rc;
-  return sample_device(ctx, d_logits, M, ldl, N, d_hist_ids, d_hist_offsets, configs, d_uniforms,
-                       d_tokens, 0, nullptr, nullptr, nullptr, nullptr, nullptr, st);
-}
-
 namespace {
 
 // The lm_head GEMV and the sampler on its M rows: one launch of the planar
-// GEMV that samples its own rows when every row is greedy or takes k <= 64
-// candidates with at most the repetition penalty (and the vocabulary fits
-// its per-wave record); otherwise the GEMV, then hs_sample_batch_device.
-// Either way the logits hold the penalised values afterwards.
+// or Q6_K GEMV that samples its own rows when every row is greedy or takes
+// k <= 64 candidates with at most the repetition penalty (and the vocabulary
+// fits its per-wave record); otherwise the GEMV, then
+// hs_sample_batch_device.  Either way the logits hold the penalised values
+// afterwards.  On a Q6_K lm_head the one launch is taken by default only
+// when every row is greedy: with sampling rows its merge (the last of 512
+// workgroups) takes longer than the sampler's own launch.
 int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const hs_weights *w,
                    float *d_logits, int64_t ldl, const int32_t *d_hist_ids,
                    const int64_t *d_hist_offsets, const hs_sample_config *configs,
                    const double *d_uniforms, int32_t *d_tokens, hipStream_t st) {
   if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
   if (!w) return fail(HS_ERR_INVALID_ARGUMENT, "null weights");
-  bool fused = ctx->fuse && hs::tern_quant_bytes(w->type) > 0 && M > 0 && w->rows > 0 && configs &&
+  const bool tern = hs::tern_quant_bytes(w->type) > 0;
+  bool fused = ctx->fuse && (tern || w->type == hs::kW_Q6_K) && M > 0 && w->rows > 0 && configs &&
                d_uniforms && d_tokens && (d_hist_ids == nullptr) == (d_hist_offsets == nullptr);
   std::vector<hs::RowPlan> plans;
   Routing rt;
@@ -1304,11 +1295,14 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
     } catch (const std::bad_alloc &) {
       return fail(HS_ERR_OUT_OF_MEMORY, "host allocation failed");
     }
-    for (const hs::RowPlan &p : plans)
+    for (const hs::RowPlan &p : plans) {
       if ((p.mode != hs::kModeGreedy && p.mode != hs::kModeSmall) || (p.pen & hs::kPenPF))
         fused = false;
+      if (!tern && ctx->fuse < 2 && p.mode != hs::kModeGreedy) fused = false;
+    }
   }
-  bool greedy = fused;   // every row greedy: the GEMV keeps the argmax alone
+  // every row greedy on a planar lm_head: the GEMV keeps the argmax alone
+  bool greedy = fused && tern;
   for (const hs::RowPlan &p : plans) greedy = greedy && p.mode == hs::kModeGreedy;
   if (fused) {
     DeviceGuard guard(ctx->device);
@@ -1318,11 +1312,19 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
     bool skip = false;
     rc = gemv_setup(ctx, d_x, M, ldx, w, d_logits, ldl, st, g, &skip);
     if (rc) return rc;
-    const int blocks = skip ? 0 : greedy ? hs::tern_argmax_grid(g) : hs::tern_sample_grid(g);
+    const int blocks = skip     ? 0
+                       : greedy ? hs::tern_argmax_grid(g)
+                       : tern   ? hs::tern_sample_grid(g)
+                                : hs::q6k_sample_grid(g);
     if (blocks > 0) {
-      const size_t nl = greedy ? 0 : (size_t)M * blocks;
-      if (!greedy)
-        HS_HIP(ctx->fuse_pool.ensure(nl * 64 * sizeof(unsigned long long) + nl * sizeof(uint32_t)));
+      const size_t nwv = greedy ? 0 : (size_t)M * blocks * hs::fuse_waves_per_block(w->type);
+      if (!greedy) {
+        HS_HIP(ctx->fuse_pool.ensure(nwv * (2 * sizeof(unsigned long long) +
+                                            hs::kFuseTileWords * sizeof(int32_t))));
+        // histograms: zero between calls (each is cleared by the workgroup that reads it)
+        rc = ensure_zeroed(ctx->fuse_hist, (size_t)M * hs::kFuseHist * sizeof(uint32_t), st);
+        if (rc) return rc;
+      }
       // counters: zero between calls (each is reset by the workgroup that counts last)
       rc = ensure_zeroed(ctx->fuse_rows, (size_t)M * sizeof(hs::FuseRow), st);
       if (rc) return rc;
@@ -1335,14 +1337,16 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
       f.uniforms = d_uniforms;
       f.tokens = d_tokens;
       f.rows = static_cast<hs::FuseRow *>(ctx->fuse_rows.p);
-      f.list = greedy ? nullptr : static_cast<unsigned long long *>(ctx->fuse_pool.p);
-      f.disc = greedy ? nullptr : reinterpret_cast<uint32_t *>(f.list + nl * 64);
+      f.wtop = greedy ? nullptr : static_cast<unsigned long long *>(ctx->fuse_pool.p);
+      f.wtiles = greedy ? nullptr : reinterpret_cast<int32_t *>(f.wtop + 2 * nwv);
+      f.hist = greedy ? nullptr : static_cast<uint32_t *>(ctx->fuse_hist.p);
       f.blocks = blocks;
       hipEvent_t *ev = nullptr;
       rc = timed_slot(ctx, hs::kGemvTimedSlot, &ev);
       if (rc) return rc;
       const hipError_t e = greedy ? hs::launch_tern_argmax(g, f, st, ev, ctx->done_ev)
-                                  : hs::launch_tern_sample(g, f, st, ev, ctx->done_ev);
+                           : tern ? hs::launch_tern_sample(g, f, st, ev, ctx->done_ev)
+                                  : hs::launch_q6k_sample(g, f, st, ev, ctx->done_ev);
       if (e != hipSuccess) {
         (void)leave_stream(ctx, st, false);
         return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
@@ -1358,6 +1362,20 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
 }
 
 }  // namespace
+
+int hs_lm_head_sample_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, int32_t K,
+                             const void *d_w, int32_t w_type, int32_t N, float *d_logits,
+                             int64_t ldl, const int32_t *d_hist_ids, const int64_t *d_hist_offsets,
+                             const hs_sample_config *configs, const double *d_uniforms,
+                             int32_t *d_tokens, void *stream) {
+  HS_LOCK(ctx);
+  if (hs::tern_quant_bytes(w_type) > 0)
+    return fail(HS_ERR_INVALID_ARGUMENT, "weight type %d is planar: use hs_lm_head_sample_device_ex",
+                w_type);
+  const hs_weights w = raw_weights(K, d_w, w_type, N);
+  return lm_head_sample(ctx, d_x, M, ldx, &w, d_logits, ldl, d_hist_ids, d_hist_offsets, configs,
+                        d_uniforms, d_tokens, static_cast<hipStream_t>(stream));
+}
 
 int hs_lm_head_sample_device_ex(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx,
                                 const hs_weights *w, float *d_logits, int64_t ldl,

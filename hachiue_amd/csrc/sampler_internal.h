@@ -291,6 +291,12 @@ struct FuseRow {
 static_assert(sizeof(FuseRow) == 16, "FuseRow layout");
 constexpr int kFuseTiles = 8;     // 16-row tiles a wave of the fused GEMV records
 constexpr int kFuseStage = 1024;  // entries the last workgroup ranks
+constexpr int kFuseHist = 4096;   // bins of a row's key histogram (the keys' top 12 bits)
+constexpr int kFuseWavesPerThread = 8;   // waves' entries a thread of the last workgroup reads
+// Per wave of a row: the tiles it recorded, [0] their count, [1 + e] tile
+// e (rows tile * 16 .. tile * 16 + 15).
+constexpr int kFuseTileWords = 16;
+static_assert(kFuseTileWords >= kFuseTiles + 1, "a wave's tiles fit");
 struct FuseArgs {
   const RowPlan *plans;      // [M]: greedy or k <= 64, repetition penalty only
   const int32_t *hist_ids;   // packed lists (hist_off[m], hist_off[m + 1]) or null
@@ -298,8 +304,10 @@ struct FuseArgs {
   const double *uniforms;    // [M]
   int32_t *tokens;           // [M]
   FuseRow *rows;             // [M]
-  unsigned long long *list;  // [M][blocks][64] each workgroup's top 64
-  uint32_t *disc;            // [M][blocks] and the largest key it left out
+  unsigned long long *wtop;  // [M][2][Bw]: each wave's largest, then its second largest
+                             //   packed candidate (Bw = blocks * waves per workgroup)
+  int32_t *wtiles;           // [M][Bw][kFuseTileWords] the tiles each wave recorded
+  uint32_t *hist;            // [M][kFuseHist] workgroup maxima by key bin, zero between calls
   int32_t blocks;            // workgroups per activation row
 };
 hipError_t launch_tern_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
@@ -312,5 +320,11 @@ int tern_argmax_grid(const GemvArgs &g);
 // Its workgroups per activation row, or 0 when N needs more tiles per wave
 // than it records (then the two-launch path is used).
 int tern_sample_grid(const GemvArgs &g);
+// Waves per workgroup of the one-launch kernel for lm_head weights of `type`.
+int fuse_waves_per_block(int type);
+// The same one launch for Q6_K lm_heads (greedy rows included), and its grid.
+hipError_t launch_q6k_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
+                             hipEvent_t *ev, hipEvent_t done);
+int q6k_sample_grid(const GemvArgs &g);
 
 }  // namespace hs

@@ -47,6 +47,7 @@
 #include <math.h>
 
 #include "hachiue_sampler.h"
+#include "q6k_gemv.h"
 #include "tern_gemv.h"
 
 namespace hs {
@@ -5392,23 +5393,26 @@ __global__ __launch_bounds__(kRowThreads) void argmax_kernel(LaunchArgs a, Works
 // GEMV's loop a tile's results are only written as logits and recorded in
 // the wave's LDS buffer.  After the loop each wave penalises its recorded
 // results where the row's history asks for it (src/sampler.ts:24-33: the
-// last 128 ids, each distinct id once; the logit is written again) and keeps
-// their top 64; the workgroup merges its waves' lists and publishes its own
-// top 64, with the largest key it left out (`disc`).  The last workgroup to
-// count itself in takes as a bound the 64th largest of the lists' first J
-// entries (J = 1 with 64 or more lists: the workgroups' maxima, distinct
-// logits, so the row has at least 64 at or above it), gathers the entries at
-// or above it (a few dozen on common rows), ranks them, and runs the row
-// kernel's tail (wave_tail, with the slot replay over the written logits
-// when equal values decide the draw).
-// Exactness, as for split rows: every logit of the row's top k (k <= 64) is
-// in its wave's and its workgroup's top 64, and at or above the bound; a
-// value equal to the k-th largest left out of a list shows as that list's
-// disc, which flags the boundary tie.  More than kFuseStage entries at or
-// above the bound (many equal values) send the row to the replay.  Greedy
-// rows keep the packed maximum instead.  No workgroup waits for another:
-// each publishes with agent-scope stores, waits for them, then counts
-// itself in; the one that counts last reads.
+// last 128 ids, each distinct id once; the logit is written again) and
+// publishes its two largest packed candidates (value, then index: distinct)
+// with the tiles it recorded; the workgroup counts its largest in the row's
+// histogram of keys (kFuseHist bins of the keys' top 12 bits, in device
+// memory; one atomic per workgroup: per wave they queued on the few bins
+// the maxima share).  The last workgroup to count itself in reads the
+// histogram and every wave's two largest in one round trip.  The
+// workgroups' maxima are distinct logits of the row, so the bin b* holding
+// the 64th largest of them bounds the row's 64th largest from below: every
+// logit of the row's top 64 (and every logit equal to its k-th largest,
+// k <= 64) lies in a bin >= b*.  Such a logit is its wave's maximum, or
+// else its wave's second largest lies there too, and that wave's tiles are
+// read again from the written logits.  The candidates gathered are ranked and the row kernel's
+// tail runs on the top 64 (wave_tail, with the slot replay over the written
+// logits when equal values decide the draw: the 65th largest candidate
+// equal to the k-th, or more than kFuseStage candidates).  Greedy rows keep
+// the packed maximum instead.  No workgroup waits for another: each
+// publishes with agent-scope stores, waits for them, then counts itself in;
+// the one that counts last reads, and clears the histogram for the next
+// call.
 
 constexpr int kFuseSetSlots = 256;   // repetition ids of a row (at most 128)
 __device__ __forceinline__ uint32_t fuse_hash(int id) {
@@ -5428,7 +5432,8 @@ __device__ __forceinline__ bool fuse_in_set(const int32_t *set, int id) {
 struct FuseSmem {
   int32_t rset[kFuseSetSlots];
   unsigned long long best[16];
-  uint32_t disc, bound, key64, lo, hi;
+  uint32_t wsum[16];
+  uint32_t key64;
   int32_t last, nf, bin, nmore;
   unsigned long long top[64];
   float rsv[64];
@@ -5443,116 +5448,27 @@ struct FuseSmem {
 // result.
 struct RecordEpi {
   float *y;
-  uint2 *wbuf;          // kFuseTiles * 16 entries
+  uint2 *wbuf;          // cap * 16 entries
   const int32_t *rset;  // the repetition ids, or null
   int nt;               // tiles recorded (wave-uniform)
+  int cap;              // tiles the buffer holds
   __device__ __forceinline__ void out(int lane, int row, float v, bool valid) {
     if (valid && !(rset && fuse_in_set(rset, row))) store_agent(y + row, v);
-    // (the launch gives no wave more than kFuseTiles tiles)
-    if (!__ballot(valid) || nt >= kFuseTiles) return;
+    // (the launch gives no wave more than cap tiles)
+    if (!__ballot(valid) || nt >= cap) return;
     if (lane < 16)
       wbuf[nt * 16 + lane] = make_uint2(__float_as_uint(v), valid ? (uint32_t)row : ~0u);
     ++nt;
   }
 };
 
-constexpr int kFuseLoad = 2048;   // list entries the last workgroup loads at first
-constexpr int kFuseBins = 1024;
-// LDS: the GEMV body's, the waves' result buffers, then the histogram and
-// the candidates; the last workgroup's loads reuse the body's and the
-// buffers' (at least kFuseLoad entries).
-__host__ __device__ inline size_t fuse_extra_off(int K, int nw) {
-  const size_t rec = gemv_tern_lds_bytes(K) + (size_t)nw * kFuseTiles * 16 * sizeof(uint2);
-  const size_t ld = (size_t)kFuseLoad * sizeof(unsigned long long);
-  return rec > ld ? rec : ld;
-}
+constexpr int kFuseMore = 1024;   // waves whose tiles the last workgroup reads again
+// LDS: the GEMV body's, the waves' result buffers, then the list of waves
+// read again, the candidates and their ranks.
 size_t tern_sample_lds_bytes(int K, int nw) {
-  return fuse_extra_off(K, nw) + kFuseBins * sizeof(uint32_t) + (size_t)kFuseStage * sizeof(unsigned long long);
-}
-
-// The top 64 of the n packed candidates at src (0: none) into fs.top
-// (descending, zeros past the count), the 65th's key into fs.key64 and the
-// largest key of the others into fs.disc.  The 64th largest key is bounded
-// from below by a histogram of the keys over [their least, their largest]
-// (kFuseBins bins, each bin's keys above the previous bin's): the entries in
-// the bins from the top down to where 64 are reached are compacted into
-// `cand` and ranked by comparison (a few dozen on common rows).  False when
-// more than `cap` reach it (many equal keys).  Every thread calls it.
-template <int NT>
-__device__ bool block_top64(const unsigned long long *src, int n, uint32_t *bins,
-                            unsigned long long *cand, int cap, FuseSmem &fs) {
-  const int tid = threadIdx.x, lane = tid & 63;
-  if (tid == 0) { fs.lo = ~0u; fs.hi = 0u; fs.bin = -1; fs.nf = 0; fs.key64 = 0u; fs.disc = 0u; }
-  for (int i = tid; i < kFuseBins; i += NT) bins[i] = 0u;
-  for (int i = tid; i < 64; i += NT) fs.top[i] = 0ull;
-  __syncthreads();
-  {
-    uint32_t lo = ~0u, hi = 0u;
-    for (int i = tid; i < n; i += NT) {
-      const uint32_t kx = cand_key(src[i]);
-      if (kx) { lo = kx < lo ? kx : lo; hi = kx > hi ? kx : hi; }
-    }
-    lo = ~wave_max_u32(~lo);
-    hi = wave_max_u32(hi);
-    if (lane == 0 && hi) { atomicMin(&fs.lo, lo); atomicMax(&fs.hi, hi); }
-  }
-  __syncthreads();
-  const uint32_t klo = fs.lo, khi = fs.hi;
-  const float bscale = (float)kFuseBins / ((float)(khi - klo) + 1.0f);
-  auto bin_of = [&](uint32_t kx) { return min(kFuseBins - 1, (int)((float)(kx - klo) * bscale)); };
-  if (khi)
-    for (int i = tid; i < n; i += NT) {
-      const uint32_t kx = cand_key(src[i]);
-      if (kx) atomicAdd(&bins[bin_of(kx)], 1u);
-    }
-  __syncthreads();
-  if (tid < 64 && khi) {   // wave 0: from the top bin down to where 64 keys are reached
-    uint32_t cum = 0;
-    for (int top = kFuseBins - 1; top >= 0; top -= 64) {
-      const int bb = top - lane;
-      const uint32_t cnt = bb >= 0 ? bins[bb] : 0u;
-      const uint32_t incl = wave_scan_incl(cnt);
-      const uint32_t tot = readlane_u32(incl, 63);
-      if (cum + tot >= 64u) {
-        const unsigned long long mk = __ballot(cum + incl >= 64u);
-        if (lane == 0) fs.bin = top - (__ffsll((long long)mk) - 1);
-        break;
-      }
-      cum += tot;
-    }
-  }
-  __syncthreads();
-  const int bstar = fs.bin < 0 ? 0 : fs.bin;   // fewer than 64 keys: all of them
-  uint32_t dm = 0u;
-  for (int i0 = 0; i0 < n; i0 += NT) {
-    const int i = i0 + tid;
-    const unsigned long long x = i < n ? src[i] : 0ull;
-    const uint32_t kx = cand_key(x);
-    const bool keep = kx != 0u && bin_of(kx) >= bstar;
-    if (kx && !keep) dm = kx > dm ? kx : dm;
-    const unsigned long long bl = __ballot(keep);
-    if (bl) {
-      int base = 0;
-      if (lane == 0) base = atomicAdd(&fs.nf, __popcll(bl));
-      base = __shfl(base, 0);
-      const int p = base + (int)lanes_below(bl);
-      if (keep && p < cap) cand[p] = x;
-    }
-  }
-  dm = wave_max_u32(dm);
-  if (lane == 0 && dm) atomicMax(&fs.disc, dm);
-  __syncthreads();
-  const int nc = fs.nf;
-  if (nc > cap) return false;
-  for (int i = tid; i < nc; i += NT) {
-    const unsigned long long xi = cand[i];
-    int rank = 0;
-    for (int j = 0; j < nc; ++j) rank += cand[j] > xi ? 1 : 0;
-    if (rank < 64) fs.top[rank] = xi;
-    if (rank == 64) fs.key64 = cand_key(xi);
-  }
-  __syncthreads();
-  return true;
+  return gemv_tern_lds_bytes(K) + (size_t)nw * kFuseTiles * 16 * sizeof(uint2) +
+         (size_t)kFuseMore * sizeof(int32_t) +
+         (size_t)kFuseStage * (sizeof(unsigned long long) + sizeof(int32_t));
 }
 
 // Counts the calling workgroup in at *cnt (after its published stores
@@ -5589,64 +5505,54 @@ __device__ __forceinline__ void fuse_rep_set(const FuseArgs &f, int m, int N, in
   }
 }
 
-// (one 16-wave workgroup per CU, as the plain GEMV)
-template <int FMT>
-__global__ __launch_bounds__(64 * tm::waves<FMT>()) void gemv_tern_sample_kernel(GemvArgs g,
-                                                                                   FuseArgs f) {
-  constexpr int NW = tm::waves<FMT>(), NT = 64 * NW;
-  extern __shared__ uint4 tlds[];
-  __shared__ FuseSmem fs;
+// After the GEMV loop of a workgroup whose waves recorded their tiles'
+// results (RecordEpi: at most `tiles` tiles a wave, wave w's at
+// rec + w * tiles * 16, the calling wave's count `nt`): the row's sampling,
+// as described above.  `more` (kFuseMore entries) and `cand` (kFuseStage
+// candidates, then kFuseStage ranks) are LDS the GEMV body no longer uses,
+// disjoint from each other and from the record buffers.  Every thread calls
+// it.
+template <int NW>
+__device__ void fuse_sample_finish(const GemvArgs &g, const FuseArgs &f, int m, int nt, int tiles,
+                                   const uint2 *rec, int32_t *more, unsigned long long *cand,
+                                   FuseSmem &fs) {
+  constexpr int NT = 64 * NW;
+  constexpr int HB = kFuseHist / NT;        // histogram bins a thread reads
+  constexpr int WPT = kFuseWavesPerThread;  // waves' entries a thread reads
+  static_assert(kFuseHist % NT == 0, "whole bins per thread");
+  // ---- this wave's results as packed candidates (penalties applied): its
+  // maximum, and for sampling rows its second largest too
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m = (int)blockIdx.y;
   const RowPlan *plan = f.plans + m;
   const int mode = load_scalar(&plan->mode);
   const bool rep = (load_scalar(&plan->pen) & kPenRep) != 0;
   float *y = g.y + (int64_t)m * g.ldy;
-
-  // the row's repetition set: history.slice(-128), ids in [0, N)
-  if (tid < kFuseSetSlots) fs.rset[tid] = -1;
-  if (tid == 0) fs.disc = 0u;
-  __syncthreads();
-  if (rep) fuse_rep_set(f, m, g.N, fs.rset);
-  // (the body's first barrier completes the set)
-
-  uint2 *wbuf = reinterpret_cast<uint2 *>(reinterpret_cast<uint8_t *>(tlds) + gemv_tern_lds_bytes(g.K)) +
-                wave * kFuseTiles * 16;
-  RecordEpi epi{y, wbuf, rep ? fs.rset : nullptr, 0};
-  tern_gemv_body<FMT>(g, tlds, epi);
-
-  // ---- this wave's results as packed candidates in its buffer (penalties
-  // applied; unused slots 0), or its maximum
+  const uint2 *wbuf = rec + wave * tiles * 16;
   const bool greedy = mode == kModeGreedy;
   const double prep = load_scalar(&plan->rep);
-  const int ne = epi.nt * 16;
-  unsigned long long *cb = reinterpret_cast<unsigned long long *>(wbuf);   // the same slots
-  unsigned long long best = 0ull;
-  for (int e = lane; e < kFuseTiles * 16; e += 64) {
-    unsigned long long c = 0ull;
-    if (e < ne) {
-      const uint2 r = wbuf[e];
-      float v = __uint_as_float(r.x);
-      if (r.y != ~0u) {
-        if (rep && fuse_in_set(fs.rset, (int)r.y)) {
-          RowPlan pr{};
-          pr.rep = prep;
-          pr.pen = kPenRep;
-          v = penalise(v, true, 0u, pr);
-          store_agent(y + r.y, v);
-        }
-        const uint32_t key = f2key(v);
-        c = key ? pack_cand(key, r.y) : 0ull;
-      }
+  const int ne = nt * 16;
+  unsigned long long m1 = 0ull, m2 = 0ull;   // this lane's largest two
+  for (int e = lane; e < ne; e += 64) {
+    const uint2 r = wbuf[e];
+    float v = __uint_as_float(r.x);
+    if (r.y == ~0u) continue;
+    if (rep && fuse_in_set(fs.rset, (int)r.y)) {
+      RowPlan pr{};
+      pr.rep = prep;
+      pr.pen = kPenRep;
+      v = penalise(v, true, 0u, pr);
+      store_agent(y + r.y, v);
     }
-    if (greedy) best = c > best ? c : best;
-    else cb[e] = c;
+    const uint32_t key = f2key(v);
+    const unsigned long long c = key ? pack_cand(key, r.y) : 0ull;
+    if (c > m1) {
+      m2 = m1;
+      m1 = c;
+    } else if (c > m2) {
+      m2 = c;
+    }
   }
-  __syncthreads();   // every wave is done with the body's LDS and its buffer
   FuseRow *fr = f.rows + m;
-  unsigned long long *buf = reinterpret_cast<unsigned long long *>(tlds);
-  uint32_t *bins = reinterpret_cast<uint32_t *>(reinterpret_cast<uint8_t *>(tlds) + fuse_extra_off(g.K, NW));
-  unsigned long long *xcand = reinterpret_cast<unsigned long long *>(bins + kFuseBins);   // kFuseStage
   LaunchArgs a{};
   a.logits = g.y;
   a.stride = g.ldy;
@@ -5656,7 +5562,7 @@ __global__ __launch_bounds__(64 * tm::waves<FMT>()) void gemv_tern_sample_kernel
   a.tokens = f.tokens;
 
   if (greedy) {   // the packed maximum; the last workgroup writes the token
-    const unsigned long long b = wave_max64(best);
+    const unsigned long long b = wave_max64(m1);
     if (lane == 0) fs.best[wave] = b;
     __syncthreads();
     if (tid == 0) {
@@ -5673,96 +5579,79 @@ __global__ __launch_bounds__(64 * tm::waves<FMT>()) void gemv_tern_sample_kernel
     return;
   }
 
-  // ---- the workgroup's top 64, published (its disc: the largest key left
-  // out; ~0u marks a workgroup whose candidates did not fit, the row is
-  // then replayed)
-  const unsigned long long *wsrc = reinterpret_cast<const unsigned long long *>(
-      reinterpret_cast<uint8_t *>(tlds) + gemv_tern_lds_bytes(g.K));
-  const bool fit = block_top64<NT>(wsrc, NW * kFuseTiles * 16, bins, xcand, kFuseStage, fs);
-  const int64_t r0 = (int64_t)m * f.blocks;
-  if (wave == 0) {
-    store_agent(f.list + (r0 + blockIdx.x) * 64 + lane, fit ? fs.top[lane] : 0ull);
-    const uint32_t d = fs.disc > fs.key64 ? fs.disc : fs.key64;
-    if (lane == 0) store_agent(f.disc + r0 + blockIdx.x, fit ? d : ~0u);
+  // ---- the wave's two largest (distinct: the index is packed in) and its
+  // tiles; the workgroup's largest counted in the row's histogram
+  const int Bw = f.blocks * NW;
+  unsigned long long *wx0 = f.wtop + (int64_t)m * 2 * Bw, *wx1 = wx0 + Bw;
+  int32_t *wt = f.wtiles + (int64_t)m * Bw * kFuseTileWords;
+  uint32_t *hist = f.hist + (int64_t)m * kFuseHist;
+  {
+    const unsigned long long x0 = wave_max64(m1);
+    const unsigned long long x1 = wave_max64(m1 == x0 ? m2 : m1);
+    const int wg = (int)blockIdx.x * NW + wave;
+    if (lane == 0) {
+      store_agent(wx0 + wg, x0);
+      store_agent(wx1 + wg, x1);
+      fs.best[wave] = x0;
+    }
+    // [0]: the count; [1 + e]: tile e, whose first lane holds its first row
+    if (lane <= nt)
+      store_agent(wt + (int64_t)wg * kFuseTileWords + lane,
+                  lane == 0 ? nt : (int32_t)(wbuf[(lane - 1) * 16].y >> 4));
+    __syncthreads();
+    if (tid == 0) {
+      unsigned long long bb = 0ull;
+      for (int w = 0; w < NW; ++w) bb = fs.best[w] > bb ? fs.best[w] : bb;
+      if (bb)
+        __hip_atomic_fetch_add(hist + (cand_key(bb) >> 20), 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   if (!fuse_arrive(&fr->arrived, (uint32_t)f.blocks, fs)) return;
 
-  // ---- the row, by the last workgroup.  The first J entries of every list
-  // (J = 4, or more when there are fewer than 16 lists, so that J * B >= 64)
-  // are distinct logits of the row, so the 64th
-  // largest of them bounds the row's 64th largest from below.  It is found
-  // by a histogram over [their least key, their largest key] (kFuseBins
-  // bins, each bin's keys above the previous bin's), then the least loaded
-  // key in the bins from the top down to where 64 are reached.  Every entry
-  // at or above it is then among the loaded ones, or in a list whose J-th
-  // entry reaches it (read whole).
-  const int B = f.blocks;
-  const unsigned long long *lists = f.list + r0 * 64;
-  const int J = min(64, max(4, (64 + B - 1) / B));   // J * B <= kFuseLoad: the launch checks
-  const int nk = B * J;
-  unsigned long long *ld = buf;                                         // kFuseLoad entries
-  unsigned long long *cand = xcand;                                     // kFuseStage entries
-  if (tid == 0) { fs.bound = ~0u; fs.disc = 0u; fs.nf = 0; fs.key64 = 0u; fs.lo = ~0u; fs.hi = 0u; fs.bin = -1; }
-  for (int i = tid; i < kFuseBins; i += NT) bins[i] = 0u;
-  __syncthreads();
-  {
-    uint32_t lo = ~0u, hi = 0u, dm = 0u;
-    for (int t = tid; t < nk; t += NT) {
-      const int i = t / J, j = t - i * J;
-      const unsigned long long x = load_agent(lists + (int64_t)i * 64 + j);
-      ld[t] = x;
-      const uint32_t kx = cand_key(x);
-      if (kx) { lo = kx < lo ? kx : lo; hi = kx > hi ? kx : hi; }
-      if (j == 0) {
-        const uint32_t d = load_agent(f.disc + r0 + i);
-        dm = d > dm ? d : dm;
-      }
-    }
-    lo = ~wave_max_u32(~lo);
-    hi = wave_max_u32(hi);
-    dm = wave_max_u32(dm);
-    if (lane == 0) {
-      if (dm) atomicMax(&fs.disc, dm);
-      if (hi) { atomicMin(&fs.lo, lo); atomicMax(&fs.hi, hi); }
-    }
+  // ---- the row, by the last workgroup: the histogram and the waves' two
+  // largest in one round trip
+  uint32_t hc[HB];
+  unsigned long long w0[WPT], w1[WPT];
+#pragma unroll
+  for (int i = 0; i < HB; ++i) hc[i] = load_agent(hist + tid * HB + i);
+#pragma unroll
+  for (int i = 0; i < WPT; ++i) {
+    const int w = tid + i * NT;
+    w0[i] = w < Bw ? load_agent(wx0 + w) : 0ull;
+    w1[i] = w < Bw ? load_agent(wx1 + w) : 0ull;
   }
-  __syncthreads();
-  const uint32_t klo = fs.lo, khi = fs.hi;
-  const float bscale = (float)kFuseBins / ((float)(khi - klo) + 1.0f);
-  auto bin_of = [&](uint32_t kx) { return min(kFuseBins - 1, (int)((float)(kx - klo) * bscale)); };
-  if (khi) {
-    for (int t = tid; t < nk; t += NT) {
-      const uint32_t kx = cand_key(ld[t]);
-      if (kx) atomicAdd(&bins[bin_of(kx)], 1u);
-    }
+  uint32_t tsum = 0;
+#pragma unroll
+  for (int i = 0; i < HB; ++i) {
+    tsum += hc[i];
+    store_agent(hist + tid * HB + i, 0u);   // zero for the next call
   }
-  __syncthreads();
-  if (wave == 0 && khi) {   // from the top bin down to where 64 keys are reached
-    uint32_t cum = 0;
-    for (int top = kFuseBins - 1; top >= 0; top -= 64) {
-      const int bb = top - lane;
-      const uint32_t cnt = bb >= 0 ? bins[bb] : 0u;
-      const uint32_t incl = wave_scan_incl(cnt);
-      const uint32_t tot = readlane_u32(incl, 63);
-      if (cum + tot >= 64u) {
-        const unsigned long long mk = __ballot(cum + incl >= 64u);
-        if (lane == 0) fs.bin = top - (__ffsll((long long)mk) - 1);
+  if (tid == 0) { fs.bin = 0; fs.nf = 0; fs.nmore = 0; fs.key64 = 0u; }
+  int32_t *rnk = reinterpret_cast<int32_t *>(cand + kFuseStage);
+  for (int i = tid; i < kFuseStage; i += NT) rnk[i] = 0;
+  for (int i = tid; i < 64; i += NT) fs.top[i] = 0ull;
+  // b*: the bin where the count of workgroup maxima from the top reaches 64
+  // (0 when there are fewer); thread t holds bins t * HB .. t * HB + HB - 1
+  const uint32_t incl = block_scan_incl<NT>(tsum, fs.wsum);
+  uint32_t total = 0;
+  for (int w = 0; w < NW; ++w) total += fs.wsum[w];
+  const uint32_t above = total - incl;   // in the bins of later threads
+  if (above < 64u && above + tsum >= 64u) {
+    uint32_t cum = above;
+#pragma unroll
+    for (int i = HB - 1; i >= 0; --i) {
+      cum += hc[i];
+      if (cum >= 64u) {
+        fs.bin = tid * HB + i;
         break;
       }
-      cum += tot;
     }
   }
   __syncthreads();
-  const int bstar = fs.bin;   // -1: fewer than 64 loaded keys, every entry counts
-  if (bstar >= 0) {
-    for (int t = tid; t < nk; t += NT) {
-      const uint32_t kx = cand_key(ld[t]);
-      if (kx && bin_of(kx) >= bstar) atomicMin(&fs.bound, kx);
-    }
-  }
-  __syncthreads();
-  const uint32_t bound = bstar >= 0 ? fs.bound : 1u;
-  auto add = [&](bool keep, unsigned long long x) {
+  const uint32_t bstar = (uint32_t)fs.bin;
+  auto in = [&](unsigned long long c) { return c != 0ull && (cand_key(c) >> 20) >= bstar; };
+  auto add = [&](bool keep, unsigned long long x) {   // every lane of the wave calls it
     const unsigned long long bl = __ballot(keep);
     if (!bl) return;
     int base = 0;
@@ -5771,36 +5660,62 @@ __global__ __launch_bounds__(64 * tm::waves<FMT>()) void gemv_tern_sample_kernel
     const int p = base + (int)lanes_below(bl);
     if (keep && p < kFuseStage) cand[p] = x;
   };
-  for (int t0 = 0; t0 < nk; t0 += NT) {
-    const int t = t0 + tid;
-    const unsigned long long x = t < nk ? ld[t] : 0ull;
-    add(x != 0ull && cand_key(x) >= bound, x);
+#pragma unroll
+  for (int i = 0; i < WPT; ++i) {
+    add(in(w0[i]), w0[i]);
+    if (in(w1[i])) {
+      const int q = atomicAdd(&fs.nmore, 1);
+      if (q < kFuseMore) more[q] = tid + i * NT;
+    }
   }
-  // lists whose J-th entry reaches the bound: the rest of the list (rare)
-  uint32_t *more = bins;   // the histogram is no longer needed
-  if (tid == 0) fs.nmore = 0;
   __syncthreads();
-  if (J < 64)
-    for (int i = tid; i < B; i += NT)
-      if (cand_key(ld[i * J + J - 1]) >= bound) more[atomicAdd(&fs.nmore, 1)] = (uint32_t)i;
-  __syncthreads();
-  for (int q = wave; q < fs.nmore; q += NW) {
-    const int i = (int)more[q];
-    const unsigned long long x = lane >= J ? load_agent(lists + (int64_t)i * 64 + lane) : 0ull;
-    add(x != 0ull && cand_key(x) >= bound, x);
+  // the waves with a second logit at b* or above: their tiles again, from
+  // the written logits (a few waves on common rows)
+  const int nmore = fs.nmore;
+  for (int q = wave; q < nmore && q < kFuseMore; q += NW) {
+    const int w = more[q];
+    const int32_t *tw = wt + (int64_t)w * kFuseTileWords;
+    const int ntw = load_agent(tw);
+    const unsigned long long x0w = load_agent(wx0 + w);   // listed already
+    for (int p = 0; p < ntw; p += 4) {
+      const int e = p + (lane >> 4);
+      unsigned long long c = 0ull;
+      if (e < ntw) {
+        const int row = load_agent(tw + 1 + e) * 16 + (lane & 15);
+        if (row < g.N) {
+          const uint32_t key = f2key(load_agent(y + row));
+          c = key ? pack_cand(key, (uint32_t)row) : 0ull;
+        }
+      }
+      add(c != x0w && in(c), c);
+    }
   }
   __syncthreads();
   const int nf = fs.nf;
-  const bool ovf = nf > kFuseStage || fs.disc == ~0u;
+  const bool ovf = nf > kFuseStage || nmore > kFuseMore;
   const int n = ovf ? 0 : nf;
-  unsigned long long *stage = cand;
-  // the top 64 and the 65th (ranks by comparison: n is small)
-  for (int i = tid; i < 64; i += NT) fs.top[i] = 0ull;
-  __syncthreads();
+  // the top 64 and the 65th: each candidate's rank is the count of larger
+  // ones, split over S threads a candidate when there are few (a few
+  // hundred on common rows)
+  const int S = n > 0 && 2 * n <= NT ? min(16, NT / n) : 1;
+  if (S > 1) {
+    const int i = tid / S, sl = tid - i * S;
+    if (i < n) {
+      const unsigned long long xi = cand[i];
+      int cnt = 0;
+      for (int j = sl; j < n; j += S) cnt += cand[j] > xi ? 1 : 0;
+      atomicAdd(&rnk[i], cnt);
+    }
+    __syncthreads();
+  }
   for (int i = tid; i < n; i += NT) {
-    const unsigned long long xi = stage[i];
+    const unsigned long long xi = cand[i];
     int rank = 0;
-    for (int j = 0; j < n; ++j) rank += stage[j] > xi ? 1 : 0;
+    if (S > 1) {
+      rank = rnk[i];
+    } else {
+      for (int j = 0; j < n; ++j) rank += cand[j] > xi ? 1 : 0;
+    }
     if (rank < 64) fs.top[rank] = xi;
     if (rank == 64) fs.key64 = cand_key(xi);
   }
@@ -5813,13 +5728,41 @@ __global__ __launch_bounds__(64 * tm::waves<FMT>()) void gemv_tern_sample_kernel
   P.min_p = load_scalar(&plan->min_p);
   P.k = load_scalar(&plan->k);
   const uint32_t Tk = cand_key(__shfl(F, P.k - 1));
-  const bool extra = Tk != 0u && (fs.key64 == Tk || fs.disc == Tk);
+  const bool extra = Tk != 0u && fs.key64 == Tk;
   // (a replay here is rare: fewer logits in flight keep the GEMV's registers)
   finish_wave<4>(a, P, m, y, F, extra, ovf, f.uniforms[m], fs.rsv, fs.rsid, fs.sp, true);
 }
 
+// (one 16-wave workgroup per CU, as the plain GEMV)
+template <int FMT>
+__global__ __launch_bounds__(64 * tm::waves<FMT>()) void gemv_tern_sample_kernel(GemvArgs g,
+                                                                                   FuseArgs f) {
+  constexpr int NW = tm::waves<FMT>();
+  extern __shared__ uint4 tlds[];
+  __shared__ FuseSmem fs;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int m = (int)blockIdx.y;
+  const bool rep = (load_scalar(&f.plans[m].pen) & kPenRep) != 0;
+  float *y = g.y + (int64_t)m * g.ldy;
+
+  // the row's repetition set: history.slice(-128), ids in [0, N)
+  if (tid < kFuseSetSlots) fs.rset[tid] = -1;
+  __syncthreads();
+  if (rep) fuse_rep_set(f, m, g.N, fs.rset);
+  // (the body's first barrier completes the set)
+
+  uint8_t *lb = reinterpret_cast<uint8_t *>(tlds);
+  uint2 *rec = reinterpret_cast<uint2 *>(lb + gemv_tern_lds_bytes(g.K));
+  RecordEpi epi{y, rec + wave * kFuseTiles * 16, rep ? fs.rset : nullptr, 0, kFuseTiles};
+  tern_gemv_body<FMT>(g, tlds, epi);
+  int32_t *more = reinterpret_cast<int32_t *>(rec + NW * kFuseTiles * 16);
+  fuse_sample_finish<NW>(g, f, m, epi.nt, kFuseTiles, rec, more,
+                         reinterpret_cast<unsigned long long *>(more + kFuseMore), fs);
+}
+
 // The fused kernel's grid: as the GEMV's (one workgroup per CU, at most one
-// per tile); 0 when a wave would get more than kFuseTiles tiles.
+// per tile); 0 when a wave would get more than kFuseTiles tiles or the last
+// workgroup's threads more than kFuseWavesPerThread waves' entries.
 template <int FMT>
 int tern_sample_blocks(const GemvArgs &g, size_t lds) {
   constexpr int nw = tm::waves<FMT>();
@@ -5827,9 +5770,8 @@ int tern_sample_blocks(const GemvArgs &g, size_t lds) {
   const int res = resident_blocks(reinterpret_cast<const void *>(gemv_tern_sample_kernel<FMT>),
                                   (uint32_t)lds, 64 * nw);
   const int blocks = ntiles < res ? ntiles : res;
-  const int J = min(64, max(4, (64 + blocks - 1) / blocks));
-  return tern_out_tiles_max(g.N, g.K, blocks, nw) <= kFuseTiles && blocks * J <= kFuseLoad &&
-                 blocks <= kFuseBins
+  return tern_out_tiles_max(g.N, g.K, blocks, nw) <= kFuseTiles &&
+                 blocks * nw <= kFuseWavesPerThread * 64 * nw
              ? blocks
              : 0;
 }
@@ -5976,6 +5918,87 @@ hipError_t launch_tern_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t 
   }
 }
 
+// ---- the Q6_K lm_head GEMV that samples its rows
+//
+// gemv_tern_sample_kernel on the Q6_K body (q6k_gemv.h): two 8-wave
+// workgroups per CU, each recording at most kQ6FuseTiles tiles a wave in
+// buffers that follow the body's LDS.  After the loop the slab rings are
+// free: the last workgroup's loads, the histogram and the candidates go
+// there.  All-greedy calls take it too (its greedy branch keeps each
+// workgroup's packed maximum).
+constexpr int kQ6FuseTiles = 4;
+__host__ __device__ inline size_t q6k_ring_off(int K) {   // the A tables, then the rings
+  return (size_t)(K / 64) * 256 + (size_t)(K / 16) * 32;
+}
+size_t q6k_sample_lds_bytes(int K) {
+  return gemv_q6k_mfma_lds_bytes(K) + (size_t)q6m::kWaves * kQ6FuseTiles * 16 * sizeof(uint2);
+}
+static_assert((size_t)q6m::kWaves * q6m::kNB * q6m::kSlabBytes >=
+                  (size_t)kFuseMore * 4 + (size_t)kFuseStage * 12,
+              "the rings hold the waves read again and the candidates");
+
+__global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_sample_kernel(GemvArgs g, FuseArgs f) {
+  constexpr int NW = q6m::kWaves;
+  extern __shared__ uint4 qlds[];
+  __shared__ FuseSmem fs;
+  const int tid = threadIdx.x, wave = tid >> 6;
+  const int m = (int)blockIdx.y;
+  const bool rep = (load_scalar(&f.plans[m].pen) & kPenRep) != 0;
+  float *y = g.y + (int64_t)m * g.ldy;
+
+  // the row's repetition set: history.slice(-128), ids in [0, N)
+  if (tid < kFuseSetSlots) fs.rset[tid] = -1;
+  __syncthreads();
+  if (rep) fuse_rep_set(f, m, g.N, fs.rset);
+  // (the body's first barrier completes the set)
+
+  uint8_t *lb = reinterpret_cast<uint8_t *>(qlds);
+  uint2 *rec = reinterpret_cast<uint2 *>(lb + gemv_q6k_mfma_lds_bytes(g.K));
+  RecordEpi epi{y, rec + wave * kQ6FuseTiles * 16, rep ? fs.rset : nullptr, 0, kQ6FuseTiles};
+  q6k_gemv_body(g, lb, epi);
+  int32_t *more = reinterpret_cast<int32_t *>(lb + q6k_ring_off(g.K));   // the rings
+  fuse_sample_finish<NW>(g, f, m, epi.nt, kQ6FuseTiles, rec, more,
+                         reinterpret_cast<unsigned long long *>(more + kFuseMore), fs);
+}
+
+// Its grid: as the Q6_K GEMV's (gemv_q6k_mfma_kernel's launch); 0 when a
+// wave would complete more than kQ6FuseTiles tiles (its whole tiles and at
+// most one part of a tail tile) or the last workgroup's threads would read
+// more than kFuseWavesPerThread waves' entries.
+int q6k_sample_grid(const GemvArgs &g) {
+  const size_t lds = q6k_sample_lds_bytes(g.K);
+  const int ntiles = (g.N + 15) / 16;
+  const int res = resident_blocks(reinterpret_cast<const void *>(gemv_q6k_sample_kernel),
+                                  (uint32_t)lds, q6m::kThreads);
+  int blocks = (ntiles + q6m::kWaves - 1) / q6m::kWaves;
+  blocks = blocks < res ? blocks : res;
+  blocks = blocks < g.part_cap / q6m::kWaves ? blocks : g.part_cap / q6m::kWaves;
+  if (blocks < 1 || !g.part || !g.tile_cnt) return 0;
+  const int nw = blocks * q6m::kWaves;
+  const int tiles = ntiles / nw + (ntiles % nw ? 1 : 0);
+  return tiles <= kQ6FuseTiles && nw <= kFuseWavesPerThread * q6m::kThreads ? blocks : 0;
+}
+
+int fuse_waves_per_block(int type) { return type == kW_Q6_K ? q6m::kWaves : 16; }
+static_assert(tm::waves<kW_Q1_0>() == 16 && tm::waves<kW_PQ2_0>() == 16 &&
+                  tm::waves<kW_PTQ1_0>() == 16,
+              "fuse_waves_per_block: the planar kernels' waves");
+
+hipError_t launch_q6k_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
+                             hipEvent_t *ev, hipEvent_t done) {
+  const int blocks = q6k_sample_grid(g);
+  if (blocks < 1 || blocks != f.blocks) return hipErrorInvalidValue;
+  const size_t lds = q6k_sample_lds_bytes(g.K);
+  const dim3 grid((unsigned)blocks, (unsigned)g.M), block(q6m::kThreads);
+  if (ev)
+    hipExtLaunchKernelGGL(gemv_q6k_sample_kernel, grid, block, lds, stream, ev[0], ev[1], 0u, g, f);
+  else if (done)
+    hipExtLaunchKernelGGL(gemv_q6k_sample_kernel, grid, block, lds, stream, nullptr, done, 0u, g, f);
+  else
+    hipLaunchKernelGGL(gemv_q6k_sample_kernel, grid, block, lds, stream, g, f);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------- launch
 
 hipError_t prepare_kernels() {
@@ -6010,6 +6033,10 @@ hipError_t prepare_kernels() {
       if ((e = hipFuncSetAttribute(fk, hipFuncAttributeMaxDynamicSharedMemorySize,
                                    (int)tern_sample_lds_bytes(kGemvMaxK, 16))) != hipSuccess)
         return e;
+    if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q6k_sample_kernel),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)q6k_sample_lds_bytes(kGemvMaxK))) != hipSuccess)
+      return e;
     const void *ak[3] = {reinterpret_cast<const void *>(&gemv_tern_argmax_kernel<kW_Q1_0>),
                          reinterpret_cast<const void *>(&gemv_tern_argmax_kernel<kW_PQ2_0>),
                          reinterpret_cast<const void *>(&gemv_tern_argmax_kernel<kW_PTQ1_0>)};
