@@ -344,7 +344,14 @@ def other_path(args) -> int:
     step, timed like the sampler."""
     from hachiue_amd import Sampler, hip, workloads
 
-    sampler = Sampler(0)
+    if args.path == "lmhead-sample":   # one launch for the sampling rows too (HS_LMHEAD_FUSE=2)
+        os.environ["HS_LMHEAD_FUSE"] = "2"
+        try:
+            sampler = Sampler(0)
+        finally:
+            del os.environ["HS_LMHEAD_FUSE"]
+    else:
+        sampler = Sampler(0)
     stream = hip.Stream()
 
     def n_sets(set_bytes: int) -> int:   # as in main(): past twice the last-level cache

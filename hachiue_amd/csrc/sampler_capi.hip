@@ -191,8 +191,7 @@ struct hs_context {
                                 //   (zero between calls), the waves' two largest, the
                                 //   rows' key histograms (zero between calls)
   // HS_LMHEAD_FUSE at creation: 0 always two launches; 1 (default) one
-  // launch for qualifying rows on planar lm_heads and for all-greedy calls
-  // on Q6_K ones; 2 also for Q6_K sampling rows
+  // launch for all-greedy calls; 2 also for calls with k <= 64 sampling rows
   int fuse = 1;
   DevBuf large_retry;           // two-pass large-k rows handed back
   DevBuf large_replay;          // slot-history replays asked for by the large-k kernel
@@ -1274,9 +1273,9 @@ namespace {
 // k <= 64 candidates with at most the repetition penalty (and the vocabulary
 // fits its per-wave record); otherwise the GEMV, then
 // hs_sample_batch_device.  Either way the logits hold the penalised values
-// afterwards.  On a Q6_K lm_head the one launch is taken by default only
-// when every row is greedy: with sampling rows its merge (the last of 512
-// workgroups) takes longer than the sampler's own launch.
+// afterwards.  By default the one launch is taken only when every row is
+// greedy: with sampling rows its merge (the last workgroup of the row) takes
+// about as long as the sampler's own launch, or longer.
 int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const hs_weights *w,
                    float *d_logits, int64_t ldl, const int32_t *d_hist_ids,
                    const int64_t *d_hist_offsets, const hs_sample_config *configs,
@@ -1298,7 +1297,7 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
     for (const hs::RowPlan &p : plans) {
       if ((p.mode != hs::kModeGreedy && p.mode != hs::kModeSmall) || (p.pen & hs::kPenPF))
         fused = false;
-      if (!tern && ctx->fuse < 2 && p.mode != hs::kModeGreedy) fused = false;
+      if (ctx->fuse < 2 && p.mode != hs::kModeGreedy) fused = false;
     }
   }
   // every row greedy on a planar lm_head: the GEMV keeps the argmax alone

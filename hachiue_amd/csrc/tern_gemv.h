@@ -143,9 +143,12 @@ __device__ __forceinline__ uint32_t tern_bfi4(uint32_t a, uint32_t b, uint32_t c
 // A lane's share of one block (its quant dwords), loaded a few items ahead
 // of use.
 template <int FMT> struct TernSlot;
-template <> struct TernSlot<kW_Q1_0> { static constexpr int kDepth = 6; uint32_t q[4]; };
+// (depths measured at 151936 x 2048, interleaved runs, kernel median: Q1_0
+// 6 -> 4 took 17.6 -> 15.9 us, PTQ1_0 3 -> 2 25.4 -> 23.4 us; PQ2_0 from 2
+// to 4 within 0.4 us; deeper was slower for all three)
+template <> struct TernSlot<kW_Q1_0> { static constexpr int kDepth = 4; uint32_t q[4]; };
 template <> struct TernSlot<kW_PQ2_0> { static constexpr int kDepth = 4; uint32_t q[8]; };
-template <> struct TernSlot<kW_PTQ1_0> { static constexpr int kDepth = 3; uint32_t q[7]; };
+template <> struct TernSlot<kW_PTQ1_0> { static constexpr int kDepth = 2; uint32_t q[7]; };
 
 // The kernel body: y row m = blockIdx.y of x W^T.  Workgroup b of the grid
 // takes the tiles b, b + G, b + 2G, ... of the T tiles of 16 rows, in

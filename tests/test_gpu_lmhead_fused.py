@@ -29,8 +29,8 @@ def unfused():
 
 @pytest.fixture(scope="module")
 def fctx():
-    """A context that takes the one launch wherever it applies (Q6_K
-    sampling rows too; by default those take two launches)."""
+    """A context that takes the one launch wherever it applies (sampling
+    rows too; by default those take two launches)."""
     s = _context({"HS_LMHEAD_FUSE": "2"})
     yield s
     s.close()
@@ -143,7 +143,7 @@ def test_fused_equal_logits_replay(sampler, fctx, fmt):
     assert tok.tolist() == res.token.tolist()
 
 
-def test_fused_hadamard_folded_and_mixed_rows(sampler, unfused):
+def test_fused_hadamard_folded_and_mixed_rows(sampler, fctx, unfused):
     """A folded PQ2_0 lm_head (the rotation runs first); then a batch with a
     k > 64 row, which takes the two launches, gives the same results."""
     wtype, K, N = o.W_PQ2_0, 1024, 151669
@@ -156,7 +156,7 @@ def test_fused_hadamard_folded_and_mixed_rows(sampler, unfused):
                   dict(temperature=0.0), dict(topK=10)],
                  [dict(temperature=0.7, topK=40), dict(temperature=1.0, topK=300, topP=0.95),
                   dict(temperature=0.0)]):
-        tok, pen, ids, off = lm_head_sample(sampler, wtype, x, w, N, hists, cfgs, u, hadamard=True)
+        tok, pen, ids, off = lm_head_sample(fctx, wtype, x, w, N, hists, cfgs, u, hadamard=True)
         raw, ref, res = expect(sampler, wtype, x, w, N, ids, off, cfgs, u, hadamard=True)
         assert np.array_equal(pen.view(np.uint32), ref.view(np.uint32))
         ok = (tok == res.token) | (res.draw_margin < 1e-6)
@@ -195,13 +195,13 @@ def test_fused_repeated_calls_reset_state(sampler, fctx, fmt):
 def test_fused_is_one_launch(sampler, fctx, unfused, fmt, cfg):
     """The qualifying call launches the lm_head kernel alone (the sampler's
     kernels do not run); the two-launch context also runs the sampler's
-    kernel.  By default a Q6_K call with a sampling row takes two launches.
+    kernel.  By default a call with a sampling row takes two launches.
     Every call gives the oracle's token."""
     wtype, K, N = FUSED[fmt], 256, 20000
     rng = np.random.default_rng(2)
     w = random_blocks(wtype, N, K, rng, scale=0.05)
     x = rng.standard_normal((1, K)).astype(np.float32)
-    default_fused = fmt != "q6_k" or cfg.get("temperature", 0.6) <= 0
+    default_fused = cfg.get("temperature", 0.6) <= 0
     for ctx, fused in ((fctx, True), (sampler, default_fused), (unfused, False)):
         ctx.set_timing(True)
         ctx.kernel_times()
