@@ -1300,8 +1300,8 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
       if (ctx->fuse < 2 && p.mode != hs::kModeGreedy) fused = false;
     }
   }
-  // every row greedy on a planar lm_head: the GEMV keeps the argmax alone
-  bool greedy = fused && tern;
+  // every row greedy: the GEMV keeps the argmax alone
+  bool greedy = fused;
   for (const hs::RowPlan &p : plans) greedy = greedy && p.mode == hs::kModeGreedy;
   if (fused) {
     DeviceGuard guard(ctx->device);

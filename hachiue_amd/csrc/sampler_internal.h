@@ -312,8 +312,9 @@ struct FuseArgs {
 };
 hipError_t launch_tern_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
                               hipEvent_t *ev, hipEvent_t done);
-// Every row greedy: the GEMV keeps each workgroup's packed maximum, the last
-// one writes the token (no candidate lists: f.list, f.disc, f.blocks unused).
+// Every row greedy (planar or Q6_K weights): the GEMV keeps each
+// workgroup's packed maximum, the last one writes the token (no candidate
+// lists: f.wtop, f.wtiles, f.hist, f.blocks unused).
 hipError_t launch_tern_argmax(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
                               hipEvent_t *ev, hipEvent_t done);
 int tern_argmax_grid(const GemvArgs &g);

@@ -5811,25 +5811,16 @@ struct ArgmaxEpi {
   }
 };
 
-template <int FMT>
-__global__ __launch_bounds__(64 * tm::waves<FMT>())
-void gemv_tern_argmax_kernel(GemvArgs g, FuseArgs f) {
-  constexpr int NW = tm::waves<FMT>();
-  extern __shared__ uint4 tlds[];
-  __shared__ int32_t rset[kFuseSetSlots];
-  __shared__ unsigned long long wbest[NW];
+// The end of an all-greedy fused GEMV (every thread calls it, after the
+// body): the workgroup's packed maximum into the row's word, then the count;
+// the last workgroup writes the token.
+template <int NW>
+__device__ __forceinline__ void fuse_argmax_finish(const GemvArgs &g, const FuseArgs &f, int m,
+                                                   unsigned long long best,
+                                                   unsigned long long *wbest) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m = (int)blockIdx.y;
-  const RowPlan *plan = f.plans + m;
-  const bool rep = (load_scalar(&plan->pen) & kPenRep) != 0;
   float *y = g.y + (int64_t)m * g.ldy;
-  if (tid < kFuseSetSlots) rset[tid] = -1;
-  __syncthreads();
-  if (rep) fuse_rep_set(f, m, g.N, rset);
-  // (the body's first barrier completes the set)
-  ArgmaxEpi epi{y, rep ? rset : nullptr, load_scalar(&plan->rep), 0ull};
-  tern_gemv_body<FMT>(g, tlds, epi);
-  const unsigned long long b = wave_max64(epi.best);
+  const unsigned long long b = wave_max64(best);
   if (lane == 0) wbest[wave] = b;
   __syncthreads();
   FuseRow *fr = f.rows + m;
@@ -5860,7 +5851,57 @@ void gemv_tern_argmax_kernel(GemvArgs g, FuseArgs f) {
   }
 }
 
+template <int FMT>
+__global__ __launch_bounds__(64 * tm::waves<FMT>())
+void gemv_tern_argmax_kernel(GemvArgs g, FuseArgs f) {
+  constexpr int NW = tm::waves<FMT>();
+  extern __shared__ uint4 tlds[];
+  __shared__ int32_t rset[kFuseSetSlots];
+  __shared__ unsigned long long wbest[NW];
+  const int tid = threadIdx.x;
+  const int m = (int)blockIdx.y;
+  const RowPlan *plan = f.plans + m;
+  const bool rep = (load_scalar(&plan->pen) & kPenRep) != 0;
+  if (tid < kFuseSetSlots) rset[tid] = -1;
+  __syncthreads();
+  if (rep) fuse_rep_set(f, m, g.N, rset);
+  // (the body's first barrier completes the set)
+  ArgmaxEpi epi{g.y + (int64_t)m * g.ldy, rep ? rset : nullptr, load_scalar(&plan->rep), 0ull};
+  tern_gemv_body<FMT>(g, tlds, epi);
+  fuse_argmax_finish<NW>(g, f, m, epi.best, wbest);
+}
+
+// The same on the Q6_K body (its grid and LDS as gemv_q6k_mfma_kernel's).
+__global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_argmax_kernel(GemvArgs g, FuseArgs f) {
+  constexpr int NW = q6m::kWaves;
+  extern __shared__ uint4 qlds[];
+  __shared__ int32_t rset[kFuseSetSlots];
+  __shared__ unsigned long long wbest[NW];
+  const int tid = threadIdx.x;
+  const int m = (int)blockIdx.y;
+  const RowPlan *plan = f.plans + m;
+  const bool rep = (load_scalar(&plan->pen) & kPenRep) != 0;
+  if (tid < kFuseSetSlots) rset[tid] = -1;
+  __syncthreads();
+  if (rep) fuse_rep_set(f, m, g.N, rset);
+  // (the body's first barrier completes the set)
+  ArgmaxEpi epi{g.y + (int64_t)m * g.ldy, rep ? rset : nullptr, load_scalar(&plan->rep), 0ull};
+  q6k_gemv_body(g, reinterpret_cast<uint8_t *>(qlds), epi);
+  fuse_argmax_finish<NW>(g, f, m, epi.best, wbest);
+}
+
+int q6k_argmax_grid(const GemvArgs &g) {
+  const int ntiles = (g.N + 15) / 16;
+  const int res = resident_blocks(reinterpret_cast<const void *>(gemv_q6k_argmax_kernel),
+                                  (uint32_t)gemv_q6k_mfma_lds_bytes(g.K), q6m::kThreads);
+  int blocks = (ntiles + q6m::kWaves - 1) / q6m::kWaves;
+  blocks = blocks < res ? blocks : res;
+  blocks = blocks < g.part_cap / q6m::kWaves ? blocks : g.part_cap / q6m::kWaves;
+  return blocks >= 1 && g.part && g.tile_cnt ? blocks : 0;
+}
+
 int tern_argmax_grid(const GemvArgs &g) {
+  if (g.type == kW_Q6_K) return q6k_argmax_grid(g);
   const int nw = g.type == kW_Q1_0 ? tm::waves<kW_Q1_0>()
                  : g.type == kW_PQ2_0 ? tm::waves<kW_PQ2_0>() : tm::waves<kW_PTQ1_0>();
   const void *k = g.type == kW_Q1_0 ? reinterpret_cast<const void *>(gemv_tern_argmax_kernel<kW_Q1_0>)
@@ -5890,6 +5931,19 @@ hipError_t launch_tern_argmax(const GemvArgs &g, const FuseArgs &f, hipStream_t 
     case kW_Q1_0: return go(gemv_tern_argmax_kernel<kW_Q1_0>, tm::waves<kW_Q1_0>());
     case kW_PQ2_0: return go(gemv_tern_argmax_kernel<kW_PQ2_0>, tm::waves<kW_PQ2_0>());
     case kW_PTQ1_0: return go(gemv_tern_argmax_kernel<kW_PTQ1_0>, tm::waves<kW_PTQ1_0>());
+    case kW_Q6_K: {
+      const int blocks = q6k_argmax_grid(g);
+      if (blocks < 1) return hipErrorInvalidValue;
+      const size_t lds = gemv_q6k_mfma_lds_bytes(g.K);
+      const dim3 grid((unsigned)blocks, (unsigned)g.M), block(q6m::kThreads);
+      if (ev)
+        hipExtLaunchKernelGGL(gemv_q6k_argmax_kernel, grid, block, lds, stream, ev[0], ev[1], 0u, g, f);
+      else if (done)
+        hipExtLaunchKernelGGL(gemv_q6k_argmax_kernel, grid, block, lds, stream, nullptr, done, 0u, g, f);
+      else
+        hipLaunchKernelGGL(gemv_q6k_argmax_kernel, grid, block, lds, stream, g, f);
+      return hipGetLastError();
+    }
     default: return hipErrorInvalidValue;
   }
 }
@@ -6036,6 +6090,10 @@ hipError_t prepare_kernels() {
     if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q6k_sample_kernel),
                                  hipFuncAttributeMaxDynamicSharedMemorySize,
                                  (int)q6k_sample_lds_bytes(kGemvMaxK))) != hipSuccess)
+      return e;
+    if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q6k_argmax_kernel),
+                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                 (int)gemv_q6k_mfma_lds_bytes(kGemvMaxK))) != hipSuccess)
       return e;
     const void *ak[3] = {reinterpret_cast<const void *>(&gemv_tern_argmax_kernel<kW_Q1_0>),
                          reinterpret_cast<const void *>(&gemv_tern_argmax_kernel<kW_PQ2_0>),
