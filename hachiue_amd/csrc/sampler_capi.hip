@@ -191,7 +191,9 @@ struct hs_context {
                                 //   (zero between calls), the waves' two largest, the
                                 //   rows' key histograms (zero between calls)
   // HS_LMHEAD_FUSE at creation: 0 always two launches; 1 (default) one
-  // launch for all-greedy calls; 2 also for calls with k <= 64 sampling rows
+  // launch for all-greedy calls on the planar and Q6_K weights; 2 also for
+  // calls with k <= 64 sampling rows there and all-greedy calls on the
+  // vector-unit weights (F32, Q4_0, Q4_1, Q4_K)
   int fuse = 1;
   DevBuf large_retry;           // two-pass large-k rows handed back
   DevBuf large_replay;          // slot-history replays asked for by the large-k kernel
@@ -1283,7 +1285,12 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
   if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
   if (!w) return fail(HS_ERR_INVALID_ARGUMENT, "null weights");
   const bool tern = hs::tern_quant_bytes(w->type) > 0;
-  bool fused = ctx->fuse && (tern || w->type == hs::kW_Q6_K) && M > 0 && w->rows > 0 && configs &&
+  // sampling rows fuse into the planar and Q6_K GEMVs only (their 16-row
+  // tiles); the vector-unit GEMVs fuse greedy rows only when asked
+  // (HS_LMHEAD_FUSE=2): their argmax launch measured 2.7 us (no penalty) to
+  // 9 us (repetition penalty) slower than the GEMV and the argmax launch
+  const bool sample_ok = tern || w->type == hs::kW_Q6_K;
+  bool fused = ctx->fuse && (sample_ok || ctx->fuse >= 2) && M > 0 && w->rows > 0 && configs &&
                d_uniforms && d_tokens && (d_hist_ids == nullptr) == (d_hist_offsets == nullptr);
   std::vector<hs::RowPlan> plans;
   Routing rt;
@@ -1297,7 +1304,7 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
     for (const hs::RowPlan &p : plans) {
       if ((p.mode != hs::kModeGreedy && p.mode != hs::kModeSmall) || (p.pen & hs::kPenPF))
         fused = false;
-      if (ctx->fuse < 2 && p.mode != hs::kModeGreedy) fused = false;
+      if ((ctx->fuse < 2 || !sample_ok) && p.mode != hs::kModeGreedy) fused = false;
     }
   }
   // every row greedy: the GEMV keeps the argmax alone
@@ -1312,7 +1319,7 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
     rc = gemv_setup(ctx, d_x, M, ldx, w, d_logits, ldl, st, g, &skip);
     if (rc) return rc;
     const int blocks = skip     ? 0
-                       : greedy ? hs::tern_argmax_grid(g)
+                       : greedy ? hs::argmax_fused_grid(g)
                        : tern   ? hs::tern_sample_grid(g)
                                 : hs::q6k_sample_grid(g);
     if (blocks > 0) {
@@ -1343,7 +1350,7 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
       hipEvent_t *ev = nullptr;
       rc = timed_slot(ctx, hs::kGemvTimedSlot, &ev);
       if (rc) return rc;
-      const hipError_t e = greedy ? hs::launch_tern_argmax(g, f, st, ev, ctx->done_ev)
+      const hipError_t e = greedy ? hs::launch_argmax_fused(g, f, st, ev, ctx->done_ev)
                            : tern ? hs::launch_tern_sample(g, f, st, ev, ctx->done_ev)
                                   : hs::launch_q6k_sample(g, f, st, ev, ctx->done_ev);
       if (e != hipSuccess) {

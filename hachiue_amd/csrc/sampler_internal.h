@@ -312,12 +312,12 @@ struct FuseArgs {
 };
 hipError_t launch_tern_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
                               hipEvent_t *ev, hipEvent_t done);
-// Every row greedy (planar or Q6_K weights): the GEMV keeps each
-// workgroup's packed maximum, the last one writes the token (no candidate
-// lists: f.wtop, f.wtiles, f.hist, f.blocks unused).
-hipError_t launch_tern_argmax(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
-                              hipEvent_t *ev, hipEvent_t done);
-int tern_argmax_grid(const GemvArgs &g);
+// Every row greedy (any weight type): the GEMV keeps each workgroup's packed
+// maximum, the last one writes the token (no candidate lists: f.wtop,
+// f.wtiles, f.hist, f.blocks unused).
+hipError_t launch_argmax_fused(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
+                               hipEvent_t *ev, hipEvent_t done);
+int argmax_fused_grid(const GemvArgs &g);
 // Its workgroups per activation row, or 0 when N needs more tiles per wave
 // than it records (then the two-launch path is used).
 int tern_sample_grid(const GemvArgs &g);

@@ -47,6 +47,7 @@
 #include <math.h>
 
 #include "hachiue_sampler.h"
+#include "blk_gemv.h"
 #include "q6k_gemv.h"
 #include "tern_gemv.h"
 
@@ -5890,6 +5891,84 @@ __global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_argmax_kernel(GemvA
   fuse_argmax_finish<NW>(g, f, m, epi.best, wbest);
 }
 
+// The same for F32, Q4_0, Q4_1 and Q4_K (the vector-unit bodies, blk_gemv.h;
+// LDSB: the block formats' LDS batches), on the GEMV's grid.
+template <int FMT, int NRU, bool LDSB>
+__global__ __launch_bounds__(kGemvThreads) void gemv_blk_argmax_kernel(GemvArgs g, FuseArgs f) {
+  constexpr int NW = kGemvThreads / 64;
+  extern __shared__ uint4 glds[];
+  __shared__ int32_t rset[kFuseSetSlots];
+  __shared__ unsigned long long wbest[NW];
+  const int tid = threadIdx.x;
+  const int m = (int)blockIdx.y;
+  const RowPlan *plan = f.plans + m;
+  const bool rep = (load_scalar(&plan->pen) & kPenRep) != 0;
+  if (tid < kFuseSetSlots) rset[tid] = -1;
+  __syncthreads();
+  if (rep) fuse_rep_set(f, m, g.N, rset);
+  __syncthreads();   // (the bodies have no barrier of their own)
+  ArgmaxEpi epi{g.y + (int64_t)m * g.ldy, rep ? rset : nullptr, load_scalar(&plan->rep), 0ull};
+  if constexpr (LDSB)
+    gemv_lds_body<FMT, NRU>(g, glds, epi);
+  else
+    gemv_vec_body<FMT, NRU>(g, epi);
+  fuse_argmax_finish<NW>(g, f, m, epi.best, wbest);
+}
+
+template <int FMT, int NRU>
+const void *blk_argmax_fn() {
+  if constexpr (FMT == kW_F32)
+    return reinterpret_cast<const void *>(gemv_blk_argmax_kernel<FMT, NRU, false>);
+  else
+    return reinterpret_cast<const void *>(gemv_blk_argmax_kernel<FMT, NRU, true>);
+}
+
+// The block formats' grid: the GEMV's (g.blocks, at most the resident
+// workgroups), and the launch.
+template <int FMT, int NRU>
+hipError_t launch_blk_argmax(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
+                             hipEvent_t *ev, hipEvent_t done, int *blocks_out) {
+  const uint32_t lds = FMT == kW_F32 ? 0u : (uint32_t)gemv_lds_bytes(FMT);
+  const int res = resident_blocks(blk_argmax_fn<FMT, NRU>(), lds, kGemvThreads);
+  const int blocks = g.blocks < res ? g.blocks : res;
+  if (blocks_out) {
+    *blocks_out = blocks;
+    return hipSuccess;
+  }
+  if (blocks < 1) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)blocks, (unsigned)g.M), block(kGemvThreads);
+  auto go = [&](auto kern) {
+    if (ev)
+      hipExtLaunchKernelGGL(kern, grid, block, lds, stream, ev[0], ev[1], 0u, g, f);
+    else if (done)
+      hipExtLaunchKernelGGL(kern, grid, block, lds, stream, nullptr, done, 0u, g, f);
+    else
+      hipLaunchKernelGGL(kern, grid, block, lds, stream, g, f);
+    return hipGetLastError();
+  };
+  if constexpr (FMT == kW_F32)
+    return go(gemv_blk_argmax_kernel<FMT, NRU, false>);
+  else
+    return go(gemv_blk_argmax_kernel<FMT, NRU, true>);
+}
+
+// blocks_out: only the grid, nothing launched
+hipError_t blk_argmax(const GemvArgs &g, const FuseArgs &f, hipStream_t stream, hipEvent_t *ev,
+                      hipEvent_t done, int *blocks_out) {
+  const bool two = g.nru == 2;
+  switch (g.type) {
+    case kW_F32: return two ? launch_blk_argmax<kW_F32, 2>(g, f, stream, ev, done, blocks_out)
+                            : launch_blk_argmax<kW_F32, 1>(g, f, stream, ev, done, blocks_out);
+    case kW_Q4_0: return two ? launch_blk_argmax<kW_Q4_0, 2>(g, f, stream, ev, done, blocks_out)
+                             : launch_blk_argmax<kW_Q4_0, 1>(g, f, stream, ev, done, blocks_out);
+    case kW_Q4_1: return two ? launch_blk_argmax<kW_Q4_1, 2>(g, f, stream, ev, done, blocks_out)
+                             : launch_blk_argmax<kW_Q4_1, 1>(g, f, stream, ev, done, blocks_out);
+    case kW_Q4_K: return two ? launch_blk_argmax<kW_Q4_K, 2>(g, f, stream, ev, done, blocks_out)
+                             : launch_blk_argmax<kW_Q4_K, 1>(g, f, stream, ev, done, blocks_out);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 int q6k_argmax_grid(const GemvArgs &g) {
   const int ntiles = (g.N + 15) / 16;
   const int res = resident_blocks(reinterpret_cast<const void *>(gemv_q6k_argmax_kernel),
@@ -5900,8 +5979,12 @@ int q6k_argmax_grid(const GemvArgs &g) {
   return blocks >= 1 && g.part && g.tile_cnt ? blocks : 0;
 }
 
-int tern_argmax_grid(const GemvArgs &g) {
+int argmax_fused_grid(const GemvArgs &g) {
   if (g.type == kW_Q6_K) return q6k_argmax_grid(g);
+  if (tern_quant_bytes(g.type) == 0) {
+    int blocks = 0;
+    return blk_argmax(g, FuseArgs{}, nullptr, nullptr, nullptr, &blocks) == hipSuccess ? blocks : 0;
+  }
   const int nw = g.type == kW_Q1_0 ? tm::waves<kW_Q1_0>()
                  : g.type == kW_PQ2_0 ? tm::waves<kW_PQ2_0>() : tm::waves<kW_PTQ1_0>();
   const void *k = g.type == kW_Q1_0 ? reinterpret_cast<const void *>(gemv_tern_argmax_kernel<kW_Q1_0>)
@@ -5912,10 +5995,10 @@ int tern_argmax_grid(const GemvArgs &g) {
   return ntiles < res ? ntiles : res;
 }
 
-hipError_t launch_tern_argmax(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
-                              hipEvent_t *ev, hipEvent_t done) {
+hipError_t launch_argmax_fused(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
+                               hipEvent_t *ev, hipEvent_t done) {
   auto go = [&](auto kern, int nw) {
-    const int blocks = tern_argmax_grid(g);
+    const int blocks = argmax_fused_grid(g);
     if (blocks < 1) return hipErrorInvalidValue;
     const size_t lds = gemv_tern_lds_bytes(g.K);
     const dim3 grid((unsigned)blocks, (unsigned)g.M), block(64 * nw);
@@ -5944,7 +6027,7 @@ hipError_t launch_tern_argmax(const GemvArgs &g, const FuseArgs &f, hipStream_t 
         hipLaunchKernelGGL(gemv_q6k_argmax_kernel, grid, block, lds, stream, g, f);
       return hipGetLastError();
     }
-    default: return hipErrorInvalidValue;
+    default: return blk_argmax(g, f, stream, ev, done, nullptr);
   }
 }
 

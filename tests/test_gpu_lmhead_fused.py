@@ -1,7 +1,8 @@
-"""GPU parity of the planar and Q6_K lm_head GEMVs that sample their own
-rows in one launch (hs_lm_head_sample_device_ex with every row greedy or
-k <= 64 and at most the repetition penalty; src/engine.ts:1493-1531 then
-src/sampler.ts).
+"""GPU parity of the lm_head GEMVs that sample their own rows in one
+launch (hs_lm_head_sample_device_ex; the planar and Q6_K formats when
+every row is greedy or takes k <= 64 candidates with at most the repetition
+penalty, the vector-unit formats when every row is greedy;
+src/engine.ts:1493-1531 then src/sampler.ts).
 The logits it leaves (penalised where the history asks, src/sampler.ts:
 24-33) must equal, bit for bit, the GEMV's own output with the oracle's
 penalties applied, and every token the oracle's on those logits; the same
@@ -214,3 +215,44 @@ def test_fused_is_one_launch(sampler, fctx, unfused, fmt, cfg):
         others = {k: v for k, v in ms.items() if v > 0 and k != "gemv_kernel"}
         assert ms["gemv_kernel"] > 0
         assert (others == {}) == fused, others
+
+
+BLOCK = {"f32": o.W_F32, "q4_0": o.W_Q4_0, "q4_1": o.W_Q4_1, "q4_k": o.W_Q4_K}
+
+
+@pytest.mark.parametrize("fmt", list(BLOCK))
+@pytest.mark.parametrize("K", [1024, 4096])
+def test_fused_greedy_vector_formats(sampler, fctx, unfused, fmt, K):
+    """Every row greedy on the vector-unit formats (both lane layouts: a row
+    on `seg` lanes at K 1024, on all 64 with two units each at K 4096): one
+    launch when HS_LMHEAD_FUSE=2 asks for it (by default two: the one launch
+    is slower on these formats), the tokens the oracle's on the GEMV's own
+    logits (first index of the maximum, logit 0 NaN -> 0), the penalised
+    logits bit for bit, and the same results as two launches.  Rows with a
+    sampling row take two launches."""
+    wtype = BLOCK[fmt]
+    N = 40000 if fmt == "f32" else 151936
+    rng = np.random.default_rng(K + wtype)
+    w = random_blocks(wtype, N, K, rng, scale=0.05)
+    cfgs = [dict(temperature=0.0), dict(temperature=0.0, repetitionPenalty=1.3),
+            dict(temperature=-1.0, repetitionPenalty=0.7)]
+    M = len(cfgs)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    hists = [rng.integers(0, N, 100) for _ in range(M)]
+    u = rng.random(M)
+    for ctx, fused in ((fctx, True), (sampler, False), (unfused, False)):
+        ctx.set_timing(True)
+        ctx.kernel_times()
+        tok, pen, ids, off = lm_head_sample(ctx, wtype, x, w, N, hists, cfgs, u)
+        ms, calls = ctx.kernel_times()
+        ctx.set_timing(False)
+        others = {k: v for k, v in ms.items() if v > 0 and k != "gemv_kernel"}
+        assert (others == {}) == fused, others
+        raw, ref, res = expect(sampler, wtype, x, w, N, ids, off, cfgs, u)
+        assert np.array_equal(pen.view(np.uint32), ref.view(np.uint32))
+        assert tok.tolist() == res.token.tolist()
+    mixed = cfgs[:2] + [dict(temperature=0.7, topK=40)]
+    tok, pen, ids, off = lm_head_sample(fctx, wtype, x, w, N, hists, mixed, u)
+    raw, ref, res = expect(sampler, wtype, x, w, N, ids, off, mixed, u)
+    assert np.array_equal(pen.view(np.uint32), ref.view(np.uint32))
+    assert ((tok == res.token) | (res.draw_margin < 1e-6)).all()
