@@ -176,6 +176,10 @@ def main() -> int:
                     choices=["sample", "greedy-route", "lmhead", "lmhead-sample", "decode"])
     ap.add_argument("--wfmt", default="q6_k", help="lm_head weight format (--path lmhead)")
     ap.add_argument("--hidden", type=int, default=2048, help="lm_head K (--path lmhead)")
+    ap.add_argument("--lm-fuse", default="1", choices=["0", "1", "2"],
+                    help="HS_LMHEAD_FUSE of the timed context (--path lmhead-sample): 0 two "
+                         "launches, 1 the library default, 2 one launch wherever it applies; "
+                         "the other two are timed beside it")
     ap.add_argument("--lm-greedy", action="store_true",
                     help="--path lmhead-sample: greedy rows (temperature 0, repetition 1.1)")
     ap.add_argument("--hadamard", action="store_true",
@@ -344,14 +348,17 @@ def other_path(args) -> int:
     step, timed like the sampler."""
     from hachiue_amd import Sampler, hip, workloads
 
-    if args.path == "lmhead-sample":   # one launch for the sampling rows too (HS_LMHEAD_FUSE=2)
-        os.environ["HS_LMHEAD_FUSE"] = "2"
+    def policy_context(fuse: str):
+        """A context created with HS_LMHEAD_FUSE=fuse (the lm_head + sampling
+        launch policy: 0 two launches, 1 the library's default, 2 one launch
+        wherever it applies)."""
+        os.environ["HS_LMHEAD_FUSE"] = fuse
         try:
-            sampler = Sampler(0)
+            return Sampler(0)
         finally:
             del os.environ["HS_LMHEAD_FUSE"]
-    else:
-        sampler = Sampler(0)
+
+    sampler = policy_context(args.lm_fuse) if args.path == "lmhead-sample" else Sampler(0)
     stream = hip.Stream()
 
     def n_sets(set_bytes: int) -> int:   # as in main(): past twice the last-level cache
@@ -441,9 +448,9 @@ def other_path(args) -> int:
                     "max_rel": float(rel.max())}
         count = rows
         if args.path == "lmhead-sample":
-            # the lm_head and the sampler on its rows (one launch when every
-            # row takes k <= 64 with at most the repetition penalty): the
-            # headline's sampling, a 64-id history per hidden state
+            # the lm_head and the sampler on its rows (one launch or two, by
+            # the context's policy): the headline's sampling, a 64-id
+            # history per hidden state
             from hachiue_amd.sampler import make_configs
             rng = np.random.default_rng(5)
             hist = rng.integers(0, vocab, (rows, 64)).astype(np.int32)
@@ -505,26 +512,26 @@ def other_path(args) -> int:
     kms, calls = sampler.kernel_times()
     sampler.set_timing(False)
     kms_avg = kms[kernel] / max(calls, 1)
-    two_launch = None
-    if args.path == "lmhead-sample":   # the same call on a context that always takes two launches
-        os.environ["HS_LMHEAD_FUSE"] = "0"
-        try:
-            other = Sampler(0)
-        finally:
-            del os.environ["HS_LMHEAD_FUSE"]
-        for i in range(args.warmup):
-            step_on(other, i)
-        hip.synchronize()
-        e0, e1 = hip.Event(), hip.Event()
-        e0.record(stream)
-        for i in range(args.steps):
-            step_on(other, i)
-        e1.record(stream)
-        e1.synchronize()
-        two_launch = round(e0.elapsed_ms(e1) / args.steps, 5)
-        other.close()
-        log(f"[bench] lmhead-sample: one launch {total_ms / args.steps * 1e3:.2f} us per step, "
-            f"two launches {two_launch * 1e3:.2f} us")
+    by_policy = None
+    if args.path == "lmhead-sample":   # the same calls on contexts of the other policies
+        by_policy = {args.lm_fuse: round(total_ms / args.steps, 5)}
+        for fuse in ("0", "1", "2"):
+            if fuse == args.lm_fuse:
+                continue
+            other = policy_context(fuse)
+            for i in range(args.warmup):
+                step_on(other, i)
+            hip.synchronize()
+            e0, e1 = hip.Event(), hip.Event()
+            e0.record(stream)
+            for i in range(args.steps):
+                step_on(other, i)
+            e1.record(stream)
+            e1.synchronize()
+            by_policy[fuse] = round(e0.elapsed_ms(e1) / args.steps, 5)
+            other.close()
+        log("[bench] lmhead-sample: us per step by HS_LMHEAD_FUSE " +
+            ", ".join(f"{k}: {by_policy[k] * 1e3:.2f}" for k in sorted(by_policy)))
     if args.copy_probe and sets > 1:   # a copy of known size for the counters' scale
         d_in[1].copy_from(d_in[0])
         hip.synchronize()
@@ -548,8 +555,9 @@ def other_path(args) -> int:
         "cpu_baseline": None,
         "parity": parity,
     }
-    if two_launch is not None:
-        line["ms_per_step_two_launches"] = two_launch
+    if by_policy is not None:
+        line["config"]["lm_head_fuse"] = args.lm_fuse
+        line["ms_per_step_by_fuse_policy"] = {k: by_policy[k] for k in sorted(by_policy)}
         line["kernels_ms"] = {k: round(v / max(calls, 1), 5) for k, v in kms.items() if v > 0}
     print(json.dumps(line), flush=True)
     sampler.close()

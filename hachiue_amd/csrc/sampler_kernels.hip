@@ -806,6 +806,119 @@ size_t pen_smem_bytes() {
 
 // ---------------------------------------------------------------- replay
 
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x);
+
+// k <= 64 slots of the scan in the lanes of one wave, sorted by (value, slot
+// index): lane j holds c = (key << 32) | slot (key: f2key, -0 == +0; an
+// empty slot, -Infinity, is 0) and the index rid of its logit (lanes >= k: c
+// = ~0), and lane 0 holds the reference's minimum (the smallest slot among
+// equal minima), key mk in slot mi.  A logit enters iff its key kL is above
+// mk (NaN and -Infinity have key 0 and never do) and takes slot mi, c' =
+// (kL, mi): lane 0 leaves, and lane j then holds the j-th smallest of lanes
+// 1..k-1 and c', which is min(c[j + 1], max(c[j], c')).  For a logit that
+// does not enter (kL <= mk, so c' <= c[0]) the same steps leave every lane
+// as it is, so take_min needs no test: three lane-parallel steps (a wave
+// shift by DPP, two 64-bit compares) and no scalar decision, which would
+// wait for the vector unit at every logit.
+__device__ __forceinline__ uint32_t wave_shl1_u32(uint32_t x) {   // lane j <- lane j + 1; lane 63 <- ~0
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)0xFFFFFFFF, (int)x, 0x130, 0xF, 0xF, false);
+}
+
+struct LaneSlots {
+  unsigned long long c;
+  int32_t rid;
+  uint32_t mk;
+  int mi, k;
+  __device__ __forceinline__ explicit LaneSlots(int k_) : rid(-1), mk(0), mi(0), k(k_) {
+    const int lane = lane_id();
+    c = lane < k ? (unsigned long long)lane : ~0ull;
+  }
+  __device__ __forceinline__ void take_min(uint32_t kL, int idx) {
+    const unsigned long long cL = ((unsigned long long)kL << 32) | (uint32_t)mi;
+    const unsigned long long nx =
+        ((unsigned long long)wave_shl1_u32((uint32_t)(c >> 32)) << 32) | wave_shl1_u32((uint32_t)c);
+    const int32_t nr = (int32_t)wave_shl1_u32((uint32_t)rid);
+    const bool below = c < cL;   // this lane's slot sorts below the new one
+    const bool shift = nx < cL;  // so does the next lane's: this lane takes it
+    const unsigned long long m = below ? cL : c;
+    const int32_t mr = below ? idx : rid;
+    c = shift ? nx : m;
+    rid = shift ? nr : mr;
+    mk = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(c >> 32));
+    mi = __builtin_amdgcn_readfirstlane((int)(uint32_t)c);
+  }
+  // the logits of one 64-logit group (lane = logit) whose keys kx are above
+  // the minimum at the group's start, in index order (those that no longer
+  // are when their turn comes leave the slots as they are)
+  __device__ __forceinline__ void scan64(uint32_t kx, int base) {
+    unsigned long long cm = __ballot(kx > mk);
+    while (cm) {
+      const int L = (int)__ffsll((long long)cm) - 1;
+      cm &= cm - 1;
+      take_min(readlane_u32(kx, L), base + L);
+    }
+  }
+  __device__ __forceinline__ void store(float *sv, int32_t *sid) const {
+    if (lane_id() < k) {
+      const int rs = (int)(uint32_t)c;
+      sv[rs] = rid >= 0 ? key2f((uint32_t)(c >> 32)) : -INFINITY;
+      sid[rs] = rid;
+    }
+  }
+};
+
+// LaneSlots for rows of fewer than 2^20 - 1 logits, one 64-bit word per
+// lane: c = ~((key << 32) | (slot << 20) | index), the index field all ones
+// for an empty slot, complemented so that lane 63, which a DPP shift leaves
+// without a source, reads 0: a slot above every other.  Per logit: a wave
+// shift of two dwords, two 64-bit compares, four selects, no index to move.
+__device__ __forceinline__ uint32_t wave_shl1_zero(uint32_t x) {   // lane j <- lane j + 1; lane 63 <- 0
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x130, 0xF, 0xF, true);
+}
+
+struct PackedSlots {
+  static constexpr uint32_t kNoIndex = 0xFFFFFu;
+  unsigned long long c;
+  uint32_t mk;
+  int mi, k;
+  __device__ __forceinline__ explicit PackedSlots(int k_) : mk(0), mi(0), k(k_) {
+    const int lane = lane_id();
+    c = lane < k ? ~(((unsigned long long)lane << 20) | kNoIndex) : 0ull;
+  }
+  __device__ __forceinline__ void take_min(uint32_t kL, int idx) {
+    // compared without its index (no slot sorts between (kL, mi) and the
+    // new word, and a logit equal to the minimum must leave lane 0 as it is)
+    const unsigned long long cK = ~(((unsigned long long)kL << 32) | ((uint32_t)mi << 20));
+    const unsigned long long cL = cK & ~(unsigned long long)kNoIndex | (kNoIndex & ~(uint32_t)idx);
+    const unsigned long long nx =
+        ((unsigned long long)wave_shl1_zero((uint32_t)(c >> 32)) << 32) | wave_shl1_zero((uint32_t)c);
+    const bool below = c > cK;   // complemented: this lane's slot sorts below the new one
+    const bool shift = nx > cK;  // so does the next lane's: this lane takes it
+    const unsigned long long m = below ? cL : c;
+    c = shift ? nx : m;
+    mk = ~(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(c >> 32));
+    mi = (int)((~(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)c) >> 20) & 63u);
+  }
+  __device__ __forceinline__ void scan64(uint32_t kx, int base) {
+    unsigned long long cm = __ballot(kx > mk);
+    while (cm) {
+      const int L = (int)__ffsll((long long)cm) - 1;
+      cm &= cm - 1;
+      take_min(readlane_u32(kx, L), base + L);
+    }
+  }
+  __device__ __forceinline__ void store(float *sv, int32_t *sid) const {
+    if (lane_id() < k) {
+      const unsigned long long v = ~c;
+      const int rs = (int)((v >> 20) & 63u);
+      const uint32_t ix = (uint32_t)v & kNoIndex;
+      sv[rs] = ix != kNoIndex ? key2f((uint32_t)(v >> 32)) : -INFINITY;
+      sid[rs] = ix != kNoIndex ? (int32_t)ix : -1;
+    }
+  }
+};
+static_assert(kRowMaxVocab < (int)PackedSlots::kNoIndex, "PackedSlots: indices below the empty mark");
+
 // Exact replace-min scan of src/sampler.ts:50-69 over the whole (penalised)
 // row by one wave: slot j holds (sv[j], sid[j]); a logit enters iff it is
 // strictly greater than the current minimum, into the first slot holding that
@@ -813,57 +926,14 @@ size_t pen_smem_bytes() {
 // step's loads are in flight while a step is scanned (one wave alone is
 // bound by the latency of its reads).  BLK is what the caller's registers
 // allow.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x);
-
 template <int BLK>
 __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, float *sv, int32_t *sid,
                                            const uint32_t *bkey = nullptr) {
   const int lane = lane_id();
-  // k <= 64: the slots live in lanes 0..k-1 sorted by (value, slot index):
-  // lane j holds a value's key rk (f2key: -0 == +0; an empty slot, -Infinity,
-  // is 0), its slot rs and its logit's index rid, and lane 0 holds the
-  // reference's minimum (the smallest slot among equal minima), key mk in
-  // slot mi.  A logit enters iff its key is above mk (NaN and -Infinity have
-  // key 0 and never do) and takes slot mi; its position p is the number of
-  // other slots below it, lanes 1..p move down one lane (a wave shift by
-  // DPP) and the new slot goes to lane p.  The next minimum is lane 0.
   const bool in_regs = k <= 64;
-  uint32_t rk = lane < k ? 0u : 0xFFFFFFFFu;
-  int32_t rid = -1;
-  int rs = lane;
-  uint32_t mk = 0;
-  int mi = 0;
-  auto take_min = [&](uint32_t kL, int idx) {
-    const bool less = lane >= 1 && lane < k && (rk < kL || (rk == kL && rs < mi));
-    const int p = __popcll(__ballot(less));
-    // lane j <- lane j + 1 (wave_shl:1)
-    const uint32_t nk = (uint32_t)__builtin_amdgcn_update_dpp((int)rk, (int)rk, 0x130, 0xF, 0xF, false);
-    const int ns = __builtin_amdgcn_update_dpp(rs, rs, 0x130, 0xF, 0xF, false);
-    const int ni = __builtin_amdgcn_update_dpp(rid, rid, 0x130, 0xF, 0xF, false);
-    const bool low = lane < p, at = lane == p;
-    rk = low ? nk : (at ? kL : rk);
-    rid = low ? ni : (at ? idx : rid);
-    rs = low ? ns : (at ? mi : rs);
-    mk = (uint32_t)__builtin_amdgcn_readfirstlane((int)rk);
-    mi = __builtin_amdgcn_readfirstlane(rs);
-  };
-  // the logits of one 64-logit group (lane = logit) whose keys kx are above
-  // the minimum at the group's start, in index order, one scalar test each
-  auto scan64 = [&](uint32_t kx, int base) {
-    unsigned long long cm = __ballot(kx > mk);
-    while (cm) {
-      const int L = (int)__ffsll((long long)cm) - 1;
-      cm &= cm - 1;
-      const uint32_t kL = readlane_u32(kx, L);
-      if (kL > mk) take_min(kL, base + L);
-    }
-  };
-  auto store_slots = [&]() {
-    if (lane < k) {
-      sv[rs] = rid >= 0 ? key2f(rk) : -INFINITY;
-      sid[rs] = rid;
-    }
-  };
+  LaneSlots ls(k);
+  auto scan64 = [&](uint32_t kx, int base) { ls.scan64(kx, base); };
+  auto store_slots = [&]() { ls.store(sv, sid); };
   if (bkey && in_regs) {
     // bkey[b]: key of the largest logit of block b (64 logits).  A block
     // whose largest logit is not above the current minimum holds no logit
@@ -882,7 +952,7 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
         while (!wm && wb + 64 < nb) {
           wb += 64;
           const uint32_t kb = wb + lane < nb ? bkey[wb + lane] : 0u;
-          wm = __ballot(kb > mk);
+          wm = __ballot(kb > ls.mk);
         }
         blk[q] = -1;
         if (wm) {
@@ -998,6 +1068,119 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
       }
     }
   }
+}
+
+// The slot replay of replay_row for k <= 64 with the whole workgroup, for
+// the row kernel's rows whose draw needs it.  After logit i the slots hold
+// the k largest logits of [0, i) (a logit enters iff it is above the
+// smallest of them), so the k-th largest of the earlier blocks' largest
+// logits is a lower bound of the scan's minimum at a block's start, and a
+// block whose largest logit (bkey) is not above it holds no logit that
+// enters.  Three kinds of work run at once, in steps separated by barriers:
+//  - wave 1 keeps the k largest block keys sorted in its lanes (ascending,
+//    updated as LaneSlots updates its slots) and lists, in index order, the
+//    blocks whose key is above the smallest of them when they come (about
+//    k + k ln(V / 64k) of the ceil(V / 64) blocks on random rows), two
+//    groups of G blocks ahead of the copies;
+//  - waves 2.. copy the keys of the group listed before into LDS (two
+//    alternating buffers);
+//  - wave 0 scans the group copied before with PackedSlots::scan64 (the
+//    steps of replay_row), reading LDS only.
+// Every thread of the workgroup calls it with the same arguments; the slots
+// end in sv / sid.  bkey (nb = ceil(V / 64) words) lies at the start of
+// `words` words of LDS, whose rest holds the buffers; ring (ring_cap words)
+// holds the list, and pub (4 words) the list's length and end, per step
+// parity.  It returns false, having done nothing, when the buffers do not
+// fit (the caller then runs replay_row).
+constexpr int kStageBlocks = 64;   // G at most
+
+template <int NT>
+__device__ __forceinline__ bool replay_staged(const float *rowp, int V, int k, uint32_t *bkey,
+                                              int words, uint32_t *ring, int ring_cap, int32_t *pub,
+                                              float *sv, int32_t *sid) {
+  constexpr int NW = NT / 64;
+  static_assert(NW >= 3, "replay_staged: a scanning wave, a listing wave and copying waves");
+  constexpr int PER = (kStageBlocks + NW - 3) / (NW - 2);   // blocks per copying wave and group
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int nb = (V + 63) >> 6;
+  const int boff = (nb + 63) & ~63;
+  const int G = min(kStageBlocks, (words - boff) / 128);
+  if (G < 8 || ring_cap < 4 * G + 64 || V > kRowMaxVocab) return false;
+  uint32_t *buf = bkey + boff;
+  // wave 1's state
+  uint32_t rk = lane < k ? 0u : 0xFFFFFFFFu;
+  int w0 = 0, n = 0;
+  PackedSlots ls(k);   // V <= kRowMaxVocab
+  int L = 0;   // blocks listed by the end of the previous step
+  for (int t = 0;; ++t) {
+    if (wave == 1) {
+      while (n < (t + 2) * G && w0 < nb) {
+        const uint32_t kb = w0 + lane < nb ? bkey[w0 + lane] : 0u;
+        const uint32_t mk = (uint32_t)__builtin_amdgcn_readfirstlane((int)rk);
+        unsigned long long cm = __ballot(kb > mk), ent = 0;
+        while (cm) {
+          const int Lb = (int)__ffsll((long long)cm) - 1;
+          cm &= cm - 1;
+          const uint32_t kL = readlane_u32(kb, Lb);
+          ent |= (unsigned long long)(kL > rk) << Lb;   // lane 0's bits are the ones read
+          rk = min(wave_shl1_u32(rk), max(rk, kL));
+        }
+        // the window's marked blocks, in index order, appended to the list
+        const unsigned long long em =
+            ((unsigned long long)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(ent >> 32))
+             << 32) |
+            (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)ent);
+        const int pos = n + (int)__builtin_amdgcn_mbcnt_hi(
+                                (uint32_t)(em >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)em, 0u));
+        if ((em >> lane) & 1ull) ring[pos % ring_cap] = (uint32_t)(w0 + lane);
+        n += __popcll(em);
+        w0 += 64;
+      }
+      if (lane == 0) {
+        pub[2 * (t & 1)] = n;
+        pub[2 * (t & 1) + 1] = w0 >= nb;
+      }
+    } else if (wave >= 2) {
+      const int g = t - 1;   // listed by the end of the previous step
+      if (g >= 0 && g * G < L) {
+        const int j0 = g * G, nj = min(G, L - j0);
+        uint32_t *dst = buf + (g & 1) * G * 64;
+        float x[PER];
+        int e[PER];
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+          const int j = (wave - 2) + (NW - 2) * q;
+          e[q] = j < nj ? 64 * (int)ring[(j0 + j) % ring_cap] + lane : V;
+          x[q] = rowp[e[q] < V ? e[q] : 0];   // always a read inside the row
+        }
+#pragma unroll
+        for (int q = 0; q < PER; ++q) {
+          const int j = (wave - 2) + (NW - 2) * q;
+          if (j < nj) dst[j * 64 + lane] = e[q] < V ? f2key(x[q]) : 0u;
+        }
+      }
+    } else {
+      const int g = t - 2;   // copied in the previous step
+      if (g >= 0 && g * G < L) {
+        const int j0 = g * G, nj = min(G, L - j0);
+        const uint32_t *src = buf + (g & 1) * G * 64;
+        const uint32_t bl = lane < nj ? ring[(j0 + lane) % ring_cap] : 0u;
+        uint32_t xn = src[lane];
+        for (int j = 0; j < nj; ++j) {
+          const uint32_t x = xn;
+          if (j + 1 < nj) xn = src[(j + 1) * 64 + lane];   // the next block's read ahead of the scan
+          ls.scan64(x, 64 * (int)readlane_u32(bl, j));
+        }
+      }
+    }
+    __syncthreads();
+    L = pub[2 * (t & 1)];
+    const bool done = pub[2 * (t & 1) + 1] != 0;
+    if (done && (t - 1) * G >= L) break;   // groups 0..t-2 scanned: every listed block
+  }
+  if (wave == 0) ls.store(sv, sid);
+  return true;
 }
 
 // ---------------------------------------------------------------- row completion
@@ -1791,13 +1974,16 @@ template <int RB = 16>
 __device__ __forceinline__ void tail_finish(const LaunchArgs &a, const RowPlan &P, int row,
                                             const float *rowp, TailState st, double u,
                                             float *rsv, int32_t *rsid, double *sp,
-                                            bool acquire_replay, const uint32_t *bkey) {
+                                            bool acquire_replay, const uint32_t *bkey,
+                                            bool staged = false) {
   const int lane = lane_id();
   const int k = P.k;
   bool replayed = false;
   if (st.need) {
-    if (acquire_replay) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    replay_row<RB>(rowp, a.vocab, k, rsv, rsid, bkey);
+    if (!staged) {   // staged: replay_staged left the slots in rsv / rsid
+      if (acquire_replay) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      replay_row<RB>(rowp, a.vocab, k, rsv, rsid, bkey);
+    }
     const bool filled = lane < k && rsid[lane] >= 0;
     unsigned long long x = filled ? pack_cand(f2key(rsv[lane]), (uint32_t)lane) : 0ull;
     x = wave_sort_desc64(x);   // value descending, slot ascending (stable sort)
@@ -1910,25 +2096,52 @@ __device__ __forceinline__ unsigned long long merge_top64(unsigned long long a, 
 // Every thread of the block: bkey[b] = key of the largest logit of logits
 // [64 b, 64 b + 64) of the row (0 when none is above -Infinity), for the slot
 // replay to skip blocks.  A 16-lane DPP row takes one block, a float4 per
-// lane; UN float4 reads per thread are in flight at a time.
+// lane.  While a step of UN slots per thread lies wholly inside a 16-byte
+// aligned row, its reads are 16-byte loads (8 per thread, 128 KiB per
+// workgroup in flight); the rest, 4 slots per thread, is read by elements.
 template <int NT>
 __device__ void block_keys(const float *rowp, int V, uint32_t *bkey) {
-  constexpr int UN = 4;
   const int tid = threadIdx.x;
   const int nf = ((V + 63) >> 6) * 16;   // float4 slots, 16 per block
-  for (int f0 = 0; f0 < nf; f0 += UN * NT) {
-    // every read issued before any is used
-    float v[UN][4];
+  // the block maximum of each thread's slot key, by its DPP row (row_shr:1,
+  // 2, 4, 8: lane 15 holds it)
+  auto put = [&](int f, uint32_t x) {
+    uint32_t y;
+    y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x111, 0xF, 0xF, false); x = x > y ? x : y;
+    y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x112, 0xF, 0xF, false); x = x > y ? x : y;
+    y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x114, 0xF, 0xF, false); x = x > y ? x : y;
+    y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x118, 0xF, 0xF, false); x = x > y ? x : y;
+    if ((tid & 15) == 15 && f < nf) bkey[f >> 4] = x;
+  };
+  int f0 = 0;
+  if ((reinterpret_cast<uintptr_t>(rowp) & 15) == 0) {
+    constexpr int UN = 8;
+    const float4 *r4 = reinterpret_cast<const float4 *>(rowp);
+    const int full = V >> 2;   // slots wholly inside the row
+    for (; f0 + UN * NT <= full; f0 += UN * NT) {
+      float4 v[UN];
 #pragma unroll
-    for (int u = 0; u < UN; ++u)
+      for (int u = 0; u < UN; ++u) v[u] = r4[f0 + u * NT + tid];
+#pragma unroll
+      for (int u = 0; u < UN; ++u) {
+        const uint32_t a = max(f2key(v[u].x), f2key(v[u].y)), b = max(f2key(v[u].z), f2key(v[u].w));
+        put(f0 + u * NT + tid, max(a, b));
+      }
+    }
+  }
+  constexpr int UT = 4;
+  for (; f0 < nf; f0 += UT * NT) {
+    // every read issued before any is used
+    float v[UT][4];
+#pragma unroll
+    for (int u = 0; u < UT; ++u)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int e = 4 * (f0 + u * NT + tid) + q;
         v[u][q] = rowp[e < V ? e : 0];   // always a read inside the row
       }
-    uint32_t key[UN];
 #pragma unroll
-    for (int u = 0; u < UN; ++u) {
+    for (int u = 0; u < UT; ++u) {
       const int f = f0 + u * NT + tid;
       uint32_t kk = 0;
 #pragma unroll
@@ -1936,18 +2149,7 @@ __device__ void block_keys(const float *rowp, int V, uint32_t *bkey) {
         const uint32_t kv = 4 * f + q < V ? f2key(v[u][q]) : 0u;
         kk = kk > kv ? kk : kv;
       }
-      key[u] = kk;
-    }
-#pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      uint32_t x = key[u], y;
-      // max over the 16 lanes of the DPP row (row_shr:1, 2, 4, 8): lane 15 holds it
-      y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x111, 0xF, 0xF, false); x = x > y ? x : y;
-      y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x112, 0xF, 0xF, false); x = x > y ? x : y;
-      y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x114, 0xF, 0xF, false); x = x > y ? x : y;
-      y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x118, 0xF, 0xF, false); x = x > y ? x : y;
-      const int f = f0 + u * NT + tid;
-      if ((tid & 15) == 15 && f < nf) bkey[f >> 4] = x;
+      put(f, kk);
     }
   }
 }
@@ -1961,6 +2163,7 @@ struct RowSmem {
   int32_t wcnt[kRowWaves];     // candidates each wave has appended (published)
   int32_t n_l, n_f, ovf, done, last;
   int32_t tie;                 // wave 0's draw needs the slot replay
+  int32_t pub[4];              // the staged replay's list length and end, per step parity
 };
 
 // SPLIT: a.split workgroups share a row, each streaming one part of it (a
@@ -2340,14 +2543,19 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     }
     __syncthreads();
     const uint32_t *bkey = nullptr;
+    bool staged = false;
     if (rs.tie) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       block_keys<kRowThreads>(rowfull, a.vocab, reinterpret_cast<uint32_t *>(cbuf));
       __syncthreads();
       bkey = reinterpret_cast<const uint32_t *>(cbuf);
+      staged = replay_staged<kRowThreads>(rowfull, a.vocab, k, reinterpret_cast<uint32_t *>(cbuf),
+                                          2 * kRowCandCap, reinterpret_cast<uint32_t *>(srt),
+                                          2 * kSortCap, rs.pub, rsv, rsid);
     }
     if (wave != 0) return;
-    tail_finish(a, P, row, rowfull, st, u, rsv, rsid, reinterpret_cast<double *>(top), true, bkey);
+    tail_finish(a, P, row, rowfull, st, u, rsv, rsid, reinterpret_cast<double *>(top), true, bkey,
+                staged);
     return;
   }
   if (!overflow && n_all <= kRowThreads) {
@@ -2386,13 +2594,18 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   }
   __syncthreads();
   const uint32_t *bkey = nullptr;
+  bool staged = false;
   if (rs.tie) {
     block_keys<kRowThreads>(rowp, V, reinterpret_cast<uint32_t *>(cbuf));
     __syncthreads();
     bkey = reinterpret_cast<const uint32_t *>(cbuf);
+    staged = replay_staged<kRowThreads>(rowp, V, k, reinterpret_cast<uint32_t *>(cbuf),
+                                        2 * kRowCandCap, reinterpret_cast<uint32_t *>(srt),
+                                        2 * kSortCap, rs.pub, rsv, rsid);
   }
   if (wave != 0) return;
-  tail_finish(a, P, row, rowp, st, u, rsv, rsid, reinterpret_cast<double *>(top), false, bkey);
+  tail_finish(a, P, row, rowp, st, u, rsv, rsid, reinterpret_cast<double *>(top), false, bkey,
+              staged);
 }
 
 // ---------------------------------------------------------------- mid kernel

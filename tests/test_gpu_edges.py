@@ -282,3 +282,35 @@ def test_every_logit_enters_the_candidate_lists(any_sampler, k):
              (inc, edge, rep, 0.9), (inc, edge, dict(temperature=0.0, repetitionPenalty=1.3), 0.5),
              (eq, edge, dict(temperature=1.0, topK=k, topP=1.0, repetitionPenalty=0.5), 0.999)]
     _run(any_sampler, cases, V, cap=64, label=f"every logit enters, k={k}")
+
+
+@pytest.mark.parametrize("k", [1, 3, 40, 64])
+def test_slot_replay_full_rows(any_sampler, k):
+    """Full-vocabulary rows whose draw falls in a group of equal logits: at
+    the top, inside the top-k, and at the k-th largest with copies before and
+    after it; one row also with the repetition penalty, one rising through
+    the row (every block can hold a logit that enters).  The replace-min scan
+    decides the order inside the group (src/sampler.ts:50-74), and the
+    candidate ids must follow it.  On the row kernel this is the staged
+    replay: one wave lists the blocks that can hold an entering logit, the
+    others copy them into LDS, a third wave scans them."""
+    V = 151936
+    r = _rng(40 + k)
+    base = r.standard_normal(V).astype(np.float32)
+    o = np.argsort(-base, kind="stable")
+    top = base.copy()
+    top[o[min(3, k)]] = top[o[0]]                  # the largest twice
+    inner = base.copy()
+    inner[o[k // 2]] = inner[o[max(0, k // 2 - 1)]]  # an equal pair inside the top-k
+    kth = base.copy()
+    kth[r.choice(V, 5, replace=False)] = kth[o[k - 1]]   # copies of the k-th largest
+    rise = (np.arange(V, dtype=np.float32) * np.float32(1e-4) +
+            r.integers(0, 3, V).astype(np.float32)).astype(np.float32)
+    hist = list(o[:3]) + list(r.integers(0, V, 20))
+    cfg = dict(temperature=0.7, topK=k, topP=1.0)
+    cases = [(top, [], cfg, 1e-4), (inner, [], cfg, 0.5), (kth, [], cfg, 0.999),
+             (kth, hist, dict(repetitionPenalty=1.2, **cfg), 0.3), (rise, [], cfg, 0.7),
+             (top, [], dict(temperature=0.0, topK=k), 0.5)]
+    got, _ = _run(any_sampler, cases, V, cap=64, label=f"slot replay, full rows, k={k}")
+    if k > 1:   # candidate outputs and a tie inside the top-k: the replay ran (HS_ROW_REPLAYED)
+        assert got.flags[0] & 0x2 and got.flags[1] & 0x2, got.flags

@@ -4,10 +4,17 @@ lanes of one wave sorted by (value, slot index): lane 0 holds the slot the
 reference's rescan finds (the first slot holding the minimum).  An entering
 logit takes lane 0's slot; its position p is the number of other slots below
 it, lanes 1..p move down one lane (a wave shift) and the new slot goes to
-lane p.  An earlier form kept each slot in its own lane with its rank.  Both
-are restated per lane here and checked against the oracle's own replace-min
-slot order (src/sampler.ts:50-69) on rows with many equal values and signed
-zeros: the ids per slot must be identical."""
+lane p.  An earlier form kept each slot in its own lane with its rank.  The
+current form (LaneSlots, and PackedSlots with the logit index inside a
+complemented 64-bit word) needs no count: lane j takes min(c[j + 1],
+max(c[j], c')), which leaves every lane as it is for a logit that does not
+enter, so the kernel applies it to every candidate without a test.  The
+staged replay lists the 64-logit blocks whose largest key is above the k-th
+largest of the earlier blocks' largest keys.  Each is restated per lane here
+and checked against the oracle's own replace-min slot order
+(src/sampler.ts:50-69) on rows with many equal values, signed zeros and NaN:
+the ids per slot must be identical, and every block holding a logit that
+enters must be listed."""
 import numpy as np
 import pytest
 
@@ -86,3 +93,122 @@ def test_rank_bookkeeping_matches_slot_scan(seed):
         ids, _ = o.topk_slots(x, n, k)
         want = np.asarray(ids)
         assert rank_replay(x.astype(np.float64), k).tolist() == want.tolist(), (seed, k, n)
+
+
+
+def f2key(x: np.ndarray) -> np.ndarray:
+    """The kernels' order-preserving key of a binary32 logit: -0 == +0, and
+    NaN and -Infinity (which never enter) are 0."""
+    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = np.where(u == 0x80000000, 0, u)
+    k = np.where(u & 0x80000000, (~u) & 0xFFFFFFFF, u | 0x80000000)
+    return np.where(np.asarray(x, np.float32) > -np.inf, k, 0).astype(np.uint64)
+
+
+def minmax_replay(x: np.ndarray, k: int, packed: bool):
+    """LaneSlots (packed=False: c = key << 32 | slot, the index in its own
+    lane) or PackedSlots (packed=True: ~(key << 32 | slot << 20 | index),
+    compared without the index), updated for every logit with a key."""
+    M = (1 << 64) - 1
+    NOI = 0xFFFFF
+    lanes = np.arange(64)
+    keys = f2key(x)
+    if packed:
+        c = [M & ~((j << 20) | NOI) if j < k else 0 for j in range(64)]
+    else:
+        c = [j if j < k else M for j in range(64)]
+    rid = [-1] * 64
+    for i, kx in enumerate(keys.tolist()):
+        if kx == 0:
+            continue
+        if packed:
+            lo = (M & ~c[0]) & 0xFFFFFFFF
+            mi = (lo >> 20) & 63
+            cK = M & ~((kx << 32) | (mi << 20))
+            cL = (cK & ~NOI) | (NOI & ~i)
+            nx = c[1:] + [0]                                  # lane 63 reads 0
+            below = [cj > cK for cj in c]
+            shift = [nj > cK for nj in nx]
+        else:
+            mi = c[0] & 0xFFFFFFFF
+            cK = cL = (kx << 32) | mi
+            nx = c[1:] + [M]                                  # lane 63 reads ~0
+            below = [cj < cK for cj in c]
+            shift = [nj < cK for nj in nx]
+            nr = rid[1:] + [-1]
+            rid = [nr[j] if shift[j] else (i if below[j] else rid[j]) for j in lanes]
+        c = [nx[j] if shift[j] else (cL if below[j] else c[j]) for j in lanes]
+    out = np.full(k, -1)
+    for j in range(k):
+        if packed:
+            v = M & ~c[j]
+            slot, ix = (v >> 20) & 63, v & NOI
+            out[slot] = -1 if ix == NOI else ix
+        else:
+            out[c[j] & 0xFFFFFFFF] = rid[j]
+    return out
+
+
+def listed_blocks(x: np.ndarray, k: int):
+    """The staged replay's block list: the k largest block keys so far in
+    lanes (ascending, min(r[j + 1], max(r[j], key)) per block), a block
+    listed when its key is above lane 0's when it comes."""
+    keys = f2key(x)
+    nb = (len(x) + 63) // 64
+    bkey = [int(keys[64 * b:64 * b + 64].max()) for b in range(nb)]
+    r = [0 if j < k else 0xFFFFFFFF for j in range(64)]
+    out = []
+    for b, kb in enumerate(bkey):
+        if kb > r[0]:
+            out.append(b)
+        nx = r[1:] + [0xFFFFFFFF]
+        r = [min(nx[j], max(r[j], kb)) for j in range(64)]
+    return set(out)
+
+
+def entering(x: np.ndarray, k: int):
+    """Indices that enter the reference's slots (src/sampler.ts:55-56)."""
+    vals = [-np.inf] * k
+    out = []
+    for i, v in enumerate(np.asarray(x, np.float64)):
+        mv = min(vals)
+        if v > mv:
+            vals[vals.index(mv)] = v
+            out.append(i)
+    return out
+
+
+def _rows(rng):
+    for _ in range(6):
+        k = int(rng.integers(1, 65))
+        n = int(rng.integers(1, 700))
+        kind = rng.random()
+        if kind < 0.4:
+            x = (rng.integers(-12, 12, n) / 4).astype(np.float32)   # many ties
+        elif kind < 0.7:
+            x = rng.standard_normal(n).astype(np.float32)
+        else:
+            x = (np.arange(n) * 1e-3 + rng.integers(0, 3, n)).astype(np.float32)   # rising
+        x[rng.integers(0, n, 3)] = np.float32(-0.0)
+        if rng.random() < 0.3:
+            x[rng.integers(0, n, 5)] = np.float32(np.nan)
+        if rng.random() < 0.2:
+            x[rng.integers(0, n, 5)] = -np.inf
+        yield k, n, x
+
+
+@pytest.mark.parametrize("seed", range(10))
+@pytest.mark.parametrize("packed", [False, True])
+def test_minmax_lanes_match_slot_scan(seed, packed):
+    rng = np.random.default_rng(300 + seed)
+    for k, n, x in _rows(rng):
+        ids, _ = o.topk_slots(x, n, k)
+        assert minmax_replay(x, k, packed).tolist() == list(ids), (seed, k, n, packed)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_listed_blocks_hold_every_entering_logit(seed):
+    rng = np.random.default_rng(400 + seed)
+    for k, n, x in _rows(rng):
+        need = {i // 64 for i in entering(x, k)}
+        assert need <= listed_blocks(x, k), (seed, k, n)
