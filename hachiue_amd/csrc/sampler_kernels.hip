@@ -879,32 +879,82 @@ __device__ __forceinline__ uint32_t wave_shl1_zero(uint32_t x) {   // lane j <- 
 struct PackedSlots {
   static constexpr uint32_t kNoIndex = 0xFFFFFu;
   unsigned long long c;
-  uint32_t mk;
-  int mi, k;
-  __device__ __forceinline__ explicit PackedSlots(int k_) : mk(0), mi(0), k(k_) {
+  // lane 0's low word with the index bits set, ~(mi << 20): the low word of
+  // every compare key, and (xor the index) of the word a logit enters with
+  uint32_t klo;
+  int k;
+  __device__ __forceinline__ explicit PackedSlots(int k_) : klo(0xFFFFFFFFu), k(k_) {
     const int lane = lane_id();
     c = lane < k ? ~(((unsigned long long)lane << 20) | kNoIndex) : 0ull;
+  }
+  __device__ __forceinline__ uint32_t min_key() const {   // mk
+    return ~(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(c >> 32));
   }
   __device__ __forceinline__ void take_min(uint32_t kL, int idx) {
     // compared without its index (no slot sorts between (kL, mi) and the
     // new word, and a logit equal to the minimum must leave lane 0 as it is)
-    const unsigned long long cK = ~(((unsigned long long)kL << 32) | ((uint32_t)mi << 20));
-    const unsigned long long cL = cK & ~(unsigned long long)kNoIndex | (kNoIndex & ~(uint32_t)idx);
+    const unsigned long long hi = (unsigned long long)~kL << 32;
+    const unsigned long long cK = hi | klo;
+    const unsigned long long cL = hi | (klo ^ (uint32_t)idx);
     const unsigned long long nx =
         ((unsigned long long)wave_shl1_zero((uint32_t)(c >> 32)) << 32) | wave_shl1_zero((uint32_t)c);
     const bool below = c > cK;   // complemented: this lane's slot sorts below the new one
     const bool shift = nx > cK;  // so does the next lane's: this lane takes it
     const unsigned long long m = below ? cL : c;
     c = shift ? nx : m;
-    mk = ~(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(c >> 32));
-    mi = (int)((~(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)c) >> 20) & 63u);
+    klo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)c) | kNoIndex;
   }
   __device__ __forceinline__ void scan64(uint32_t kx, int base) {
-    unsigned long long cm = __ballot(kx > mk);
+    unsigned long long cm = __ballot(kx > min_key());
     while (cm) {
       const int L = (int)__ffsll((long long)cm) - 1;
       cm &= cm - 1;
       take_min(readlane_u32(kx, L), base + L);
+    }
+  }
+  // the logits [64 * b_begin, 64 * b_end) of a row read from memory, in
+  // index order, eight blocks' reads in flight.  From the row's start, when
+  // its first k logits all have keys (the usual case), they fill slots
+  // 0..k-1 in order, so the lanes are those k words sorted (one wave sort)
+  // rather than k steps of take_min.
+  __device__ __forceinline__ void scan_memory(const float *rowp, int V, int b_begin, int nblk) {
+    const int lane = lane_id();
+    constexpr int B = 8;
+    float nx[B];
+#pragma unroll
+    for (int q = 0; q < B; ++q) {
+      const int e = (b_begin + q) * 64 + lane;
+      nx[q] = rowp[b_begin + q < nblk && e < V ? e : 0];   // always a read inside the row
+    }
+    int from = 0;   // lanes of the first block still to scan
+    if (b_begin == 0 && nblk > 0) {
+      const uint32_t k0 = lane < V ? f2key(nx[0]) : 0u;
+      const unsigned long long first = k >= 64 ? ~0ull : (1ull << k) - 1;
+      if ((__ballot(lane < k && k0 != 0u) & first) == first) {
+        c = lane < k ? ~(((unsigned long long)k0 << 32) | ((uint32_t)lane << 20) | (uint32_t)lane)
+                     : 0ull;
+        c = wave_sort_desc64(c);   // complemented: lane 0 the smallest (key, slot)
+        klo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)c) | kNoIndex;
+        from = k;
+      }
+    }
+    for (int b0 = b_begin; b0 < nblk; b0 += B) {
+      float x[B];
+#pragma unroll
+      for (int q = 0; q < B; ++q) x[q] = nx[q];
+      if (b0 + B < nblk) {
+#pragma unroll
+        for (int q = 0; q < B; ++q) {
+          const int e = (b0 + B + q) * 64 + lane;
+          nx[q] = rowp[b0 + B + q < nblk && e < V ? e : 0];
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < B; ++q) {
+        const int e = (b0 + q) * 64 + lane;
+        const bool in = e < V && (b0 + q > 0 || lane >= from);
+        if (b0 + q < nblk) scan64(in ? f2key(x[q]) : 0u, (b0 + q) * 64);
+      }
     }
   }
   __device__ __forceinline__ void store(float *sv, int32_t *sid) const {
@@ -1080,23 +1130,28 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
 //  - wave 1 keeps the k largest block keys sorted in its lanes (ascending,
 //    updated as LaneSlots updates its slots) and lists, in index order, the
 //    blocks whose key is above the smallest of them when they come (about
-//    k + k ln(V / 64k) of the ceil(V / 64) blocks on random rows), two
-//    groups of G blocks ahead of the copies;
+//    k + k ln(V / 64k) of the ceil(V / 64) blocks on random rows), a group
+//    of G blocks ahead of the copies;
 //  - waves 2.. copy the keys of the group listed before into LDS (two
 //    alternating buffers);
 //  - wave 0 scans the group copied before with PackedSlots::scan64 (the
 //    steps of replay_row), reading LDS only.
-// Every thread of the workgroup calls it with the same arguments; the slots
-// end in sv / sid.  bkey (nb = ceil(V / 64) words) lies at the start of
-// `words` words of LDS, whose rest holds the buffers; ring (ring_cap words)
-// holds the list, and pub (4 words) the list's length and end, per step
-// parity.  It returns false, having done nothing, when the buffers do not
-// fit (the caller then runs replay_row).
-constexpr int kStageBlocks = 64;   // G at most
+// Every thread of the workgroup calls it with the same arguments; wave 0's
+// ls holds the slots after the blocks below hm (its caller scans them from
+// memory, the dense head of the row, while the other waves take the block
+// keys), wave 0 scans blocks hm..h0-1 from memory while wave 1 lists the
+// first group, and the list starts at block h0.  The slots end in sv / sid.  bkey
+// (nb = ceil(V / 64) words) lies at the start of `words` words of LDS, whose
+// rest holds the buffers; ring (ring_cap words) holds the list, and pub (4
+// words) the list's length and end, per step parity.  It returns false,
+// having done nothing, when the buffers do not fit (the caller then runs
+// replay_row).
+constexpr int kStageBlocks = 32;   // G at most
 
 template <int NT>
-__device__ __forceinline__ bool replay_staged(const float *rowp, int V, int k, uint32_t *bkey,
-                                              int words, uint32_t *ring, int ring_cap, int32_t *pub,
+__device__ __forceinline__ bool replay_staged(const float *rowp, int V, int k, PackedSlots &ls,
+                                              int hm, int h0, uint32_t *bkey, int words,
+                                              uint32_t *ring, int ring_cap, int32_t *pub,
                                               float *sv, int32_t *sid) {
   constexpr int NW = NT / 64;
   static_assert(NW >= 3, "replay_staged: a scanning wave, a listing wave and copying waves");
@@ -1106,16 +1161,15 @@ __device__ __forceinline__ bool replay_staged(const float *rowp, int V, int k, u
   const int nb = (V + 63) >> 6;
   const int boff = (nb + 63) & ~63;
   const int G = min(kStageBlocks, (words - boff) / 128);
-  if (G < 8 || ring_cap < 4 * G + 64 || V > kRowMaxVocab) return false;
+  if (G < 8 || ring_cap < 3 * G + 64 || V > kRowMaxVocab) return false;
   uint32_t *buf = bkey + boff;
   // wave 1's state
   uint32_t rk = lane < k ? 0u : 0xFFFFFFFFu;
   int w0 = 0, n = 0;
-  PackedSlots ls(k);   // V <= kRowMaxVocab
   int L = 0;   // blocks listed by the end of the previous step
   for (int t = 0;; ++t) {
     if (wave == 1) {
-      while (n < (t + 2) * G && w0 < nb) {
+      while (n < (t + 1) * G && w0 < nb) {
         const uint32_t kb = w0 + lane < nb ? bkey[w0 + lane] : 0u;
         const uint32_t mk = (uint32_t)__builtin_amdgcn_readfirstlane((int)rk);
         unsigned long long cm = __ballot(kb > mk), ent = 0;
@@ -1127,10 +1181,12 @@ __device__ __forceinline__ bool replay_staged(const float *rowp, int V, int k, u
           rk = min(wave_shl1_u32(rk), max(rk, kL));
         }
         // the window's marked blocks, in index order, appended to the list
+        // (blocks below h0 were scanned already)
         const unsigned long long em =
-            ((unsigned long long)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(ent >> 32))
-             << 32) |
-            (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)ent);
+            (((unsigned long long)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(ent >> 32))
+              << 32) |
+             (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)ent)) &
+            (w0 >= h0 ? ~0ull : w0 + 64 <= h0 ? 0ull : ~0ull << (h0 - w0));
         const int pos = n + (int)__builtin_amdgcn_mbcnt_hi(
                                 (uint32_t)(em >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)em, 0u));
         if ((em >> lane) & 1ull) ring[pos % ring_cap] = (uint32_t)(w0 + lane);
@@ -1161,6 +1217,7 @@ __device__ __forceinline__ bool replay_staged(const float *rowp, int V, int k, u
         }
       }
     } else {
+      if (t == 0) ls.scan_memory(rowp, V, hm, h0);   // the rest of the head, while the list starts
       const int g = t - 2;   // copied in the previous step
       if (g >= 0 && g * G < L) {
         const int j0 = g * G, nj = min(G, L - j0);
@@ -2093,15 +2150,14 @@ __device__ __forceinline__ unsigned long long merge_top64(unsigned long long a, 
   return c;
 }
 
-// Every thread of the block: bkey[b] = key of the largest logit of logits
-// [64 b, 64 b + 64) of the row (0 when none is above -Infinity), for the slot
-// replay to skip blocks.  A 16-lane DPP row takes one block, a float4 per
-// lane.  While a step of UN slots per thread lies wholly inside a 16-byte
-// aligned row, its reads are 16-byte loads (8 per thread, 128 KiB per
-// workgroup in flight); the rest, 4 slots per thread, is read by elements.
+// NT threads (tid: 0..NT-1, whole waves): bkey[b] = key of the largest logit
+// of logits [64 b, 64 b + 64) of the row (0 when none is above -Infinity),
+// for the slot replay to skip blocks.  A 16-lane DPP row takes one block, a
+// float4 per lane.  In a 16-byte aligned row every read is a 16-byte load (8
+// per thread in flight, 120-128 KiB per workgroup); otherwise 4 slots per
+// thread are read by elements.
 template <int NT>
-__device__ void block_keys(const float *rowp, int V, uint32_t *bkey) {
-  const int tid = threadIdx.x;
+__device__ void block_keys(const float *rowp, int V, uint32_t *bkey, int tid) {
   const int nf = ((V + 63) >> 6) * 16;   // float4 slots, 16 per block
   // the block maximum of each thread's slot key, by its DPP row (row_shr:1,
   // 2, 4, 8: lane 15 holds it)
@@ -2113,22 +2169,33 @@ __device__ void block_keys(const float *rowp, int V, uint32_t *bkey) {
     y = (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, 0x118, 0xF, 0xF, false); x = x > y ? x : y;
     if ((tid & 15) == 15 && f < nf) bkey[f >> 4] = x;
   };
-  int f0 = 0;
-  if ((reinterpret_cast<uintptr_t>(rowp) & 15) == 0) {
+  const int full = V >> 2;   // slots wholly inside the row
+  if ((reinterpret_cast<uintptr_t>(rowp) & 15) == 0 && full > 0) {
+    // every slot read as one float4 (clamped to the last whole one); the
+    // slot holding the row's last logits (V % 4 of them) takes them one by
+    // one, and slots past the row have key 0
     constexpr int UN = 8;
     const float4 *r4 = reinterpret_cast<const float4 *>(rowp);
-    const int full = V >> 2;   // slots wholly inside the row
-    for (; f0 + UN * NT <= full; f0 += UN * NT) {
+    for (int f0 = 0; f0 < nf; f0 += UN * NT) {
       float4 v[UN];
 #pragma unroll
-      for (int u = 0; u < UN; ++u) v[u] = r4[f0 + u * NT + tid];
+      for (int u = 0; u < UN; ++u) v[u] = r4[min(f0 + u * NT + tid, full - 1)];
 #pragma unroll
       for (int u = 0; u < UN; ++u) {
-        const uint32_t a = max(f2key(v[u].x), f2key(v[u].y)), b = max(f2key(v[u].z), f2key(v[u].w));
-        put(f0 + u * NT + tid, max(a, b));
+        const int f = f0 + u * NT + tid;
+        uint32_t kk = 0;
+        if (f < full) {
+          const uint32_t a = max(f2key(v[u].x), f2key(v[u].y)), b = max(f2key(v[u].z), f2key(v[u].w));
+          kk = max(a, b);
+        } else if (f == full) {
+          for (int e = 4 * f; e < V; ++e) kk = max(kk, f2key(rowp[e]));
+        }
+        put(f, kk);
       }
     }
+    return;
   }
+  int f0 = 0;
   constexpr int UT = 4;
   for (; f0 < nf; f0 += UT * NT) {
     // every read issued before any is used
@@ -2546,12 +2613,20 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     bool staged = false;
     if (rs.tie) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      block_keys<kRowThreads>(rowfull, a.vocab, reinterpret_cast<uint32_t *>(cbuf));
+      // as for a whole row: wave 0 replays the first k blocks from memory
+      // while the others take the block keys
+      PackedSlots ls(k);
+      const int h0 = min(k, (a.vocab + 63) >> 6), hm = h0 >> 1;
+      if (wave == 0)
+        ls.scan_memory(rowfull, a.vocab, 0, hm);
+      else
+        block_keys<kRowThreads - 64>(rowfull, a.vocab, reinterpret_cast<uint32_t *>(cbuf), tid - 64);
       __syncthreads();
       bkey = reinterpret_cast<const uint32_t *>(cbuf);
-      staged = replay_staged<kRowThreads>(rowfull, a.vocab, k, reinterpret_cast<uint32_t *>(cbuf),
-                                          2 * kRowCandCap, reinterpret_cast<uint32_t *>(srt),
-                                          2 * kSortCap, rs.pub, rsv, rsid);
+      staged = replay_staged<kRowThreads>(rowfull, a.vocab, k, ls, hm, h0,
+                                          reinterpret_cast<uint32_t *>(cbuf), 2 * kRowCandCap,
+                                          reinterpret_cast<uint32_t *>(srt), 2 * kSortCap, rs.pub,
+                                          rsv, rsid);
     }
     if (wave != 0) return;
     tail_finish(a, P, row, rowfull, st, u, rsv, rsid, reinterpret_cast<double *>(top), true, bkey,
@@ -2596,10 +2671,19 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   const uint32_t *bkey = nullptr;
   bool staged = false;
   if (rs.tie) {
-    block_keys<kRowThreads>(rowp, V, reinterpret_cast<uint32_t *>(cbuf));
+    // wave 0 replays the first k blocks from memory (the slots fill there and
+    // most of the row's entering logits lie there): half while the others
+    // take the block keys, the rest while wave 1 starts its list; then the
+    // staged replay of the blocks listed after them
+    PackedSlots ls(k);
+    const int h0 = min(k, (V + 63) >> 6), hm = h0 >> 1;
+    if (wave == 0)
+      ls.scan_memory(rowp, V, 0, hm);
+    else
+      block_keys<kRowThreads - 64>(rowp, V, reinterpret_cast<uint32_t *>(cbuf), tid - 64);
     __syncthreads();
     bkey = reinterpret_cast<const uint32_t *>(cbuf);
-    staged = replay_staged<kRowThreads>(rowp, V, k, reinterpret_cast<uint32_t *>(cbuf),
+    staged = replay_staged<kRowThreads>(rowp, V, k, ls, hm, h0, reinterpret_cast<uint32_t *>(cbuf),
                                         2 * kRowCandCap, reinterpret_cast<uint32_t *>(srt),
                                         2 * kSortCap, rs.pub, rsv, rsid);
   }

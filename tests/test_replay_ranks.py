@@ -105,10 +105,13 @@ def f2key(x: np.ndarray) -> np.ndarray:
     return np.where(np.asarray(x, np.float32) > -np.inf, k, 0).astype(np.uint64)
 
 
-def minmax_replay(x: np.ndarray, k: int, packed: bool):
+def minmax_replay(x: np.ndarray, k: int, packed: bool, fill: bool = False):
     """LaneSlots (packed=False: c = key << 32 | slot, the index in its own
     lane) or PackedSlots (packed=True: ~(key << 32 | slot << 20 | index),
-    compared without the index), updated for every logit with a key."""
+    compared without the index), updated for every logit with a key.  With
+    fill (PackedSlots::scan_memory from the row's start), when the first k
+    logits all have keys the lanes start as those k words sorted, and the
+    scan starts at logit k."""
     M = (1 << 64) - 1
     NOI = 0xFFFFF
     lanes = np.arange(64)
@@ -118,14 +121,19 @@ def minmax_replay(x: np.ndarray, k: int, packed: bool):
     else:
         c = [j if j < k else M for j in range(64)]
     rid = [-1] * 64
+    start = 0
+    if fill and packed and len(keys) >= k and all(int(v) != 0 for v in keys[:k]):
+        words = sorted(M & ~((int(keys[j]) << 32) | (j << 20) | j) for j in range(k))[::-1]
+        c = words + [0] * (64 - k)
+        start = k
     for i, kx in enumerate(keys.tolist()):
-        if kx == 0:
+        if kx == 0 or i < start:
             continue
         if packed:
-            lo = (M & ~c[0]) & 0xFFFFFFFF
-            mi = (lo >> 20) & 63
-            cK = M & ~((kx << 32) | (mi << 20))
-            cL = (cK & ~NOI) | (NOI & ~i)
+            klo = (c[0] & 0xFFFFFFFF) | NOI                   # lane 0's low word, index bits set
+            hi = ((~kx) & 0xFFFFFFFF) << 32
+            cK = hi | klo
+            cL = hi | (klo ^ i)
             nx = c[1:] + [0]                                  # lane 63 reads 0
             below = [cj > cK for cj in c]
             shift = [nj > cK for nj in nx]
@@ -198,12 +206,12 @@ def _rows(rng):
 
 
 @pytest.mark.parametrize("seed", range(10))
-@pytest.mark.parametrize("packed", [False, True])
-def test_minmax_lanes_match_slot_scan(seed, packed):
+@pytest.mark.parametrize("packed,fill", [(False, False), (True, False), (True, True)])
+def test_minmax_lanes_match_slot_scan(seed, packed, fill):
     rng = np.random.default_rng(300 + seed)
     for k, n, x in _rows(rng):
         ids, _ = o.topk_slots(x, n, k)
-        assert minmax_replay(x, k, packed).tolist() == list(ids), (seed, k, n, packed)
+        assert minmax_replay(x, k, packed, fill).tolist() == list(ids), (seed, k, n, packed, fill)
 
 
 @pytest.mark.parametrize("seed", range(10))
