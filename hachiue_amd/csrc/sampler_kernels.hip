@@ -875,6 +875,9 @@ struct LaneSlots {
 __device__ __forceinline__ uint32_t wave_shl1_zero(uint32_t x) {   // lane j <- lane j + 1; lane 63 <- 0
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x130, 0xF, 0xF, true);
 }
+__device__ __forceinline__ uint32_t wave_shr1_u32(uint32_t x) {   // lane j <- lane j - 1; lane 0 <- 0
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x138, 0xF, 0xF, true);
+}
 
 struct PackedSlots {
   static constexpr uint32_t kNoIndex = 0xFFFFFu;
@@ -912,49 +915,28 @@ struct PackedSlots {
       take_min(readlane_u32(kx, L), base + L);
     }
   }
-  // the logits [64 * b_begin, 64 * b_end) of a row read from memory, in
-  // index order, eight blocks' reads in flight.  From the row's start, when
-  // its first k logits all have keys (the usual case), they fill slots
-  // 0..k-1 in order, so the lanes are those k words sorted (one wave sort)
-  // rather than k steps of take_min.
-  __device__ __forceinline__ void scan_memory(const float *rowp, int V, int b_begin, int nblk) {
+  // the keys of a row's first nblk blocks of 64 logits, from LDS (keys[64 b
+  // + lane], 0 past the row), in index order.  When the row's first k
+  // logits all have keys (the usual case) they fill slots 0..k-1 in order,
+  // so the lanes are those k words sorted (one wave sort) rather than k
+  // steps of take_min.
+  __device__ __forceinline__ void scan_keys(const uint32_t *keys, int nblk) {
+    if (nblk <= 0) return;
     const int lane = lane_id();
-    constexpr int B = 8;
-    float nx[B];
-#pragma unroll
-    for (int q = 0; q < B; ++q) {
-      const int e = (b_begin + q) * 64 + lane;
-      nx[q] = rowp[b_begin + q < nblk && e < V ? e : 0];   // always a read inside the row
-    }
+    uint32_t x = keys[lane];
     int from = 0;   // lanes of the first block still to scan
-    if (b_begin == 0 && nblk > 0) {
-      const uint32_t k0 = lane < V ? f2key(nx[0]) : 0u;
-      const unsigned long long first = k >= 64 ? ~0ull : (1ull << k) - 1;
-      if ((__ballot(lane < k && k0 != 0u) & first) == first) {
-        c = lane < k ? ~(((unsigned long long)k0 << 32) | ((uint32_t)lane << 20) | (uint32_t)lane)
-                     : 0ull;
-        c = wave_sort_desc64(c);   // complemented: lane 0 the smallest (key, slot)
-        klo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)c) | kNoIndex;
-        from = k;
-      }
+    const unsigned long long first = k >= 64 ? ~0ull : (1ull << k) - 1;
+    if ((__ballot(lane < k && x != 0u) & first) == first) {
+      c = lane < k ? ~(((unsigned long long)x << 32) | ((uint32_t)lane << 20) | (uint32_t)lane)
+                   : 0ull;
+      c = wave_sort_desc64(c);   // complemented: lane 0 the smallest (key, slot)
+      klo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)c) | kNoIndex;
+      from = k;
     }
-    for (int b0 = b_begin; b0 < nblk; b0 += B) {
-      float x[B];
-#pragma unroll
-      for (int q = 0; q < B; ++q) x[q] = nx[q];
-      if (b0 + B < nblk) {
-#pragma unroll
-        for (int q = 0; q < B; ++q) {
-          const int e = (b0 + B + q) * 64 + lane;
-          nx[q] = rowp[b0 + B + q < nblk && e < V ? e : 0];
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < B; ++q) {
-        const int e = (b0 + q) * 64 + lane;
-        const bool in = e < V && (b0 + q > 0 || lane >= from);
-        if (b0 + q < nblk) scan64(in ? f2key(x[q]) : 0u, (b0 + q) * 64);
-      }
+    for (int b = 0; b < nblk; ++b) {
+      const uint32_t xb = x;
+      if (b + 1 < nblk) x = keys[(b + 1) * 64 + lane];   // the next block's read ahead of the scan
+      scan64(b > 0 || lane >= from ? xb : 0u, b * 64);
     }
   }
   __device__ __forceinline__ void store(float *sv, int32_t *sid) const {
@@ -964,6 +946,28 @@ struct PackedSlots {
       const uint32_t ix = (uint32_t)v & kNoIndex;
       sv[rs] = ix != kNoIndex ? key2f((uint32_t)(v >> 32)) : -INFINITY;
       sid[rs] = ix != kNoIndex ? (int32_t)ix : -1;
+    }
+  }
+  // The slots in the stable sort's order (src/sampler.ts:72-74: value
+  // descending, equal values by slot ascending, empty slots last): lane j
+  // (ascending by (key, slot)) goes to position (k - 1 - the last lane of its
+  // key's run) + (j - the run's first lane).  sv / sid are indexed by that
+  // position; sid holds the logit index.
+  __device__ __forceinline__ void store_ordered(float *sv, int32_t *sid) const {
+    const int lane = lane_id();
+    const unsigned long long v = ~c;
+    const uint32_t key = (uint32_t)(v >> 32);
+    const uint32_t prev = wave_shr1_u32(key);
+    const unsigned long long runs = __ballot(lane < k && (lane == 0 || key != prev));
+    const unsigned long long upto = lane >= 63 ? ~0ull : (2ull << lane) - 1;
+    const int first = 63 - __clzll(runs & upto);
+    const unsigned long long above = runs & ~upto;
+    const int last = above ? __ffsll((long long)above) - 2 : k - 1;
+    if (lane < k) {
+      const int pos = (k - 1 - last) + (lane - first);
+      const uint32_t ix = (uint32_t)v & kNoIndex;
+      sv[pos] = ix != kNoIndex ? key2f(key) : -INFINITY;
+      sid[pos] = ix != kNoIndex ? (int32_t)ix : -1;
     }
   }
 };
@@ -1120,6 +1124,35 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
   }
 }
 
+// The staged replay's LDS beside the block keys: its list (a ring of
+// kReplayRing words) and the keys of the row's first kHeadBlocks blocks,
+// together in the fallback sort's kSortCap words.
+constexpr int kReplayRing = 256;
+constexpr int kHeadBlocks = 60;
+static_assert(kReplayRing + 64 * kHeadBlocks <= 2 * kSortCap, "replay: ring and head in srt");
+
+// Waves 1.. of the workgroup: keys[64 b + lane] = f2key of logit 64 b + lane
+// (0 past the row) for the first h0 blocks, one block per wave at a time.
+template <int NT>
+__device__ __forceinline__ void replay_head_keys(const float *rowp, int V, int h0, uint32_t *keys) {
+  constexpr int NW = NT / 64;
+  const int lane = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  if (wave == 0) return;
+  constexpr int PER = (kHeadBlocks + NW - 2) / (NW - 1);
+  float x[PER];
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int e = ((wave - 1) + (NW - 1) * q) * 64 + lane;
+    x[q] = rowp[e < 64 * h0 && e < V ? e : 0];   // always a read inside the row
+  }
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int b = (wave - 1) + (NW - 1) * q, e = b * 64 + lane;
+    if (b < h0) keys[e] = e < V ? f2key(x[q]) : 0u;
+  }
+}
+
 // The slot replay of replay_row for k <= 64 with the whole workgroup, for
 // the row kernel's rows whose draw needs it.  After logit i the slots hold
 // the k largest logits of [0, i) (a logit enters iff it is above the
@@ -1137,10 +1170,10 @@ __device__ __forceinline__ void replay_row(const float *rowp, int vocab, int k, 
 //  - wave 0 scans the group copied before with PackedSlots::scan64 (the
 //    steps of replay_row), reading LDS only.
 // Every thread of the workgroup calls it with the same arguments; wave 0's
-// ls holds the slots after the blocks below hm (its caller scans them from
-// memory, the dense head of the row, while the other waves take the block
-// keys), wave 0 scans blocks hm..h0-1 from memory while wave 1 lists the
-// first group, and the list starts at block h0.  The slots end in sv / sid.  bkey
+// ls holds the slots after the blocks below h0 (the dense head of the row,
+// which its caller scans while the other waves take the block keys), and
+// the list starts at block h0.  The slots end in sv / sid in the stable
+// sort's order (PackedSlots::store_ordered).  bkey
 // (nb = ceil(V / 64) words) lies at the start of `words` words of LDS, whose
 // rest holds the buffers; ring (ring_cap words) holds the list, and pub (4
 // words) the list's length and end, per step parity.  It returns false,
@@ -1150,9 +1183,9 @@ constexpr int kStageBlocks = 32;   // G at most
 
 template <int NT>
 __device__ __forceinline__ bool replay_staged(const float *rowp, int V, int k, PackedSlots &ls,
-                                              int hm, int h0, uint32_t *bkey, int words,
-                                              uint32_t *ring, int ring_cap, int32_t *pub,
-                                              float *sv, int32_t *sid) {
+                                              int h0, uint32_t *bkey, int words, uint32_t *ring,
+                                              int ring_cap, int32_t *pub, float *sv,
+                                              int32_t *sid) {
   constexpr int NW = NT / 64;
   static_assert(NW >= 3, "replay_staged: a scanning wave, a listing wave and copying waves");
   constexpr int PER = (kStageBlocks + NW - 3) / (NW - 2);   // blocks per copying wave and group
@@ -1217,7 +1250,6 @@ __device__ __forceinline__ bool replay_staged(const float *rowp, int V, int k, P
         }
       }
     } else {
-      if (t == 0) ls.scan_memory(rowp, V, hm, h0);   // the rest of the head, while the list starts
       const int g = t - 2;   // copied in the previous step
       if (g >= 0 && g * G < L) {
         const int j0 = g * G, nj = min(G, L - j0);
@@ -1236,7 +1268,7 @@ __device__ __forceinline__ bool replay_staged(const float *rowp, int V, int k, P
     const bool done = pub[2 * (t & 1) + 1] != 0;
     if (done && (t - 1) * G >= L) break;   // groups 0..t-2 scanned: every listed block
   }
-  if (wave == 0) ls.store(sv, sid);
+  if (wave == 0) ls.store_ordered(sv, sid);
   return true;
 }
 
@@ -2037,13 +2069,15 @@ __device__ __forceinline__ void tail_finish(const LaunchArgs &a, const RowPlan &
   const int k = P.k;
   bool replayed = false;
   if (st.need) {
-    if (!staged) {   // staged: replay_staged left the slots in rsv / rsid
+    if (!staged) {   // staged: replay_staged left the slots in rsv / rsid, in order
       if (acquire_replay) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       replay_row<RB>(rowp, a.vocab, k, rsv, rsid, bkey);
     }
     const bool filled = lane < k && rsid[lane] >= 0;
     unsigned long long x = filled ? pack_cand(f2key(rsv[lane]), (uint32_t)lane) : 0ull;
-    x = wave_sort_desc64(x);   // value descending, slot ascending (stable sort)
+    // value descending, slot ascending (stable sort); the staged replay
+    // stored its slots in that order already
+    if (!staged) x = wave_sort_desc64(x);
     st.n = __popcll(__ballot(filled));
     st.key = cand_key(x);
     st.id = lane < st.n ? rsid[cand_idx(x)] : -1;
@@ -2613,20 +2647,22 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
     bool staged = false;
     if (rs.tie) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      // as for a whole row: wave 0 replays the first k blocks from memory
-      // while the others take the block keys
+      // as for a whole row: the first k blocks copied into LDS, replayed by
+      // wave 0 while the others take the block keys
       PackedSlots ls(k);
-      const int h0 = min(k, (a.vocab + 63) >> 6), hm = h0 >> 1;
+      const int h0 = min(min(k, (a.vocab + 63) >> 6), kHeadBlocks);
+      uint32_t *ring = reinterpret_cast<uint32_t *>(srt), *hkeys = ring + kReplayRing;
+      replay_head_keys<kRowThreads>(rowfull, a.vocab, h0, hkeys);
+      __syncthreads();
       if (wave == 0)
-        ls.scan_memory(rowfull, a.vocab, 0, hm);
+        ls.scan_keys(hkeys, h0);
       else
         block_keys<kRowThreads - 64>(rowfull, a.vocab, reinterpret_cast<uint32_t *>(cbuf), tid - 64);
       __syncthreads();
       bkey = reinterpret_cast<const uint32_t *>(cbuf);
-      staged = replay_staged<kRowThreads>(rowfull, a.vocab, k, ls, hm, h0,
-                                          reinterpret_cast<uint32_t *>(cbuf), 2 * kRowCandCap,
-                                          reinterpret_cast<uint32_t *>(srt), 2 * kSortCap, rs.pub,
-                                          rsv, rsid);
+      staged = replay_staged<kRowThreads>(rowfull, a.vocab, k, ls, h0,
+                                          reinterpret_cast<uint32_t *>(cbuf), 2 * kRowCandCap, ring,
+                                          kReplayRing, rs.pub, rsv, rsid);
     }
     if (wave != 0) return;
     tail_finish(a, P, row, rowfull, st, u, rsv, rsid, reinterpret_cast<double *>(top), true, bkey,
@@ -2671,21 +2707,23 @@ __global__ __launch_bounds__(kRowThreads) void row_kernel(LaunchArgs a, Workspac
   const uint32_t *bkey = nullptr;
   bool staged = false;
   if (rs.tie) {
-    // wave 0 replays the first k blocks from memory (the slots fill there and
-    // most of the row's entering logits lie there): half while the others
-    // take the block keys, the rest while wave 1 starts its list; then the
-    // staged replay of the blocks listed after them
+    // the first k blocks (the slots fill there and most of the row's
+    // entering logits lie there) are copied into LDS, and wave 0 replays them
+    // while the others take the block keys; then the staged replay of the
+    // blocks listed after them
     PackedSlots ls(k);
-    const int h0 = min(k, (V + 63) >> 6), hm = h0 >> 1;
+    const int h0 = min(min(k, (V + 63) >> 6), kHeadBlocks);
+    uint32_t *ring = reinterpret_cast<uint32_t *>(srt), *hkeys = ring + kReplayRing;
+    replay_head_keys<kRowThreads>(rowp, V, h0, hkeys);
+    __syncthreads();
     if (wave == 0)
-      ls.scan_memory(rowp, V, 0, hm);
+      ls.scan_keys(hkeys, h0);
     else
       block_keys<kRowThreads - 64>(rowp, V, reinterpret_cast<uint32_t *>(cbuf), tid - 64);
     __syncthreads();
     bkey = reinterpret_cast<const uint32_t *>(cbuf);
-    staged = replay_staged<kRowThreads>(rowp, V, k, ls, hm, h0, reinterpret_cast<uint32_t *>(cbuf),
-                                        2 * kRowCandCap, reinterpret_cast<uint32_t *>(srt),
-                                        2 * kSortCap, rs.pub, rsv, rsid);
+    staged = replay_staged<kRowThreads>(rowp, V, k, ls, h0, reinterpret_cast<uint32_t *>(cbuf),
+                                        2 * kRowCandCap, ring, kReplayRing, rs.pub, rsv, rsid);
   }
   if (wave != 0) return;
   tail_finish(a, P, row, rowp, st, u, rsv, rsid, reinterpret_cast<double *>(top), false, bkey,

@@ -157,6 +157,21 @@ def minmax_replay(x: np.ndarray, k: int, packed: bool, fill: bool = False):
     return out
 
 
+def ordered_positions(lanes_asc):
+    """PackedSlots::store_ordered on lanes sorted ascending by (key, slot):
+    lane j goes to (k - 1 - last lane of its key's run) + (j - first lane)."""
+    k = len(lanes_asc)
+    keys = [kk for kk, _ in lanes_asc]
+    runs = [j for j in range(k) if j == 0 or keys[j] != keys[j - 1]]
+    pos = []
+    for j in range(k):
+        first = max(r for r in runs if r <= j)
+        above = [r for r in runs if r > j]
+        last = above[0] - 1 if above else k - 1
+        pos.append((k - 1 - last) + (j - first))
+    return pos
+
+
 def listed_blocks(x: np.ndarray, k: int):
     """The staged replay's block list: the k largest block keys so far in
     lanes (ascending, min(r[j + 1], max(r[j], key)) per block), a block
@@ -220,3 +235,21 @@ def test_listed_blocks_hold_every_entering_logit(seed):
     for k, n, x in _rows(rng):
         need = {i // 64 for i in entering(x, k)}
         assert need <= listed_blocks(x, k), (seed, k, n)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_ordered_store_is_the_stable_sort(seed):
+    """The positions store_ordered gives the final slots equal the
+    reference's order (src/sampler.ts:72-74): the slots sorted by value
+    descending, equal values by slot ascending, empty slots (-Infinity) last."""
+    rng = np.random.default_rng(500 + seed)
+    for k, n, x in _rows(rng):
+        ids, vals = o.topk_slots(x, n, k)
+        keys = [int(f2key(np.float32(v))) if i >= 0 else 0 for i, v in zip(ids, vals)]
+        lanes = sorted((keys[s], s) for s in range(k))          # ascending (key, slot)
+        pos = ordered_positions(lanes)
+        got = [None] * k
+        for (kk, slot), p in zip(lanes, pos):
+            got[p] = slot
+        want = sorted(range(k), key=lambda s: (-keys[s], s))      # stable, value descending
+        assert got == want, (seed, k, n)
