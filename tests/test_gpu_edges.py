@@ -314,3 +314,26 @@ def test_slot_replay_full_rows(any_sampler, k):
     got, _ = _run(any_sampler, cases, V, cap=64, label=f"slot replay, full rows, k={k}")
     if k > 1:   # candidate outputs and a tie inside the top-k: the replay ran (HS_ROW_REPLAYED)
         assert got.flags[0] & 0x2 and got.flags[1] & 0x2, got.flags
+
+
+@pytest.mark.parametrize("k", [2, 40, 64])
+def test_slot_replay_ragged_rows(any_sampler, k):
+    """The staged replay on rows that are not 16-byte aligned (stride V + 1,
+    V not a multiple of 4 or 64), whose first k logits hold -Infinity or NaN
+    (no sorted fill: the slots fill by insertion), and with fewer finite
+    logits than k after the first block."""
+    V = 150001
+    r = _rng(70 + k)
+    base = r.standard_normal(V).astype(np.float32)
+    o = np.argsort(-base, kind="stable")
+    top = base.copy()
+    top[o[min(2, k - 1)]] = top[o[0]]                    # the largest twice (k >= 2)
+    holes = top.copy()
+    holes[[0, 3, k // 2]] = -np.inf
+    holes[5] = np.nan
+    sparse = np.full(V, -np.inf, np.float32)
+    sparse[r.choice(V, k + 3, replace=False)] = r.integers(0, 3, k + 3).astype(np.float32)
+    cfg = dict(temperature=0.8, topK=k, topP=1.0)
+    cases = [(top, [], cfg, 1e-4), (holes, [], cfg, 1e-4), (sparse, [], cfg, 0.6),
+             (holes, list(o[:4]), dict(repetitionPenalty=1.3, **cfg), 0.2)]
+    _run(any_sampler, cases, V, stride=V + 1, cap=64, label=f"slot replay, ragged rows, k={k}")
