@@ -8,10 +8,11 @@
 // in place: F32, Q4_0 (18 B / 32 weights), Q4_1 (20 B / 32), Q4_K (144 B /
 // 256), Q6_K (210 B / 256).
 //
-// Q6_K runs on the matrix cores (gemv_q6k_mfma_kernel, described there).  The
-// other formats use the vector units, one wave per group of rows:
-//   every lane owns a fixed "unit" of each row: 32 weights (F32, Q4_0, Q4_1,
-//   Q4_K: half of a 32-byte quant pair).  Its slice of x stays in registers
+// Q4_K and Q6_K run on the matrix cores (gemv_kq_mfma_kernel; the bodies in
+// q4k_gemv.h and q6k_gemv.h).  F32, Q4_0 and Q4_1 use the vector units, one
+// wave per group of rows:
+//   every lane owns a fixed "unit" of each row: 32 weights.  Its slice of x
+//   stays in registers
 //   for every row, with the sums the formats' offsets need (sum x over a
 //   group).  A row takes `seg` lanes (the row's units rounded up to a power of
 //   two; 64 / seg rows per wave step), or all 64 lanes with two units each.
@@ -24,7 +25,7 @@
 // specification: WGSL leaves contraction and evaluation to the compiler).
 #include "sampler_internal.h"
 #include "blk_gemv.h"
-#include "q6k_gemv.h"
+#include "kq_gemv.h"
 #include "tern_gemv.h"
 
 #include <hip/hip_ext.h>
@@ -36,7 +37,7 @@
 namespace hs {
 
 
-// ---- F32, Q4_0, Q4_1, Q4_K on the vector units (the bodies: blk_gemv.h)
+// ---- F32, Q4_0, Q4_1 on the vector units (the bodies: blk_gemv.h)
 
 namespace {
 // Each row's (or tile's) results straight to y.
@@ -61,13 +62,14 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_lds_kernel(GemvArgs g) {
   gemv_lds_body<FMT, NRU>(g, glds, epi);
 }
 
-// ---- Q6_K on the matrix cores (the body: q6k_gemv.h)
+// ---- Q4_K and Q6_K on the matrix cores (the bodies: q4k_gemv.h, q6k_gemv.h)
 
 // 2 workgroups per CU (16 waves): at most 128 VGPRs
-__global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_mfma_kernel(GemvArgs g) {
+template <int FMT>
+__global__ __launch_bounds__(KqBody<FMT>::kThreads, 2) void gemv_kq_mfma_kernel(GemvArgs g) {
   extern __shared__ uint4 qlds[];
   StoreRow epi{g.y + (int64_t)blockIdx.y * g.ldy};
-  q6k_gemv_body(g, reinterpret_cast<uint8_t *>(qlds), epi);
+  KqBody<FMT>::run(g, reinterpret_cast<uint8_t *>(qlds), epi);
 }
 
 // ---- Q1_0 / PQ2_0 / PTQ1_0 on the matrix cores (the body: tern_gemv.h)
@@ -173,23 +175,25 @@ hipError_t launch_fmt(GemvArgs g, hipStream_t stream, hipEvent_t *ev, hipEvent_t
   return hipGetLastError();
 }
 
-hipError_t launch_q6k_mfma(GemvArgs g, hipStream_t stream, hipEvent_t *ev, hipEvent_t done) {
-  const size_t lds = gemv_q6k_mfma_lds_bytes(g.K);
+template <int FMT>
+hipError_t launch_kq_mfma(GemvArgs g, hipStream_t stream, hipEvent_t *ev, hipEvent_t done) {
+  using B = KqBody<FMT>;
+  const size_t lds = B::lds(g.K);
   const int ntiles = (g.N + 15) / 16;
-  const int res = resident_blocks(reinterpret_cast<const void *>(gemv_q6k_mfma_kernel), (uint32_t)lds,
-                                  q6m::kThreads);
-  int blocks = (ntiles + q6m::kWaves - 1) / q6m::kWaves;
+  const int res = resident_blocks(reinterpret_cast<const void *>(gemv_kq_mfma_kernel<FMT>),
+                                  (uint32_t)lds, B::kThreads);
+  int blocks = (ntiles + B::kWaves - 1) / B::kWaves;
   blocks = blocks < res ? blocks : res;
   // every wave of an activation row owns a hand-over slot
-  blocks = blocks < g.part_cap / q6m::kWaves ? blocks : g.part_cap / q6m::kWaves;
+  blocks = blocks < g.part_cap / B::kWaves ? blocks : g.part_cap / B::kWaves;
   if (blocks < 1 || !g.part || !g.tile_cnt) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)blocks, (unsigned)g.M), block(q6m::kThreads);
+  const dim3 grid((unsigned)blocks, (unsigned)g.M), block(B::kThreads);
   if (ev)
-    hipExtLaunchKernelGGL(gemv_q6k_mfma_kernel, grid, block, lds, stream, ev[0], ev[1], 0u, g);
+    hipExtLaunchKernelGGL(gemv_kq_mfma_kernel<FMT>, grid, block, lds, stream, ev[0], ev[1], 0u, g);
   else if (done)
-    hipExtLaunchKernelGGL(gemv_q6k_mfma_kernel, grid, block, lds, stream, nullptr, done, 0u, g);
+    hipExtLaunchKernelGGL(gemv_kq_mfma_kernel<FMT>, grid, block, lds, stream, nullptr, done, 0u, g);
   else
-    hipLaunchKernelGGL(gemv_q6k_mfma_kernel, grid, block, lds, stream, g);
+    hipLaunchKernelGGL(gemv_kq_mfma_kernel<FMT>, grid, block, lds, stream, g);
   return hipGetLastError();
 }
 
@@ -216,9 +220,13 @@ hipError_t launch_tern(GemvArgs g, hipStream_t stream, hipEvent_t *ev, hipEvent_
 // Per device, once (with the sampler's kernels): the matrix-core kernels'
 // dynamic LDS limits.
 hipError_t prepare_gemv() {
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_q6k_mfma_kernel),
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_kq_mfma_kernel<kW_Q6_K>),
                                      hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)gemv_q6k_mfma_lds_bytes(kGemvMaxK));
+                                     (int)KqBody<kW_Q6_K>::lds(kGemvMaxK));
+  if (e == hipSuccess)
+    e = hipFuncSetAttribute(reinterpret_cast<const void *>(gemv_kq_mfma_kernel<kW_Q4_K>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)KqBody<kW_Q4_K>::lds(kGemvMaxK));
   const void *tk[3] = {reinterpret_cast<const void *>(gemv_tern_kernel<kW_Q1_0>),
                        reinterpret_cast<const void *>(gemv_tern_kernel<kW_PQ2_0>),
                        reinterpret_cast<const void *>(gemv_tern_kernel<kW_PTQ1_0>)};
@@ -242,8 +250,8 @@ hipError_t launch_gemv(const GemvArgs &g, hipStream_t stream, hipEvent_t *ev, hi
     case kW_F32: return two ? launch_fmt<kW_F32, 2>(g, stream, ev, done) : launch_fmt<kW_F32, 1>(g, stream, ev, done);
     case kW_Q4_0: return two ? launch_fmt<kW_Q4_0, 2>(g, stream, ev, done) : launch_fmt<kW_Q4_0, 1>(g, stream, ev, done);
     case kW_Q4_1: return two ? launch_fmt<kW_Q4_1, 2>(g, stream, ev, done) : launch_fmt<kW_Q4_1, 1>(g, stream, ev, done);
-    case kW_Q4_K: return two ? launch_fmt<kW_Q4_K, 2>(g, stream, ev, done) : launch_fmt<kW_Q4_K, 1>(g, stream, ev, done);
-    case kW_Q6_K: return launch_q6k_mfma(g, stream, ev, done);
+    case kW_Q4_K: return launch_kq_mfma<kW_Q4_K>(g, stream, ev, done);
+    case kW_Q6_K: return launch_kq_mfma<kW_Q6_K>(g, stream, ev, done);
     case kW_Q1_0: return launch_tern<kW_Q1_0>(g, stream, ev, done);
     case kW_PQ2_0: return launch_tern<kW_PQ2_0>(g, stream, ev, done);
     case kW_PTQ1_0: return launch_tern<kW_PTQ1_0>(g, stream, ev, done);

@@ -185,15 +185,15 @@ struct hs_context {
   // workspace
   DevBuf plans, cand, cand_count, info;
   DevBuf split_list, split_meta, split_cnt;   // split rows (split_cnt: zero between calls)
-  DevBuf gemv_part, gemv_cnt;   // Q6_K GEMV tiles cut between waves (gemv_cnt: zero between calls)
+  DevBuf gemv_part, gemv_cnt;   // Q4_K/Q6_K GEMV tiles cut between waves (gemv_cnt: zero between calls)
   DevBuf gemv_rot;              // the Hadamard-rotated input of a folded weight
   DevBuf fuse_rows, fuse_pool, fuse_hist;   // lm_head GEMV that samples its rows: counters
                                 //   (zero between calls), the waves' two largest, the
                                 //   rows' key histograms (zero between calls)
   // HS_LMHEAD_FUSE at creation: 0 always two launches; 1 (default) one
-  // launch for all-greedy calls on the planar and Q6_K weights; 2 also for
-  // calls with k <= 64 sampling rows there and all-greedy calls on the
-  // vector-unit weights (F32, Q4_0, Q4_1, Q4_K)
+  // launch for all-greedy calls on the planar, Q4_K and Q6_K weights; 2 also
+  // for calls with k <= 64 sampling rows there and all-greedy calls on the
+  // vector-unit weights (F32, Q4_0, Q4_1)
   int fuse = 1;
   DevBuf large_retry;           // two-pass large-k rows handed back
   DevBuf large_replay;          // slot-history replays asked for by the large-k kernel
@@ -756,7 +756,7 @@ int gemv_setup(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, const 
   const int64_t wpb = hs::kGemvThreads / 64;
   g.blocks = (int32_t)std::min<int64_t>((steps + wpb - 1) / wpb, 1 << 20);
   if (M > 65535) return fail(HS_ERR_UNSUPPORTED, "M %d above 65535", M);
-  if (w_type == hs::kW_Q6_K) {   // the hand-over slots of tiles cut between waves
+  if (w_type == hs::kW_Q6_K || w_type == hs::kW_Q4_K) {   // the hand-over slots of tiles cut between waves
     int cus = 0;
     HS_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device));
     g.part_cap = cus * hs::kGemvWavesPerCU;
@@ -1274,8 +1274,8 @@ int hs_gemv_device_ex(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx,
 
 namespace {
 
-// The lm_head GEMV and the sampler on its M rows: one launch of the planar
-// or Q6_K GEMV that samples its own rows when every row is greedy or takes
+// The lm_head GEMV and the sampler on its M rows: one launch of the planar,
+// Q4_K or Q6_K GEMV that samples its own rows when every row is greedy or takes
 // k <= 64 candidates with at most the repetition penalty (and the vocabulary
 // fits its per-wave record); otherwise the GEMV, then
 // hs_sample_batch_device.  Either way the logits hold the penalised values
@@ -1289,11 +1289,11 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
   if (!ctx) return fail(HS_ERR_INVALID_ARGUMENT, "null context");
   if (!w) return fail(HS_ERR_INVALID_ARGUMENT, "null weights");
   const bool tern = hs::tern_quant_bytes(w->type) > 0;
-  // sampling rows fuse into the planar and Q6_K GEMVs only (their 16-row
-  // tiles); the vector-unit GEMVs fuse greedy rows only when asked
+  // sampling rows fuse into the planar, Q4_K and Q6_K GEMVs only (their
+  // 16-row tiles); the vector-unit GEMVs fuse greedy rows only when asked
   // (HS_LMHEAD_FUSE=2): their argmax launch measured 2.7 us (no penalty) to
   // 9 us (repetition penalty) slower than the GEMV and the argmax launch
-  const bool sample_ok = tern || w->type == hs::kW_Q6_K;
+  const bool sample_ok = tern || w->type == hs::kW_Q6_K || w->type == hs::kW_Q4_K;
   bool fused = ctx->fuse && (sample_ok || ctx->fuse >= 2) && M > 0 && w->rows > 0 && configs &&
                d_uniforms && d_tokens && (d_hist_ids == nullptr) == (d_hist_offsets == nullptr);
   std::vector<hs::RowPlan> plans;
@@ -1325,7 +1325,7 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
     const int blocks = skip     ? 0
                        : greedy ? hs::argmax_fused_grid(g)
                        : tern   ? hs::tern_sample_grid(g)
-                                : hs::q6k_sample_grid(g);
+                                : hs::kq_sample_grid(g);
     if (blocks > 0) {
       const size_t nwv = greedy ? 0 : (size_t)M * blocks * hs::fuse_waves_per_block(w->type);
       if (!greedy) {
@@ -1356,7 +1356,7 @@ int lm_head_sample(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx, co
       if (rc) return rc;
       const hipError_t e = greedy ? hs::launch_argmax_fused(g, f, st, ev, ctx->done_ev)
                            : tern ? hs::launch_tern_sample(g, f, st, ev, ctx->done_ev)
-                                  : hs::launch_q6k_sample(g, f, st, ev, ctx->done_ev);
+                                  : hs::launch_kq_sample(g, f, st, ev, ctx->done_ev);
       if (e != hipSuccess) {
         (void)leave_stream(ctx, st, false);
         return fail(HS_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));

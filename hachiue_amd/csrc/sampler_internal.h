@@ -238,7 +238,7 @@ struct GemvArgs {
 // of 512), from x [M][ldx] and optional +-1 signs [K].
 hipError_t launch_hadamard(const float *x, int64_t ldx, const float *signs, float *out, int M,
                            int K, hipStream_t stream);
-constexpr int kGemvWavesPerCU = 16;   // Q6_K: the part_cap a CU needs
+constexpr int kGemvWavesPerCU = 16;   // Q4_K, Q6_K: the part_cap a CU needs
 // Block formats go through LDS in batches of row steps (a step: the rows of
 // one wave pass, 64 units): steps per batch and 16-byte reads per lane that
 // hold a batch (its bytes plus the alignment of its start).
@@ -323,9 +323,10 @@ int argmax_fused_grid(const GemvArgs &g);
 int tern_sample_grid(const GemvArgs &g);
 // Waves per workgroup of the one-launch kernel for lm_head weights of `type`.
 int fuse_waves_per_block(int type);
-// The same one launch for Q6_K lm_heads (greedy rows included), and its grid.
-hipError_t launch_q6k_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
-                             hipEvent_t *ev, hipEvent_t done);
-int q6k_sample_grid(const GemvArgs &g);
+// The same one launch for Q4_K and Q6_K lm_heads (greedy rows included), and
+// its grid.
+hipError_t launch_kq_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
+                            hipEvent_t *ev, hipEvent_t done);
+int kq_sample_grid(const GemvArgs &g);
 
 }  // namespace hs

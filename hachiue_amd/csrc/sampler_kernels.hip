@@ -48,7 +48,7 @@
 
 #include "hachiue_sampler.h"
 #include "blk_gemv.h"
-#include "q6k_gemv.h"
+#include "kq_gemv.h"
 #include "tern_gemv.h"
 
 namespace hs {
@@ -6207,9 +6207,11 @@ void gemv_tern_argmax_kernel(GemvArgs g, FuseArgs f) {
   fuse_argmax_finish<NW>(g, f, m, epi.best, wbest);
 }
 
-// The same on the Q6_K body (its grid and LDS as gemv_q6k_mfma_kernel's).
-__global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_argmax_kernel(GemvArgs g, FuseArgs f) {
-  constexpr int NW = q6m::kWaves;
+// The same on the Q4_K and Q6_K bodies (the grid and LDS of the plain
+// matrix-core GEMV, gemv_kq_mfma_kernel).
+template <int FMT>
+__global__ __launch_bounds__(KqBody<FMT>::kThreads, 2) void gemv_kq_argmax_kernel(GemvArgs g, FuseArgs f) {
+  constexpr int NW = KqBody<FMT>::kWaves;
   extern __shared__ uint4 qlds[];
   __shared__ int32_t rset[kFuseSetSlots];
   __shared__ unsigned long long wbest[NW];
@@ -6222,7 +6224,7 @@ __global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_argmax_kernel(GemvA
   if (rep) fuse_rep_set(f, m, g.N, rset);
   // (the body's first barrier completes the set)
   ArgmaxEpi epi{g.y + (int64_t)m * g.ldy, rep ? rset : nullptr, load_scalar(&plan->rep), 0ull};
-  q6k_gemv_body(g, reinterpret_cast<uint8_t *>(qlds), epi);
+  KqBody<FMT>::run(g, reinterpret_cast<uint8_t *>(qlds), epi);
   fuse_argmax_finish<NW>(g, f, m, epi.best, wbest);
 }
 
@@ -6304,18 +6306,38 @@ hipError_t blk_argmax(const GemvArgs &g, const FuseArgs &f, hipStream_t stream, 
   }
 }
 
-int q6k_argmax_grid(const GemvArgs &g) {
+template <int FMT>
+int kq_argmax_grid(const GemvArgs &g) {
+  using B = KqBody<FMT>;
   const int ntiles = (g.N + 15) / 16;
-  const int res = resident_blocks(reinterpret_cast<const void *>(gemv_q6k_argmax_kernel),
-                                  (uint32_t)gemv_q6k_mfma_lds_bytes(g.K), q6m::kThreads);
-  int blocks = (ntiles + q6m::kWaves - 1) / q6m::kWaves;
+  const int res = resident_blocks(reinterpret_cast<const void *>(gemv_kq_argmax_kernel<FMT>),
+                                  (uint32_t)B::lds(g.K), B::kThreads);
+  int blocks = (ntiles + B::kWaves - 1) / B::kWaves;
   blocks = blocks < res ? blocks : res;
-  blocks = blocks < g.part_cap / q6m::kWaves ? blocks : g.part_cap / q6m::kWaves;
+  blocks = blocks < g.part_cap / B::kWaves ? blocks : g.part_cap / B::kWaves;
   return blocks >= 1 && g.part && g.tile_cnt ? blocks : 0;
 }
 
+template <int FMT>
+hipError_t launch_kq_argmax(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
+                            hipEvent_t *ev, hipEvent_t done) {
+  using B = KqBody<FMT>;
+  const int blocks = kq_argmax_grid<FMT>(g);
+  if (blocks < 1) return hipErrorInvalidValue;
+  const size_t lds = B::lds(g.K);
+  const dim3 grid((unsigned)blocks, (unsigned)g.M), block(B::kThreads);
+  if (ev)
+    hipExtLaunchKernelGGL(gemv_kq_argmax_kernel<FMT>, grid, block, lds, stream, ev[0], ev[1], 0u, g, f);
+  else if (done)
+    hipExtLaunchKernelGGL(gemv_kq_argmax_kernel<FMT>, grid, block, lds, stream, nullptr, done, 0u, g, f);
+  else
+    hipLaunchKernelGGL(gemv_kq_argmax_kernel<FMT>, grid, block, lds, stream, g, f);
+  return hipGetLastError();
+}
+
 int argmax_fused_grid(const GemvArgs &g) {
-  if (g.type == kW_Q6_K) return q6k_argmax_grid(g);
+  if (g.type == kW_Q6_K) return kq_argmax_grid<kW_Q6_K>(g);
+  if (g.type == kW_Q4_K) return kq_argmax_grid<kW_Q4_K>(g);
   if (tern_quant_bytes(g.type) == 0) {
     int blocks = 0;
     return blk_argmax(g, FuseArgs{}, nullptr, nullptr, nullptr, &blocks) == hipSuccess ? blocks : 0;
@@ -6349,19 +6371,8 @@ hipError_t launch_argmax_fused(const GemvArgs &g, const FuseArgs &f, hipStream_t
     case kW_Q1_0: return go(gemv_tern_argmax_kernel<kW_Q1_0>, tm::waves<kW_Q1_0>());
     case kW_PQ2_0: return go(gemv_tern_argmax_kernel<kW_PQ2_0>, tm::waves<kW_PQ2_0>());
     case kW_PTQ1_0: return go(gemv_tern_argmax_kernel<kW_PTQ1_0>, tm::waves<kW_PTQ1_0>());
-    case kW_Q6_K: {
-      const int blocks = q6k_argmax_grid(g);
-      if (blocks < 1) return hipErrorInvalidValue;
-      const size_t lds = gemv_q6k_mfma_lds_bytes(g.K);
-      const dim3 grid((unsigned)blocks, (unsigned)g.M), block(q6m::kThreads);
-      if (ev)
-        hipExtLaunchKernelGGL(gemv_q6k_argmax_kernel, grid, block, lds, stream, ev[0], ev[1], 0u, g, f);
-      else if (done)
-        hipExtLaunchKernelGGL(gemv_q6k_argmax_kernel, grid, block, lds, stream, nullptr, done, 0u, g, f);
-      else
-        hipLaunchKernelGGL(gemv_q6k_argmax_kernel, grid, block, lds, stream, g, f);
-      return hipGetLastError();
-    }
+    case kW_Q6_K: return launch_kq_argmax<kW_Q6_K>(g, f, stream, ev, done);
+    case kW_Q4_K: return launch_kq_argmax<kW_Q4_K>(g, f, stream, ev, done);
     default: return blk_argmax(g, f, stream, ev, done, nullptr);
   }
 }
@@ -6390,27 +6401,26 @@ hipError_t launch_tern_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t 
   }
 }
 
-// ---- the Q6_K lm_head GEMV that samples its rows
+// ---- the Q4_K and Q6_K lm_head GEMVs that sample their rows
 //
-// gemv_tern_sample_kernel on the Q6_K body (q6k_gemv.h): two 8-wave
-// workgroups per CU, each recording at most kQ6FuseTiles tiles a wave in
-// buffers that follow the body's LDS.  After the loop the slab rings are
-// free: the last workgroup's loads, the histogram and the candidates go
+// gemv_tern_sample_kernel on the K-quant bodies (q4k_gemv.h, q6k_gemv.h):
+// two 8-wave workgroups per CU, each recording at most kKqFuseTiles tiles a
+// wave in buffers that follow the body's LDS.  After the loop the slab rings
+// are free: the last workgroup's loads, the histogram and the candidates go
 // there.  All-greedy calls take it too (its greedy branch keeps each
 // workgroup's packed maximum).
-constexpr int kQ6FuseTiles = 4;
-__host__ __device__ inline size_t q6k_ring_off(int K) {   // the A tables, then the rings
-  return (size_t)(K / 64) * 256 + (size_t)(K / 16) * 32;
+constexpr int kKqFuseTiles = 4;
+template <int FMT>
+size_t kq_sample_lds_bytes(int K) {
+  return KqBody<FMT>::lds(K) + (size_t)KqBody<FMT>::kWaves * kKqFuseTiles * 16 * sizeof(uint2);
 }
-size_t q6k_sample_lds_bytes(int K) {
-  return gemv_q6k_mfma_lds_bytes(K) + (size_t)q6m::kWaves * kQ6FuseTiles * 16 * sizeof(uint2);
-}
-static_assert((size_t)q6m::kWaves * q6m::kNB * q6m::kSlabBytes >=
-                  (size_t)kFuseMore * 4 + (size_t)kFuseStage * 12,
+static_assert(KqBody<kW_Q6_K>::kRingBytes >= (size_t)kFuseMore * 4 + (size_t)kFuseStage * 12 &&
+                  KqBody<kW_Q4_K>::kRingBytes >= (size_t)kFuseMore * 4 + (size_t)kFuseStage * 12,
               "the rings hold the waves read again and the candidates");
 
-__global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_sample_kernel(GemvArgs g, FuseArgs f) {
-  constexpr int NW = q6m::kWaves;
+template <int FMT>
+__global__ __launch_bounds__(KqBody<FMT>::kThreads, 2) void gemv_kq_sample_kernel(GemvArgs g, FuseArgs f) {
+  constexpr int NW = KqBody<FMT>::kWaves;
   extern __shared__ uint4 qlds[];
   __shared__ FuseSmem fs;
   const int tid = threadIdx.x, wave = tid >> 6;
@@ -6425,50 +6435,70 @@ __global__ __launch_bounds__(q6m::kThreads, 2) void gemv_q6k_sample_kernel(GemvA
   // (the body's first barrier completes the set)
 
   uint8_t *lb = reinterpret_cast<uint8_t *>(qlds);
-  uint2 *rec = reinterpret_cast<uint2 *>(lb + gemv_q6k_mfma_lds_bytes(g.K));
-  RecordEpi epi{y, rec + wave * kQ6FuseTiles * 16, rep ? fs.rset : nullptr, 0, kQ6FuseTiles};
-  q6k_gemv_body(g, lb, epi);
-  int32_t *more = reinterpret_cast<int32_t *>(lb + q6k_ring_off(g.K));   // the rings
-  fuse_sample_finish<NW>(g, f, m, epi.nt, kQ6FuseTiles, rec, more,
+  uint2 *rec = reinterpret_cast<uint2 *>(lb + KqBody<FMT>::lds(g.K));
+  RecordEpi epi{y, rec + wave * kKqFuseTiles * 16, rep ? fs.rset : nullptr, 0, kKqFuseTiles};
+  KqBody<FMT>::run(g, lb, epi);
+  int32_t *more = reinterpret_cast<int32_t *>(lb + KqBody<FMT>::ring_off(g.K));   // the rings
+  fuse_sample_finish<NW>(g, f, m, epi.nt, kKqFuseTiles, rec, more,
                          reinterpret_cast<unsigned long long *>(more + kFuseMore), fs);
 }
 
-// Its grid: as the Q6_K GEMV's (gemv_q6k_mfma_kernel's launch); 0 when a
-// wave would complete more than kQ6FuseTiles tiles (its whole tiles and at
+// Its grid: as the plain GEMV's (gemv_kq_mfma_kernel's launch); 0 when a
+// wave would complete more than kKqFuseTiles tiles (its whole tiles and at
 // most one part of a tail tile) or the last workgroup's threads would read
 // more than kFuseWavesPerThread waves' entries.
-int q6k_sample_grid(const GemvArgs &g) {
-  const size_t lds = q6k_sample_lds_bytes(g.K);
+template <int FMT>
+int kq_sample_grid_t(const GemvArgs &g) {
+  using B = KqBody<FMT>;
+  const size_t lds = kq_sample_lds_bytes<FMT>(g.K);
   const int ntiles = (g.N + 15) / 16;
-  const int res = resident_blocks(reinterpret_cast<const void *>(gemv_q6k_sample_kernel),
-                                  (uint32_t)lds, q6m::kThreads);
-  int blocks = (ntiles + q6m::kWaves - 1) / q6m::kWaves;
+  const int res = resident_blocks(reinterpret_cast<const void *>(gemv_kq_sample_kernel<FMT>),
+                                  (uint32_t)lds, B::kThreads);
+  int blocks = (ntiles + B::kWaves - 1) / B::kWaves;
   blocks = blocks < res ? blocks : res;
-  blocks = blocks < g.part_cap / q6m::kWaves ? blocks : g.part_cap / q6m::kWaves;
+  blocks = blocks < g.part_cap / B::kWaves ? blocks : g.part_cap / B::kWaves;
   if (blocks < 1 || !g.part || !g.tile_cnt) return 0;
-  const int nw = blocks * q6m::kWaves;
+  const int nw = blocks * B::kWaves;
   const int tiles = ntiles / nw + (ntiles % nw ? 1 : 0);
-  return tiles <= kQ6FuseTiles && nw <= kFuseWavesPerThread * q6m::kThreads ? blocks : 0;
+  return tiles <= kKqFuseTiles && nw <= kFuseWavesPerThread * B::kThreads ? blocks : 0;
 }
 
-int fuse_waves_per_block(int type) { return type == kW_Q6_K ? q6m::kWaves : 16; }
+int kq_sample_grid(const GemvArgs &g) {
+  return g.type == kW_Q6_K   ? kq_sample_grid_t<kW_Q6_K>(g)
+         : g.type == kW_Q4_K ? kq_sample_grid_t<kW_Q4_K>(g)
+                             : 0;
+}
+
+int fuse_waves_per_block(int type) {
+  return type == kW_Q6_K ? KqBody<kW_Q6_K>::kWaves : type == kW_Q4_K ? KqBody<kW_Q4_K>::kWaves : 16;
+}
 static_assert(tm::waves<kW_Q1_0>() == 16 && tm::waves<kW_PQ2_0>() == 16 &&
                   tm::waves<kW_PTQ1_0>() == 16,
               "fuse_waves_per_block: the planar kernels' waves");
 
-hipError_t launch_q6k_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
-                             hipEvent_t *ev, hipEvent_t done) {
-  const int blocks = q6k_sample_grid(g);
+template <int FMT>
+hipError_t launch_kq_sample_t(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
+                              hipEvent_t *ev, hipEvent_t done) {
+  const int blocks = kq_sample_grid_t<FMT>(g);
   if (blocks < 1 || blocks != f.blocks) return hipErrorInvalidValue;
-  const size_t lds = q6k_sample_lds_bytes(g.K);
-  const dim3 grid((unsigned)blocks, (unsigned)g.M), block(q6m::kThreads);
+  const size_t lds = kq_sample_lds_bytes<FMT>(g.K);
+  const dim3 grid((unsigned)blocks, (unsigned)g.M), block(KqBody<FMT>::kThreads);
   if (ev)
-    hipExtLaunchKernelGGL(gemv_q6k_sample_kernel, grid, block, lds, stream, ev[0], ev[1], 0u, g, f);
+    hipExtLaunchKernelGGL(gemv_kq_sample_kernel<FMT>, grid, block, lds, stream, ev[0], ev[1], 0u, g, f);
   else if (done)
-    hipExtLaunchKernelGGL(gemv_q6k_sample_kernel, grid, block, lds, stream, nullptr, done, 0u, g, f);
+    hipExtLaunchKernelGGL(gemv_kq_sample_kernel<FMT>, grid, block, lds, stream, nullptr, done, 0u, g, f);
   else
-    hipLaunchKernelGGL(gemv_q6k_sample_kernel, grid, block, lds, stream, g, f);
+    hipLaunchKernelGGL(gemv_kq_sample_kernel<FMT>, grid, block, lds, stream, g, f);
   return hipGetLastError();
+}
+
+hipError_t launch_kq_sample(const GemvArgs &g, const FuseArgs &f, hipStream_t stream,
+                            hipEvent_t *ev, hipEvent_t done) {
+  switch (g.type) {
+    case kW_Q6_K: return launch_kq_sample_t<kW_Q6_K>(g, f, stream, ev, done);
+    case kW_Q4_K: return launch_kq_sample_t<kW_Q4_K>(g, f, stream, ev, done);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 // ---------------------------------------------------------------- launch
@@ -6505,14 +6535,16 @@ hipError_t prepare_kernels() {
       if ((e = hipFuncSetAttribute(fk, hipFuncAttributeMaxDynamicSharedMemorySize,
                                    (int)tern_sample_lds_bytes(kGemvMaxK, 16))) != hipSuccess)
         return e;
-    if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q6k_sample_kernel),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 (int)q6k_sample_lds_bytes(kGemvMaxK))) != hipSuccess)
-      return e;
-    if ((e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_q6k_argmax_kernel),
-                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                 (int)gemv_q6k_mfma_lds_bytes(kGemvMaxK))) != hipSuccess)
-      return e;
+    const void *kk[4] = {reinterpret_cast<const void *>(&gemv_kq_sample_kernel<kW_Q6_K>),
+                         reinterpret_cast<const void *>(&gemv_kq_sample_kernel<kW_Q4_K>),
+                         reinterpret_cast<const void *>(&gemv_kq_argmax_kernel<kW_Q6_K>),
+                         reinterpret_cast<const void *>(&gemv_kq_argmax_kernel<kW_Q4_K>)};
+    const size_t kl[4] = {kq_sample_lds_bytes<kW_Q6_K>(kGemvMaxK), kq_sample_lds_bytes<kW_Q4_K>(kGemvMaxK),
+                          KqBody<kW_Q6_K>::lds(kGemvMaxK), KqBody<kW_Q4_K>::lds(kGemvMaxK)};
+    for (int i = 0; i < 4; ++i)
+      if ((e = hipFuncSetAttribute(kk[i], hipFuncAttributeMaxDynamicSharedMemorySize, (int)kl[i])) !=
+          hipSuccess)
+        return e;
     const void *ak[3] = {reinterpret_cast<const void *>(&gemv_tern_argmax_kernel<kW_Q1_0>),
                          reinterpret_cast<const void *>(&gemv_tern_argmax_kernel<kW_PQ2_0>),
                          reinterpret_cast<const void *>(&gemv_tern_argmax_kernel<kW_PTQ1_0>)};

@@ -195,10 +195,10 @@ int hs_argmax(hs_context *ctx, const float *logits, int32_t rows,
  * 12 Q4_K, 14 Q6_K), N rows of K weights back to back, as the reference
  * uploads them (src/engine.ts:772-800).  K a multiple of the block size,
  * K <= 4096, W at most 4 GiB and 16-byte aligned.  Results differ from the
- * reference's binary32 sums by rounding only.  Q6_K runs on the matrix cores
- * with x held as integer limbs: a non-finite element of an x row makes every
- * result of that row NaN (the reference's binary32 sums give NaN or
- * +-Infinity there).  Asynchronous on `stream`. */
+ * reference's binary32 sums by rounding only.  Q4_K and Q6_K run on the
+ * matrix cores with x held as integer limbs: a non-finite element of an x row
+ * makes every result of that row NaN (the reference's binary32 sums give NaN
+ * or +-Infinity there).  Asynchronous on `stream`. */
 int hs_gemv_device(hs_context *ctx, const float *d_x, int32_t M, int64_t ldx,
                    int32_t K, const void *d_w, int32_t w_type, int32_t N,
                    float *d_y, int64_t ldy, void *stream);

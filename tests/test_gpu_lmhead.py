@@ -119,12 +119,13 @@ def test_lm_head_then_sample(sampler):
     assert np.array_equal(pen.view(np.uint32), ref.view(np.uint32))
 
 
-def test_q6k_heavy_tailed_activations(sampler):
-    """The Q6_K kernel holds x as four int8 limbs per 16-position scale group,
-    exact to 2^-28 of the group's largest |x|.  Hidden states with outlier
-    channels (a few positions 100-1000x the rest) and exact zeros stay within
-    the bound."""
-    wtype, K, N = o.W_Q6_K, 2048, 4099
+@pytest.mark.parametrize("fmt", ["q4_k", "q6_k"])
+def test_kquant_heavy_tailed_activations(sampler, fmt):
+    """The Q4_K and Q6_K kernels hold x as four int8 limbs per 16-position
+    group, exact to 2^-28 of the group's largest |x|.  Hidden states with
+    outlier channels (a few positions 100-1000x the rest) and exact zeros
+    stay within the bound."""
+    wtype, K, N = FORMATS[fmt], 2048, 4099
     rng = np.random.default_rng(77)
     w = random_blocks(wtype, N, K, rng)
     x = rng.standard_normal((3, K)).astype(np.float32)
@@ -309,10 +310,11 @@ def test_lm_head_then_sample_planar_folded(sampler):
     assert np.array_equal(pen.view(np.uint32), ref.view(np.uint32))
 
 
-def test_gemv_q6k_nonfinite_input(sampler):
-    """The Q6_K matrix-core kernel holds x as integer limbs: a row of x with a
-    NaN or an infinity gives NaN for every result of that row."""
-    wtype, K, N = o.W_Q6_K, 512, 40
+@pytest.mark.parametrize("fmt", ["q4_k", "q6_k"])
+def test_gemv_kquant_nonfinite_input(sampler, fmt):
+    """The Q4_K and Q6_K matrix-core kernels hold x as integer limbs: a row of
+    x with a NaN or an infinity gives NaN for every result of that row."""
+    wtype, K, N = FORMATS[fmt], 512, 40
     rng = np.random.default_rng(6)
     w = random_blocks(wtype, N, K, rng)
     x = rng.standard_normal((3, K)).astype(np.float32)

@@ -1,7 +1,7 @@
 """GPU parity of the lm_head GEMVs that sample their own rows in one
-launch (hs_lm_head_sample_device_ex; the planar and Q6_K formats when
-every row is greedy or takes k <= 64 candidates with at most the repetition
-penalty, the vector-unit formats when every row is greedy;
+launch (hs_lm_head_sample_device_ex; the planar, Q4_K and Q6_K formats
+when every row is greedy or takes k <= 64 candidates with at most the
+repetition penalty, the vector-unit formats when every row is greedy;
 src/engine.ts:1493-1531 then src/sampler.ts).
 The logits it leaves (penalised where the history asks, src/sampler.ts:
 24-33) must equal, bit for bit, the GEMV's own output with the oracle's
@@ -80,7 +80,7 @@ CFGS = [dict(temperature=0.7, topK=40, topP=0.9, repetitionPenalty=1.1),
         dict(temperature=0.9, topK=1)]
 
 
-FUSED = dict(PLANAR, q6_k=o.W_Q6_K)
+FUSED = dict(PLANAR, q4_k=o.W_Q4_K, q6_k=o.W_Q6_K)
 
 
 @pytest.mark.parametrize("fmt", list(FUSED))
@@ -104,7 +104,7 @@ def test_fused_full_vocabulary(sampler, fctx, unfused, fmt):
     assert np.array_equal(pen.view(np.uint32), pen2.view(np.uint32))
 
 
-@pytest.mark.parametrize("fmt", ["q1_0", "q6_k"])
+@pytest.mark.parametrize("fmt", ["q1_0", "q4_k", "q6_k"])
 @pytest.mark.parametrize("N", [1, 15, 17, 1000, 4099, 65537])
 def test_fused_small_and_ragged_vocabularies(sampler, fctx, N, fmt):
     wtype, K = FUSED[fmt], 256
@@ -167,7 +167,7 @@ def test_fused_hadamard_folded_and_mixed_rows(sampler, fctx, unfused):
         assert np.array_equal(pen.view(np.uint32), pen2.view(np.uint32))
 
 
-@pytest.mark.parametrize("fmt", ["q1_0", "q6_k"])
+@pytest.mark.parametrize("fmt", ["q1_0", "q4_k", "q6_k"])
 def test_fused_repeated_calls_reset_state(sampler, fctx, fmt):
     """Per-row state (pool, bound, counters) is zero between calls: the same
     call three times, then a call with fewer rows, each exact."""
@@ -191,7 +191,7 @@ def test_fused_repeated_calls_reset_state(sampler, fctx, fmt):
     assert tok.tolist() == want[:2]
 
 
-@pytest.mark.parametrize("fmt", ["q1_0", "q6_k"])
+@pytest.mark.parametrize("fmt", ["q1_0", "q4_k", "q6_k"])
 @pytest.mark.parametrize("cfg", [dict(topK=40), dict(temperature=0.0, repetitionPenalty=1.2)])
 def test_fused_is_one_launch(sampler, fctx, unfused, fmt, cfg):
     """The qualifying call launches the lm_head kernel alone (the sampler's
@@ -217,7 +217,7 @@ def test_fused_is_one_launch(sampler, fctx, unfused, fmt, cfg):
         assert (others == {}) == fused, others
 
 
-BLOCK = {"f32": o.W_F32, "q4_0": o.W_Q4_0, "q4_1": o.W_Q4_1, "q4_k": o.W_Q4_K}
+BLOCK = {"f32": o.W_F32, "q4_0": o.W_Q4_0, "q4_1": o.W_Q4_1}
 
 
 @pytest.mark.parametrize("fmt", list(BLOCK))
