@@ -1,4 +1,4 @@
-// The F32, Q4_0, Q4_1 and Q4_K lm_head GEMVs on the vector units, as
+// The F32, Q4_0 and Q4_1 lm_head GEMVs on the vector units, as
 // device-function bodies shared by the GEMV kernels (lmhead_kernels.hip) and
 // the all-greedy GEMV that keeps its rows' argmax (sampler_kernels.hip): the
 // kernels differ only in what happens to each row's result (the epilogue).
@@ -192,60 +192,6 @@ template <> struct Unit<kW_Q4_1> {
       hi = dot4u8((a.b[v + 1] >> 4) & 0x0F0F0F0Fu, x + 16 + 4 * v, hi);
     }
     return fmaf(h2f(a.b[0]), lo + hi, h2f(a.b[0] >> 16) * s[0]);
-  }
-};
-
-// Q4_K: super-block s = j / 8 (header: d, dmin, 12 bytes of 6-bit scales and
-// mins; 128 bytes of nibbles), part t = j % 8: the 16 bytes
-// 16 + 32 (t / 2) + 16 (t % 2) of the nibbles.  Their low nibbles are
-// weights 64 p + 16 h + i of sub-block 2 p, the high ones 64 p + 32 + 16 h + i
-// of sub-block 2 p + 1 (p = t / 2, h = t % 2, i < 16);
-// w = d sc q - dmin mn.
-template <> struct Unit<kW_Q4_K> {
-  static constexpr int W = 32;
-  struct Raw { uint32_t hd[4], q[4]; };
-  static __device__ __forceinline__ int xidx(int j, int i) {
-    const int s = j >> 3, t = j & 7, p = t >> 1, h = t & 1;
-    return 256 * s + 64 * p + 16 * h + (i < 16 ? i : 16 + i);
-  }
-  static __device__ __forceinline__ void sums(const float *x, float *s) {
-    float a = 0.f, b = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) { a += x[i]; b += x[16 + i]; }
-    s[0] = a;
-    s[1] = b;
-  }
-  template <typename S>
-  static __device__ __forceinline__ void load(const S &r, uint32_t rb, int j, Raw &a) {
-    const int sb = j >> 3, t = j & 7, p = t >> 1, h = t & 1;
-    const uint32_t o = rb + 144u * sb;
-    r.q4(o, a.hd);
-    r.q4(o + 16u + 32u * p + 16u * h, a.q);
-  }
-  static __device__ __forceinline__ float dot(const Raw &a, int j, const float *x, const float *s) {
-    const int p = (j & 7) >> 1;
-    // 6-bit scale / min of sub-block k (src/gguf.ts:178-186).  Header bytes
-    // 4..7, 8..11, 12..15 are hd[1], hd[2], hd[3]; byte k & 3 of each is
-    // taken with a shift, so no register is indexed at run time.
-    auto scmin = [&](int k, float &sc, float &mn) {
-      const uint32_t sh = 8u * (uint32_t)(k & 3);
-      const uint32_t b1 = a.hd[1] >> sh, b2 = a.hd[2] >> sh, b3 = a.hd[3] >> sh;
-      const uint32_t u = k < 4 ? (b1 & 63u) : ((b3 & 15u) | (((b1 >> 6) & 3u) << 4));
-      const uint32_t c = k < 4 ? (b2 & 63u) : (((b3 >> 4) & 15u) | (((b2 >> 6) & 3u) << 4));
-      sc = (float)u;
-      mn = (float)c;
-    };
-    float sc0, mn0, sc1, mn1;
-    scmin(2 * p, sc0, mn0);
-    scmin(2 * p + 1, sc1, mn1);
-    float lo = 0.f, hi = 0.f;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      lo = dot4u8(a.q[v] & 0x0F0F0F0Fu, x + 4 * v, lo);
-      hi = dot4u8((a.q[v] >> 4) & 0x0F0F0F0Fu, x + 16 + 4 * v, hi);
-    }
-    const float d = h2f(a.hd[0]), dmin = h2f(a.hd[0] >> 16);
-    return d * fmaf(sc0, lo, sc1 * hi) - dmin * fmaf(mn0, s[0], mn1 * s[1]);
   }
 };
 

@@ -6228,7 +6228,7 @@ __global__ __launch_bounds__(KqBody<FMT>::kThreads, 2) void gemv_kq_argmax_kerne
   fuse_argmax_finish<NW>(g, f, m, epi.best, wbest);
 }
 
-// The same for F32, Q4_0, Q4_1 and Q4_K (the vector-unit bodies, blk_gemv.h;
+// The same for F32, Q4_0 and Q4_1 (the vector-unit bodies, blk_gemv.h;
 // LDSB: the block formats' LDS batches), on the GEMV's grid.
 template <int FMT, int NRU, bool LDSB>
 __global__ __launch_bounds__(kGemvThreads) void gemv_blk_argmax_kernel(GemvArgs g, FuseArgs f) {
@@ -6300,8 +6300,6 @@ hipError_t blk_argmax(const GemvArgs &g, const FuseArgs &f, hipStream_t stream, 
                              : launch_blk_argmax<kW_Q4_0, 1>(g, f, stream, ev, done, blocks_out);
     case kW_Q4_1: return two ? launch_blk_argmax<kW_Q4_1, 2>(g, f, stream, ev, done, blocks_out)
                              : launch_blk_argmax<kW_Q4_1, 1>(g, f, stream, ev, done, blocks_out);
-    case kW_Q4_K: return two ? launch_blk_argmax<kW_Q4_K, 2>(g, f, stream, ev, done, blocks_out)
-                             : launch_blk_argmax<kW_Q4_K, 1>(g, f, stream, ev, done, blocks_out);
     default: return hipErrorInvalidValue;
   }
 }
