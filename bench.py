@@ -544,6 +544,11 @@ def other_path(args) -> int:
         log(f"[bench] copy probe: {d_in[0].nbytes} bytes device to device")
     ms_per_step = total_ms / args.steps
     achieved = alg / (kms_avg * 1e-3) / 1e9
+    # measured HBM traffic of the matrix-core K-quant GEMV at its committed shape
+    traffic, traffic_note = None, None
+    if (args.path == "lmhead" and rows == 1 and not args.hadamard and lh.fmt in ("q4_k", "q6_k")):
+        traffic, traffic_note = load_traffic(f"lmhead_{lh.fmt.replace('_', '')}_{vocab}x{K}",
+                                             "gemv_kq_mfma_kernel")
     line = {
         "metric": f"{args.path}: {unit} and HBM GB/s (% roofline)",
         "value": round(count / (ms_per_step * 1e-3), 1),
@@ -556,8 +561,8 @@ def other_path(args) -> int:
                    "algorithmic_bytes_per_step": alg},
         "roofline": {"bound": "hbm", "kernel": kernel, "achieved": round(achieved, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel_ms": round(kms_avg, 5)},
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                     "traffic_source": traffic_note, "kernel_ms": round(kms_avg, 5)},
         "cpu_baseline": None,
         "parity": parity,
     }
